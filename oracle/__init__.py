@@ -1,0 +1,259 @@
+"""CPU oracle for the dense-contraction path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg import this package, and only as the checker (or the
+timed CPU baseline).  The product package ``cudeep_amd`` never imports it and
+has no CPU fallback.
+
+The arithmetic lives in ``oracle/oracle.c`` (built by ``oracle/Makefile``
+into ``liboracle.so``); each C routine cites the reference file:line it
+restates.  This module adds numpy wrappers and the error metrics used by the
+parity gates:
+
+* ``sgemm_seqfma``   -- reference SGEMM numerics, bit-exact
+  (``src/kernels/matmul_kernel.cu:499-520``, ``:632-647``).
+* ``dgemm``          -- fp64 yardstick.
+* ``gemm_tf32emu``   -- reference TF32 tensor-core GEMM, emulated
+  (``matmul_kernel.cu:179-214``; ``ptx_intrinsics.cuh:316-335``, ``:639-649``).
+* ``im2col`` / ``transpose_bias`` / ``conv2d_direct64``
+  (``src/kernels/conv_kernel.cu:32-65``, ``:74-93``, ``:113-159``).
+* ``colsum`` (``src/kernels/unary_kernel.cu:204-238``).
+* ``gelu`` / ``gelu_grad`` / ``relu`` / ``relu_grad``
+  (``src/kernels/activation_kernel.cu:19-52``, ``:256-319``).
+
+The reference itself cannot be built here (CUDA sources with inline PTX, no
+CUDA toolchain), so there is no ``oracle/_ref``; the restatements are pinned
+by the reference's own known-answer tests and by closed forms (see
+``tests/test_oracle.py``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so from oracle.c with the committed Makefile."""
+    src = os.path.join(_HERE, "oracle.c")
+    if force or not os.path.exists(_LIB_PATH) or \
+            os.path.getmtime(_LIB_PATH) < os.path.getmtime(src):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "all"],
+                       check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.orc_sgemm_seqfma_rows.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64,
+                                            _int, _int, _i64, _i64, _i64, _i64]
+        L.orc_dgemm_rows_f32in.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64,
+                                           _int, _int, _i64, _i64, _i64, _i64]
+        L.orc_dgemm_f64.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64,
+                                    _int, _int, _i64, _i64]
+        L.orc_gemm_tf32emu.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _int]
+        L.orc_tf32_round.argtypes = [ctypes.c_float, _int]
+        L.orc_tf32_round.restype = ctypes.c_float
+        L.orc_im2col.argtypes = [_vp, _vp] + [_i64] * 10
+        L.orc_transpose_bias.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64]
+        L.orc_conv2d_direct64.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 11
+        L.orc_colsum.argtypes = [_vp, _vp, _i64, _i64]
+        L.orc_gelu_vec.argtypes = [_vp, _vp, _i64]
+        L.orc_gelu_grad_vec.argtypes = [_vp, _vp, _i64]
+        L.orc_num_threads.restype = _int
+        L.orc_set_num_threads.argtypes = [_int]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(int(n))
+
+
+def _op_shape(X, trans):
+    r, c = X.shape
+    return (c, r) if trans else (r, c)
+
+
+def sgemm_seqfma(A, B, transA=False, transB=False, rows=None):
+    """op(A) @ op(B) with the reference SGEMM's per-output sequential fp32
+    FMA chain over ascending k (bit-exact restatement).  ``rows=(r0, r1)``
+    computes only output rows [r0, r1)."""
+    A, B = _c32(A), _c32(B)
+    M, K = _op_shape(A, transA)
+    K2, N = _op_shape(B, transB)
+    assert K == K2, (A.shape, B.shape, transA, transB)
+    r0, r1 = (0, M) if rows is None else rows
+    C = np.empty((r1 - r0, N), np.float32)
+    lib().orc_sgemm_seqfma_rows(_p(A), _p(B), _p(C), M, N, K, int(transA),
+                                int(transB), A.shape[1], B.shape[1], r0, r1)
+    return C
+
+
+def dgemm(A, B, transA=False, transB=False, rows=None):
+    """fp64 op(A) @ op(B) of fp32 (or fp64) operands; rows as above."""
+    if A.dtype == np.float64 and B.dtype == np.float64 and rows is None:
+        A, B = np.ascontiguousarray(A), np.ascontiguousarray(B)
+        M, K = _op_shape(A, transA)
+        _, N = _op_shape(B, transB)
+        C = np.empty((M, N), np.float64)
+        lib().orc_dgemm_f64(_p(A), _p(B), _p(C), M, N, K, int(transA),
+                            int(transB), A.shape[1], B.shape[1])
+        return C
+    A, B = _c32(A), _c32(B)
+    M, K = _op_shape(A, transA)
+    K2, N = _op_shape(B, transB)
+    assert K == K2
+    r0, r1 = (0, M) if rows is None else rows
+    C = np.empty((r1 - r0, N), np.float64)
+    lib().orc_dgemm_rows_f32in(_p(A), _p(B), _p(C), M, N, K, int(transA),
+                               int(transB), A.shape[1], B.shape[1], r0, r1)
+    return C
+
+
+def tf32_round(x, mode: str = "rz"):
+    """Round fp32 values to TF32 (10-bit mantissa); mode 'rz' or 'rne'."""
+    x = _c32(x)
+    u = x.view(np.uint32).copy()
+    finite = (u & 0x7F800000) != 0x7F800000
+    if mode == "rne":
+        lsb = (u >> 13) & 1
+        u = np.where(finite, u + np.uint32(0x0FFF) + lsb, u).astype(np.uint32)
+    elif mode != "rz":
+        raise ValueError(mode)
+    u = np.where(finite, u & np.uint32(0xFFFFE000), u).astype(np.uint32)
+    return u.view(np.float32)
+
+
+def gemm_tf32emu(A, B, mode: str = "rz"):
+    """Emulated reference TF32 tensor-core GEMM (ideal MMA, 8-term k chunks)."""
+    A, B = _c32(A), _c32(B)
+    M, K = A.shape
+    _, N = B.shape
+    C = np.empty((M, N), np.float32)
+    lib().orc_gemm_tf32emu(_p(A), _p(B), _p(C), M, N, K,
+                           {"rz": 0, "rne": 1}[mode])
+    return C
+
+
+def conv_out_size(i, k, s, p):
+    """conv_kernel.cu:235-236."""
+    return (i + 2 * p - k) // s + 1
+
+
+def im2col(x, KH, KW, SH=1, SW=1, PH=0, PW=0):
+    """Bit-exact im2col, layout [IC*KH*KW, B*OH*OW] (conv_kernel.cu:32-65)."""
+    x = _c32(x)
+    Bn, IC, IH, IW = x.shape
+    OH, OW = conv_out_size(IH, KH, SH, PH), conv_out_size(IW, KW, SW, PW)
+    col = np.empty((IC * KH * KW, Bn * OH * OW), np.float32)
+    lib().orc_im2col(_p(x), _p(col), Bn, IC, IH, IW, KH, KW, SH, SW, PH, PW)
+    return col
+
+
+def transpose_bias(src, OC, batch, spatial, bias=None):
+    """[OC, B*S] -> [B, OC, S] (+bias[oc]) (conv_kernel.cu:74-93)."""
+    src = _c32(src)
+    dst = np.empty((batch, OC, spatial), np.float32)
+    b = None if bias is None else _c32(bias)
+    lib().orc_transpose_bias(_p(src), _p(dst), None if b is None else _p(b),
+                             OC, batch, spatial)
+    return dst
+
+
+def conv2d_direct64(x, w, bias=None, stride=(1, 1), padding=(0, 0)):
+    """fp64 direct cross-correlation (conv_kernel.cu:113-159)."""
+    x, w = _c32(x), _c32(w)
+    Bn, IC, IH, IW = x.shape
+    OC, IC2, KH, KW = w.shape
+    assert IC == IC2
+    SH, SW = stride
+    PH, PW = padding
+    OH, OW = conv_out_size(IH, KH, SH, PH), conv_out_size(IW, KW, SW, PW)
+    out = np.empty((Bn, OC, OH, OW), np.float64)
+    b = None if bias is None else _c32(bias)
+    lib().orc_conv2d_direct64(_p(x), _p(w), None if b is None else _p(b), _p(out),
+                              Bn, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW)
+    return out
+
+
+def conv2d_ref_im2col(x, w, bias=None, stride=(1, 1), padding=(0, 0)):
+    """The reference's explicit im2col route restated on the CPU
+    (conv_kernel.cu:279-334): im2col -> seq-FMA SGEMM W[OC,Kcol]·col ->
+    transpose + bias.  Its error vs fp64 is the conv parity yardstick."""
+    x, w = _c32(x), _c32(w)
+    Bn = x.shape[0]
+    OC, IC, KH, KW = w.shape
+    col = im2col(x, KH, KW, stride[0], stride[1], padding[0], padding[1])
+    flat = sgemm_seqfma(w.reshape(OC, -1), col)
+    OH = conv_out_size(x.shape[2], KH, stride[0], padding[0])
+    OW = conv_out_size(x.shape[3], KW, stride[1], padding[1])
+    out = transpose_bias(flat, OC, Bn, OH * OW, bias)
+    return out.reshape(Bn, OC, OH, OW)
+
+
+def colsum(x):
+    """Serial fp32 column sums (unary_kernel.cu:204-238)."""
+    x = _c32(x)
+    r, c = x.shape
+    out = np.empty((c,), np.float32)
+    lib().orc_colsum(_p(x), _p(out), r, c)
+    return out
+
+
+def gelu(x):
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty_like(x)
+    lib().orc_gelu_vec(_p(x), _p(y), x.size)
+    return y
+
+
+def gelu_grad(x):
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty_like(x)
+    lib().orc_gelu_grad_vec(_p(x), _p(y), x.size)
+    return y
+
+
+def relu(x):
+    x = np.asarray(x, dtype=np.float64)
+    return np.where(x > 0, x, 0.0)
+
+
+def relu_grad(x):
+    return (np.asarray(x) > 0).astype(np.float64)
+
+
+def rel_fro(C, Cref) -> float:
+    """Relative Frobenius error ||C - Cref||_F / ||Cref||_F (in fp64)."""
+    C = np.asarray(C, dtype=np.float64)
+    Cref = np.asarray(Cref, dtype=np.float64)
+    num = np.linalg.norm((C - Cref).ravel())
+    den = np.linalg.norm(Cref.ravel())
+    return float(num / den) if den > 0 else float(num)

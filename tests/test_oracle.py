@@ -1,0 +1,284 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Every oracle routine is checked against (i) the reference's own known-answer
+tests (tests/golden/kats.json, from the reference's test files), and (ii)
+facts the mathematics fixes independently of the oracle's code: exact
+rational arithmetic on tiny inputs, closed forms, special cases that reduce
+to a library routine (numpy / torch fp64), and hand-built inputs whose result
+changes if a term is dropped, the order of accumulation changes, or the FMA
+is split into a multiply and an add.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle
+
+
+# ---------------------------------------------------------------------------
+# exact rational helpers (independent of the C code)
+# ---------------------------------------------------------------------------
+
+def round_f32(q: Fraction) -> np.float32:
+    """Correctly rounded (RNE) conversion of an exact rational to fp32."""
+    if q == 0:
+        return np.float32(0.0)
+    sign = -1 if q < 0 else 1
+    q = abs(q)
+    e = q.numerator.bit_length() - q.denominator.bit_length()
+    # normalise so that 2^e <= q < 2^(e+1)
+    while Fraction(2) ** e > q:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= q:
+        e += 1
+    e = max(e, -126)                      # subnormal range keeps exponent -126
+    ulp = Fraction(2) ** (e - 23)
+    n = q / ulp
+    fl = n.numerator // n.denominator
+    rem = n - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return np.float32(sign * float(fl * ulp))
+
+
+def fma_f32(a, b, c) -> np.float32:
+    return round_f32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+# ---------------------------------------------------------------------------
+# sequential-FMA SGEMM (matmul_kernel.cu:499-520)
+# ---------------------------------------------------------------------------
+
+def test_sgemm_kats(kats):
+    k = kats["matmul_2x2"]
+    C = oracle.sgemm_seqfma(np.array(k["A"], np.float32), np.array(k["B"], np.float32))
+    assert np.array_equal(C, np.array(k["C"], np.float32))
+    k = kats["matmul_diag_identity"]
+    C = oracle.sgemm_seqfma(np.array(k["A"], np.float32), np.array(k["B"], np.float32))
+    assert np.array_equal(C, np.array(k["C"], np.float32))
+    k = kats["matmul_partial_identity"]
+    C = oracle.sgemm_seqfma(np.array(k["A"], np.float32), np.array(k["B"], np.float32))
+    assert np.array_equal(C[0], np.array(k["C_row0"], np.float32))
+    k = kats["matmul_scaled_identity_8"]
+    A = np.array(k["A"], np.float32)
+    C = oracle.sgemm_seqfma(A, np.eye(8, dtype=np.float32))
+    assert np.allclose(C, A, atol=k["atol"])
+    for name in ("mma_identity", "mma_integer_pattern"):
+        k = kats[name]
+        C = oracle.sgemm_seqfma(np.array(k["A"], np.float32), np.array(k["B"], np.float32))
+        assert np.array_equal(C, np.array(k["C"], np.float32)), name
+
+
+def test_sgemm_is_fused_not_mul_add():
+    # (1+2^-12)^2 - 1 = 2^-11 + 2^-24 exactly with one rounding (FMA);
+    # a separate multiply rounds the product to 1+2^-11 first.
+    a = np.float32(1 + 2.0 ** -12)
+    A = np.array([[-1.0, a]], np.float32)
+    B = np.array([[1.0], [a]], np.float32)
+    C = oracle.sgemm_seqfma(A, B)
+    assert C[0, 0] == np.float32(2.0 ** -11 + 2.0 ** -24)
+
+
+def test_sgemm_accumulates_in_ascending_k():
+    # acc: 1e8 -> 1e8 (+1 lost, ulp=8) -> 0 -> 1.  Any other order gives 0 or 2.
+    A = np.array([[1e8, 1.0, -1e8, 1.0]], np.float32)
+    B = np.ones((4, 1), np.float32)
+    assert oracle.sgemm_seqfma(A, B)[0, 0] == np.float32(1.0)
+    # reversed k order starting from the other end gives a different value
+    assert oracle.sgemm_seqfma(A[:, ::-1].copy(), B)[0, 0] == np.float32(0.0)
+
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+def test_sgemm_matches_exact_fma_chain(tA, tB):
+    rng = np.random.default_rng(7)
+    M, N, K = 3, 5, 17
+    A = rng.standard_normal((K, M) if tA else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if tB else (K, N)).astype(np.float32)
+    opA = A.T if tA else A
+    opB = B.T if tB else B
+    C = oracle.sgemm_seqfma(A, B, transA=tA, transB=tB)
+    for i in range(M):
+        for j in range(N):
+            acc = np.float32(0.0)
+            for k in range(K):
+                acc = fma_f32(opA[i, k], opB[k, j], acc)
+            assert C[i, j] == acc, (i, j)
+
+
+def test_sgemm_blocked_equals_rowsample_and_fp64_error():
+    rng = np.random.default_rng(3)
+    M, N, K = 300, 520, 257           # crosses the 16-row / 256-col blocks
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    C = oracle.sgemm_seqfma(A, B)
+    part = oracle.sgemm_seqfma(A, B, rows=(37, 101))
+    assert np.array_equal(C[37:101], part)
+    C64 = A.astype(np.float64) @ B.astype(np.float64)
+    err = oracle.rel_fro(C, C64)
+    assert 1e-8 < err < 1e-6           # fp32 chain error at K=257
+    D = oracle.dgemm(A, B)
+    assert oracle.rel_fro(D, C64) < 1e-14
+    Dt = oracle.dgemm(A.T.copy(), B.T.copy(), transA=True, transB=True)
+    assert oracle.rel_fro(Dt, C64) < 1e-14
+
+
+# ---------------------------------------------------------------------------
+# TF32 emulation (matmul_kernel.cu:179-214)
+# ---------------------------------------------------------------------------
+
+def test_tf32_round_known_values():
+    one_half_ulp = np.float32(1 + 2.0 ** -11)     # exactly half a tf32 ulp
+    assert oracle.tf32_round(one_half_ulp, "rz") == 1.0
+    assert oracle.tf32_round(one_half_ulp, "rne") == 1.0            # tie -> even
+    x = np.float32(1 + 2.0 ** -10 + 2.0 ** -11)                    # tie, odd lsb
+    assert oracle.tf32_round(x, "rne") == np.float32(1 + 2.0 ** -9)
+    assert oracle.tf32_round(x, "rz") == np.float32(1 + 2.0 ** -10)
+    y = np.float32(-(1 + 2.0 ** -11 + 2.0 ** -20))                  # above half
+    assert oracle.tf32_round(y, "rne") == np.float32(-(1 + 2.0 ** -10))
+    assert oracle.tf32_round(y, "rz") == np.float32(-1.0)
+    assert np.isinf(oracle.tf32_round(np.float32(np.inf), "rne"))
+    # C routine agrees with the numpy one
+    L = oracle.lib()
+    for v in (one_half_ulp, x, y, np.float32(3.14159)):
+        assert L.orc_tf32_round(float(v), 1) == oracle.tf32_round(v, "rne")
+        assert L.orc_tf32_round(float(v), 0) == oracle.tf32_round(v, "rz")
+
+
+def test_tf32emu_integer_exact_and_chunked():
+    rng = np.random.default_rng(5)
+    A = rng.integers(-8, 9, (20, 24)).astype(np.float32)
+    B = rng.integers(-8, 9, (24, 12)).astype(np.float32)
+    for mode in ("rz", "rne"):
+        assert np.array_equal(oracle.gemm_tf32emu(A, B, mode), A @ B)
+    # exact rational restatement on tiny random input: chunks of 8, one
+    # rounding per chunk into the fp32 accumulator
+    A = rng.standard_normal((2, 19)).astype(np.float32)
+    B = rng.standard_normal((19, 3)).astype(np.float32)
+    for mode in ("rz", "rne"):
+        C = oracle.gemm_tf32emu(A, B, mode)
+        Ar, Br = oracle.tf32_round(A, mode), oracle.tf32_round(B, mode)
+        for i in range(2):
+            for j in range(3):
+                acc = np.float32(0)
+                for k0 in range(0, 19, 8):
+                    s = sum(Fraction(float(Ar[i, k])) * Fraction(float(Br[k, j]))
+                            for k in range(k0, min(k0 + 8, 19)))
+                    acc = round_f32(Fraction(float(acc)) + s)
+                assert C[i, j] == acc
+
+
+def test_tf32emu_error_scale():
+    rng = np.random.default_rng(11)
+    A = rng.standard_normal((128, 512)).astype(np.float32)
+    B = rng.standard_normal((512, 96)).astype(np.float32)
+    C64 = A.astype(np.float64) @ B.astype(np.float64)
+    e_rz = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rz"), C64)
+    e_rne = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rne"), C64)
+    assert 2e-4 < e_rne < e_rz < 5e-3
+
+
+# ---------------------------------------------------------------------------
+# im2col / transpose_bias / direct conv (conv_kernel.cu:32-159)
+# ---------------------------------------------------------------------------
+
+def _conv_kat(k):
+    x = np.array(k["x"], np.float32).reshape(k["x_shape"])
+    w = np.array(k["w"], np.float32).reshape(k["w_shape"])
+    b = None if k["bias"] is None else np.array(k["bias"], np.float32)
+    return x, w, b
+
+
+@pytest.mark.parametrize("name", ["conv_identity_1x1", "conv_3x3_ones",
+                                  "conv_3x3_bias", "conv_3x3_pad1"])
+def test_conv_kats(kats, name):
+    k = kats[name]
+    x, w, b = _conv_kat(k)
+    y = np.array(k["y"], np.float64)
+    d = oracle.conv2d_direct64(x, w, b, k["stride"], k["padding"])
+    assert np.array_equal(d.ravel(), y)
+    r = oracle.conv2d_ref_im2col(x, w, b, k["stride"], k["padding"])
+    assert np.array_equal(r.ravel(), y.astype(np.float32))
+
+
+def test_im2col_1x1_is_relayout():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((3, 5, 4, 6)).astype(np.float32)
+    col = oracle.im2col(x, 1, 1)
+    assert np.array_equal(col, x.transpose(1, 0, 2, 3).reshape(5, -1))
+
+
+def test_im2col_zero_count_and_values():
+    # every col entry is either an input value or an inserted zero; the number
+    # of zeros is fixed by the geometry
+    rng = np.random.default_rng(4)
+    Bn, C, H, W, KH, KW, S, P = 2, 3, 7, 5, 3, 2, 2, 1
+    x = (rng.standard_normal((Bn, C, H, W)) + 10).astype(np.float32)  # no zeros
+    col = oracle.im2col(x, KH, KW, S, S, P, P)
+    OH, OW = oracle.conv_out_size(H, KH, S, P), oracle.conv_out_size(W, KW, S, P)
+    assert col.shape == (C * KH * KW, Bn * OH * OW)
+    valid_h = sum(1 for oh in range(OH) for kh in range(KH) if 0 <= oh * S - P + kh < H)
+    valid_w = sum(1 for ow in range(OW) for kw in range(KW) if 0 <= ow * S - P + kw < W)
+    assert np.count_nonzero(col) == Bn * C * valid_h * valid_w
+    assert set(np.unique(col[col != 0])) <= set(np.unique(x))
+
+
+@pytest.mark.parametrize("geom", [(2, 3, 8, 9, 4, 3, 3, 1, 1, 1, 1),
+                                  (1, 2, 7, 7, 3, 5, 3, 2, 1, 2, 0),
+                                  (3, 4, 6, 5, 2, 1, 1, 1, 1, 0, 0)])
+def test_im2col_gemm_equals_direct_conv_and_torch(geom):
+    torch = pytest.importorskip("torch")
+    Bn, IC, H, W, OC, KH, KW, SH, SW, PH, PW = geom
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((Bn, IC, H, W)).astype(np.float32)
+    w = rng.standard_normal((OC, IC, KH, KW)).astype(np.float32)
+    b = rng.standard_normal(OC).astype(np.float32)
+    col = oracle.im2col(x, KH, KW, SH, SW, PH, PW)
+    flat = w.reshape(OC, -1).astype(np.float64) @ col.astype(np.float64)
+    OH = oracle.conv_out_size(H, KH, SH, PH)
+    OW = oracle.conv_out_size(W, KW, SW, PW)
+    via_col = flat.reshape(OC, Bn, OH, OW).transpose(1, 0, 2, 3) + b[None, :, None, None]
+    direct = oracle.conv2d_direct64(x, w, b, (SH, SW), (PH, PW))
+    lib_ref = torch.nn.functional.conv2d(
+        torch.from_numpy(x).double(), torch.from_numpy(w).double(),
+        torch.from_numpy(b).double(), stride=(SH, SW), padding=(PH, PW)).numpy()
+    assert np.allclose(direct, lib_ref, rtol=1e-12, atol=1e-12)
+    assert np.allclose(via_col, lib_ref, rtol=1e-12, atol=1e-12)
+
+
+def test_transpose_bias_vs_numpy():
+    rng = np.random.default_rng(6)
+    OC, Bn, S = 5, 3, 11
+    src = rng.standard_normal((OC, Bn * S)).astype(np.float32)
+    bias = rng.standard_normal(OC).astype(np.float32)
+    got = oracle.transpose_bias(src, OC, Bn, S, bias)
+    want = src.reshape(OC, Bn, S).transpose(1, 0, 2) + bias[None, :, None]
+    assert np.array_equal(got, want.astype(np.float32))
+    assert np.array_equal(oracle.transpose_bias(src, OC, Bn, S),
+                          src.reshape(OC, Bn, S).transpose(1, 0, 2))
+
+
+# ---------------------------------------------------------------------------
+# column sum and activations
+# ---------------------------------------------------------------------------
+
+def test_colsum():
+    rng = np.random.default_rng(8)
+    x = rng.integers(-50, 50, (333, 17)).astype(np.float32)
+    assert np.array_equal(oracle.colsum(x), x.astype(np.float64).sum(0).astype(np.float32))
+    y = rng.standard_normal((1000, 9)).astype(np.float32)
+    assert np.allclose(oracle.colsum(y), y.astype(np.float64).sum(0), rtol=1e-4, atol=1e-4)
+
+
+def test_gelu_against_torch_and_derivative():
+    torch = pytest.importorskip("torch")
+    x = np.linspace(-6, 6, 1001)
+    ref = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    # the reference's constant 0.7978845608 is sqrt(2/pi) to 10 digits
+    assert np.allclose(oracle.gelu(x), ref, rtol=1e-9, atol=1e-10)
+    h = 1e-6
+    num = (oracle.gelu(x + h) - oracle.gelu(x - h)) / (2 * h)
+    assert np.allclose(oracle.gelu_grad(x), num, atol=1e-7)
+    assert oracle.gelu(np.array([0.0]))[0] == 0.0
+    assert np.array_equal(oracle.relu(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 2.0])
+    assert np.array_equal(oracle.relu_grad(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 1.0])
