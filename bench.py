@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X dense-contraction path (one GPU).
+
+Headline (BASELINE.json metric): FP32 GEMM TFLOP/s at M=N=K=4096 (config
+C2, A, B ~ N(0,1), beta=0) and its fraction of the MI355X FP32 MFMA peak
+(157.3 TFLOP/s).  A "step" is one 4096^3 FP32 GEMM through cdx_sgemm_f32,
+with A, B, C resident in HBM.  The same run also reports, under "extra":
+TF32-mode (bf16x3) GEMM at 2048^3 / 4096^3 (C3), the MLP Linear stack (C4)
+and the im2col + GEMM Conv2d (C5).
+
+Timing: W untimed warmup steps, then K steps bracketed by
+torch.cuda.synchronize(); kernel durations come from HIP events recorded on
+the stream the library launches on (torch's current stream).
+
+cpu_baseline: the repo's host reference SGEMM (oracle/, the sequential-FMA
+restatement of the reference SGEMM, OpenMP over all host cores) timed on
+the same 4096^3 problem: 1 warmup + median of 3.  It is a reported
+baseline, not the optimisation target.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP32_PEAK_TFLOPS = 157.3      # MI355X dense FP32 MFMA
+BF16_PEAK_TFLOPS = 2516.6     # MI355X dense BF16 MFMA; bf16x3 logical ceiling = /3
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--headline-only", action="store_true",
+                   help="time only the 4096^3 FP32 GEMM (for profiler runs)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    return p.parse_args()
+
+
+def time_launches(fn, steps, warmup):
+    """Runs fn() warmup times, then `steps` times with a HIP event pair
+    around each launch on the current stream.  Returns (mean ms per step
+    from the bracketing events, list of per-launch ms)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    outer0 = torch.cuda.Event(enable_timing=True)
+    outer1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    outer0.record()
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    outer1.record()
+    torch.cuda.synchronize()
+    per = [e0.elapsed_time(e1) for e0, e1 in evs]
+    return outer0.elapsed_time(outer1) / steps, per
+
+
+def bench_gemm(n, precision, steps, warmup, seed):
+    import torch
+    import cudeep_amd.ops as ops
+    import cudeep_amd as cd
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    A = torch.randn((n, n), device="cuda", generator=g)
+    B = torch.randn((n, n), device="cuda", generator=g)
+    C = torch.empty((n, n), device="cuda")
+    f = ops.sgemm if precision == cd.PREC_FP32 else ops.gemm_tf32mode
+    ms, per = time_launches(lambda: f(A, B, out=C), steps, warmup)
+    flops = 2.0 * n ** 3
+    return {"n": n, "ms_per_step": ms, "kernel_ms_mean": statistics.mean(per),
+            "kernel_ms_median": statistics.median(per),
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "tflops_kernel_median": flops / (statistics.median(per) * 1e-3) / 1e12}
+
+
+def bench_mlp(steps, warmup, precision):
+    """C4: 784 -> 256 -> 10, batch 8192: fused forward (bias+ReLU epilogue)
+    and backward GEMMs (dX, dW per layer) + bias-grad column sums."""
+    import torch
+    import cudeep_amd.ops as ops
+    import cudeep_amd as cd
+    g = torch.Generator(device="cuda").manual_seed(4)
+    X = torch.randn((8192, 784), device="cuda", generator=g)
+    W1 = (torch.rand((256, 784), device="cuda", generator=g) * 2 - 1) * (6 / (784 + 256)) ** 0.5
+    W2 = (torch.rand((10, 256), device="cuda", generator=g) * 2 - 1) * (6 / (256 + 10)) ** 0.5
+    b1 = torch.randn((256,), device="cuda", generator=g) * 0.1
+    b2 = torch.randn((10,), device="cuda", generator=g) * 0.1
+    dY2 = torch.randn((8192, 10), device="cuda", generator=g)
+    H = torch.empty((8192, 256), device="cuda")
+    Y = torch.empty((8192, 10), device="cuda")
+    dH = torch.empty((8192, 256), device="cuda")
+    dZ = torch.empty((8192, 256), device="cuda")
+    gW2 = torch.empty((10, 256), device="cuda")
+    gW1 = torch.empty((256, 784), device="cuda")
+    gX = torch.empty((8192, 784), device="cuda")
+    gb1 = torch.empty((256,), device="cuda")
+    gb2 = torch.empty((10,), device="cuda")
+
+    def fwd():
+        ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
+                 precision=precision, out=H)
+        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y)
+
+    def bwd():
+        ops.gemm(dY2, W2, precision=precision, out=dH)                 # dH = dY2 W2
+        ops.gemm(dY2, H, transA=True, precision=precision, out=gW2)   # dW2 = dY2^T H
+        ops.sum_reduce_rows(dY2, out=gb2)
+        ops.activation_backward(dH, H, cd.EPI_RELU, out=dZ)          # ReLU mask (H>0 <=> Z>0)
+        ops.gemm(dZ, W1, precision=precision, out=gX)                 # dX = dZ W1
+        ops.gemm(dZ, X, transA=True, precision=precision, out=gW1)    # dW1 = dZ^T X
+        ops.sum_reduce_rows(dZ, out=gb1)
+
+    fwd_ms, _ = time_launches(fwd, steps, warmup)
+    bwd_ms, _ = time_launches(bwd, steps, warmup)
+    fwd_flops = 2.0 * 8192 * (784 * 256 + 256 * 10)
+    bwd_flops = 2 * fwd_flops
+    # per-GEMM timing of the big forward GEMM
+    l1_ms, _ = time_launches(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
+                                              epilogue=cd.EPI_RELU, precision=precision, out=H),
+                             steps, warmup)
+    return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
+            "fwd_tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12,
+            "bwd_tflops": bwd_flops / (bwd_ms * 1e-3) / 1e12,
+            "fwd1_fused_ms": l1_ms,
+            "fwd1_fused_tflops": 2.0 * 8192 * 784 * 256 / (l1_ms * 1e-3) / 1e12}
+
+
+def bench_conv(steps, warmup, precision):
+    """C5: N=32, C=64, 56x56 -> 64, 3x3, s1, p1: im2col + GEMM (bias in the
+    epilogue, output written NCHW)."""
+    import torch
+    import cudeep_amd.ops as ops
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((32, 64, 56, 56), device="cuda", generator=g)
+    w = torch.randn((64, 64, 3, 3), device="cuda", generator=g) * (2.0 / 576) ** 0.5
+    b = torch.randn((64,), device="cuda", generator=g) * 0.1
+    ws = torch.empty(ops.conv2d_workspace_bytes(x.shape, w.shape, (1, 1), (1, 1)) // 4,
+                     device="cuda")
+    y = torch.empty((32, 64, 56, 56), device="cuda")
+    col = ws.view(576, 100352)
+    conv_ms, _ = time_launches(lambda: ops.conv2d_forward(x, w, b, (1, 1), (1, 1), precision,
+                                                          workspace=ws, out=y), steps, warmup)
+    im_ms, _ = time_launches(lambda: ops.im2col(x, 3, 3, (1, 1), (1, 1), out=col), steps, warmup)
+    flops = 2.0 * 32 * 64 * 56 * 56 * 64 * 9
+    im2col_bytes = 576 * 100352 * 4 + 32 * 64 * 56 * 56 * 4
+    return {"conv_ms": conv_ms, "conv_tflops": flops / (conv_ms * 1e-3) / 1e12,
+            "im2col_ms": im_ms, "im2col_gbs": im2col_bytes / (im_ms * 1e-3) / 1e9,
+            "gemm_ms_est": conv_ms - im_ms,
+            "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12}
+
+
+def cpu_baseline(n=4096):
+    """Repo host reference SGEMM (oracle, seq-FMA restatement), all cores."""
+    import numpy as np
+    import oracle
+    oracle.build()
+    cores = os.cpu_count() or 1
+    oracle.set_num_threads(cores)
+    rng = np.random.default_rng(2)
+    A = rng.standard_normal((n, n)).astype(np.float32)
+    B = rng.standard_normal((n, n)).astype(np.float32)
+    oracle.sgemm_seqfma(A, B)                      # warmup
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        oracle.sgemm_seqfma(A, B)
+        ts.append(time.perf_counter() - t)
+    t_med = statistics.median(ts)
+    t = time.perf_counter()
+    A @ B
+    t_np = time.perf_counter() - t
+    flops = 2.0 * n ** 3
+    return {"value": flops / t_med / 1e12, "unit": "TFLOP/s", "cores": oracle.num_threads(),
+            "kind": "port",
+            "sample": f"full {n}^3 FP32 GEMM, seq-FMA host reference (oracle/oracle.c), "
+                      f"1 warmup + median of 3 ({t_med:.2f} s each)",
+            "numpy_f32_tflops": flops / t_np / 1e12}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    import cudeep_amd as cd
+    props = torch.cuda.get_device_properties(0)
+    log("device", props.name, getattr(props, "gcnArchName", ""), "CUs", props.multi_processor_count)
+
+    log("headline: fp32 4096^3")
+    head = bench_gemm(4096, cd.PREC_FP32, args.steps, args.warmup, seed=2)
+    log("fp32 4096^3:", head)
+    extra = {}
+    if not args.headline_only:
+        for n in (4096, 2048):
+            r = bench_gemm(n, cd.PREC_TF32MODE, args.steps, args.warmup, seed=3)
+            r["frac_of_bf16x3_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 3)
+            extra[f"tf32mode_{n}"] = r
+            log(f"tf32mode {n}^3:", r)
+        for prec, name in ((cd.PREC_FP32, "fp32"), (cd.PREC_TF32MODE, "tf32mode")):
+            extra[f"mlp_c4_{name}"] = bench_mlp(args.steps, args.warmup, prec)
+            log(f"mlp {name}:", extra[f"mlp_c4_{name}"])
+            extra[f"conv_c5_{name}"] = bench_conv(args.steps, args.warmup, prec)
+            log(f"conv {name}:", extra[f"conv_c5_{name}"])
+        r = bench_gemm(512, cd.PREC_FP32, 200, 50, seed=1)
+        extra["fp32_512"] = r
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline()
+        log("cpu:", cpu)
+
+    achieved = 2.0 * 4096 ** 3 / (head["kernel_ms_mean"] * 1e-3) / 1e12
+    out = {
+        "metric": "FP32 GEMM TFLOP/s at 4096^3 (+% of FP32 MFMA peak); TF32-mode TFLOP/s",
+        "value": round(head["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic N(0,1) fp32 operands generated on the GPU (seeded)",
+        "config": {"workload": "C2: FP32 SGEMM C=A*B, M=N=K=4096, row-major, beta=0",
+                   "M": 4096, "N": 4096, "K": 4096, "entry_point": "cdx_sgemm_f32"},
+        "pct_of_fp32_mfma_peak": round(100 * head["tflops"] / FP32_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,277 @@
+// extern "C" entry points of libcudeep_amd.so (declared in
+// include/cudeep_amd.h).  This layer validates every argument on the host,
+// turns problems into status codes with a per-thread message, and then
+// calls the gfx950 launchers.  No exception crosses the boundary; nothing
+// here falls back to the CPU.
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "cdx_internal.hpp"
+
+namespace cdx {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_error(hipError_t e, const char* what) {
+    if (e == hipSuccess) return CDX_OK;
+    return set_error(CDX_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace cdx
+
+using cdx::set_error;
+
+namespace {
+
+constexpr int64_t kMaxDim = (int64_t)1 << 40;
+
+bool bad_dim(int64_t d) { return d < 0 || d > kMaxDim; }
+
+// Validates a GEMM request; returns CDX_OK or an error code (with message).
+int check_gemm(const char* fn, int opA, int opB, int64_t M, int64_t N, int64_t K,
+               const void* A, int64_t lda, const void* B, int64_t ldb,
+               const void* C, int64_t ldc) {
+    if (opA != CDX_OP_N && opA != CDX_OP_T) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad opA");
+    if (opB != CDX_OP_N && opB != CDX_OP_T) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad opB");
+    if (bad_dim(M) || bad_dim(N) || bad_dim(K))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": dimensions must be in [0, 2^40]");
+    if (M == 0 || N == 0) return CDX_OK;
+    if (!C) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": C is NULL");
+    if (K > 0 && (!A || !B)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": A or B is NULL");
+    const int64_t a_cols = opA == CDX_OP_N ? K : M;
+    const int64_t b_cols = opB == CDX_OP_N ? N : K;
+    if (lda < (a_cols > 1 ? a_cols : 1)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": lda too small");
+    if (ldb < (b_cols > 1 ? b_cols : 1)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": ldb too small");
+    if (ldc < N) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": ldc too small");
+    return CDX_OK;
+}
+
+int run_gemm(int precision, cdx::GemmArgs g, hipStream_t stream) {
+    if (g.M == 0 || g.N == 0) return CDX_OK;
+    if (precision == CDX_PREC_FP32) return cdx::launch_gemm_f32(g, stream);
+    if (precision == CDX_PREC_TF32MODE) return cdx::launch_gemm_bf16x3(g, stream);
+    return set_error(CDX_ERR_INVALID_ARG, "gemm: unknown precision");
+}
+
+int64_t conv_out(int64_t in, int64_t k, int64_t s, int64_t p) { return (in + 2 * p - k) / s + 1; }
+
+int check_conv(const char* fn, int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+               int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    if (bad_dim(batch) || bad_dim(IC) || bad_dim(OC) || bad_dim(IH) || bad_dim(IW) ||
+        KH <= 0 || KW <= 0 || SH <= 0 || SW <= 0 || PH < 0 || PW < 0 ||
+        KH > kMaxDim || KW > kMaxDim || SH > kMaxDim || SW > kMaxDim || PH > kMaxDim || PW > kMaxDim)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": invalid geometry");
+    if (IH + 2 * PH < KH || IW + 2 * PW < KW)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": kernel larger than padded input");
+    // every flat index must fit in int64 with room to spare
+    const int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    long double col = (long double)IC * KH * KW * batch * OH * OW;
+    if (col > (long double)((int64_t)1 << 46))
+        return set_error(CDX_ERR_UNSUPPORTED, std::string(fn) + ": problem too large");
+    return CDX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cdx_last_error(void) { return cdx::g_last_error.c_str(); }
+
+const char* cdx_version(void) { return "cudeep_amd 0.1.0 (gfx950)"; }
+
+int cdx_sgemm_f32(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                  hipStream_t stream) {
+    int st = check_gemm("cdx_sgemm_f32", CDX_OP_N, CDX_OP_N, M, N, K, A, K > 1 ? K : 1, B,
+                        N > 1 ? N : 1, C, N);
+    if (st) return st;
+    cdx::GemmArgs g{CDX_OP_N, CDX_OP_N, M, N, K, A, K, B, N, C, N, 0, 0,
+                    nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+    return run_gemm(CDX_PREC_FP32, g, stream);
+}
+
+int cdx_gemm_tf32mode(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                      hipStream_t stream) {
+    int st = check_gemm("cdx_gemm_tf32mode", CDX_OP_N, CDX_OP_N, M, N, K, A, K > 1 ? K : 1, B,
+                        N > 1 ? N : 1, C, N);
+    if (st) return st;
+    cdx::GemmArgs g{CDX_OP_N, CDX_OP_N, M, N, K, A, K, B, N, C, N, 0, 0,
+                    nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+    return run_gemm(CDX_PREC_TF32MODE, g, stream);
+}
+
+int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K,
+                const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
+                const float* bias, int bias_mode, int epilogue, hipStream_t stream) {
+    int st = check_gemm("cdx_gemm_ex", opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
+    if (st) return st;
+    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad precision");
+    if (bias_mode != CDX_BIAS_NONE && bias_mode != CDX_BIAS_ROW && bias_mode != CDX_BIAS_COL)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad bias_mode");
+    if (bias_mode != CDX_BIAS_NONE && !bias && M > 0 && N > 0)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bias is NULL");
+    if (epilogue != CDX_EPI_NONE && epilogue != CDX_EPI_RELU && epilogue != CDX_EPI_GELU)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad epilogue");
+    cdx::GemmArgs g{opA, opB, M, N, K, A, lda, B, ldb, C, ldc, 0, 0, bias, bias_mode, epilogue};
+    return run_gemm(precision, g, stream);
+}
+
+int cdx_matmul_fused_act(const float* A, const float* B, float* C, int64_t M, int64_t N,
+                         int64_t K, int epilogue, hipStream_t stream) {
+    return cdx_gemm_ex(CDX_PREC_TF32MODE, CDX_OP_N, CDX_OP_N, M, N, K, A, K > 1 ? K : 1, B,
+                       N > 1 ? N : 1, C, N, nullptr, CDX_BIAS_NONE, epilogue, stream);
+}
+
+int cdx_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K, const double* A, int64_t lda,
+              const double* B, int64_t ldb, double* C, int64_t ldc, hipStream_t stream) {
+    int st = check_gemm("cdx_dgemm", opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
+    if (st) return st;
+    if (M == 0 || N == 0) return CDX_OK;
+    return cdx::launch_dgemm(opA, opB, M, N, K, A, lda, B, ldb, C, ldc, stream);
+}
+
+int cdx_im2col_f32(const float* input, float* col, int64_t batch, int64_t in_channels,
+                   int64_t in_h, int64_t in_w, int64_t kernel_h, int64_t kernel_w,
+                   int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                   hipStream_t stream) {
+    int st = check_conv("cdx_im2col_f32", batch, in_channels, 1, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (batch * in_channels == 0) return CDX_OK;
+    if (!input || !col) return set_error(CDX_ERR_INVALID_ARG, "cdx_im2col_f32: NULL pointer");
+    return cdx::launch_im2col_f32(input, col, batch, in_channels, in_h, in_w, kernel_h, kernel_w,
+                                  stride_h, stride_w, pad_h, pad_w, stream);
+}
+
+size_t cdx_conv2d_forward_workspace_size(int64_t batch, int64_t in_channels, int64_t in_h,
+                                         int64_t in_w, int64_t kernel_h, int64_t kernel_w,
+                                         int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                                         int64_t pad_w) {
+    if (check_conv("cdx_conv2d_forward_workspace_size", batch, in_channels, 1, in_h, in_w,
+                   kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w))
+        return 0;
+    const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
+    const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
+    return (size_t)(in_channels * kernel_h * kernel_w) * (size_t)(batch * OH * OW) * sizeof(float);
+}
+
+int cdx_conv2d_forward_f32(const float* input, const float* weight, const float* bias,
+                           float* output, int64_t batch, int64_t in_channels,
+                           int64_t out_channels, int64_t in_h, int64_t in_w, int64_t kernel_h,
+                           int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                           int64_t pad_w, int precision, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+    int st = check_conv("cdx_conv2d_forward_f32", batch, in_channels, out_channels, in_h, in_w,
+                        kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: bad precision");
+    const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
+    const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
+    const int64_t S = OH * OW, BS = batch * S, Kc = in_channels * kernel_h * kernel_w;
+    if (batch == 0 || out_channels == 0 || S == 0) return CDX_OK;
+    if (!output || !weight || (Kc > 0 && !input))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: NULL pointer");
+    const size_t need = (size_t)Kc * (size_t)BS * sizeof(float);
+    float* col = static_cast<float*>(workspace);
+    bool owned = false;
+    if (workspace) {
+        if (workspace_bytes < need)
+            return set_error(CDX_ERR_WORKSPACE, "cdx_conv2d_forward_f32: workspace too small");
+    } else if (need > 0) {
+        st = cdx::hip_error(hipMallocAsync(reinterpret_cast<void**>(&col), need, stream),
+                            "cdx_conv2d_forward_f32: hipMallocAsync");
+        if (st) return st;
+        owned = true;
+    }
+    if (Kc > 0) {
+        st = cdx::launch_im2col_f32(input, col, batch, in_channels, in_h, in_w, kernel_h,
+                                    kernel_w, stride_h, stride_w, pad_h, pad_w, stream);
+    }
+    if (!st) {
+        // weight[OC, Kc] * col[Kc, B*S] -> NCHW: addr = oc*S + (n/S)*OC*S + n%S
+        cdx::GemmArgs g{CDX_OP_N, CDX_OP_N, out_channels, BS, Kc, weight, Kc > 0 ? Kc : 1,
+                        col, BS, output, S, S, out_channels * S,
+                        bias, bias ? CDX_BIAS_ROW : CDX_BIAS_NONE, CDX_EPI_NONE};
+        st = run_gemm(precision, g, stream);
+    }
+    if (owned) {
+        int st2 = cdx::hip_error(hipFreeAsync(col, stream), "cdx_conv2d_forward_f32: hipFreeAsync");
+        if (!st) st = st2;
+    }
+    return st;
+}
+
+size_t cdx_sum_reduce_rows_workspace_size(int64_t rows, int64_t cols) {
+    if (bad_dim(rows) || bad_dim(cols)) return 0;
+    return (size_t)cdx::colsum_partial_rows(rows, cols) * (size_t)cols * sizeof(float);
+}
+
+int cdx_sum_reduce_rows_f32(const float* input, float* output, int64_t rows, int64_t cols,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (bad_dim(rows) || bad_dim(cols))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_sum_reduce_rows_f32: bad dims");
+    if (cols == 0) return CDX_OK;
+    if (!output || (rows > 0 && !input))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_sum_reduce_rows_f32: NULL pointer");
+    const int64_t pr = cdx::colsum_partial_rows(rows, cols);
+    const size_t need = (size_t)pr * (size_t)cols * sizeof(float);
+    float* part = static_cast<float*>(workspace);
+    bool owned = false;
+    int st = CDX_OK;
+    if (workspace) {
+        if (workspace_bytes < need)
+            return set_error(CDX_ERR_WORKSPACE, "cdx_sum_reduce_rows_f32: workspace too small");
+    } else if (need > 0) {
+        st = cdx::hip_error(hipMallocAsync(reinterpret_cast<void**>(&part), need, stream),
+                            "cdx_sum_reduce_rows_f32: hipMallocAsync");
+        if (st) return st;
+        owned = true;
+    }
+    st = cdx::launch_colsum_f32(input, output, rows, cols, part, pr, stream);
+    if (owned) {
+        int st2 = cdx::hip_error(hipFreeAsync(part, stream), "cdx_sum_reduce_rows_f32: hipFreeAsync");
+        if (!st) st = st2;
+    }
+    return st;
+}
+
+int cdx_broadcast_add_row_f32(const float* matrix, const float* row, float* out, int64_t rows,
+                              int64_t cols, hipStream_t stream) {
+    if (bad_dim(rows) || bad_dim(cols))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_broadcast_add_row_f32: bad dims");
+    if (rows == 0 || cols == 0) return CDX_OK;
+    if (!matrix || !row || !out)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_broadcast_add_row_f32: NULL pointer");
+    return cdx::launch_broadcast_add_row_f32(matrix, row, out, rows, cols, stream);
+}
+
+int cdx_activation_forward_f32(const float* input, float* output, int64_t n, int act,
+                               hipStream_t stream) {
+    if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_forward_f32: bad n");
+    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_forward_f32: act must be RELU or GELU");
+    if (n == 0) return CDX_OK;
+    if (!input || !output)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_forward_f32: NULL pointer");
+    return cdx::launch_activation_f32(input, output, n, act, stream);
+}
+
+int cdx_activation_backward_f32(const float* grad_output, const float* input, float* grad_input,
+                                int64_t n, int act, hipStream_t stream) {
+    if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: bad n");
+    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: act must be RELU or GELU");
+    if (n == 0) return CDX_OK;
+    if (!grad_output || !input || !grad_input)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: NULL pointer");
+    return cdx::launch_activation_backward_f32(grad_output, input, grad_input, n, act, stream);
+}
+
+}  // extern "C"

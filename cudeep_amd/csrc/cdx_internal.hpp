@@ -1,0 +1,95 @@
+// Internal declarations shared by the gfx950 kernels and the C-ABI layer.
+// Nothing here crosses the library boundary; the public contract is
+// include/cudeep_amd.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+#include "../../include/cudeep_amd.h"
+
+namespace cdx {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short shortx8 __attribute__((ext_vector_type(8)));
+
+// Records a message for cdx_last_error() on this thread and returns `code`.
+int set_error(int code, const std::string& msg);
+int hip_error(hipError_t e, const char* what);
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// One GEMM problem in the library's internal form.  Element (i, j) of op(A)
+// is A[i*lda + j] (opA = N) or A[j*lda + i] (opA = T); likewise for B.
+// C is written through the output map:
+//   addr(m, n) = m * ldc + (n / n_split) * ldc_split + (n % n_split)
+// n_split = 0 means the plain row-major map addr = m * ldc + n.  The split
+// map writes the conv GEMM's [OC, B*S] result straight into NCHW.
+struct GemmArgs {
+    int opA, opB;
+    int64_t M, N, K;
+    const float* A; int64_t lda;
+    const float* B; int64_t ldb;
+    float* C; int64_t ldc;
+    int64_t n_split, ldc_split;
+    const float* bias; int bias_mode;   // CDX_BIAS_*
+    int epilogue;                       // CDX_EPI_*
+};
+
+// Launchers (no argument validation: the C-ABI validates first).
+int launch_gemm_f32(const GemmArgs& g, hipStream_t stream);
+int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream);
+int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
+                 const double* A, int64_t lda, const double* B, int64_t ldb,
+                 double* C, int64_t ldc, hipStream_t stream);
+
+int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
+                      int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                      int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                      hipStream_t stream);
+
+int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,
+                      float* partials, int64_t partial_rows, hipStream_t stream);
+int64_t colsum_partial_rows(int64_t rows, int64_t cols);
+
+int launch_broadcast_add_row_f32(const float* m, const float* row, float* out,
+                                 int64_t rows, int64_t cols, hipStream_t stream);
+int launch_activation_f32(const float* in, float* out, int64_t n, int act,
+                          hipStream_t stream);
+int launch_activation_backward_f32(const float* grad_out, const float* in,
+                                   float* grad_in, int64_t n, int act,
+                                   hipStream_t stream);
+
+// GELU, tanh form 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3)
+// (Hendrycks & Gimpel 2016; the reference's constants 0.7978845608 and
+// 0.044715, activation_kernel.cu:40-46).  Evaluated through the identity
+// 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)), which has no cancellation in
+// either tail: gelu(x) = x / (1 + exp(-2u)).
+__device__ __forceinline__ float gelu_f32(float x) {
+    const float c = 0.7978845608f, k = 0.044715f;
+    float u = c * (x + k * x * x * x);
+    return x / (1.0f + expf(-2.0f * u));
+}
+
+// d gelu / dx = s + 2 x s (1 - s) du/dx with s = 1 / (1 + exp(-2u)),
+// since 0.5 (1 - tanh^2 u) = 2 s (1 - s); 1 - s = 1 / (1 + exp(2u)) is
+// computed directly so neither factor cancels or overflows to inf * 0.
+__device__ __forceinline__ float gelu_grad_f32(float x) {
+    const float c = 0.7978845608f, k = 0.044715f;
+    float u = c * (x + k * x * x * x);
+    float s = 1.0f / (1.0f + expf(-2.0f * u));
+    float one_minus_s = 1.0f / (1.0f + expf(2.0f * u));
+    float du = c * (1.0f + 3.0f * k * x * x);
+    return s + 2.0f * x * s * one_minus_s * du;
+}
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+    if (act == CDX_EPI_RELU) return v > 0.0f ? v : 0.0f;
+    if (act == CDX_EPI_GELU) return gelu_f32(v);
+    return v;
+}
+
+}  // namespace cdx

@@ -1,0 +1,133 @@
+// Small bandwidth kernels nn.Linear needs around its GEMMs:
+//   * column sums (bias gradient), replacing sum_reduce_rows_kernel
+//     (src/kernels/unary_kernel.cu:204-238), which runs one thread per 4
+//     columns serially down all rows (64 active threads for 256 columns).
+//     Here: pass 1 splits the rows into chunks of kColsumRows, 4 row-lanes x
+//     64 columns per workgroup, fixed-order fp32 sums into a partials
+//     buffer; pass 2 adds the partials in chunk order.  Deterministic.
+//   * broadcast row add (elementwise_kernel.cu:186-204).
+//   * ReLU / GELU forward and backward (activation_kernel.cu:19-52,
+//     :256-319); the GELU is the tanh form written through exp
+//     (cdx_internal.hpp), not an approximate-instruction sequence.
+#include "cdx_internal.hpp"
+
+namespace cdx {
+namespace {
+
+constexpr int kColsumRows = 256;   // rows per pass-1 chunk
+constexpr int kColsumCols = 64;    // columns per pass-1 workgroup
+
+__global__ __launch_bounds__(256)
+void colsum_partial_kernel(const float* __restrict__ in, float* __restrict__ part,
+                           int64_t rows, int64_t cols) {
+    __shared__ float red[4][kColsumCols];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int64_t c = (int64_t)blockIdx.x * kColsumCols + tx;
+    const int64_t r0 = (int64_t)blockIdx.y * kColsumRows;
+    int64_t r1 = r0 + kColsumRows;
+    if (r1 > rows) r1 = rows;
+    float acc = 0.0f;
+    if (c < cols)
+        for (int64_t r = r0 + ty; r < r1; r += 4) acc += in[r * cols + c];
+    red[ty][tx] = acc;
+    __syncthreads();
+    if (ty == 0 && c < cols)
+        part[(int64_t)blockIdx.y * cols + c] = ((red[0][tx] + red[1][tx]) + red[2][tx]) + red[3][tx];
+}
+
+__global__ __launch_bounds__(256)
+void colsum_final_kernel(const float* __restrict__ part, float* __restrict__ out,
+                         int64_t chunks, int64_t cols) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    float acc = 0.0f;
+    for (int64_t i = 0; i < chunks; ++i) acc += part[i * cols + c];
+    out[c] = acc;
+}
+
+__global__ __launch_bounds__(256)
+void bias_row_kernel(const float* __restrict__ m, const float* __restrict__ row,
+                     float* __restrict__ out, int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = m[i] + row[i % cols];
+}
+
+__global__ __launch_bounds__(256)
+void act_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n, int act) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = apply_act(x[i], act);
+}
+
+__global__ __launch_bounds__(256)
+void act_bwd_kernel(const float* __restrict__ go, const float* __restrict__ x,
+                    float* __restrict__ gi, int64_t n, int act) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = x[i];
+        gi[i] = act == CDX_EPI_RELU ? (v > 0.0f ? go[i] : 0.0f) : go[i] * gelu_grad_f32(v);
+    }
+}
+
+__global__ __launch_bounds__(256)
+void fill_kernel(float* __restrict__ y, int64_t n, float v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = v;
+}
+
+unsigned grid_for(int64_t n) {
+    int64_t b = ceil_div(n, 256);
+    if (b > 65536) b = 65536;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+}  // namespace
+
+int64_t colsum_partial_rows(int64_t rows, int64_t cols) {
+    (void)cols;
+    return ceil_div(rows, kColsumRows);
+}
+
+int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,
+                      float* partials, int64_t partial_rows, hipStream_t stream) {
+    if (cols <= 0) return CDX_OK;
+    if (partial_rows > 65535) return set_error(CDX_ERR_UNSUPPORTED, "sum_reduce_rows: too many rows");
+    if (rows <= 0) {   // empty sum: zeros (a fill kernel, capture-safe)
+        hipLaunchKernelGGL(fill_kernel, dim3(grid_for(cols)), dim3(256), 0, stream, out, cols, 0.0f);
+        return hip_error(hipGetLastError(), "fill_kernel launch");
+    }
+    dim3 g1((unsigned)ceil_div(cols, kColsumCols), (unsigned)partial_rows);
+    hipLaunchKernelGGL(colsum_partial_kernel, g1, dim3(256), 0, stream, in, partials, rows, cols);
+    int st = hip_error(hipGetLastError(), "colsum_partial_kernel launch");
+    if (st) return st;
+    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0,
+                       stream, partials, out, partial_rows, cols);
+    return hip_error(hipGetLastError(), "colsum_final_kernel launch");
+}
+
+int launch_broadcast_add_row_f32(const float* m, const float* row, float* out,
+                                 int64_t rows, int64_t cols, hipStream_t stream) {
+    if (rows * cols == 0) return CDX_OK;
+    hipLaunchKernelGGL(bias_row_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, stream,
+                       m, row, out, rows, cols);
+    return hip_error(hipGetLastError(), "bias_row_kernel launch");
+}
+
+int launch_activation_f32(const float* in, float* out, int64_t n, int act, hipStream_t stream) {
+    if (n == 0) return CDX_OK;
+    hipLaunchKernelGGL(act_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n, act);
+    return hip_error(hipGetLastError(), "act_fwd_kernel launch");
+}
+
+int launch_activation_backward_f32(const float* go, const float* in, float* gi, int64_t n,
+                                   int act, hipStream_t stream) {
+    if (n == 0) return CDX_OK;
+    hipLaunchKernelGGL(act_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, stream, go, in, gi, n, act);
+    return hip_error(hipGetLastError(), "act_bwd_kernel launch");
+}
+
+}  // namespace cdx

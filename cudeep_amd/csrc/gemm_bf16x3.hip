@@ -1,0 +1,313 @@
+// "TF32-mode" GEMM: explicit bf16x3 split-precision MFMA on gfx950
+// (v_mfma_f32_16x16x32_bf16).
+//
+// Replaces the reference's TF32 tensor-core kernels (sgemm_tc_kernel,
+// sgemm_tc_general_kernel, sgemm_persistent_kernel, ...;
+// src/kernels/matmul_kernel.cu:78-452, :942-1143), which feed raw fp32 bits
+// to mma.sync...tf32.  CDNA4 has no TF32 datapath, so each fp32 operand x is
+// split once, while it is staged into LDS, into
+//     hi = bf16_rne(x),   lo = bf16_rne(x - hi)        (x - hi is exact)
+// and every product is formed as  hi*hi + hi*lo + lo*hi  with fp32
+// accumulation.  |x - hi - lo| <= 2^-16 |x|, and the dropped lo*lo term is
+// <= 2^-16 |ab|, so each product carries a relative error of at most about
+// 3 * 2^-16 ~= 4.6e-5 -- against ~1e-3 for TF32 operand truncation.
+//
+// Structure: BM x BN output tile per workgroup; fp32 global loads into VGPRs
+// (double-buffered against the MFMAs of the current k-tile), split in
+// registers, written to LDS as k-contiguous bf16 hi / lo planes ([mn][BK+8]),
+// so every MFMA operand is one 16-byte LDS read (8 consecutive k).
+// m/n-contiguous operands are transposed in registers on the way in (each
+// thread loads a 4x4 block and writes four k-runs).  Epilogue as in the
+// FP32 kernel (bias per row/column, ReLU/GELU, plain or NCHW output map).
+#include "cdx_internal.hpp"
+
+namespace cdx {
+namespace {
+
+struct KParams {
+    const float* A; const float* B; float* C; const float* bias;
+    int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
+    int bias_mode, epilogue;
+};
+
+__device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
+    __bf16 h = (__bf16)x;
+    float r = x - (float)h;
+    __bf16 l = (__bf16)r;
+    hi = __builtin_bit_cast(unsigned short, h);
+    lo = __builtin_bit_cast(unsigned short, l);
+}
+
+__device__ __forceinline__ float ld_guard(const float* p, bool ok) { return ok ? *p : 0.0f; }
+
+// Loads an operand tile for the k-range [k0, k0+BK) and mn-range
+// [mn0, mn0+BMN) into registers, as 4x4 blocks (4 mn x 4 k).  KCONTIG says
+// whether k is the contiguous dimension in memory.
+template <int BMN, int BK, int NT, bool KCONTIG, bool CHECK>
+struct SplitLoader {
+    static constexpr int NB = (BMN / 4) * (BK / 4);   // 4x4 blocks in the tile
+    static constexpr int NV = (NB + NT - 1) / NT;
+    static_assert(NB % NT == 0 || NB < NT, "tile not divisible by thread count");
+    float4 v[NV][4];  // v[blk][q]: KCONTIG -> mn row q, 4 k;  else k row q, 4 mn
+
+    __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld,
+                                         int64_t mn0, int64_t k0, int64_t mnmax,
+                                         int64_t kmax, bool vec, int tid) {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            // blocks ordered so consecutive threads walk the contiguous dim
+            int bc, br;   // block index along contiguous / strided dimension
+            if (KCONTIG) { bc = blk % (BK / 4); br = blk / (BK / 4); }
+            else         { bc = blk % (BMN / 4); br = blk / (BMN / 4); }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int64_t gr, gc, rmax, cmax;
+                if (KCONTIG) { gr = mn0 + br * 4 + q; gc = k0 + bc * 4; rmax = mnmax; cmax = kmax; }
+                else         { gr = k0 + br * 4 + q;  gc = mn0 + bc * 4; rmax = kmax; cmax = mnmax; }
+                const float* p = X + gr * ld + gc;
+                if (!CHECK) {
+                    v[b][q] = *reinterpret_cast<const float4*>(p);
+                } else if (vec && gr < rmax && gc + 3 < cmax) {
+                    v[b][q] = *reinterpret_cast<const float4*>(p);
+                } else {
+                    bool rok = gr < rmax;
+                    v[b][q].x = ld_guard(p + 0, rok && gc + 0 < cmax);
+                    v[b][q].y = ld_guard(p + 1, rok && gc + 1 < cmax);
+                    v[b][q].z = ld_guard(p + 2, rok && gc + 2 < cmax);
+                    v[b][q].w = ld_guard(p + 3, rok && gc + 3 < cmax);
+                }
+            }
+        }
+    }
+
+    // Writes hi / lo planes, layout [mn][STRIDE] (k contiguous), ushort units.
+    template <int STRIDE>
+    __device__ __forceinline__ void store(unsigned short* __restrict__ hi,
+                                          unsigned short* __restrict__ lo, int tid) const {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;
+            if (KCONTIG) { bc = blk % (BK / 4); br = blk / (BK / 4); }
+            else         { bc = blk % (BMN / 4); br = blk / (BMN / 4); }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {       // r indexes mn within the block
+                float x[4];                     // 4 consecutive k at this mn
+                if (KCONTIG) {
+                    x[0] = v[b][r].x; x[1] = v[b][r].y; x[2] = v[b][r].z; x[3] = v[b][r].w;
+                } else {
+                    // v[b][q] holds k row q; pick component r
+                    for (int q = 0; q < 4; ++q) {
+                        const float4& t = v[b][q];
+                        x[q] = r == 0 ? t.x : r == 1 ? t.y : r == 2 ? t.z : t.w;
+                    }
+                }
+                unsigned short h[4], l[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) split_bf16(x[q], h[q], l[q]);
+                int mn = (KCONTIG ? br : bc) * 4 + r;
+                int kk = (KCONTIG ? bc : br) * 4;
+                uint2 hv, lv;
+                hv.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+                hv.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+                lv.x = (uint32_t)l[0] | ((uint32_t)l[1] << 16);
+                lv.y = (uint32_t)l[2] | ((uint32_t)l[3] << 16);
+                *reinterpret_cast<uint2*>(hi + mn * STRIDE + kk) = hv;
+                *reinterpret_cast<uint2*>(lo + mn * STRIDE + kk) = lv;
+            }
+        }
+    }
+};
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int GROUP_M = GROUP_M_;
+    static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
+    static constexpr int NT = WAVES_M * WAVES_N * 64;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+};
+
+__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int group_m,
+                                              int& tm, int& tn) {
+    int nb = gridDim.x;
+    int bid = blockIdx.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    int per_group = group_m * tiles_n;
+    int g = bid / per_group;
+    int first_m = g * group_m;
+    int gsize = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
+    int in_g = bid - g * per_group;
+    tm = first_m + in_g % gsize;
+    tn = in_g / gsize;
+}
+
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN>
+__global__ __launch_bounds__(CF::NT)
+void gemm_bf16x3_kernel(KParams p, int vec) {
+    constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
+    constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
+    static_assert(BK % 32 == 0, "BK must be a multiple of 32");
+    constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
+    constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
+    constexpr int STAGE = 2 * A_PLANE + 2 * B_PLANE;
+    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave / CF::WAVES_N) * CF::WM;
+    const int wn0 = (wave % CF::WAVES_N) * CF::WN;
+    const int l16 = lane & 15;
+    const int lq = lane >> 4;
+
+    int tiles_m = (int)ceil_div(p.M, BM), tiles_n = (int)ceil_div(p.N, BN);
+    int tm, tn;
+    tile_of_block(tiles_m, tiles_n, CF::GROUP_M, tm, tn);
+    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+    const bool v = vec != 0;
+
+    SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK> la;
+    SplitLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK> lb;
+
+    auto load_tiles = [&](int64_t k0) {
+        la.load(p.A, p.lda, bm, k0, p.M, p.K, v, tid);
+        lb.load(p.B, p.ldb, bn, k0, p.N, p.K, v, tid);
+    };
+    auto store_tiles = [&](int buf) {
+        unsigned short* s = lds + buf * STAGE;
+        la.template store<STRIDE>(s, s + A_PLANE, tid);
+        lb.template store<STRIDE>(s + 2 * A_PLANE, s + 2 * A_PLANE + B_PLANE, tid);
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t nk = ceil_div(p.K, BK);
+    load_tiles(0);
+    store_tiles(0);
+    __syncthreads();
+
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int buf = (int)(kt & 1);
+        const bool has_next = kt + 1 < nk;
+        if (has_next) load_tiles((kt + 1) * BK);
+
+        const unsigned short* s = lds + buf * STAGE;
+        const unsigned short* sAh = s;
+        const unsigned short* sAl = s + A_PLANE;
+        const unsigned short* sBh = s + 2 * A_PLANE;
+        const unsigned short* sBl = sBh + B_PLANE;
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int off = (wm0 + i * 16 + l16) * STRIDE + kk + 8 * lq;
+                ah[i] = *reinterpret_cast<const bf16x8*>(sAh + off);
+                al[i] = *reinterpret_cast<const bf16x8*>(sAl + off);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int off = (wn0 + j * 16 + l16) * STRIDE + kk + 8 * lq;
+                bh[j] = *reinterpret_cast<const bf16x8*>(sBh + off);
+                bl[j] = *reinterpret_cast<const bf16x8*>(sBl + off);
+            }
+            // small cross terms first, then the dominant hi*hi term
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+        }
+
+        if (has_next) store_tiles(buf ^ 1);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int jn = 0; jn < FN; ++jn) {
+            const int64_t n = bn + wn0 + jn * 16 + l16;
+            if (n >= p.N) continue;
+            int64_t col_off = n;
+            if (SPLITN) col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
+            float bias_n = 0.0f;
+            if (p.bias_mode == CDX_BIAS_COL) bias_n = p.bias[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = bm + wm0 + i * 16 + 4 * lq + r;
+                if (m >= p.M) continue;
+                float val = acc[i][jn][r];
+                if (p.bias_mode == CDX_BIAS_COL) val += bias_n;
+                else if (p.bias_mode == CDX_BIAS_ROW) val += p.bias[m];
+                val = apply_act(val, p.epilogue);
+                p.C[m * p.ldc + col_off] = val;
+            }
+        }
+    }
+}
+
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN>
+int launch_cfg(const KParams& kp, int vec, hipStream_t stream) {
+    int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
+    if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN>),
+                       dim3((unsigned)tiles), dim3(CF::NT), 0, stream, kp, vec);
+    return hip_error(hipGetLastError(), "gemm_bf16x3_kernel launch");
+}
+
+template <class CF, int OPA, int OPB>
+int launch_mode(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
+    bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&
+               g.lda % 4 == 0 && g.ldb % 4 == 0;
+    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 && g.K % CF::BK == 0;
+    bool split = g.n_split > 0;
+    if (aligned)
+        return split ? launch_cfg<CF, OPA, OPB, false, true>(kp, 1, stream)
+                     : launch_cfg<CF, OPA, OPB, false, false>(kp, 1, stream);
+    return split ? launch_cfg<CF, OPA, OPB, true, true>(kp, vec, stream)
+                 : launch_cfg<CF, OPA, OPB, true, false>(kp, vec, stream);
+}
+
+template <class CF>
+int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
+    if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, kp, stream);
+    if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, kp, stream);
+    if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, kp, stream);
+    return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, kp, stream);
+}
+
+using CfgLarge = Cfg<128, 128, 32, 64, 64, 8>;
+using CfgSkinnyM = Cfg<64, 256, 32, 32, 128, 1>;
+using CfgSmall = Cfg<64, 64, 32, 32, 32, 8>;
+
+}  // namespace
+
+int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue};
+    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, kp, stream);
+    int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);
+    if (large_tiles >= 256) return launch_ops<CfgLarge>(g, kp, stream);
+    return launch_ops<CfgSmall>(g, kp, stream);
+}
+
+}  // namespace cdx

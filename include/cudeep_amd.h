@@ -1,0 +1,171 @@
+/*
+ * cudeep_amd.h -- C-ABI of the MI355X (gfx950) dense-contraction library.
+ *
+ * This is the drop-in boundary for cuDeep's dense-contraction hot path:
+ * the FP32 SGEMM, the "TF32" GEMM (here an explicit bf16x3 split-precision
+ * MFMA GEMM), the fused-epilogue GEMM, the fp64 GEMM, im2col and the
+ * im2col-Conv2d forward, plus the small helpers nn.Linear needs (bias
+ * broadcast, column sums, ReLU/GELU forward and backward).
+ *
+ * Each entry point names the reference interface it replaces
+ * (/root/reference = KevinWeiss1995/cuDeep, file:line).
+ *
+ * Conventions
+ *  - All pointers are device pointers (hipMalloc'd or equivalent) unless
+ *    stated; sizes are 64-bit element counts.  Matrices are row-major and
+ *    dense unless a leading dimension is given.
+ *  - Every entry point returns CDX_OK (0) or a CDX_ERR_* code and never
+ *    throws; cdx_last_error() gives a message for the calling thread.
+ *  - Work is enqueued on `stream` (NULL = the null stream) and is
+ *    asynchronous: execution faults surface at the caller's next sync.
+ *  - The library keeps no global device state: concurrent calls on different
+ *    streams are safe.  Routines that need scratch take a `workspace`
+ *    pointer; passing NULL makes the library allocate and free it
+ *    stream-ordered (hipMallocAsync / hipFreeAsync), as the reference does.
+ */
+#ifndef CUDEEP_AMD_H
+#define CUDEEP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define CDX_OK                 0
+#define CDX_ERR_INVALID_ARG    1   /* null pointer, bad dims, bad enum      */
+#define CDX_ERR_UNSUPPORTED    2   /* valid request the library cannot do   */
+#define CDX_ERR_HIP            3   /* a HIP runtime call failed             */
+#define CDX_ERR_WORKSPACE      4   /* workspace given but too small         */
+
+/* ---- enums ------------------------------------------------------------- */
+#define CDX_OP_N 0                 /* use the operand as stored             */
+#define CDX_OP_T 1                 /* use its transpose                     */
+
+/* Epilogues; values follow cudeep::kernels::GemmEpilogue
+ * (include/cudeep/kernels/matmul.cuh:32-38) for the ones implemented. */
+#define CDX_EPI_NONE 0
+#define CDX_EPI_RELU 1
+#define CDX_EPI_GELU 2
+
+#define CDX_BIAS_NONE 0
+#define CDX_BIAS_ROW  1            /* C[m][n] += bias[m]  (conv: per channel) */
+#define CDX_BIAS_COL  2            /* C[m][n] += bias[n]  (Linear)            */
+
+#define CDX_PREC_FP32     0        /* true-FP32 MFMA (v_mfma_f32_16x16x4_f32) */
+#define CDX_PREC_TF32MODE 1        /* bf16x3 split MFMA, |rel err| <= ~3*2^-16 per product */
+
+/* ---- library --------------------------------------------------------- */
+const char* cdx_last_error(void);
+const char* cdx_version(void);
+
+/* ---- GEMM ------------------------------------------------------------ */
+
+/* C[M,N] = A[M,K] * B[K,N], FP32 MFMA, C overwritten.
+ * Replaces cudeep::kernels::launch_matmul_kernel_fp32<float>
+ * (include/cudeep/kernels/matmul.cuh:14-18, src/kernels/matmul_kernel.cu:1851-1863). */
+int cdx_sgemm_f32(const float* A, const float* B, float* C,
+                  int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* Same product in TF32 mode (bf16x3 split-precision MFMA).
+ * Replaces cudeep::kernels::launch_matmul_kernel<float>, whose SM>=8 path is
+ * the TF32 tensor-core GEMM (matmul.cuh:8-12, matmul_kernel.cu:1785-1841). */
+int cdx_gemm_tf32mode(const float* A, const float* B, float* C,
+                      int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* General form: C = epi(op(A) * op(B) + bias), with leading dimensions,
+ * transposes, a bias vector (per row or per column) and a ReLU/GELU
+ * epilogue.  op(A) is M x K, op(B) is K x N.  Backs the reference's
+ * launch_matmul_fused_act (matmul.cuh:40-44) and lets nn.Linear run
+ * x*W^T + b with ReLU in one launch instead of the strided copy,
+ * broadcast_add and activation kernels (python/cuDeep/nn.py:110-115,
+ * src/tensor.cu:26-68, src/kernels/elementwise_kernel.cu:186-204). */
+int cdx_gemm_ex(int precision, int opA, int opB,
+                int64_t M, int64_t N, int64_t K,
+                const float* A, int64_t lda,
+                const float* B, int64_t ldb,
+                float* C, int64_t ldc,
+                const float* bias, int bias_mode, int epilogue,
+                hipStream_t stream);
+
+/* C = act(A * B), TF32 mode, no bias.
+ * Replaces cudeep::kernels::launch_matmul_fused_act
+ * (matmul.cuh:40-44, matmul_kernel.cu:1884-1924); epilogue is CDX_EPI_*. */
+int cdx_matmul_fused_act(const float* A, const float* B, float* C,
+                         int64_t M, int64_t N, int64_t K, int epilogue,
+                         hipStream_t stream);
+
+/* C[M,N] = op(A) * op(B) in fp64 (v_mfma_f64_16x16x4_f64).
+ * Replaces cudeep::kernels::launch_matmul_kernel<double>
+ * (matmul_kernel.cu:1843-1849, sgemm_double_kernel :691-743). */
+int cdx_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
+              const double* A, int64_t lda, const double* B, int64_t ldb,
+              double* C, int64_t ldc, hipStream_t stream);
+
+/* ---- convolution ------------------------------------------------------ */
+
+/* col[K_col, B*OH*OW] from NCHW input, K_col = IC*KH*KW; bit-exact with
+ * im2col_kernel (src/kernels/conv_kernel.cu:32-65). */
+int cdx_im2col_f32(const float* input, float* col,
+                   int64_t batch, int64_t in_channels, int64_t in_h, int64_t in_w,
+                   int64_t kernel_h, int64_t kernel_w,
+                   int64_t stride_h, int64_t stride_w,
+                   int64_t pad_h, int64_t pad_w, hipStream_t stream);
+
+/* Bytes of workspace cdx_conv2d_forward_f32 needs (the im2col buffer). */
+size_t cdx_conv2d_forward_workspace_size(
+    int64_t batch, int64_t in_channels, int64_t in_h, int64_t in_w,
+    int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+    int64_t pad_h, int64_t pad_w);
+
+/* NCHW conv forward: im2col -> one GEMM weight[OC,K_col] * col -> NCHW
+ * output with the bias added in the GEMM epilogue (no transpose pass).
+ * Replaces cudeep::kernels::launch_conv2d_forward_kernel<float>
+ * (include/cudeep/kernels/conv.cuh:8-16, src/kernels/conv_kernel.cu:225-335).
+ * bias may be NULL.  precision is CDX_PREC_*.  workspace may be NULL. */
+int cdx_conv2d_forward_f32(const float* input, const float* weight,
+                           const float* bias, float* output,
+                           int64_t batch, int64_t in_channels, int64_t out_channels,
+                           int64_t in_h, int64_t in_w,
+                           int64_t kernel_h, int64_t kernel_w,
+                           int64_t stride_h, int64_t stride_w,
+                           int64_t pad_h, int64_t pad_w, int precision,
+                           void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+/* ---- Linear helpers ---------------------------------------------------- */
+
+/* out[j] = sum_i in[i][j] over a row-major [rows, cols] matrix.
+ * Replaces cudeep::kernels::launch_sum_reduce_rows_kernel<float>
+ * (include/cudeep/kernels/unary.cuh:32-35, src/kernels/unary_kernel.cu:204-245).
+ * Deterministic two-pass reduction; workspace may be NULL. */
+size_t cdx_sum_reduce_rows_workspace_size(int64_t rows, int64_t cols);
+int cdx_sum_reduce_rows_f32(const float* input, float* output,
+                            int64_t rows, int64_t cols,
+                            void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
+/* out[i][j] = m[i][j] + row[j].  Replaces
+ * cudeep::kernels::launch_broadcast_add_row_kernel<float>
+ * (include/cudeep/kernels/elementwise.cuh:26-29, elementwise_kernel.cu:186-204). */
+int cdx_broadcast_add_row_f32(const float* matrix, const float* row, float* out,
+                              int64_t rows, int64_t cols, hipStream_t stream);
+
+/* ReLU / GELU forward and backward (act = CDX_EPI_RELU or CDX_EPI_GELU).
+ * Replace launch_activation_forward_kernel / launch_activation_backward_kernel
+ * for those two activations (include/cudeep/kernels/activation.cuh:17-31,
+ * src/kernels/activation_kernel.cu:19-52, :256-319). */
+int cdx_activation_forward_f32(const float* input, float* output, int64_t n,
+                               int act, hipStream_t stream);
+int cdx_activation_backward_f32(const float* grad_output, const float* input,
+                                float* grad_input, int64_t n, int act,
+                                hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUDEEP_AMD_H */

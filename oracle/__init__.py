@@ -66,6 +66,8 @@ def lib():
         L.orc_dgemm_f64.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64,
                                     _int, _int, _i64, _i64]
         L.orc_gemm_tf32emu.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _int]
+        L.orc_gemm_tf32emu_rows.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _int,
+                                            _i64, _i64]
         L.orc_tf32_round.argtypes = [ctypes.c_float, _int]
         L.orc_tf32_round.restype = ctypes.c_float
         L.orc_im2col.argtypes = [_vp, _vp] + [_i64] * 10
@@ -151,14 +153,16 @@ def tf32_round(x, mode: str = "rz"):
     return u.view(np.float32)
 
 
-def gemm_tf32emu(A, B, mode: str = "rz"):
-    """Emulated reference TF32 tensor-core GEMM (ideal MMA, 8-term k chunks)."""
+def gemm_tf32emu(A, B, mode: str = "rz", rows=None):
+    """Emulated reference TF32 tensor-core GEMM (ideal MMA, 8-term k chunks).
+    ``rows=(r0, r1)`` computes only output rows [r0, r1)."""
     A, B = _c32(A), _c32(B)
     M, K = A.shape
     _, N = B.shape
-    C = np.empty((M, N), np.float32)
-    lib().orc_gemm_tf32emu(_p(A), _p(B), _p(C), M, N, K,
-                           {"rz": 0, "rne": 1}[mode])
+    r0, r1 = (0, M) if rows is None else rows
+    C = np.empty((r1 - r0, N), np.float32)
+    lib().orc_gemm_tf32emu_rows(_p(A), _p(B), _p(C), M, N, K,
+                                {"rz": 0, "rne": 1}[mode], r0, r1)
     return C
 
 

@@ -185,23 +185,42 @@ float orc_tf32_round(float x, int mode) { return tf32_round(x, mode); }
  * (matmul_kernel.cu:179-214: 4 MMA k-steps of 8 per BK_TC=32 tile).
  * An 11-bit x 11-bit product is exact in double and 8 of them sum exactly.
  */
+void orc_gemm_tf32emu_rows(const float* A, const float* B, float* C,
+                           int64_t M, int64_t N, int64_t K, int round_mode,
+                           int64_t row0, int64_t row1) {
+    (void)M;
+    /* Round B once (a copy); A is rounded on the fly. */
+    float* Br = (float*)malloc((size_t)K * (size_t)N * sizeof(float));
+    #pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < K * N; ++t) Br[t] = tf32_round(B[t], round_mode);
+    #pragma omp parallel
+    {
+        double* chunk = (double*)malloc((size_t)N * sizeof(double));
+        float* acc = (float*)malloc((size_t)N * sizeof(float));
+        #pragma omp for schedule(dynamic, 1)
+        for (int64_t i = row0; i < row1; ++i) {
+            for (int64_t j = 0; j < N; ++j) acc[j] = 0.0f;
+            for (int64_t k0 = 0; k0 < K; k0 += 8) {
+                int64_t k1 = k0 + 8 < K ? k0 + 8 : K;
+                for (int64_t j = 0; j < N; ++j) chunk[j] = 0.0;
+                for (int64_t k = k0; k < k1; ++k) {
+                    double a = (double)tf32_round(A[i * K + k], round_mode);
+                    const float* brow = Br + k * N;
+                    for (int64_t j = 0; j < N; ++j) chunk[j] += a * (double)brow[j];
+                }
+                for (int64_t j = 0; j < N; ++j) acc[j] = (float)((double)acc[j] + chunk[j]);
+            }
+            for (int64_t j = 0; j < N; ++j) C[(i - row0) * N + j] = acc[j];
+        }
+        free(chunk);
+        free(acc);
+    }
+    free(Br);
+}
+
 void orc_gemm_tf32emu(const float* A, const float* B, float* C,
                       int64_t M, int64_t N, int64_t K, int round_mode) {
-    #pragma omp parallel for schedule(dynamic, 4)
-    for (int64_t i = 0; i < M; ++i) {
-        for (int64_t j = 0; j < N; ++j) {
-            float acc = 0.0f;
-            for (int64_t k0 = 0; k0 < K; k0 += 8) {
-                double chunk = 0.0;
-                int64_t k1 = k0 + 8 < K ? k0 + 8 : K;
-                for (int64_t k = k0; k < k1; ++k)
-                    chunk += (double)tf32_round(A[i * K + k], round_mode) *
-                             (double)tf32_round(B[k * N + j], round_mode);
-                acc = (float)((double)acc + chunk);
-            }
-            C[i * N + j] = acc;
-        }
-    }
+    orc_gemm_tf32emu_rows(A, B, C, M, N, K, round_mode, 0, M);
 }
 
 static inline int64_t conv_out(int64_t in, int64_t k, int64_t s, int64_t p) {

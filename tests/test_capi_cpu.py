@@ -1,0 +1,93 @@
+"""CPU-side checks of the C-ABI boundary (no GPU, no compute calls):
+the library loads, exports every entry point include/cudeep_amd.h declares,
+and rejects bad arguments with status codes before any HIP call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cudeep_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cudeep_amd.h")
+
+
+def declared_symbols():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(cdx_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    for must in ("cdx_sgemm_f32", "cdx_gemm_tf32mode", "cdx_gemm_ex", "cdx_im2col_f32",
+                 "cdx_conv2d_forward_f32", "cdx_sum_reduce_rows_f32", "cdx_dgemm"):
+        assert must in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the Python signature table covers exactly the header
+    assert sorted(L.SIGNATURES) == declared_symbols()
+
+
+def test_version_string():
+    assert b"gfx950" in L.lib().cdx_version()
+
+
+def _status(name, *args):
+    return getattr(L.lib(), name)(*args)
+
+
+def test_gemm_argument_validation():
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: validation fails first
+    assert _status("cdx_gemm_ex", 0, 7, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 0, None) \
+        == L.CDX_ERR_INVALID_ARG
+    assert b"opA" in L.lib().cdx_last_error()
+    assert _status("cdx_gemm_ex", 0, 0, 0, -1, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 0, None) \
+        == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, fake, 3, fake, 4, fake, 4, None, 0, 0, None) \
+        == L.CDX_ERR_INVALID_ARG          # lda < K
+    assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, None, 4, fake, 4, fake, 4, None, 0, 0, None) \
+        == L.CDX_ERR_INVALID_ARG          # NULL A
+    assert _status("cdx_gemm_ex", 9, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 0, None) \
+        == L.CDX_ERR_INVALID_ARG          # precision
+    assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 2, 0, None) \
+        == L.CDX_ERR_INVALID_ARG          # bias mode without bias
+    assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 5, None) \
+        == L.CDX_ERR_INVALID_ARG          # epilogue
+    assert _status("cdx_sgemm_f32", fake, fake, None, 4, 4, 4, None) == L.CDX_ERR_INVALID_ARG
+    # empty problems are a successful no-op and touch nothing
+    assert _status("cdx_sgemm_f32", None, None, None, 0, 4, 4, None) == L.CDX_OK
+    assert _status("cdx_gemm_tf32mode", None, None, None, 4, 0, 4, None) == L.CDX_OK
+    assert _status("cdx_dgemm", 0, 0, 0, 0, 0, None, 1, None, 1, None, 1, None) == L.CDX_OK
+
+
+def test_conv_argument_validation():
+    fake = ctypes.c_void_p(0x1000)
+    # kernel larger than padded input
+    assert _status("cdx_im2col_f32", fake, fake, 1, 1, 2, 2, 5, 5, 1, 1, 0, 0, None) \
+        == L.CDX_ERR_INVALID_ARG
+    # zero stride
+    assert _status("cdx_conv2d_forward_f32", fake, fake, None, fake, 1, 1, 1, 4, 4, 3, 3,
+                   0, 1, 0, 0, 0, None, 0, None) == L.CDX_ERR_INVALID_ARG
+    # workspace too small
+    assert _status("cdx_conv2d_forward_f32", fake, fake, None, fake, 1, 1, 1, 4, 4, 3, 3,
+                   1, 1, 0, 0, 0, fake, 4, None) == L.CDX_ERR_WORKSPACE
+    # workspace size query = K_col * B * OH * OW * 4
+    assert L.lib().cdx_conv2d_forward_workspace_size(32, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
+        == 576 * 32 * 56 * 56 * 4
+    assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 32 * 256 * 4
+    assert _status("cdx_activation_forward_f32", fake, fake, 4, 0, None) == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_sum_reduce_rows_f32", None, fake, 4, 4, None, 0, None) \
+        == L.CDX_ERR_INVALID_ARG
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(L, "_lib", None)
+    monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "nope.so"))
+    with pytest.raises(ImportError):
+        L.lib()

@@ -1,0 +1,142 @@
+"""GPU parity of im2col and the im2col-Conv2d forward.
+
+  * im2col: bit-exact (compared as uint32 bit patterns) with the oracle's
+    restatement of conv_kernel.cu:32-65, including the full C5 geometry.
+  * conv forward: relFro vs the fp64 direct convolution <= 2 x that of the
+    reference route restated on the CPU (im2col -> seq-FMA SGEMM ->
+    transpose + bias); TF32 mode against the emulated TF32 route.
+  * the reference's conv known answers (identity, 3x3 ones, bias, padding).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_util import dev, host, normal, require_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def ops():
+    import cudeep_amd.ops as o
+    return o
+
+
+GEOMS = [  # (B, C, H, W, KH, KW, SH, SW, PH, PW)
+    (1, 1, 4, 4, 1, 1, 1, 1, 0, 0),
+    (2, 3, 8, 9, 3, 3, 1, 1, 1, 1),
+    (1, 2, 7, 7, 3, 5, 2, 1, 2, 0),
+    (3, 4, 6, 5, 2, 1, 1, 1, 0, 0),       # spatial % 4 != 0 -> scalar stores
+    (2, 5, 11, 13, 5, 5, 2, 2, 2, 2),
+    (4, 16, 28, 28, 3, 3, 1, 1, 1, 1),
+    (2, 8, 15, 17, 1, 1, 2, 2, 0, 0),
+    (1, 3, 3, 3, 3, 3, 1, 1, 0, 0),       # single output pixel
+]
+
+
+@pytest.mark.parametrize("g", GEOMS)
+def test_im2col_bit_exact(g):
+    Bn, C, H, W, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    x[0, 0, 0, 0] = -0.0                   # sign of zero must survive
+    say("im2col", g)
+    col = host(ops().im2col(dev(x), KH, KW, (SH, SW), (PH, PW)))
+    want = oracle.im2col(x, KH, KW, SH, SW, PH, PW)
+    assert col.shape == want.shape
+    assert np.array_equal(col.view(np.uint32), want.view(np.uint32))
+
+
+def test_im2col_c5_full_bit_exact():
+    """C5 geometry: N=32, C=64, 56x56, 3x3, s1, p1 -> col [576, 100352]."""
+    rng = np.random.default_rng(555)
+    x = normal(rng, (32, 64, 56, 56))
+    say("im2col C5 full")
+    col = host(ops().im2col(dev(x), 3, 3, (1, 1), (1, 1)))
+    want = oracle.im2col(x, 3, 3, 1, 1, 1, 1)
+    assert col.shape == (576, 100352)
+    assert np.array_equal(col.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", ["conv_identity_1x1", "conv_3x3_ones", "conv_3x3_bias",
+                                  "conv_3x3_pad1"])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_kats(kats, name, prec):
+    k = kats[name]
+    x = np.array(k["x"], np.float32).reshape(k["x_shape"])
+    w = np.array(k["w"], np.float32).reshape(k["w_shape"])
+    b = None if k["bias"] is None else dev(np.array(k["bias"], np.float32))
+    say("conv kat", name, prec)
+    y = host(ops().conv2d_forward(dev(x), dev(w), b, k["stride"], k["padding"], precision=prec))
+    assert np.array_equal(y.ravel(), np.array(k["y"], np.float32))
+
+
+def _conv_gate(x, w, b, stride, padding, y):
+    d64 = oracle.conv2d_direct64(x, w, b, stride, padding)
+    ref = oracle.conv2d_ref_im2col(x, w, b, stride, padding)
+    return oracle.rel_fro(y, d64), oracle.rel_fro(ref, d64)
+
+
+@pytest.mark.parametrize("g", GEOMS[1:6])
+def test_conv_forward_parity(g):
+    Bn, C, H, W, KH, KW, SH, SW, PH, PW = g
+    OC = 7
+    rng = np.random.default_rng(100 + sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    w = normal(rng, (OC, C, KH, KW), std=np.sqrt(2.0 / (C * KH * KW)))
+    b = normal(rng, (OC,), 0.1)
+    say("conv fwd", g)
+    y = host(ops().conv2d_forward(dev(x), dev(w), dev(b), (SH, SW), (PH, PW)))
+    e, e_ref = _conv_gate(x, w, b, (SH, SW), (PH, PW), y)
+    assert e <= 2 * e_ref + 2.0 ** -24, (e, e_ref)
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_c5_full_batch_sampled(prec):
+    """C5: N=32, C=64, 56x56 -> 64, 3x3, s1, p1, He-normal weights, seeded
+    bias.  GPU runs the full batch; the oracle checks batch items 0 and 31
+    (conv outputs are independent per batch item)."""
+    rng = np.random.default_rng(5050)
+    x = normal(rng, (32, 64, 56, 56))
+    w = normal(rng, (64, 64, 3, 3), std=np.sqrt(2.0 / 576))
+    b = normal(rng, (64,), 0.1)
+    say("conv C5 full batch prec", prec)
+    y = host(ops().conv2d_forward(dev(x), dev(w), dev(b), (1, 1), (1, 1), precision=prec))
+    assert y.shape == (32, 64, 56, 56) and np.isfinite(y).all()
+    for i in (0, 31):
+        xi = x[i:i + 1]
+        d64 = oracle.conv2d_direct64(xi, w, b, (1, 1), (1, 1))
+        e = oracle.rel_fro(y[i:i + 1], d64)
+        if prec == 0:
+            e_ref = oracle.rel_fro(oracle.conv2d_ref_im2col(xi, w, b, (1, 1), (1, 1)), d64)
+            print(f"C5 item {i}: fp32 gpu={e:.3e} seqfma-route={e_ref:.3e}")
+            assert e <= 2 * e_ref
+        else:
+            col = oracle.im2col(xi, 3, 3, 1, 1, 1, 1)
+            errs = []
+            for mode in ("rz", "rne"):
+                flat = oracle.gemm_tf32emu(w.reshape(64, -1), col, mode)
+                yr = oracle.transpose_bias(flat, 64, 1, 3136, b).reshape(1, 64, 56, 56)
+                errs.append(oracle.rel_fro(yr, d64))
+            print(f"C5 item {i}: tf32mode gpu={e:.3e} tf32 route rz/rne={errs}")
+            assert e <= min(errs)
+
+
+def test_conv_workspace_and_no_bias():
+    import torch
+    rng = np.random.default_rng(77)
+    x = normal(rng, (2, 3, 9, 9))
+    w = normal(rng, (5, 3, 3, 3))
+    nbytes = ops().conv2d_workspace_bytes(x.shape, w.shape, (1, 1), (1, 1))
+    assert nbytes == 27 * 2 * 81 * 4
+    ws = torch.empty(nbytes // 4, device="cuda")
+    say("conv with workspace")
+    y1 = host(ops().conv2d_forward(dev(x), dev(w), None, (1, 1), (1, 1), workspace=ws))
+    y2 = host(ops().conv2d_forward(dev(x), dev(w), None, (1, 1), (1, 1)))
+    assert np.array_equal(y1, y2)
+    e, e_ref = _conv_gate(x, w, None, (1, 1), (1, 1), y1)
+    assert e <= 2 * e_ref + 2.0 ** -24

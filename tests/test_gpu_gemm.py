@@ -1,0 +1,288 @@
+"""GPU parity of the GEMM entry points against the CPU oracle.
+
+Gates (the north_star bars):
+  * FP32: relFro(gpu vs fp64) <= 2 x relFro(seq-FMA restatement of the
+    reference SGEMM vs fp64), on the same seeded inputs.
+  * TF32 mode (bf16x3): relFro(gpu vs fp64) <= min over {RZ, RNE} of the
+    emulated reference TF32 kernel's relFro.
+  * integer-valued inputs (reference MMA KATs): exact.
+At 4096^3 the CPU oracle runs on a sample of rows; the full output is
+checked by a size-independent identity: column sums of C equal
+(column sums of A) @ B, computed in fp64.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_util import F32_FLOOR, dev, host, normal, require_gpu, say, uniform
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+    import cudeep_amd.ops  # noqa: F401  (loads libcudeep_amd.so)
+
+
+def ops():
+    import cudeep_amd.ops as o
+    return o
+
+
+def _ref_errors(A, B, tA=False, tB=False, rows=None):
+    C64 = oracle.dgemm(A, B, tA, tB, rows=rows)
+    Cs = oracle.sgemm_seqfma(A, B, tA, tB, rows=rows)
+    return C64, oracle.rel_fro(Cs, C64)
+
+
+# ---------------------------------------------------------------------------
+# reference known answers (tests/golden/kats.json)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["matmul_2x2", "matmul_diag_identity", "mma_identity",
+                                  "mma_integer_pattern"])
+@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+def test_gemm_kats_exact(kats, name, mode):
+    k = kats[name]
+    A = np.array(k["A"], np.float32)
+    B = np.array(k["B"], np.float32)
+    say("kat", name, mode)
+    f = ops().sgemm if mode == "fp32" else ops().gemm_tf32mode
+    C = host(f(dev(A), dev(B)))
+    assert np.array_equal(C, np.array(k["C"], np.float32))
+
+
+def test_gemm_kat_partial_identity_and_scaled(kats):
+    k = kats["matmul_partial_identity"]
+    say("kat partial identity")
+    C = host(ops().sgemm(dev(np.array(k["A"], np.float32)), dev(np.array(k["B"], np.float32))))
+    assert np.array_equal(C[0], np.array(k["C_row0"], np.float32))
+    k = kats["matmul_scaled_identity_8"]
+    A = np.array(k["A"], np.float32)
+    for f in (ops().sgemm, ops().gemm_tf32mode):
+        C = host(f(dev(A), dev(np.eye(8, dtype=np.float32))))
+        assert np.allclose(C, A, atol=k["atol"])
+
+
+def test_randn_times_identity_rtol_1e5():
+    # tests/unit/test_tensor_ops.py:220-227: randn(N,N) @ I within rtol 1e-5
+    rng = np.random.default_rng(21)
+    A = normal(rng, (96, 96))
+    say("randn @ I")
+    for f in (ops().sgemm, ops().gemm_tf32mode):
+        C = host(f(dev(A), dev(np.eye(96, dtype=np.float32))))
+        assert np.allclose(C, A, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+def test_integer_inputs_exact_any_shape(mode):
+    rng = np.random.default_rng(22)
+    for (M, N, K) in [(16, 8, 8), (130, 70, 200), (256, 256, 64)]:
+        A = rng.integers(-8, 9, (M, K)).astype(np.float32)
+        B = rng.integers(-8, 9, (K, N)).astype(np.float32)
+        say("integer", mode, M, N, K)
+        f = ops().sgemm if mode == "fp32" else ops().gemm_tf32mode
+        assert np.array_equal(host(f(dev(A), dev(B))), A.astype(np.float64) @ B)
+
+
+# ---------------------------------------------------------------------------
+# FP32 parity vs the sequential-FMA restatement
+# ---------------------------------------------------------------------------
+
+SHAPES = [(1, 1, 1), (2, 3, 5), (17, 33, 65), (64, 64, 16), (128, 128, 128),
+          (127, 255, 33), (300, 200, 784), (8192, 10, 256), (10, 8192, 256),
+          (64, 4096, 576), (256, 512, 1000), (513, 129, 4099)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+def test_fp32_gemm_parity_shapes(M, N, K, tA, tB):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K + 2 * tA + tB)
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (N, K) if tB else (K, N))
+    say("fp32", M, N, K, "tA", tA, "tB", tB)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB))
+    C64, e_ref = _ref_errors(A, B, tA, tB)
+    e = oracle.rel_fro(C, C64)
+    floor = F32_FLOOR if K < 64 else 0.0
+    assert e <= 2 * e_ref + floor, (e, e_ref)
+
+
+def test_fp32_c1_512_uniform():
+    """C1: 512^3, A, B ~ U[-1, 1]."""
+    rng = np.random.default_rng(101)
+    A = uniform(rng, (512, 512))
+    B = uniform(rng, (512, 512))
+    say("C1 512^3")
+    C = host(ops().sgemm(dev(A), dev(B)))
+    C64, e_ref = _ref_errors(A, B)
+    e = oracle.rel_fro(C, C64)
+    print(f"C1 relFro gpu={e:.3e} seqfma={e_ref:.3e}")
+    assert e <= 2 * e_ref
+
+
+def _checksum_identity(A, B, C):
+    """e^T C == (e^T A) B in fp64; returns the relative error."""
+    lhs = C.astype(np.float64).sum(0)
+    rhs = A.astype(np.float64).sum(0) @ B.astype(np.float64)
+    return np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs)
+
+
+def test_fp32_c2_4096_sampled_rows_and_checksum():
+    """C2: 4096^3, A, B ~ N(0, 1)."""
+    rng = np.random.default_rng(202)
+    n = 4096
+    A = normal(rng, (n, n))
+    B = normal(rng, (n, n))
+    say("C2 4096^3 fp32")
+    C = host(ops().sgemm(dev(A), dev(B)))
+    assert np.isfinite(C).all()
+    errs = []
+    for r0 in (0, 1792, n - 128):
+        rows = (r0, r0 + 128)
+        C64, e_ref = _ref_errors(A, B, rows=rows)
+        e = oracle.rel_fro(C[r0:r0 + 128], C64)
+        errs.append((e, e_ref))
+        assert e <= 2 * e_ref, (rows, e, e_ref)
+    print("C2 sampled relFro (gpu, seqfma):", errs)
+    assert _checksum_identity(A, B, C) < 1e-5
+
+
+@pytest.mark.parametrize("n", [2048, 4096])
+def test_tf32mode_c3(n):
+    """C3: TF32 mode at 2048^3 / 4096^3, inputs N(0,1): raw fp32 (the bits
+    the reference feeds its MMA) and pre-rounded to TF32 (RNE)."""
+    rng = np.random.default_rng(303 + n)
+    A = normal(rng, (n, n))
+    B = normal(rng, (n, n))
+    say("C3 tf32mode", n)
+    C = host(ops().gemm_tf32mode(dev(A), dev(B)))
+    rows = (n // 2, n // 2 + 96)
+    C64 = oracle.dgemm(A, B, rows=rows)
+    e = oracle.rel_fro(C[rows[0]:rows[1]], C64)
+    e_rz = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rz", rows=rows), C64)
+    e_rne = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rne", rows=rows), C64)
+    print(f"C3 n={n} raw: bf16x3={e:.3e} tf32(rz)={e_rz:.3e} tf32(rne)={e_rne:.3e}")
+    assert e <= min(e_rz, e_rne)
+    assert _checksum_identity(A, B, C) < 1e-4
+
+
+def test_tf32mode_parity_shapes():
+    rng = np.random.default_rng(304)
+    for (M, N, K) in [(17, 33, 65), (300, 200, 784), (8192, 10, 256), (64, 1000, 576)]:
+        A = normal(rng, (M, K))
+        B = normal(rng, (K, N))
+        say("tf32 shape", M, N, K)
+        C = host(ops().gemm_tf32mode(dev(A), dev(B)))
+        C64 = oracle.dgemm(A, B)
+        e = oracle.rel_fro(C, C64)
+        e_rne = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rne"), C64)
+        assert e <= e_rne, (M, N, K, e, e_rne)
+
+
+@pytest.mark.parametrize("tA,tB", [(False, True), (True, False), (True, True)])
+def test_tf32mode_transposes(tA, tB):
+    import cudeep_amd as cd
+    rng = np.random.default_rng(305)
+    M, N, K = 200, 300, 500
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (N, K) if tB else (K, N))
+    say("tf32 transposes", tA, tB)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, precision=cd.PREC_TF32MODE))
+    C64 = oracle.dgemm(A, B, tA, tB)
+    opA = A.T if tA else A
+    opB = B.T if tB else B
+    e_rne = oracle.rel_fro(oracle.gemm_tf32emu(np.ascontiguousarray(opA),
+                                               np.ascontiguousarray(opB), "rne"), C64)
+    assert oracle.rel_fro(C, C64) <= e_rne
+
+
+# ---------------------------------------------------------------------------
+# fused epilogues (bias per row / column, ReLU, GELU)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+@pytest.mark.parametrize("epi", ["none", "relu", "gelu"])
+@pytest.mark.parametrize("bias_mode", ["none", "row", "col"])
+def test_fused_epilogue(mode, epi, bias_mode):
+    import cudeep_amd as cd
+    rng = np.random.default_rng(401)
+    M, N, K = 333, 257, 200
+    A = normal(rng, (M, K))
+    B = normal(rng, (K, N))
+    bias = normal(rng, (M if bias_mode == "row" else N,))
+    bm = {"none": cd.BIAS_NONE, "row": cd.BIAS_ROW, "col": cd.BIAS_COL}[bias_mode]
+    ep = {"none": cd.EPI_NONE, "relu": cd.EPI_RELU, "gelu": cd.EPI_GELU}[epi]
+    prec = cd.PREC_FP32 if mode == "fp32" else cd.PREC_TF32MODE
+    say("epilogue", mode, epi, bias_mode)
+    C = host(ops().gemm(dev(A), dev(B), precision=prec, bias=dev(bias) if bm else None,
+                        bias_mode=bm, epilogue=ep))
+    Z = oracle.dgemm(A, B)
+    if bias_mode == "row":
+        Z = Z + bias[:, None]
+    elif bias_mode == "col":
+        Z = Z + bias[None, :]
+    want = {"none": Z, "relu": oracle.relu(Z), "gelu": oracle.gelu(Z)}[epi]
+    scale = np.abs(Z).max()
+    # GEMM error (<= ~1e-6 relative) plus the epilogue's own few-ulp error
+    assert np.max(np.abs(C - want)) <= 2e-5 * scale + 1e-6
+
+
+def test_matmul_fused_act_entry_point():
+    import ctypes
+    import torch
+    from cudeep_amd import _lib as L
+    rng = np.random.default_rng(402)
+    A = normal(rng, (128, 64))
+    B = normal(rng, (64, 96))
+    dA, dB = dev(A), dev(B)
+    out = torch.empty((128, 96), device="cuda")
+    say("matmul_fused_act relu")
+    L.call("cdx_matmul_fused_act", dA.data_ptr(), dB.data_ptr(), out.data_ptr(), 128, 96, 64,
+           L.EPI_RELU, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    C = host(out)
+    want = oracle.relu(oracle.dgemm(A, B))
+    assert np.max(np.abs(C - want)) <= 1e-4
+
+
+# ---------------------------------------------------------------------------
+# fp64 GEMM, degenerate shapes
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("tA,tB", [(False, False), (True, True), (False, True)])
+def test_dgemm(tA, tB):
+    rng = np.random.default_rng(501)
+    M, N, K = 129, 77, 300
+    A = rng.standard_normal((K, M) if tA else (M, K))
+    B = rng.standard_normal((N, K) if tB else (K, N))
+    say("dgemm", tA, tB)
+    C = host(ops().dgemm(dev(A), dev(B), tA, tB))
+    want = (A.T if tA else A) @ (B.T if tB else B)
+    assert np.allclose(C, want, rtol=1e-12, atol=1e-12)
+
+
+def test_k_zero_gives_bias_only():
+    import torch
+    import cudeep_amd as cd
+    say("K=0")
+    A = torch.empty((5, 0), device="cuda")
+    B = torch.empty((0, 7), device="cuda")
+    bias = torch.arange(7, dtype=torch.float32, device="cuda")
+    for prec in (cd.PREC_FP32, cd.PREC_TF32MODE):
+        C = host(ops().gemm(A, B, precision=prec, bias=bias, bias_mode=cd.BIAS_COL))
+        assert np.array_equal(C, np.tile(np.arange(7, dtype=np.float32), (5, 1)))
+
+
+def test_leading_dimension_views():
+    """op(A) with lda > K: a column window of a wider matrix."""
+    rng = np.random.default_rng(502)
+    big = normal(rng, (200, 300))
+    B = normal(rng, (120, 90))
+    dbig = dev(big)
+    view = dbig[:, 40:160]          # 200 x 120, lda = 300
+    say("lda view")
+    C = host(ops().gemm(view, dev(B)))
+    C64 = oracle.dgemm(big[:, 40:160], B)
+    _, e_ref = _ref_errors(np.ascontiguousarray(big[:, 40:160]), B)
+    assert oracle.rel_fro(C, C64) <= 2 * e_ref

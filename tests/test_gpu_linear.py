@@ -1,0 +1,174 @@
+"""GPU parity of the Linear path (C4: MLP 784 -> 256 -> 10, batch 8192).
+
+The reference's nn.Linear forward is matmul(x, W^T) + broadcast bias, then
+the activation module (python/cuDeep/nn.py:110-115); backward is
+dX = dY W, dW = dY^T X, db = column sums of dY (tensor.py:430-443,
+:617-631).  Here the forward is one fused GEMM (bias + ReLU epilogue) and
+the backward uses transposed-operand GEMMs.  Gate: relFro vs fp64 <= 2 x
+the error of the reference route restated on the CPU (seq-FMA SGEMM, then
+one fp32 bias add, then the activation).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_util import dev, host, normal, require_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    require_gpu()
+
+
+def ops():
+    import cudeep_amd.ops as o
+    return o
+
+
+def xavier(rng, fan_out, fan_in):
+    bound = np.sqrt(6.0 / (fan_in + fan_out))    # init.py:28-40, gain 1
+    return rng.uniform(-bound, bound, (fan_out, fan_in)).astype(np.float32)
+
+
+@pytest.fixture(scope="module")
+def mlp():
+    rng = np.random.default_rng(4040)
+    X = normal(rng, (8192, 784))
+    W1 = xavier(rng, 256, 784)
+    W2 = xavier(rng, 10, 256)
+    b1 = normal(rng, (256,), 0.1)
+    b2 = normal(rng, (10,), 0.1)
+    dY2 = normal(rng, (8192, 10))
+    return X, W1, b1, W2, b2, dY2
+
+
+def _ref_route_linear(x, W, b, act):
+    z = oracle.sgemm_seqfma(x, W, transB=True)
+    z = (z + b[None, :]).astype(np.float32)
+    if act == "relu":
+        z = np.maximum(z, np.float32(0))
+    return z
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_mlp_forward_fused(mlp, prec):
+    import cudeep_amd as cd
+    X, W1, b1, W2, b2, _ = mlp
+    say("C4 forward prec", prec)
+    dX, dW1, db1, dW2, db2 = map(dev, (X, W1, b1, W2, b2))
+    H = ops().gemm(dX, dW1, transB=True, bias=db1, bias_mode=cd.BIAS_COL,
+                   epilogue=cd.EPI_RELU, precision=prec)
+    Y = ops().gemm(H, dW2, transB=True, bias=db2, bias_mode=cd.BIAS_COL, precision=prec)
+    H, Y = host(H), host(Y)
+    H64 = oracle.relu(oracle.dgemm(X, W1, transB=True) + b1[None, :])
+    e1 = oracle.rel_fro(H, H64)
+    e1_ref = oracle.rel_fro(_ref_route_linear(X, W1, b1, "relu"), H64)
+    # layer 2 judged on the GPU's own H (errors do not compound in the gate)
+    Y64 = oracle.dgemm(H, W2, transB=True) + b2[None, :]
+    e2 = oracle.rel_fro(Y, Y64)
+    e2_ref = oracle.rel_fro(_ref_route_linear(H, W2, b2, None), Y64)
+    print(f"C4 fwd prec={prec}: L1 {e1:.3e} (ref {e1_ref:.3e})  L2 {e2:.3e} (ref {e2_ref:.3e})")
+    assert e1 <= 2 * e1_ref and e2 <= 2 * e2_ref
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_mlp_backward(mlp, prec):
+    import cudeep_amd as cd
+    X, W1, b1, W2, b2, dY2 = mlp
+    rng = np.random.default_rng(4041)
+    dY1 = normal(rng, (8192, 256))
+    say("C4 backward prec", prec)
+    gX, gW1, gY1 = dev(X), dev(W1), dev(dY1)
+    dX1 = host(ops().gemm(gY1, gW1, precision=prec))                    # dY W
+    dW1 = host(ops().gemm(gY1, gX, transA=True, precision=prec))        # dY^T X
+    db1 = host(ops().sum_reduce_rows(gY1))
+    dX2 = host(ops().gemm(dev(dY2), dev(W2), precision=prec))           # K = 10
+    dW2 = host(ops().gemm(dev(dY2), gY1, transA=True, precision=prec))  # M = 10
+    cases = [
+        ("dX1", dX1, dY1, W1, False), ("dW1", dW1, dY1, X, True),
+        ("dX2", dX2, dY2, W2, False), ("dW2", dW2, dY2, dY1, True)]
+    for name, got, a, bm, tA in cases:
+        ref64 = oracle.dgemm(a, bm, transA=tA)
+        e = oracle.rel_fro(got, ref64)
+        e_ref = oracle.rel_fro(oracle.sgemm_seqfma(a, bm, transA=tA), ref64)
+        print(f"C4 bwd prec={prec} {name}: {e:.3e} (ref {e_ref:.3e})")
+        if prec == 0:
+            assert e <= 2 * e_ref, name
+        else:
+            e_tf = oracle.rel_fro(oracle.gemm_tf32emu(
+                np.ascontiguousarray(a.T if tA else a), bm, "rne"), ref64)
+            assert e <= e_tf, name
+    db64 = dY1.astype(np.float64).sum(0)
+    e = oracle.rel_fro(db1, db64)
+    e_ref = oracle.rel_fro(oracle.colsum(dY1), db64)
+    assert e <= 2 * e_ref + 2.0 ** -24
+
+
+def test_linear_kats(kats):
+    import cudeep_amd as cd
+    for name in ("linear_fixed_weight", "linear_identity_bias"):
+        k = kats[name]
+        say("linear kat", name)
+        y = host(ops().gemm(dev(np.array(k["x"], np.float32)), dev(np.array(k["W"], np.float32)),
+                            transB=True, bias=dev(np.array(k["b"], np.float32)),
+                            bias_mode=cd.BIAS_COL))
+        assert np.array_equal(y, np.array(k["y"], np.float32))
+
+
+def test_autograd_kat_via_gemms(kats):
+    """grads of sum(A @ B): dA = 1 B^T, dB = A^T 1 (test_autograd.py:85-94)."""
+    k = kats["autograd_sum_matmul"]
+    A = np.array(k["A"], np.float32)
+    B = np.array(k["B"], np.float32)
+    ones = np.ones((2, 2), np.float32)
+    say("autograd kat")
+    dA = host(ops().gemm(dev(ones), dev(B), transB=True))
+    dB = host(ops().gemm(dev(A), dev(ones), transA=True))
+    assert np.array_equal(dA, np.array(k["dA"], np.float32))
+    assert np.array_equal(dB, np.array(k["dB"], np.float32))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 3), (8192, 256), (8192, 10), (1000, 1000),
+                                       (0, 5)])
+def test_sum_reduce_rows(rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    x = rng.integers(-100, 100, (rows, cols)).astype(np.float32)
+    say("colsum", rows, cols)
+    got = host(ops().sum_reduce_rows(dev(x)))
+    assert np.array_equal(got, x.astype(np.float64).sum(0).astype(np.float32))
+    y = normal(rng, (rows, cols))
+    got = host(ops().sum_reduce_rows(dev(y)))
+    want = y.astype(np.float64).sum(0)
+    if rows:
+        e_ref = oracle.rel_fro(oracle.colsum(y), want)
+        assert oracle.rel_fro(got, want) <= 2 * e_ref + 2.0 ** -24
+
+
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+def test_activations(act):
+    import cudeep_amd as cd
+    a = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU}[act]
+    x = np.linspace(-8, 8, 100003).astype(np.float32)
+    go = np.random.default_rng(9).standard_normal(x.shape).astype(np.float32)
+    say("activation", act)
+    y = host(ops().activation(dev(x), a))
+    g = host(ops().activation_backward(dev(go), dev(x), a))
+    if act == "relu":
+        assert np.array_equal(y, np.maximum(x, 0))
+        assert np.array_equal(g, np.where(x > 0, go, 0).astype(np.float32))
+    else:
+        want = oracle.gelu(x)
+        assert np.max(np.abs(y - want) / np.maximum(np.abs(want), 1e-3)) < 2e-6
+        wg = go * oracle.gelu_grad(x)
+        assert np.max(np.abs(g - wg)) < 1e-5 * max(1.0, np.abs(wg).max())
+
+
+def test_broadcast_add_row():
+    rng = np.random.default_rng(11)
+    m = normal(rng, (300, 77))
+    r = normal(rng, (77,))
+    say("broadcast add")
+    got = host(ops().broadcast_add_row(dev(m), dev(r)))
+    assert np.array_equal(got, (m + r[None, :]).astype(np.float32))
