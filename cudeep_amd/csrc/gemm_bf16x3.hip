@@ -295,7 +295,14 @@ int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
     return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, kp, stream);
 }
 
-using CfgLarge = Cfg<128, 128, 32, 64, 64, 8>;
+// Tile configurations (measured on MI355X, NN):
+//  * Huge: 256x256x32, 8 waves of 128x64; 160 KiB of LDS (one workgroup
+//    per CU); ~366 logical TFLOP/s at 4096^3.
+//  * Large: 128x128x64, 8 waves of 32x64; ~215 at 2048^3.
+//  * Small: 64x64x32, 4 waves of 32x32, for small / narrow problems.
+//  * SkinnyM: M <= 64 with a long N (conv GEMM).
+using CfgHuge = Cfg<256, 256, 32, 128, 64, 8>;
+using CfgLarge = Cfg<128, 128, 64, 32, 64, 8>;
 using CfgSkinnyM = Cfg<64, 256, 32, 32, 128, 1>;
 using CfgSmall = Cfg<64, 64, 32, 32, 32, 8>;
 
@@ -305,8 +312,8 @@ int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue};
     if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, kp, stream);
-    int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);
-    if (large_tiles >= 256) return launch_ops<CfgLarge>(g, kp, stream);
+    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_ops<CfgHuge>(g, kp, stream);
+    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge>(g, kp, stream);
     return launch_ops<CfgSmall>(g, kp, stream);
 }
 

@@ -50,8 +50,9 @@ struct KParams {
 template <int ROWS, int COLS, int NT, int MODE>
 struct TileLoader {
     static constexpr int C4 = COLS / 4;
-    static constexpr int NV = ROWS * C4 / NT;
-    static_assert(ROWS * C4 % NT == 0, "tile not divisible by thread count");
+    static constexpr int TOTAL = ROWS * C4;           // float4 slots in the tile
+    static constexpr int NV = (TOTAL + NT - 1) / NT;
+    static constexpr bool PARTIAL = TOTAL % NT != 0;  // last pass: some threads idle
     float4 v[NV];
 
     __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld,
@@ -60,6 +61,7 @@ struct TileLoader {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             int idx = tid + i * NT;
+            if (PARTIAL && idx >= TOTAL) break;
             int r = idx / C4, c = (idx % C4) * 4;
             int64_t gr = r0 + r, gc = c0 + c;
             const float* p = X + gr * ld + gc;
@@ -82,6 +84,7 @@ struct TileLoader {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             int idx = tid + i * NT;
+            if (PARTIAL && idx >= TOTAL) break;
             int r = idx / C4, c = (idx % C4) * 4;
             *reinterpret_cast<float4*>(s + r * LDS_STRIDE + c) = v[i];
         }
@@ -282,10 +285,15 @@ int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
     return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, kp, stream);
 }
 
-// Tile configurations.
-using CfgLarge = Cfg<128, 128, 16, 64, 64, 8>;   // big square-ish problems
-using CfgSkinnyM = Cfg<64, 256, 16, 32, 128, 1>;  // M <= 64 (conv: M = OC)
-using CfgSmall = Cfg<64, 64, 16, 32, 32, 8>;      // small or narrow problems
+// Tile configurations (chosen by measurement on MI355X; 4096^3 NN):
+//  * Large: 128x128x16, 8 waves of 32x64 -> 2 waves per SIMD, 64 fp32
+//    accumulators per lane; ~132 TFLOP/s at 4096^3, ~112 at 2048^3.
+//  * Medium: 64x64x16, 8 waves of 16x32, for problems with too few large
+//    tiles to fill 256 CUs (~67 TFLOP/s at 1024^3 vs 27 with Large).
+//  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels).
+using CfgLarge = Cfg<128, 128, 16, 32, 64, 8>;
+using CfgMedium = Cfg<64, 64, 16, 16, 32, 8>;
+using CfgSkinnyM = Cfg<64, 256, 16, 32, 128, 1>;
 
 }  // namespace
 
@@ -293,9 +301,10 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue};
     if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, kp, stream);
+    // Large tiles once there are at least two per CU (256 CUs).
     int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);
-    if (large_tiles >= 256) return launch_ops<CfgLarge>(g, kp, stream);
-    return launch_ops<CfgSmall>(g, kp, stream);
+    if (large_tiles >= 512) return launch_ops<CfgLarge>(g, kp, stream);
+    return launch_ops<CfgMedium>(g, kp, stream);
 }
 
 }  // namespace cdx

@@ -5,8 +5,9 @@
 // tile, 4 waves of 32x32, LDS-staged k-tiles of 16 with bounds-checked
 // loads (fp64 is off the graded path; the kernel favours simplicity).
 // Fragment feeding as in the FP32 kernel: A lane l holds row l%16, k l/16;
-// B lane l holds k l/16, column l%16; the 16x16 fp64 result sits 4 doubles
-// per lane, rows 4*(l/16)+r, column l%16.
+// B lane l holds k l/16, column l%16.  The 16x16 fp64 result sits 4 doubles
+// per lane, interleaved unlike the fp32 16x16x4 layout: register r of lane
+// l holds row 4*r + l/16, column l%16.
 #include "cdx_internal.hpp"
 
 namespace cdx {
@@ -57,7 +58,7 @@ void dgemm_kernel(int opA, int opB, int64_t M, int64_t N, int64_t K,
     for (int i = 0; i < 2; ++i)
         for (int j = 0; j < 2; ++j)
             for (int r = 0; r < 4; ++r) {
-                int64_t m = bm + wm0 + i * 16 + 4 * (lane >> 4) + r;
+                int64_t m = bm + wm0 + i * 16 + 4 * r + (lane >> 4);
                 int64_t n = bn + wn0 + j * 16 + (lane & 15);
                 if (m < M && n < N) C[m * ldc + n] = acc[i][j][r];
             }

@@ -242,8 +242,10 @@ def test_matmul_fused_act_entry_point():
     L.call("cdx_matmul_fused_act", dA.data_ptr(), dB.data_ptr(), out.data_ptr(), 128, 96, 64,
            L.EPI_RELU, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     C = host(out)
-    want = oracle.relu(oracle.dgemm(A, B))
-    assert np.max(np.abs(C - want)) <= 1e-4
+    Z = oracle.dgemm(A, B)
+    want = oracle.relu(Z)
+    # TF32 mode (bf16x3): per-product relative error <= ~3 * 2^-16
+    assert np.max(np.abs(C - want)) <= 2e-5 * np.abs(Z).max()
 
 
 # ---------------------------------------------------------------------------
