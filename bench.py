@@ -48,6 +48,9 @@ def parse():
     p.add_argument("--headline-only", action="store_true",
                    help="time only the 4096^3 FP32 GEMM (for profiler runs)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also run a plain 256 MiB device copy (reference point for "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return p.parse_args()
 
 
@@ -209,6 +212,14 @@ def main():
     import cudeep_amd as cd
     props = torch.cuda.get_device_properties(0)
     log("device", props.name, getattr(props, "gcnArchName", ""), "CUs", props.multi_processor_count)
+
+    if args.copy_calibration:
+        src = torch.randn((64, 1024, 1024), device="cuda")     # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 256 MiB device copies (268435456 B read + written each)")
 
     log("headline: fp32 4096^3")
     head = bench_gemm(4096, cd.PREC_FP32, args.steps, args.warmup, seed=2)

@@ -46,6 +46,47 @@ int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
                  const double* A, int64_t lda, const double* B, int64_t ldb,
                  double* C, int64_t ldc, hipStream_t stream);
 
+// Split-K reduction: C = epi(sum_s P[s] + bias) through the output map, the
+// partials summed in slice order (deterministic).  P is [splits][M][N].
+int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStream_t stream);
+
+// Split-K policy shared by the GEMM kernels: split only when the tile grid
+// cannot fill the GPU (fewer than 128 tiles) and K is long; aim at ~512
+// workgroups with at least 512 k per slice.  Returns the slice count and
+// sets *k_chunk (a multiple of bk).
+inline int choose_splitk(int64_t tiles, int64_t K, int bk, int64_t* k_chunk) {
+    *k_chunk = K;
+    if (tiles >= 128 || K < 2048) return 1;
+    int64_t s = 512 / tiles;
+    if (s > K / 512) s = K / 512;
+    if (s < 2) return 1;
+    int64_t kc = ceil_div(ceil_div(K, s), bk) * bk;
+    *k_chunk = kc;
+    return (int)ceil_div(K, kc);
+}
+
+// Runs a GEMM whose tile grid is `tiles` through split-K when the policy
+// asks for it: allocates the partials stream-ordered, calls
+// launch(kparams-adjusted GemmArgs, splits, k_chunk) and reduces.
+template <class LaunchFn>
+int with_splitk(const GemmArgs& g, int64_t tiles, int bk, hipStream_t stream, LaunchFn launch) {
+    int64_t k_chunk;
+    const int splits = choose_splitk(tiles, g.K, bk, &k_chunk);
+    if (splits == 1) return launch(g, 1, g.K);
+    float* part = nullptr;
+    const size_t bytes = (size_t)splits * (size_t)g.M * (size_t)g.N * sizeof(float);
+    int st = hip_error(hipMallocAsync(reinterpret_cast<void**>(&part), bytes, stream),
+                       "gemm split-K: hipMallocAsync");
+    if (st) return st;
+    GemmArgs q = g;
+    q.C = part; q.ldc = g.N; q.n_split = 0; q.ldc_split = 0;
+    q.bias = nullptr; q.bias_mode = CDX_BIAS_NONE; q.epilogue = CDX_EPI_NONE;
+    st = launch(q, splits, k_chunk);
+    if (!st) st = launch_splitk_reduce(part, splits, g, stream);
+    int st2 = hip_error(hipFreeAsync(part, stream), "gemm split-K: hipFreeAsync");
+    return st ? st : st2;
+}
+
 int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,
                       int64_t SH, int64_t SW, int64_t PH, int64_t PW,

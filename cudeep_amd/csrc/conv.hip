@@ -5,13 +5,21 @@
 //   ih = oh*SH - PH + kh,  iw = ow*SW - PW + kw.
 //
 // Since k * B_spatial + b * spatial + s == (k * batch + b) * spatial + s,
-// the column buffer is one flat sequence over (k, b, s).  Each thread owns
-// VS = 4 consecutive s of one (k, b) run and writes them with one 16-byte
-// store, so a wavefront writes 1 KiB of contiguous HBM; the matching input
-// reads walk consecutive iw (stride SW) of one input row.  The per-element
-// index math is 32-bit (s < spatial, k < K_col); only the flat offsets are
-// 64-bit, so results agree with the reference wherever its int indices do
-// not overflow and stay correct beyond that.
+// the column buffer is one flat sequence of rows (k, b), each `spatial`
+// long.  Two kernels:
+//  * plane kernel (input plane <= 64 KiB): one workgroup per (b, ic) input
+//    plane.  The plane is read from HBM once, coalesced, into LDS; the
+//    workgroup then writes the KH*KW column rows that plane feeds.  Each
+//    thread owns 4 consecutive s, computes (oh, ow) once, and for every
+//    (kh, kw) gathers from LDS and issues one 16-byte store, so every
+//    wavefront writes 1 KiB contiguous runs.  HBM traffic is the
+//    compulsory minimum: the input once plus the column buffer once.
+//  * generic kernel (larger planes): one thread per 4 consecutive s of one
+//    (k, b) row, gathering straight from global memory.
+// Index math is 32-bit where the value is bounded by one plane or one row
+// (s < spatial, k < K_col); flat offsets are 64-bit, so results agree with
+// the reference wherever its int indices do not overflow and stay correct
+// beyond that.
 #include "cdx_internal.hpp"
 
 namespace cdx {
@@ -57,6 +65,57 @@ void im2col_kernel(const float* __restrict__ in, float* __restrict__ col, Im2col
     }
 }
 
+constexpr int kPlaneMaxFloats = 16384;   // 64 KiB of LDS per input plane
+
+template <int VS>
+__global__ __launch_bounds__(256)
+void im2col_plane_kernel(const float* __restrict__ in, float* __restrict__ col, Im2colGeom g) {
+    extern __shared__ float plane[];
+    const int64_t bc = blockIdx.x;                  // b * IC + ic
+    const int b = (int)(bc / g.IC), ic = (int)(bc % g.IC);
+    const int IH = (int)g.IH, IW = (int)g.IW, plane_n = IH * IW;
+    const float* src = in + bc * (int64_t)plane_n;
+    for (int i = threadIdx.x; i < plane_n; i += blockDim.x) plane[i] = src[i];
+    __syncthreads();
+
+    const int spatial = (int)g.spatial, OW = (int)g.OW;
+    const int KH = (int)g.KH, KW = (int)g.KW;
+    const int runs_per_row = (spatial + VS - 1) / VS;
+    // row (k, b) starts at ((ic*KH*KW + kk) * batch + b) * spatial
+    float* row0 = col + ((int64_t)ic * KH * KW * g.batch + b) * g.spatial;
+    const int64_t row_step = g.batch * g.spatial;   // next kk
+    for (int t = threadIdx.x; t < runs_per_row; t += blockDim.x) {
+        const int s0 = t * VS;
+        int ih0[VS], iw0[VS];
+#pragma unroll
+        for (int e = 0; e < VS; ++e) {
+            const int s = s0 + e < spatial ? s0 + e : spatial - 1;
+            const int oh = s / OW, ow = s - (s / OW) * OW;
+            ih0[e] = oh * (int)g.SH - (int)g.PH;
+            iw0[e] = ow * (int)g.SW - (int)g.PW;
+        }
+        float* dst = row0 + s0;
+        for (int kh = 0; kh < KH; ++kh) {
+            for (int kw = 0; kw < KW; ++kw) {
+                float v[VS];
+#pragma unroll
+                for (int e = 0; e < VS; ++e) {
+                    const int ih = ih0[e] + kh, iw = iw0[e] + kw;
+                    v[e] = (ih >= 0 && ih < IH && iw >= 0 && iw < IW) ? plane[ih * IW + iw] : 0.0f;
+                }
+                if (VS == 4) {
+                    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VS; ++e)
+                        if (s0 + e < spatial) dst[e] = v[e];
+                }
+                dst += row_step;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
@@ -74,6 +133,17 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
     // 16-byte stores need every run to start 16-byte aligned.
     const bool vec = g.spatial % 4 == 0 && (uintptr_t)col % 16 == 0;
     const int VS = vec ? 4 : 1;
+    if (IH * IW <= kPlaneMaxFloats && batch * IC <= INT32_MAX && g.spatial <= INT32_MAX &&
+        KH * KW <= 4096) {
+        const size_t lds = (size_t)(IH * IW) * sizeof(float);
+        if (vec)
+            hipLaunchKernelGGL(im2col_plane_kernel<4>, dim3((unsigned)(batch * IC)), dim3(256),
+                               lds, stream, in, col, g);
+        else
+            hipLaunchKernelGGL(im2col_plane_kernel<1>, dim3((unsigned)(batch * IC)), dim3(256),
+                               lds, stream, in, col, g);
+        return hip_error(hipGetLastError(), "im2col_plane_kernel launch");
+    }
     const int64_t threads = g.runs * ((g.spatial + VS - 1) / VS);
     int64_t blocks = ceil_div(threads, 256);
     if (blocks > (int64_t)1 << 30) blocks = (int64_t)1 << 30;

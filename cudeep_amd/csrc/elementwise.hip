@@ -78,6 +78,25 @@ void fill_kernel(float* __restrict__ y, int64_t n, float v) {
         y[i] = v;
 }
 
+__global__ __launch_bounds__(256)
+void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t M, int64_t N,
+                          float* __restrict__ C, int64_t ldc, int64_t n_split,
+                          int64_t ldc_split, const float* __restrict__ bias, int bias_mode,
+                          int act) {
+    const int64_t MN = M * N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = i / N, n = i - m * N;
+        float v = P[i];
+        for (int s = 1; s < splits; ++s) v += P[(int64_t)s * MN + i];
+        if (bias_mode == CDX_BIAS_COL) v += bias[n];
+        else if (bias_mode == CDX_BIAS_ROW) v += bias[m];
+        v = apply_act(v, act);
+        const int64_t col = n_split > 0 ? (n / n_split) * ldc_split + n % n_split : n;
+        C[m * ldc + col] = v;
+    }
+}
+
 unsigned grid_for(int64_t n) {
     int64_t b = ceil_div(n, 256);
     if (b > 65536) b = 65536;
@@ -86,6 +105,13 @@ unsigned grid_for(int64_t n) {
 }
 
 }  // namespace
+
+int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStream_t stream) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(g.M * g.N)), dim3(256), 0, stream,
+                       P, splits, g.M, g.N, g.C, g.ldc, g.n_split, g.ldc_split, g.bias,
+                       g.bias_mode, g.epilogue);
+    return hip_error(hipGetLastError(), "splitk_reduce_kernel launch");
+}
 
 int64_t colsum_partial_rows(int64_t rows, int64_t cols) {
     (void)cols;

@@ -28,6 +28,7 @@ struct KParams {
     const float* A; const float* B; float* C; const float* bias;
     int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
     int bias_mode, epilogue;
+    int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
 };
 
 __device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
@@ -168,6 +169,16 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     int tm, tn;
     tile_of_block(tiles_m, tiles_n, CF::GROUP_M, tm, tn);
     const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+
+    // Split-K slice: blockIdx.y owns k in [y*k_chunk, min(K, (y+1)*k_chunk))
+    // and writes a plain [M, N] partial (the reduction applies the epilogue).
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A += OPA == CDX_OP_N ? k0 : k0 * p.lda;
+        p.B += OPB == CDX_OP_N ? k0 * p.ldb : k0;
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
     const bool v = vec != 0;
 
     SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK> la;
@@ -266,33 +277,40 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
 }
 
 template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN>
-int launch_cfg(const KParams& kp, int vec, hipStream_t stream) {
+int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
     hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN>),
-                       dim3((unsigned)tiles), dim3(CF::NT), 0, stream, kp, vec);
+                       dim3((unsigned)tiles, (unsigned)splits), dim3(CF::NT), 0, stream, kp, vec);
     return hip_error(hipGetLastError(), "gemm_bf16x3_kernel launch");
 }
 
 template <class CF, int OPA, int OPB>
-int launch_mode(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
+int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
     bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&
                g.lda % 4 == 0 && g.ldb % 4 == 0;
-    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 && g.K % CF::BK == 0;
+    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
+                   g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned)
-        return split ? launch_cfg<CF, OPA, OPB, false, true>(kp, 1, stream)
-                     : launch_cfg<CF, OPA, OPB, false, false>(kp, 1, stream);
-    return split ? launch_cfg<CF, OPA, OPB, true, true>(kp, vec, stream)
-                 : launch_cfg<CF, OPA, OPB, true, false>(kp, vec, stream);
+        return split ? launch_cfg<CF, OPA, OPB, false, true>(kp, 1, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, false, false>(kp, 1, splits, stream);
+    return split ? launch_cfg<CF, OPA, OPB, true, true>(kp, vec, splits, stream)
+                 : launch_cfg<CF, OPA, OPB, true, false>(kp, vec, splits, stream);
 }
 
 template <class CF>
-int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
-    if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, kp, stream);
-    if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, kp, stream);
-    if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, kp, stream);
-    return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, kp, stream);
+int launch_ops(const GemmArgs& g0, hipStream_t stream) {
+    const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
+    return with_splitk(g0, tiles, CF::BK, stream,
+                       [&](const GemmArgs& g, int splits, int64_t k_chunk) {
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, splits, k_chunk, stream);
+        return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, splits, k_chunk, stream);
+    });
 }
 
 // Tile configurations (measured on MI355X, NN):
@@ -300,21 +318,20 @@ int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
 //    per CU); ~366 logical TFLOP/s at 4096^3.
 //  * Large: 128x128x64, 8 waves of 32x64; ~215 at 2048^3.
 //  * Small: 64x64x32, 4 waves of 32x32, for small / narrow problems.
-//  * SkinnyM: M <= 64 with a long N (conv GEMM).
+//  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x32, 4 waves of
+//    32x32 (~108 logical TFLOP/s on 64 x 100352 x 576).
 using CfgHuge = Cfg<256, 256, 32, 128, 64, 8>;
 using CfgLarge = Cfg<128, 128, 64, 32, 64, 8>;
-using CfgSkinnyM = Cfg<64, 256, 32, 32, 128, 1>;
+using CfgSkinnyM = Cfg<64, 64, 32, 32, 32, 1>;
 using CfgSmall = Cfg<64, 64, 32, 32, 32, 8>;
 
 }  // namespace
 
 int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream) {
-    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
-               g.n_split, g.ldc_split, g.bias_mode, g.epilogue};
-    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, kp, stream);
-    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_ops<CfgHuge>(g, kp, stream);
-    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge>(g, kp, stream);
-    return launch_ops<CfgSmall>(g, kp, stream);
+    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
+    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_ops<CfgHuge>(g, stream);
+    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge>(g, stream);
+    return launch_ops<CfgSmall>(g, stream);
 }
 
 }  // namespace cdx

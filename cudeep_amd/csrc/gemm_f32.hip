@@ -42,6 +42,7 @@ struct KParams {
     const float* A; const float* B; float* C; const float* bias;
     int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
     int bias_mode, epilogue;
+    int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
 };
 
 // Loads a ROWS x COLS tile (COLS contiguous in memory) starting at (r0, c0)
@@ -143,6 +144,16 @@ void gemm_f32_mfma_kernel(KParams p) {
     int tm, tn;
     tile_of_block(tiles_m, tiles_n, CF::GROUP_M, tm, tn);
     const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+
+    // Split-K slice: blockIdx.y owns k in [y*k_chunk, min(K, (y+1)*k_chunk))
+    // and writes a plain [M, N] partial (the reduction applies the epilogue).
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A += OPA == CDX_OP_N ? k0 : k0 * p.lda;
+        p.B += OPB == CDX_OP_N ? k0 * p.ldb : k0;
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
 
     // Global tile loaders in memory orientation.
     using LA = TileLoader<OPA == CDX_OP_N ? BM : BK, OPA == CDX_OP_N ? BK : BM, NT, MODE>;
@@ -247,42 +258,46 @@ void gemm_f32_mfma_kernel(KParams p) {
 }
 
 template <class CF, int OPA, int OPB, int MODE, bool SPLITN>
-int launch_cfg(const KParams& kp, hipStream_t stream) {
+int launch_cfg(const KParams& kp, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<CF, OPA, OPB, MODE, SPLITN>),
-                       dim3((unsigned)tiles), dim3(CF::NT), 0, stream, kp);
+                       dim3((unsigned)tiles, (unsigned)splits), dim3(CF::NT), 0, stream, kp);
     return hip_error(hipGetLastError(), "gemm_f32_mfma_kernel launch");
 }
 
 template <class CF, int OPA, int OPB>
-int launch_mode(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
+int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
     // 16-byte loads need 16-byte aligned bases and leading dimensions.
     bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&
                g.lda % 4 == 0 && g.ldb % 4 == 0;
-    const int64_t rowsA = OPA == CDX_OP_N ? g.M : g.K, colsA = OPA == CDX_OP_N ? g.K : g.M;
-    const int64_t rowsB = OPB == CDX_OP_N ? g.K : g.N, colsB = OPB == CDX_OP_N ? g.N : g.K;
-    (void)rowsA; (void)colsA; (void)rowsB; (void)colsB;
-    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 && g.K % CF::BK == 0;
+    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
+                   g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned) {
-        return split ? launch_cfg<CF, OPA, OPB, kLoadAlignedVec, true>(kp, stream)
-                     : launch_cfg<CF, OPA, OPB, kLoadAlignedVec, false>(kp, stream);
+        return split ? launch_cfg<CF, OPA, OPB, kLoadAlignedVec, true>(kp, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, kLoadAlignedVec, false>(kp, splits, stream);
     }
     if (vec) {
-        return split ? launch_cfg<CF, OPA, OPB, kLoadCheckedVec, true>(kp, stream)
-                     : launch_cfg<CF, OPA, OPB, kLoadCheckedVec, false>(kp, stream);
+        return split ? launch_cfg<CF, OPA, OPB, kLoadCheckedVec, true>(kp, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, kLoadCheckedVec, false>(kp, splits, stream);
     }
-    return split ? launch_cfg<CF, OPA, OPB, kLoadScalar, true>(kp, stream)
-                 : launch_cfg<CF, OPA, OPB, kLoadScalar, false>(kp, stream);
+    return split ? launch_cfg<CF, OPA, OPB, kLoadScalar, true>(kp, splits, stream)
+                 : launch_cfg<CF, OPA, OPB, kLoadScalar, false>(kp, splits, stream);
 }
 
 template <class CF>
-int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
-    if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, kp, stream);
-    if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, kp, stream);
-    if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, kp, stream);
-    return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, kp, stream);
+int launch_ops(const GemmArgs& g0, hipStream_t stream) {
+    const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
+    return with_splitk(g0, tiles, CF::BK, stream,
+                       [&](const GemmArgs& g, int splits, int64_t k_chunk) {
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, splits, k_chunk, stream);
+        return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, splits, k_chunk, stream);
+    });
 }
 
 // Tile configurations (chosen by measurement on MI355X; 4096^3 NN):
@@ -290,21 +305,21 @@ int launch_ops(const GemmArgs& g, const KParams& kp, hipStream_t stream) {
 //    accumulators per lane; ~132 TFLOP/s at 4096^3, ~112 at 2048^3.
 //  * Medium: 64x64x16, 8 waves of 16x32, for problems with too few large
 //    tiles to fill 256 CUs (~67 TFLOP/s at 1024^3 vs 27 with Large).
-//  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels).
+//  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
+//    64x64x16, 4 waves of 32x32 (~86 TFLOP/s on 64 x 100352 x 576, against
+//    49 with 64x256 tiles).
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8>;
 using CfgMedium = Cfg<64, 64, 16, 16, 32, 8>;
-using CfgSkinnyM = Cfg<64, 256, 16, 32, 128, 1>;
+using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1>;
 
 }  // namespace
 
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
-    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
-               g.n_split, g.ldc_split, g.bias_mode, g.epilogue};
-    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, kp, stream);
+    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
     // Large tiles once there are at least two per CU (256 CUs).
     int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);
-    if (large_tiles >= 512) return launch_ops<CfgLarge>(g, kp, stream);
-    return launch_ops<CfgMedium>(g, kp, stream);
+    if (large_tiles >= 512) return launch_ops<CfgLarge>(g, stream);
+    return launch_ops<CfgMedium>(g, stream);
 }
 
 }  // namespace cdx

@@ -35,6 +35,8 @@ GEOMS = [  # (B, C, H, W, KH, KW, SH, SW, PH, PW)
     (4, 16, 28, 28, 3, 3, 1, 1, 1, 1),
     (2, 8, 15, 17, 1, 1, 2, 2, 0, 0),
     (1, 3, 3, 3, 3, 3, 1, 1, 0, 0),       # single output pixel
+    (1, 2, 130, 131, 3, 3, 1, 1, 1, 1),   # plane > 64 KiB -> generic gather kernel
+    (2, 1, 129, 130, 3, 2, 2, 1, 0, 1),   # generic kernel, odd spatial
 ]
 
 

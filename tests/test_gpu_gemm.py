@@ -288,3 +288,34 @@ def test_leading_dimension_views():
     C64 = oracle.dgemm(big[:, 40:160], B)
     _, e_ref = _ref_errors(np.ascontiguousarray(big[:, 40:160]), B)
     assert oracle.rel_fro(C, C64) <= 2 * e_ref
+
+
+# ---------------------------------------------------------------------------
+# split-K (few output tiles, long K): partial slices + ordered reduction
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K,tA", [(64, 64, 8192, False), (100, 50, 5000, False),
+                                      (256, 784, 8192, True), (10, 256, 8192, True),
+                                      (33, 17, 3001, True)])
+@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+def test_split_k_parity(M, N, K, tA, mode):
+    import cudeep_amd as cd
+    rng = np.random.default_rng(M + N + K)
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (K, N))
+    bias = normal(rng, (N,))
+    prec = cd.PREC_FP32 if mode == "fp32" else cd.PREC_TF32MODE
+    say("split-K", mode, M, N, K, tA)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, precision=prec, bias=dev(bias),
+                        bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU))
+    Z64 = oracle.dgemm(A, B, transA=tA) + bias[None, :]
+    want = oracle.relu(Z64)
+    if mode == "fp32":
+        Zs = oracle.sgemm_seqfma(A, B, transA=tA) + bias[None, :]
+        e_ref = oracle.rel_fro(oracle.relu(Zs.astype(np.float32)), want)
+        assert oracle.rel_fro(C, want) <= 2 * e_ref
+    else:
+        opA = np.ascontiguousarray(A.T if tA else A)
+        Zt = oracle.gemm_tf32emu(opA, B, "rne") + bias[None, :]
+        e_ref = oracle.rel_fro(oracle.relu(Zt.astype(np.float32)), want)
+        assert oracle.rel_fro(C, want) <= e_ref
