@@ -46,7 +46,22 @@ SIGNATURES = {
     "cdx_broadcast_add_row_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "cdx_activation_forward_f32": (_int, [_vp, _vp, _i64, _int, _vp]),
     "cdx_activation_backward_f32": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
+    "cdx_col2im_f32": (_int, [_vp, _vp] + [_i64] * 10 + [_vp]),
+    "cdx_conv2d_backward_data_workspace_size": (_sz, [_i64] * 11),
+    "cdx_conv2d_backward_data_f32": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),
+    "cdx_conv2d_backward_weight_workspace_size": (_sz, [_i64] * 11),
+    "cdx_conv2d_backward_weight_f32": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),
+    "cdx_conv2d_backward_bias_f32": (_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
+    "cdx_strided_copy": (_int, [_vp, _vp, _int, _vp, _vp, _int, _vp]),
+    "cdx_fill": (_int, [_vp, _i64, ctypes.c_double, _int, _vp]),
+    "cdx_binary": (_int, [_int, _int, _vp, _vp, _vp, _i64, _vp]),
+    "cdx_randn": (_int, [_vp, _i64, _int, ctypes.c_uint64, ctypes.c_uint64, _vp]),
+    "cdx_sum_workspace_size": (_sz, [_int]),
+    "cdx_sum": (_int, [_vp, _vp, _i64, _int, _vp, _sz, _vp]),
 }
+
+DTYPE_F32, DTYPE_F64 = 0, 1
+BINARY_ADD, BINARY_SUB, BINARY_MUL = 0, 1, 2
 
 _lib = None
 

@@ -208,6 +208,192 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight, const float*
     return st;
 }
 
+int cdx_col2im_f32(const float* col, float* grad_input, int64_t batch, int64_t in_channels,
+                   int64_t in_h, int64_t in_w, int64_t kernel_h, int64_t kernel_w,
+                   int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                   hipStream_t stream) {
+    int st = check_conv("cdx_col2im_f32", batch, in_channels, 1, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (batch * in_channels * in_h * in_w == 0) return CDX_OK;
+    if (!col || !grad_input) return set_error(CDX_ERR_INVALID_ARG, "cdx_col2im_f32: NULL pointer");
+    return cdx::launch_col2im_f32(col, grad_input, batch, in_channels, in_h, in_w, kernel_h,
+                                  kernel_w, stride_h, stride_w, pad_h, pad_w, stream);
+}
+
+namespace {
+
+struct ConvSizes {
+    int64_t OH, OW, S, BS, Kc;
+};
+
+ConvSizes conv_sizes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                     int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    ConvSizes z;
+    z.OH = conv_out(IH, KH, SH, PH);
+    z.OW = conv_out(IW, KW, SW, PW);
+    z.S = z.OH * z.OW;
+    z.BS = batch * z.S;
+    z.Kc = IC * KH * KW;
+    return z;
+}
+
+// Stream-ordered scratch: the caller's workspace, or a hipMallocAsync block
+// freed on the same stream when the call ends.
+struct Scratch {
+    void* ptr = nullptr;
+    bool owned = false;
+    hipStream_t stream = nullptr;
+    int acquire(void* ws, size_t ws_bytes, size_t need, hipStream_t s, const char* fn) {
+        stream = s;
+        if (ws) {
+            if (ws_bytes < need) return set_error(CDX_ERR_WORKSPACE, std::string(fn) + ": workspace too small");
+            ptr = ws;
+            return CDX_OK;
+        }
+        if (need == 0) return CDX_OK;
+        int st = cdx::hip_error(hipMallocAsync(&ptr, need, s), fn);
+        owned = st == CDX_OK;
+        return st;
+    }
+    int release(int st) {
+        if (owned) {
+            int st2 = cdx::hip_error(hipFreeAsync(ptr, stream), "hipFreeAsync");
+            owned = false;
+            if (!st) st = st2;
+        }
+        return st;
+    }
+};
+
+}  // namespace
+
+size_t cdx_conv2d_backward_data_workspace_size(int64_t batch, int64_t in_channels,
+                                               int64_t out_channels, int64_t in_h, int64_t in_w,
+                                               int64_t kernel_h, int64_t kernel_w,
+                                               int64_t stride_h, int64_t stride_w,
+                                               int64_t pad_h, int64_t pad_w) {
+    if (check_conv("cdx_conv2d_backward_data_workspace_size", batch, in_channels, out_channels,
+                   in_h, in_w, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w))
+        return 0;
+    ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                             stride_w, pad_h, pad_w);
+    // grad_col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
+    size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
+    return n * sizeof(float);
+}
+
+int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight, float* grad_input,
+                                 int64_t batch, int64_t in_channels, int64_t out_channels,
+                                 int64_t in_h, int64_t in_w, int64_t kernel_h, int64_t kernel_w,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                 int precision, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+    const char* fn = "cdx_conv2d_backward_data_f32";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
+    if (batch * in_channels * in_h * in_w == 0) return CDX_OK;
+    if (!grad_input || (out_channels > 0 && (!grad_output || !weight)))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                             stride_w, pad_h, pad_w);
+    const size_t need = cdx_conv2d_backward_data_workspace_size(
+        batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
+        pad_h, pad_w);
+    Scratch ws;
+    st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
+    if (st) return st;
+    float* grad_col = static_cast<float*>(ws.ptr);
+    const float* dy_cm = grad_output;                   // batch 1: NCHW is [OC, S] already
+    if (batch > 1) {
+        float* t = grad_col + (size_t)z.Kc * z.BS;
+        st = cdx::launch_nchw_to_cm_f32(grad_output, t, batch, out_channels, z.S, stream);
+        dy_cm = t;
+    }
+    if (!st) {
+        // grad_col[Kc, BS] = weight^T [Kc, OC] * dy_cm [OC, BS]
+        cdx::GemmArgs g{CDX_OP_T, CDX_OP_N, z.Kc, z.BS, out_channels, weight, z.Kc,
+                        dy_cm, z.BS, grad_col, z.BS, 0, 0, nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+        st = run_gemm(precision, g, stream);
+    }
+    if (!st)
+        st = cdx::launch_col2im_f32(grad_col, grad_input, batch, in_channels, in_h, in_w,
+                                    kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, stream);
+    return ws.release(st);
+}
+
+size_t cdx_conv2d_backward_weight_workspace_size(int64_t batch, int64_t in_channels,
+                                                 int64_t out_channels, int64_t in_h, int64_t in_w,
+                                                 int64_t kernel_h, int64_t kernel_w,
+                                                 int64_t stride_h, int64_t stride_w,
+                                                 int64_t pad_h, int64_t pad_w) {
+    if (check_conv("cdx_conv2d_backward_weight_workspace_size", batch, in_channels, out_channels,
+                   in_h, in_w, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w))
+        return 0;
+    ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                             stride_w, pad_h, pad_w);
+    // col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
+    size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
+    return n * sizeof(float);
+}
+
+int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
+                                   float* grad_weight, int64_t batch, int64_t in_channels,
+                                   int64_t out_channels, int64_t in_h, int64_t in_w,
+                                   int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                   int64_t stride_w, int64_t pad_h, int64_t pad_w, int precision,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const char* fn = "cdx_conv2d_backward_weight_f32";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
+    ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                             stride_w, pad_h, pad_w);
+    if (out_channels * z.Kc == 0) return CDX_OK;
+    if (!grad_weight || (z.BS > 0 && (!grad_output || !input)))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    const size_t need = cdx_conv2d_backward_weight_workspace_size(
+        batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
+        pad_h, pad_w);
+    Scratch ws;
+    st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
+    if (st) return st;
+    float* col = static_cast<float*>(ws.ptr);
+    const float* dy_cm = grad_output;
+    if (z.BS > 0)
+        st = cdx::launch_im2col_f32(input, col, batch, in_channels, in_h, in_w, kernel_h,
+                                    kernel_w, stride_h, stride_w, pad_h, pad_w, stream);
+    if (!st && batch > 1) {
+        float* t = col + (size_t)z.Kc * z.BS;
+        st = cdx::launch_nchw_to_cm_f32(grad_output, t, batch, out_channels, z.S, stream);
+        dy_cm = t;
+    }
+    if (!st) {
+        // grad_weight[OC, Kc] = dy_cm [OC, BS] * col^T [BS, Kc]
+        cdx::GemmArgs g{CDX_OP_N, CDX_OP_T, out_channels, z.Kc, z.BS, dy_cm, z.BS > 0 ? z.BS : 1,
+                        col, z.BS > 0 ? z.BS : 1, grad_weight, z.Kc, 0, 0, nullptr,
+                        CDX_BIAS_NONE, CDX_EPI_NONE};
+        st = run_gemm(precision, g, stream);
+    }
+    return ws.release(st);
+}
+
+int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias, int64_t batch,
+                                 int64_t out_channels, int64_t spatial, hipStream_t stream) {
+    if (bad_dim(batch) || bad_dim(out_channels) || bad_dim(spatial))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_backward_bias_f32: bad dims");
+    if (out_channels == 0) return CDX_OK;
+    if (!grad_bias || (batch * spatial > 0 && !grad_output))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_backward_bias_f32: NULL pointer");
+    return cdx::launch_conv_bias_grad_f32(grad_output, grad_bias, batch, out_channels, spatial,
+                                          stream);
+}
+
 size_t cdx_sum_reduce_rows_workspace_size(int64_t rows, int64_t cols) {
     if (bad_dim(rows) || bad_dim(cols)) return 0;
     return (size_t)cdx::colsum_partial_rows(rows, cols) * (size_t)cols * sizeof(float);
@@ -272,6 +458,64 @@ int cdx_activation_backward_f32(const float* grad_output, const float* input, fl
     if (!grad_output || !input || !grad_input)
         return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: NULL pointer");
     return cdx::launch_activation_backward_f32(grad_output, input, grad_input, n, act, stream);
+}
+
+static bool bad_dtype(int dtype) { return dtype != CDX_DTYPE_F32 && dtype != CDX_DTYPE_F64; }
+
+int cdx_strided_copy(const void* src, void* dst, int ndim, const int64_t* shape,
+                     const int64_t* src_strides, int dtype, hipStream_t stream) {
+    if (ndim < 0 || ndim > 8) return set_error(CDX_ERR_UNSUPPORTED, "cdx_strided_copy: ndim must be <= 8");
+    if (bad_dtype(dtype)) return set_error(CDX_ERR_INVALID_ARG, "cdx_strided_copy: bad dtype");
+    if (ndim > 0 && (!shape || !src_strides))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_strided_copy: NULL shape/strides");
+    int64_t n = 1;
+    for (int d = 0; d < ndim; ++d) {
+        if (bad_dim(shape[d]) || src_strides[d] < 0)
+            return set_error(CDX_ERR_INVALID_ARG, "cdx_strided_copy: bad shape/stride");
+        n *= shape[d];
+    }
+    if (n == 0) return CDX_OK;
+    if (!src || !dst) return set_error(CDX_ERR_INVALID_ARG, "cdx_strided_copy: NULL pointer");
+    return cdx::launch_strided_copy(src, dst, ndim, shape, src_strides, dtype, stream);
+}
+
+int cdx_fill(void* dst, int64_t n, double value, int dtype, hipStream_t stream) {
+    if (bad_dim(n) || bad_dtype(dtype)) return set_error(CDX_ERR_INVALID_ARG, "cdx_fill: bad args");
+    if (n == 0) return CDX_OK;
+    if (!dst) return set_error(CDX_ERR_INVALID_ARG, "cdx_fill: NULL pointer");
+    return cdx::launch_fill(dst, n, value, dtype, stream);
+}
+
+int cdx_binary(int op, int dtype, const void* a, const void* b, void* out, int64_t n,
+               hipStream_t stream) {
+    if (op != CDX_BINARY_ADD && op != CDX_BINARY_SUB && op != CDX_BINARY_MUL)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_binary: bad op");
+    if (bad_dim(n) || bad_dtype(dtype)) return set_error(CDX_ERR_INVALID_ARG, "cdx_binary: bad args");
+    if (n == 0) return CDX_OK;
+    if (!a || !b || !out) return set_error(CDX_ERR_INVALID_ARG, "cdx_binary: NULL pointer");
+    return cdx::launch_binary(op, dtype, a, b, out, n, stream);
+}
+
+int cdx_randn(void* dst, int64_t n, int dtype, uint64_t seed, uint64_t offset, hipStream_t stream) {
+    if (bad_dim(n) || bad_dtype(dtype)) return set_error(CDX_ERR_INVALID_ARG, "cdx_randn: bad args");
+    if (n == 0) return CDX_OK;
+    if (!dst) return set_error(CDX_ERR_INVALID_ARG, "cdx_randn: NULL pointer");
+    return cdx::launch_randn(dst, n, dtype, seed, offset, stream);
+}
+
+size_t cdx_sum_workspace_size(int dtype) {
+    return (size_t)cdx::sum_partials() * (dtype == CDX_DTYPE_F64 ? sizeof(double) : sizeof(float));
+}
+
+int cdx_sum(const void* x, void* out, int64_t n, int dtype, void* workspace,
+            size_t workspace_bytes, hipStream_t stream) {
+    if (bad_dim(n) || bad_dtype(dtype)) return set_error(CDX_ERR_INVALID_ARG, "cdx_sum: bad args");
+    if (!out || (n > 0 && !x)) return set_error(CDX_ERR_INVALID_ARG, "cdx_sum: NULL pointer");
+    Scratch ws;
+    int st = ws.acquire(workspace, workspace_bytes, cdx_sum_workspace_size(dtype), stream, "cdx_sum");
+    if (st) return st;
+    st = cdx::launch_sum(x, out, n, dtype, ws.ptr, stream);
+    return ws.release(st);
 }
 
 }  // extern "C"

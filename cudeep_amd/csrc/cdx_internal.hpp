@@ -92,6 +92,25 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
                       int64_t SH, int64_t SW, int64_t PH, int64_t PW,
                       hipStream_t stream);
 
+int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t IC,
+                      int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                      int64_t SH, int64_t SW, int64_t PH, int64_t PW, hipStream_t stream);
+int launch_nchw_to_cm_f32(const float* src, float* dst, int64_t batch, int64_t C, int64_t S,
+                          hipStream_t stream);
+int launch_conv_bias_grad_f32(const float* dy, float* db, int64_t batch, int64_t C, int64_t S,
+                              hipStream_t stream);
+
+int launch_strided_copy(const void* src, void* dst, int ndim, const int64_t* shape,
+                        const int64_t* strides, int dtype, hipStream_t stream);
+int launch_fill(void* dst, int64_t n, double v, int dtype, hipStream_t stream);
+int launch_binary(int op, int dtype, const void* a, const void* b, void* y, int64_t n,
+                  hipStream_t stream);
+int launch_randn(void* dst, int64_t n, int dtype, uint64_t seed, uint64_t offset,
+                 hipStream_t stream);
+int64_t sum_partials();
+int launch_sum(const void* x, void* out, int64_t n, int dtype, void* partials,
+               hipStream_t stream);
+
 int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,
                       float* partials, int64_t partial_rows, hipStream_t stream);
 int64_t colsum_partial_rows(int64_t rows, int64_t cols);

@@ -116,7 +116,124 @@ void im2col_plane_kernel(const float* __restrict__ in, float* __restrict__ col, 
     }
 }
 
+// col2im gather, bit-exact with the reference's col2im_kernel
+// (src/kernels/conv_kernel.cu:344-380): one thread per input element,
+// fp32 sum over kh (outer) then kw (inner), both ascending, starting from
+// 0, of every column entry that element was copied to.
+__global__ __launch_bounds__(256)
+void col2im_kernel(const float* __restrict__ col, float* __restrict__ grad_in, Im2colGeom g) {
+    const int64_t total = g.batch * g.IC * g.IH * g.IW;
+    const int64_t B_spatial = g.batch * g.spatial;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t iw = idx % g.IW;
+        const int64_t ih = (idx / g.IW) % g.IH;
+        const int64_t ic = (idx / (g.IW * g.IH)) % g.IC;
+        const int64_t b = idx / (g.IW * g.IH * g.IC);
+        float acc = 0.0f;
+        for (int64_t kh = 0; kh < g.KH; ++kh) {
+            const int64_t oh_num = ih + g.PH - kh;
+            if (oh_num < 0 || oh_num % g.SH != 0) continue;
+            const int64_t oh = oh_num / g.SH;
+            if (oh >= g.OH) continue;
+            for (int64_t kw = 0; kw < g.KW; ++kw) {
+                const int64_t ow_num = iw + g.PW - kw;
+                if (ow_num < 0 || ow_num % g.SW != 0) continue;
+                const int64_t ow = ow_num / g.SW;
+                if (ow >= g.OW) continue;
+                const int64_t k = (ic * g.KH + kh) * g.KW + kw;
+                acc += col[k * B_spatial + b * g.spatial + oh * g.OW + ow];
+            }
+        }
+        grad_in[idx] = acc;
+    }
+}
+
+// [B, C, S] -> [C, B*S] (NCHW grad_output to the GEMM's channel-major
+// matrix), conv_kernel.cu:383-399.  Writes are coalesced along B*S; reads
+// walk contiguous s of one (b, c) plane.
+__global__ __launch_bounds__(256)
+void nchw_to_cm_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                       int64_t batch, int64_t C, int64_t S) {
+    const int64_t BS = batch * S, total = C * BS;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t c = i / BS, bs = i - c * BS;
+        const int64_t b = bs / S, s = bs - b * S;
+        dst[i] = src[(b * C + c) * S + s];
+    }
+}
+
+// db[c] = sum over b, s of dy[b, c, s]: one workgroup per channel, fixed
+// per-thread order then a fixed LDS tree -- deterministic.  Replaces the
+// host-side NumPy sum of the reference's Conv2dOp (python/cuDeep/tensor.py:718-721).
+__global__ __launch_bounds__(256)
+void conv_bias_grad_kernel(const float* __restrict__ dy, float* __restrict__ db,
+                           int64_t batch, int64_t C, int64_t S) {
+    __shared__ float red[256];
+    const int64_t c = blockIdx.x;
+    float acc = 0.0f;
+    for (int64_t b = 0; b < batch; ++b) {
+        const float* plane = dy + (b * C + c) * S;
+        for (int64_t s = threadIdx.x; s < S; s += blockDim.x) acc += plane[s];
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) db[c] = red[0];
+}
+
+unsigned grid_for(int64_t n) {
+    int64_t b = ceil_div(n, 256);
+    if (b > 65536) b = 65536;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+Im2colGeom make_geom(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                     int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    Im2colGeom g;
+    g.batch = batch; g.IC = IC; g.IH = IH; g.IW = IW; g.KH = KH; g.KW = KW;
+    g.SH = SH; g.SW = SW; g.PH = PH; g.PW = PW;
+    g.OH = (IH + 2 * PH - KH) / SH + 1;
+    g.OW = (IW + 2 * PW - KW) / SW + 1;
+    g.spatial = g.OH * g.OW;
+    g.runs = IC * KH * KW * batch;
+    return g;
+}
+
 }  // namespace
+
+int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t IC,
+                      int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                      int64_t SH, int64_t SW, int64_t PH, int64_t PW, hipStream_t stream) {
+    Im2colGeom g = make_geom(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW);
+    const int64_t total = batch * IC * IH * IW;
+    if (total == 0) return CDX_OK;
+    hipLaunchKernelGGL(col2im_kernel, dim3(grid_for(total)), dim3(256), 0, stream, col, grad_in, g);
+    return hip_error(hipGetLastError(), "col2im_kernel launch");
+}
+
+int launch_nchw_to_cm_f32(const float* src, float* dst, int64_t batch, int64_t C, int64_t S,
+                          hipStream_t stream) {
+    const int64_t total = batch * C * S;
+    if (total == 0) return CDX_OK;
+    hipLaunchKernelGGL(nchw_to_cm_kernel, dim3(grid_for(total)), dim3(256), 0, stream,
+                       src, dst, batch, C, S);
+    return hip_error(hipGetLastError(), "nchw_to_cm_kernel launch");
+}
+
+int launch_conv_bias_grad_f32(const float* dy, float* db, int64_t batch, int64_t C, int64_t S,
+                              hipStream_t stream) {
+    if (C == 0) return CDX_OK;
+    if (C > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "conv bias grad: too many channels");
+    hipLaunchKernelGGL(conv_bias_grad_kernel, dim3((unsigned)C), dim3(256), 0, stream,
+                       dy, db, batch, C, S);
+    return hip_error(hipGetLastError(), "conv_bias_grad_kernel launch");
+}
 
 int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,

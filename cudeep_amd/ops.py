@@ -8,6 +8,8 @@ from __future__ import annotations
 
 import torch
 
+import ctypes
+
 from . import _lib as L
 
 
@@ -216,4 +218,125 @@ def activation_backward(grad_out, x, act, out=None):
         out = torch.empty_like(x)
     L.call("cdx_activation_backward_f32", grad_out.data_ptr(), x.data_ptr(), out.data_ptr(),
            x.numel(), act, _stream())
+    return out
+
+
+def col2im(col, x_shape, KH, KW, stride=(1, 1), padding=(0, 0), out=None):
+    _need(col, "col")
+    Bn, C, H, W = x_shape
+    OH = conv_out_size(H, KH, stride[0], padding[0])
+    OW = conv_out_size(W, KW, stride[1], padding[1])
+    if tuple(col.shape) != (C * KH * KW, Bn * OH * OW) or not col.is_contiguous():
+        raise ValueError("col2im: col has the wrong shape")
+    if out is None:
+        out = torch.empty(tuple(x_shape), device=col.device, dtype=torch.float32)
+    L.call("cdx_col2im_f32", col.data_ptr(), out.data_ptr(), Bn, C, H, W, KH, KW,
+           stride[0], stride[1], padding[0], padding[1], _stream())
+    return out
+
+
+def _conv_geom(x_shape, w_shape, stride, padding):
+    Bn, C, H, W = x_shape
+    OC, C2, KH, KW = w_shape
+    if C != C2:
+        raise ValueError("conv2d: channel mismatch")
+    OH = conv_out_size(H, KH, stride[0], padding[0])
+    OW = conv_out_size(W, KW, stride[1], padding[1])
+    if OH <= 0 or OW <= 0:
+        raise ValueError("conv2d: kernel larger than padded input")
+    return Bn, C, H, W, OC, KH, KW, OH, OW
+
+
+def conv2d_backward_data(grad_out, w, x_shape, stride=(1, 1), padding=(0, 0),
+                         precision=L.PREC_FP32, out=None):
+    _need(grad_out, "grad_output")
+    _need(w, "weight")
+    Bn, C, H, W, OC, KH, KW, OH, OW = _conv_geom(tuple(x_shape), tuple(w.shape), stride, padding)
+    if tuple(grad_out.shape) != (Bn, OC, OH, OW) or not grad_out.is_contiguous() \
+            or not w.is_contiguous():
+        raise ValueError("conv2d_backward_data: bad grad_output / weight")
+    if out is None:
+        out = torch.empty((Bn, C, H, W), device=w.device, dtype=torch.float32)
+    L.call("cdx_conv2d_backward_data_f32", grad_out.data_ptr(), w.data_ptr(), out.data_ptr(),
+           Bn, C, OC, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1], precision,
+           None, 0, _stream())
+    return out
+
+
+def conv2d_backward_weight(grad_out, x, w_shape, stride=(1, 1), padding=(0, 0),
+                           precision=L.PREC_FP32, out=None):
+    _need(grad_out, "grad_output")
+    _need(x, "input")
+    Bn, C, H, W, OC, KH, KW, OH, OW = _conv_geom(tuple(x.shape), tuple(w_shape), stride, padding)
+    if tuple(grad_out.shape) != (Bn, OC, OH, OW) or not grad_out.is_contiguous() \
+            or not x.is_contiguous():
+        raise ValueError("conv2d_backward_weight: bad grad_output / input")
+    if out is None:
+        out = torch.empty(tuple(w_shape), device=x.device, dtype=torch.float32)
+    L.call("cdx_conv2d_backward_weight_f32", grad_out.data_ptr(), x.data_ptr(), out.data_ptr(),
+           Bn, C, OC, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1], precision,
+           None, 0, _stream())
+    return out
+
+
+def conv2d_backward_bias(grad_out, out=None):
+    _need(grad_out, "grad_output")
+    if grad_out.dim() != 4 or not grad_out.is_contiguous():
+        raise ValueError("conv2d_backward_bias: grad_output must be contiguous NCHW")
+    Bn, OC, OH, OW = grad_out.shape
+    if out is None:
+        out = torch.empty((OC,), device=grad_out.device, dtype=torch.float32)
+    L.call("cdx_conv2d_backward_bias_f32", grad_out.data_ptr(), out.data_ptr(), Bn, OC, OH * OW,
+           _stream())
+    return out
+
+
+def _dtype_code(t):
+    if t.dtype == torch.float32:
+        return L.DTYPE_F32
+    if t.dtype == torch.float64:
+        return L.DTYPE_F64
+    raise TypeError("only float32 / float64 tensors")
+
+
+def strided_copy(view):
+    """Contiguous copy of a strided device view (cdx_strided_copy)."""
+    if not view.is_cuda:
+        raise ValueError("device tensor expected")
+    code = _dtype_code(view)
+    out = torch.empty(tuple(view.shape), device=view.device, dtype=view.dtype)
+    nd = view.dim()
+    shape = (ctypes.c_int64 * max(nd, 1))(*view.shape)
+    strides = (ctypes.c_int64 * max(nd, 1))(*view.stride())
+    L.call("cdx_strided_copy", view.data_ptr(), out.data_ptr(), nd, shape, strides, code, _stream())
+    return out
+
+
+def fill(t, value):
+    L.call("cdx_fill", t.data_ptr(), t.numel(), float(value), _dtype_code(t), _stream())
+    return t
+
+
+def binary(op, a, b, out=None):
+    if a.shape != b.shape or a.dtype != b.dtype or not (a.is_contiguous() and b.is_contiguous()):
+        raise ValueError("binary: operands must match and be contiguous")
+    if out is None:
+        out = torch.empty_like(a)
+    L.call("cdx_binary", op, _dtype_code(a), a.data_ptr(), b.data_ptr(), out.data_ptr(),
+           a.numel(), _stream())
+    return out
+
+
+def randn(shape, dtype=torch.float32, seed=0, offset=0):
+    out = torch.empty(tuple(shape), device="cuda", dtype=dtype)
+    L.call("cdx_randn", out.data_ptr(), out.numel(), _dtype_code(out), int(seed), int(offset),
+           _stream())
+    return out
+
+
+def total_sum(x):
+    if not x.is_contiguous():
+        raise ValueError("sum: input must be contiguous")
+    out = torch.empty((1,), device=x.device, dtype=x.dtype)
+    L.call("cdx_sum", x.data_ptr(), out.data_ptr(), x.numel(), _dtype_code(x), None, 0, _stream())
     return out

@@ -58,6 +58,13 @@ extern "C" {
 #define CDX_PREC_FP32     0        /* true-FP32 MFMA (v_mfma_f32_16x16x4_f32) */
 #define CDX_PREC_TF32MODE 1        /* bf16x3 split MFMA, |rel err| <= ~3*2^-16 per product */
 
+#define CDX_DTYPE_F32 0
+#define CDX_DTYPE_F64 1
+
+#define CDX_BINARY_ADD 0
+#define CDX_BINARY_SUB 1
+#define CDX_BINARY_MUL 2
+
 /* ---- library --------------------------------------------------------- */
 const char* cdx_last_error(void);
 const char* cdx_version(void);
@@ -136,6 +143,61 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight,
                            void* workspace, size_t workspace_bytes,
                            hipStream_t stream);
 
+/* grad_input[B, IC, IH, IW] from grad_col[K_col, B*OH*OW]: sums, per input
+ * element, every column entry it was copied to (kh then kw ascending, fp32);
+ * bit-exact with col2im_kernel (src/kernels/conv_kernel.cu:344-380). */
+int cdx_col2im_f32(const float* col, float* grad_input,
+                   int64_t batch, int64_t in_channels, int64_t in_h, int64_t in_w,
+                   int64_t kernel_h, int64_t kernel_w,
+                   int64_t stride_h, int64_t stride_w,
+                   int64_t pad_h, int64_t pad_w, hipStream_t stream);
+
+/* Conv backward data: grad_col = weight^T * grad_out[OC, B*S] (one GEMM with
+ * a transposed operand, no weight transpose pass), then col2im.
+ * Replaces cudeep::kernels::launch_conv2d_backward_data_kernel<float>
+ * (include/cudeep/kernels/conv.cuh:18-26, src/kernels/conv_kernel.cu:417-478).
+ * grad_input is overwritten.  workspace may be NULL. */
+size_t cdx_conv2d_backward_data_workspace_size(
+    int64_t batch, int64_t in_channels, int64_t out_channels, int64_t in_h, int64_t in_w,
+    int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+    int64_t pad_h, int64_t pad_w);
+int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight,
+                                 float* grad_input,
+                                 int64_t batch, int64_t in_channels, int64_t out_channels,
+                                 int64_t in_h, int64_t in_w,
+                                 int64_t kernel_h, int64_t kernel_w,
+                                 int64_t stride_h, int64_t stride_w,
+                                 int64_t pad_h, int64_t pad_w, int precision,
+                                 void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream);
+
+/* Conv backward weight: grad_weight[OC, K_col] = grad_out[OC, B*S] * col^T
+ * (the col buffer read transposed by the GEMM -- no col transpose pass; the
+ * long K = B*S is split across workgroups and reduced in a fixed order).
+ * Replaces cudeep::kernels::launch_conv2d_backward_weight_kernel<float>
+ * (include/cudeep/kernels/conv.cuh:28-36, src/kernels/conv_kernel.cu:486-545).
+ * grad_weight is overwritten.  workspace may be NULL. */
+size_t cdx_conv2d_backward_weight_workspace_size(
+    int64_t batch, int64_t in_channels, int64_t out_channels, int64_t in_h, int64_t in_w,
+    int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+    int64_t pad_h, int64_t pad_w);
+int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
+                                   float* grad_weight,
+                                   int64_t batch, int64_t in_channels, int64_t out_channels,
+                                   int64_t in_h, int64_t in_w,
+                                   int64_t kernel_h, int64_t kernel_w,
+                                   int64_t stride_h, int64_t stride_w,
+                                   int64_t pad_h, int64_t pad_w, int precision,
+                                   void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream);
+
+/* grad_bias[c] = sum over b, s of grad_output[b, c, s] (NCHW, S = OH*OW),
+ * deterministic.  Replaces the host-side NumPy reduction of the reference's
+ * Conv2dOp.backward (python/cuDeep/tensor.py:718-721). */
+int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias,
+                                 int64_t batch, int64_t out_channels, int64_t spatial,
+                                 hipStream_t stream);
+
 /* ---- Linear helpers ---------------------------------------------------- */
 
 /* out[j] = sum_i in[i][j] over a row-major [rows, cols] matrix.
@@ -163,6 +225,38 @@ int cdx_activation_forward_f32(const float* input, float* output, int64_t n,
 int cdx_activation_backward_f32(const float* grad_output, const float* input,
                                 float* grad_input, int64_t n, int act,
                                 hipStream_t stream);
+
+/* ---- tensor runtime ----------------------------------------------------- */
+
+/* dst (contiguous) <- src viewed with `shape` / `src_strides` (elements,
+ * ndim <= 8; shape and strides are host arrays).  dtype is CDX_DTYPE_*.
+ * Replaces launch_strided_copy / strided_copy_kernel (src/tensor.cu:26-68)
+ * without its device allocation, H2D copies and stream synchronize. */
+int cdx_strided_copy(const void* src, void* dst, int ndim, const int64_t* shape,
+                     const int64_t* src_strides, int dtype, hipStream_t stream);
+
+/* dst[i] = value for i < n.  Replaces launch_fill_kernel<T>
+ * (include/cudeep/kernels/elementwise.cuh:23-24). */
+int cdx_fill(void* dst, int64_t n, double value, int dtype, hipStream_t stream);
+
+/* out = a (+|-|*) b elementwise, op = CDX_BINARY_*.  Replaces
+ * launch_add_kernel / launch_sub_kernel / launch_mul_kernel
+ * (include/cudeep/kernels/elementwise.cuh:8-15). */
+int cdx_binary(int op, int dtype, const void* a, const void* b, void* out, int64_t n,
+               hipStream_t stream);
+
+/* dst[i] ~ N(0, 1): a pure function of (seed, offset, i) (SplitMix64 +
+ * Box-Muller).  Replaces Tensor::randn's cuRAND generator
+ * (src/tensor.cu:158-206); `offset` lets callers draw disjoint streams. */
+int cdx_randn(void* dst, int64_t n, int dtype, uint64_t seed, uint64_t offset,
+              hipStream_t stream);
+
+/* out[0] = sum of x[0..n), deterministic two-stage reduction.  Replaces
+ * launch_sum_kernel<T> (include/cudeep/kernels/reduce.cuh:9,
+ * src/kernels/reduce_kernel.cu:21-195).  workspace may be NULL. */
+size_t cdx_sum_workspace_size(int dtype);
+int cdx_sum(const void* x, void* out, int64_t n, int dtype, void* workspace,
+            size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@ parity gates:
   (``matmul_kernel.cu:179-214``; ``ptx_intrinsics.cuh:316-335``, ``:639-649``).
 * ``im2col`` / ``transpose_bias`` / ``conv2d_direct64``
   (``src/kernels/conv_kernel.cu:32-65``, ``:74-93``, ``:113-159``).
+* ``col2im`` and the backward-conv routes (``conv_kernel.cu:344-545``).
 * ``colsum`` (``src/kernels/unary_kernel.cu:204-238``).
 * ``gelu`` / ``gelu_grad`` / ``relu`` / ``relu_grad``
   (``src/kernels/activation_kernel.cu:19-52``, ``:256-319``).
@@ -74,6 +75,8 @@ def lib():
         L.orc_transpose_bias.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64]
         L.orc_conv2d_direct64.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 11
         L.orc_colsum.argtypes = [_vp, _vp, _i64, _i64]
+        L.orc_col2im.argtypes = [_vp, _vp] + [_i64] * 10
+        L.orc_col2im64.argtypes = [_vp, _vp] + [_i64] * 10
         L.orc_gelu_vec.argtypes = [_vp, _vp, _i64]
         L.orc_gelu_grad_vec.argtypes = [_vp, _vp, _i64]
         L.orc_num_threads.restype = _int
@@ -220,6 +223,70 @@ def conv2d_ref_im2col(x, w, bias=None, stride=(1, 1), padding=(0, 0)):
     OW = conv_out_size(x.shape[3], KW, stride[1], padding[1])
     out = transpose_bias(flat, OC, Bn, OH * OW, bias)
     return out.reshape(Bn, OC, OH, OW)
+
+
+def col2im(col, x_shape, KH, KW, SH=1, SW=1, PH=0, PW=0):
+    """fp32 col2im gather, kh then kw ascending (conv_kernel.cu:344-380).
+    A float64 ``col`` runs the same gather in double."""
+    Bn, IC, IH, IW = x_shape
+    if np.asarray(col).dtype == np.float64:
+        col = np.ascontiguousarray(col, dtype=np.float64)
+        out = np.empty(x_shape, np.float64)
+        lib().orc_col2im64(_p(col), _p(out), Bn, IC, IH, IW, KH, KW, SH, SW, PH, PW)
+        return out
+    col = _c32(col)
+    out = np.empty(x_shape, np.float32)
+    lib().orc_col2im(_p(col), _p(out), Bn, IC, IH, IW, KH, KW, SH, SW, PH, PW)
+    return out
+
+
+def nchw_to_cm(y):
+    """[B, C, H, W] -> [C, B*H*W] (conv_kernel.cu:383-399)."""
+    Bn, C = y.shape[:2]
+    return np.ascontiguousarray(np.asarray(y).reshape(Bn, C, -1).transpose(1, 0, 2).reshape(C, -1))
+
+
+def conv2d_backward_data_ref(dy, w, x_shape, stride=(1, 1), padding=(0, 0), mode="fp32"):
+    """The reference's backward-data route (conv_kernel.cu:417-478):
+    grad_col = W^T [Kc, OC] @ dY [OC, B*S] (seq-FMA for fp32, the TF32
+    emulation for mode 'rz' / 'rne'), then fp32 col2im."""
+    OC = w.shape[0]
+    KH, KW = w.shape[2], w.shape[3]
+    wt = np.ascontiguousarray(np.asarray(w, np.float32).reshape(OC, -1).T)
+    go = nchw_to_cm(np.asarray(dy, np.float32))
+    if mode == "fp32":
+        gcol = sgemm_seqfma(wt, go)
+    else:
+        gcol = gemm_tf32emu(wt, go, mode)
+    return col2im(gcol, x_shape, KH, KW, stride[0], stride[1], padding[0], padding[1])
+
+
+def conv2d_backward_data64(dy, w, x_shape, stride=(1, 1), padding=(0, 0)):
+    """fp64 grad_input: fp64 W^T dY then the fp64 col2im gather."""
+    OC = w.shape[0]
+    KH, KW = w.shape[2], w.shape[3]
+    gcol = np.asarray(w, np.float64).reshape(OC, -1).T @ nchw_to_cm(np.asarray(dy, np.float64))
+    return col2im(gcol, x_shape, KH, KW, stride[0], stride[1], padding[0], padding[1])
+
+
+def conv2d_backward_weight_ref(dy, x, w_shape, stride=(1, 1), padding=(0, 0), mode="fp32"):
+    """The reference's backward-weight route (conv_kernel.cu:486-545):
+    dW [OC, Kc] = dY [OC, B*S] @ col^T (seq-FMA, or the TF32 emulation)."""
+    OC, IC, KH, KW = w_shape
+    col = im2col(x, KH, KW, stride[0], stride[1], padding[0], padding[1])
+    go = nchw_to_cm(np.asarray(dy, np.float32))
+    if mode == "fp32":
+        dw = sgemm_seqfma(go, col, transB=True)
+    else:
+        dw = gemm_tf32emu(go, np.ascontiguousarray(col.T), mode)
+    return dw.reshape(w_shape)
+
+
+def conv2d_backward_weight64(dy, x, w_shape, stride=(1, 1), padding=(0, 0)):
+    OC, IC, KH, KW = w_shape
+    col = im2col(x, KH, KW, stride[0], stride[1], padding[0], padding[1])
+    go = nchw_to_cm(np.asarray(dy, np.float32))
+    return dgemm(go, col, transB=True).reshape(w_shape)
 
 
 def colsum(x):

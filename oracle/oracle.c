@@ -19,12 +19,14 @@
  *   orc_transpose_bias  src/kernels/conv_kernel.cu:74-93.
  *   orc_conv2d_direct64 src/kernels/conv_kernel.cu:113-159 (naive kernel:
  *                       cross-correlation, zero padding), output size :235-236.
+ *   orc_col2im          src/kernels/conv_kernel.cu:344-380 (fp32, kh then kw).
+ *   orc_col2im64        the same gather in double (yardstick).
  *   orc_colsum          src/kernels/unary_kernel.cu:204-238 (serial fp32 sum
  *                       down each column).
  *   orc_gelu / relu     src/kernels/activation_kernel.cu:19-52 (forward) and
  *                       :256-319 (backward), written in double.
  *
- * Build: oracle/Makefile (gcc -O3 -march=native -ffp-contract=off -fopenmp).
+ * Build: oracle/Makefile (gcc -O3 -march=x86-64-v3 -ffp-contract=off -fopenmp).
  * -ffp-contract=off keeps every fma explicit (fmaf) and forbids the compiler
  * from fusing anything else, so the sequential-FMA SGEMM is bit-reproducible.
  */
@@ -299,6 +301,72 @@ void orc_conv2d_direct64(const float* input, const float* weight, const float* b
                         }
                     out[((b * OC + oc) * OH + oh) * OW + ow] = acc;
                 }
+}
+
+/*
+ * col2im, restatement of col2im_kernel (conv_kernel.cu:344-380): for each
+ * input element (b, ic, ih, iw), acc = 0 then, for kh ascending and kw
+ * ascending, acc += col[k * B_spatial + b * spatial + oh * OW + ow] over
+ * the (oh, ow) the element was copied to.  fp32 accumulation.
+ */
+void orc_col2im(const float* col, float* grad_in,
+                int64_t batch, int64_t IC, int64_t IH, int64_t IW,
+                int64_t KH, int64_t KW, int64_t SH, int64_t SW,
+                int64_t PH, int64_t PW) {
+    int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    int64_t spatial = OH * OW, B_spatial = batch * spatial;
+    int64_t total = batch * IC * IH * IW;
+    #pragma omp parallel for schedule(static)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        int64_t iw = idx % IW, ih = (idx / IW) % IH, ic = (idx / (IW * IH)) % IC;
+        int64_t b = idx / (IW * IH * IC);
+        float acc = 0.0f;
+        for (int64_t kh = 0; kh < KH; ++kh) {
+            int64_t oh_num = ih + PH - kh;
+            if (oh_num < 0 || oh_num % SH != 0) continue;
+            int64_t oh = oh_num / SH;
+            if (oh >= OH) continue;
+            for (int64_t kw = 0; kw < KW; ++kw) {
+                int64_t ow_num = iw + PW - kw;
+                if (ow_num < 0 || ow_num % SW != 0) continue;
+                int64_t ow = ow_num / SW;
+                if (ow >= OW) continue;
+                int64_t k = (ic * KH + kh) * KW + kw;
+                acc += col[k * B_spatial + b * spatial + oh * OW + ow];
+            }
+        }
+        grad_in[idx] = acc;
+    }
+}
+
+void orc_col2im64(const double* col, double* grad_in,
+                  int64_t batch, int64_t IC, int64_t IH, int64_t IW,
+                  int64_t KH, int64_t KW, int64_t SH, int64_t SW,
+                  int64_t PH, int64_t PW) {
+    int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    int64_t spatial = OH * OW, B_spatial = batch * spatial;
+    int64_t total = batch * IC * IH * IW;
+    #pragma omp parallel for schedule(static)
+    for (int64_t idx = 0; idx < total; ++idx) {
+        int64_t iw = idx % IW, ih = (idx / IW) % IH, ic = (idx / (IW * IH)) % IC;
+        int64_t b = idx / (IW * IH * IC);
+        double acc = 0.0;
+        for (int64_t kh = 0; kh < KH; ++kh) {
+            int64_t oh_num = ih + PH - kh;
+            if (oh_num < 0 || oh_num % SH != 0) continue;
+            int64_t oh = oh_num / SH;
+            if (oh >= OH) continue;
+            for (int64_t kw = 0; kw < KW; ++kw) {
+                int64_t ow_num = iw + PW - kw;
+                if (ow_num < 0 || ow_num % SW != 0) continue;
+                int64_t ow = ow_num / SW;
+                if (ow >= OW) continue;
+                int64_t k = (ic * KH + kh) * KW + kw;
+                acc += col[k * B_spatial + b * spatial + oh * OW + ow];
+            }
+        }
+        grad_in[idx] = acc;
+    }
 }
 
 /* Column sums of a row-major [rows, cols] fp32 matrix, serial fp32

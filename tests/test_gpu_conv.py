@@ -142,3 +142,104 @@ def test_conv_workspace_and_no_bias():
     assert np.array_equal(y1, y2)
     e, e_ref = _conv_gate(x, w, None, (1, 1), (1, 1), y1)
     assert e <= 2 * e_ref + 2.0 ** -24
+
+
+# ---------------------------------------------------------------------------
+# backward: col2im (bit-exact), data / weight / bias gradients
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("g", GEOMS[:8])
+def test_col2im_bit_exact(g):
+    Bn, C, H, W, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(7 + sum(g))
+    OH = oracle.conv_out_size(H, KH, SH, PH)
+    OW = oracle.conv_out_size(W, KW, SW, PW)
+    col = normal(rng, (C * KH * KW, Bn * OH * OW))
+    say("col2im", g)
+    got = host(ops().col2im(dev(col), (Bn, C, H, W), KH, KW, (SH, SW), (PH, PW)))
+    want = oracle.col2im(col, (Bn, C, H, W), KH, KW, SH, SW, PH, PW)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_conv_backward_kats(kats):
+    k = kats["conv_bwd_data_1x1_w2"]
+    say("conv bwd kats")
+    dx = host(ops().conv2d_backward_data(
+        dev(np.array(k["dy"], np.float32).reshape(k["dy_shape"])),
+        dev(np.array(k["w"], np.float32).reshape(k["w_shape"])), k["x_shape"],
+        k["stride"], k["padding"]))
+    assert np.array_equal(dx.ravel(), np.array(k["dx"], np.float32))
+    k = kats["conv_bwd_weight_ones"]
+    dw = host(ops().conv2d_backward_weight(
+        dev(np.array(k["dy"], np.float32).reshape(k["dy_shape"])),
+        dev(np.array(k["x"], np.float32).reshape(k["x_shape"])), k["w_shape"],
+        k["stride"], k["padding"]))
+    assert np.array_equal(dw.ravel(), np.array(k["dw"], np.float32))
+
+
+BWD_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
+    (2, 3, 8, 9, 4, 3, 3, 1, 1, 1, 1),
+    (1, 2, 7, 7, 3, 3, 5, 2, 1, 2, 0),
+    (3, 4, 6, 5, 5, 2, 2, 1, 1, 1, 0),
+    (4, 16, 28, 28, 32, 3, 3, 1, 1, 1, 1),
+    (2, 8, 15, 17, 6, 1, 1, 2, 2, 0, 0),
+]
+
+
+@pytest.mark.parametrize("g", BWD_GEOMS)
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_backward_parity(g, prec):
+    Bn, C, H, W, OC, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(200 + sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    w = normal(rng, (OC, C, KH, KW), std=np.sqrt(2.0 / (C * KH * KW)))
+    OH = oracle.conv_out_size(H, KH, SH, PH)
+    OW = oracle.conv_out_size(W, KW, SW, PW)
+    dy = normal(rng, (Bn, OC, OH, OW))
+    st, pd = (SH, SW), (PH, PW)
+    say("conv bwd", g, "prec", prec)
+    dx = host(ops().conv2d_backward_data(dev(dy), dev(w), x.shape, st, pd, precision=prec))
+    dw = host(ops().conv2d_backward_weight(dev(dy), dev(x), w.shape, st, pd, precision=prec))
+    db = host(ops().conv2d_backward_bias(dev(dy)))
+    dx64 = oracle.conv2d_backward_data64(dy, w, x.shape, st, pd)
+    dw64 = oracle.conv2d_backward_weight64(dy, x, w.shape, st, pd)
+    if prec == 0:
+        ex_ref = oracle.rel_fro(oracle.conv2d_backward_data_ref(dy, w, x.shape, st, pd), dx64)
+        ew_ref = oracle.rel_fro(oracle.conv2d_backward_weight_ref(dy, x, w.shape, st, pd), dw64)
+        floor = 2.0 ** -24
+        assert oracle.rel_fro(dx, dx64) <= 2 * ex_ref + floor
+        assert oracle.rel_fro(dw, dw64) <= 2 * ew_ref + floor
+    else:
+        ex_ref = min(oracle.rel_fro(oracle.conv2d_backward_data_ref(dy, w, x.shape, st, pd, m), dx64)
+                     for m in ("rz", "rne"))
+        ew_ref = min(oracle.rel_fro(oracle.conv2d_backward_weight_ref(dy, x, w.shape, st, pd, m), dw64)
+                     for m in ("rz", "rne"))
+        assert oracle.rel_fro(dx, dx64) <= ex_ref
+        assert oracle.rel_fro(dw, dw64) <= ew_ref
+    db64 = dy.astype(np.float64).sum(axis=(0, 2, 3))
+    # reference: NumPy float32 sum over (0, 2, 3) (tensor.py:718-721)
+    e_ref = oracle.rel_fro(dy.sum(axis=(0, 2, 3)).astype(np.float32), db64)
+    assert oracle.rel_fro(db, db64) <= 2 * e_ref + 2.0 ** -24
+
+
+def test_conv_backward_c5_full():
+    """C5 backward at full size: N=32, C=64, 56x56, OC=64, 3x3, s1, p1.
+    dW checked against the fp64 oracle in full (it reduces over the whole
+    batch); dX on batch items 0 and 31."""
+    rng = np.random.default_rng(5151)
+    x = normal(rng, (32, 64, 56, 56))
+    w = normal(rng, (64, 64, 3, 3), std=np.sqrt(2.0 / 576))
+    dy = normal(rng, (32, 64, 56, 56))
+    say("conv bwd C5 full")
+    dx = host(ops().conv2d_backward_data(dev(dy), dev(w), x.shape, (1, 1), (1, 1)))
+    dw = host(ops().conv2d_backward_weight(dev(dy), dev(x), w.shape, (1, 1), (1, 1)))
+    dw64 = oracle.conv2d_backward_weight64(dy, x, w.shape, (1, 1), (1, 1))
+    ew_ref = oracle.rel_fro(oracle.conv2d_backward_weight_ref(dy, x, w.shape, (1, 1), (1, 1)), dw64)
+    ew = oracle.rel_fro(dw, dw64)
+    print(f"C5 dW relFro gpu={ew:.3e} ref-route={ew_ref:.3e}")
+    assert ew <= 2 * ew_ref
+    for i in (0, 31):
+        d64 = oracle.conv2d_backward_data64(dy[i:i + 1], w, (1, 64, 56, 56), (1, 1), (1, 1))
+        e_ref = oracle.rel_fro(oracle.conv2d_backward_data_ref(dy[i:i + 1], w, (1, 64, 56, 56),
+                                                               (1, 1), (1, 1)), d64)
+        assert oracle.rel_fro(dx[i:i + 1], d64) <= 2 * e_ref

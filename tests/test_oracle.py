@@ -282,3 +282,63 @@ def test_gelu_against_torch_and_derivative():
     assert oracle.gelu(np.array([0.0]))[0] == 0.0
     assert np.array_equal(oracle.relu(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 2.0])
     assert np.array_equal(oracle.relu_grad(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 1.0])
+
+
+# ---------------------------------------------------------------------------
+# col2im and the backward-conv routes (conv_kernel.cu:344-545)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("geom", [(2, 3, 8, 9, 3, 3, 1, 1, 1, 1), (1, 2, 7, 7, 3, 5, 2, 1, 2, 0),
+                                  (2, 4, 9, 6, 2, 2, 2, 2, 0, 1)])
+def test_col2im_is_adjoint_of_im2col(geom):
+    """<im2col(x), C> == <x, col2im(C)> for every x, C (fp64 gather)."""
+    Bn, IC, H, W, KH, KW, SH, SW, PH, PW = geom
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((Bn, IC, H, W)).astype(np.float32)
+    col = oracle.im2col(x, KH, KW, SH, SW, PH, PW)
+    C = rng.standard_normal(col.shape)
+    back = oracle.col2im(C, x.shape, KH, KW, SH, SW, PH, PW)
+    lhs = float((col.astype(np.float64) * C).sum())
+    rhs = float((x.astype(np.float64) * back).sum())
+    assert abs(lhs - rhs) <= 1e-9 * max(1.0, abs(lhs))
+    # fp32 gather on exactly representable (integer) data equals the fp64 one
+    Ci = rng.integers(-20, 20, col.shape).astype(np.float32)
+    assert np.array_equal(oracle.col2im(Ci, x.shape, KH, KW, SH, SW, PH, PW),
+                          oracle.col2im(Ci.astype(np.float64), x.shape, KH, KW, SH, SW, PH, PW))
+
+
+def test_conv_backward_kats(kats):
+    k = kats["conv_bwd_data_1x1_w2"]
+    dy = np.array(k["dy"], np.float32).reshape(k["dy_shape"])
+    w = np.array(k["w"], np.float32).reshape(k["w_shape"])
+    dx = oracle.conv2d_backward_data_ref(dy, w, tuple(k["x_shape"]), k["stride"], k["padding"])
+    assert np.array_equal(dx.ravel(), np.array(k["dx"], np.float32))
+    k = kats["conv_bwd_weight_ones"]
+    dy = np.array(k["dy"], np.float32).reshape(k["dy_shape"])
+    x = np.array(k["x"], np.float32).reshape(k["x_shape"])
+    dw = oracle.conv2d_backward_weight_ref(dy, x, tuple(k["w_shape"]), k["stride"], k["padding"])
+    assert np.array_equal(dw.ravel(), np.array(k["dw"], np.float32))
+
+
+@pytest.mark.parametrize("geom", [(2, 3, 8, 9, 4, 3, 3, 1, 1, 1, 1), (1, 2, 7, 7, 3, 3, 5, 2, 1, 2, 0),
+                                  (3, 4, 6, 5, 2, 2, 1, 1, 1, 0, 0)])
+def test_conv_backward_vs_torch_fp64(geom):
+    torch = pytest.importorskip("torch")
+    Bn, IC, H, W, OC, KH, KW, SH, SW, PH, PW = geom
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((Bn, IC, H, W)).astype(np.float32)
+    w = rng.standard_normal((OC, IC, KH, KW)).astype(np.float32)
+    OH = oracle.conv_out_size(H, KH, SH, PH)
+    OW = oracle.conv_out_size(W, KW, SW, PW)
+    dy = rng.standard_normal((Bn, OC, OH, OW)).astype(np.float32)
+    tx, tw, tdy = (torch.from_numpy(a).double() for a in (x, w, dy))
+    dx_t = torch.nn.grad.conv2d_input(x.shape, tw, tdy, stride=(SH, SW), padding=(PH, PW)).numpy()
+    dw_t = torch.nn.grad.conv2d_weight(tx, w.shape, tdy, stride=(SH, SW), padding=(PH, PW)).numpy()
+    dx64 = oracle.conv2d_backward_data64(dy, w, x.shape, (SH, SW), (PH, PW))
+    dw64 = oracle.conv2d_backward_weight64(dy, x, w.shape, (SH, SW), (PH, PW))
+    assert np.allclose(dx64, dx_t, rtol=1e-10, atol=1e-10)
+    assert np.allclose(dw64, dw_t, rtol=1e-10, atol=1e-10)
+    # the fp32 reference routes sit at fp32 error from them
+    dx32 = oracle.conv2d_backward_data_ref(dy, w, x.shape, (SH, SW), (PH, PW))
+    dw32 = oracle.conv2d_backward_weight_ref(dy, x, w.shape, (SH, SW), (PH, PW))
+    assert oracle.rel_fro(dx32, dx64) < 1e-6 and oracle.rel_fro(dw32, dw64) < 1e-6
