@@ -58,6 +58,10 @@ SIGNATURES = {
     "cdx_randn": (_int, [_vp, _i64, _int, ctypes.c_uint64, ctypes.c_uint64, _vp]),
     "cdx_sum_workspace_size": (_sz, [_int]),
     "cdx_sum": (_int, [_vp, _vp, _i64, _int, _vp, _sz, _vp]),
+    "cdx_broadcast_add_row_f64": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "cdx_sum_reduce_rows_f64": (_int, [_vp, _vp, _i64, _i64, _vp, _sz, _vp]),
+    "cdx_activation_forward_f64": (_int, [_vp, _vp, _i64, _int, _vp]),
+    "cdx_activation_backward_f64": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
 }
 
 DTYPE_F32, DTYPE_F64 = 0, 1

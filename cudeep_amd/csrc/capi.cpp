@@ -396,68 +396,113 @@ int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias, int
 
 size_t cdx_sum_reduce_rows_workspace_size(int64_t rows, int64_t cols) {
     if (bad_dim(rows) || bad_dim(cols)) return 0;
-    return (size_t)cdx::colsum_partial_rows(rows, cols) * (size_t)cols * sizeof(float);
+    // sized for fp64 partials so one query serves both dtypes
+    return (size_t)cdx::colsum_partial_rows(rows, cols) * (size_t)cols * sizeof(double);
 }
+
+extern "C++" {
+template <typename T, typename Launch>
+static int sum_reduce_rows_impl(const char* fn, const T* input, T* output, int64_t rows,
+                                int64_t cols, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream, Launch launch) {
+    if (bad_dim(rows) || bad_dim(cols))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad dims");
+    if (cols == 0) return CDX_OK;
+    if (!output || (rows > 0 && !input))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    const int64_t pr = cdx::colsum_partial_rows(rows, cols);
+    Scratch ws;
+    int st = ws.acquire(workspace, workspace_bytes, (size_t)pr * (size_t)cols * sizeof(T), stream, fn);
+    if (st) return st;
+    st = launch(input, output, rows, cols, static_cast<T*>(ws.ptr), pr, stream);
+    return ws.release(st);
+}
+}  // extern "C++"
 
 int cdx_sum_reduce_rows_f32(const float* input, float* output, int64_t rows, int64_t cols,
                             void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (bad_dim(rows) || bad_dim(cols))
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_sum_reduce_rows_f32: bad dims");
-    if (cols == 0) return CDX_OK;
-    if (!output || (rows > 0 && !input))
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_sum_reduce_rows_f32: NULL pointer");
-    const int64_t pr = cdx::colsum_partial_rows(rows, cols);
-    const size_t need = (size_t)pr * (size_t)cols * sizeof(float);
-    float* part = static_cast<float*>(workspace);
-    bool owned = false;
-    int st = CDX_OK;
-    if (workspace) {
-        if (workspace_bytes < need)
-            return set_error(CDX_ERR_WORKSPACE, "cdx_sum_reduce_rows_f32: workspace too small");
-    } else if (need > 0) {
-        st = cdx::hip_error(hipMallocAsync(reinterpret_cast<void**>(&part), need, stream),
-                            "cdx_sum_reduce_rows_f32: hipMallocAsync");
-        if (st) return st;
-        owned = true;
-    }
-    st = cdx::launch_colsum_f32(input, output, rows, cols, part, pr, stream);
-    if (owned) {
-        int st2 = cdx::hip_error(hipFreeAsync(part, stream), "cdx_sum_reduce_rows_f32: hipFreeAsync");
-        if (!st) st = st2;
-    }
-    return st;
+    return sum_reduce_rows_impl("cdx_sum_reduce_rows_f32", input, output, rows, cols, workspace,
+                                workspace_bytes, stream, cdx::launch_colsum_f32);
 }
+
+int cdx_sum_reduce_rows_f64(const double* input, double* output, int64_t rows, int64_t cols,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return sum_reduce_rows_impl("cdx_sum_reduce_rows_f64", input, output, rows, cols, workspace,
+                                workspace_bytes, stream, cdx::launch_colsum_f64);
+}
+
+extern "C++" {
+template <typename T, typename Launch>
+static int bias_row_impl(const char* fn, const T* matrix, const T* row, T* out, int64_t rows,
+                         int64_t cols, hipStream_t stream, Launch launch) {
+    if (bad_dim(rows) || bad_dim(cols))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad dims");
+    if (rows == 0 || cols == 0) return CDX_OK;
+    if (!matrix || !row || !out) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    return launch(matrix, row, out, rows, cols, stream);
+}
+}  // extern "C++"
 
 int cdx_broadcast_add_row_f32(const float* matrix, const float* row, float* out, int64_t rows,
                               int64_t cols, hipStream_t stream) {
-    if (bad_dim(rows) || bad_dim(cols))
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_broadcast_add_row_f32: bad dims");
-    if (rows == 0 || cols == 0) return CDX_OK;
-    if (!matrix || !row || !out)
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_broadcast_add_row_f32: NULL pointer");
-    return cdx::launch_broadcast_add_row_f32(matrix, row, out, rows, cols, stream);
+    return bias_row_impl("cdx_broadcast_add_row_f32", matrix, row, out, rows, cols, stream,
+                         cdx::launch_broadcast_add_row_f32);
 }
+
+int cdx_broadcast_add_row_f64(const double* matrix, const double* row, double* out, int64_t rows,
+                              int64_t cols, hipStream_t stream) {
+    return bias_row_impl("cdx_broadcast_add_row_f64", matrix, row, out, rows, cols, stream,
+                         cdx::launch_broadcast_add_row_f64);
+}
+
+extern "C++" {
+template <typename T, typename Launch>
+static int act_impl(const char* fn, const T* input, T* output, int64_t n, int act,
+                    hipStream_t stream, Launch launch) {
+    if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad n");
+    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU or GELU");
+    if (n == 0) return CDX_OK;
+    if (!input || !output) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    return launch(input, output, n, act, stream);
+}
+}  // extern "C++"
+
+extern "C++" {
+template <typename T, typename Launch>
+static int act_bwd_impl(const char* fn, const T* go, const T* input, T* gi, int64_t n, int act,
+                        hipStream_t stream, Launch launch) {
+    if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad n");
+    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU or GELU");
+    if (n == 0) return CDX_OK;
+    if (!go || !input || !gi) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    return launch(go, input, gi, n, act, stream);
+}
+}  // extern "C++"
 
 int cdx_activation_forward_f32(const float* input, float* output, int64_t n, int act,
                                hipStream_t stream) {
-    if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_forward_f32: bad n");
-    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_forward_f32: act must be RELU or GELU");
-    if (n == 0) return CDX_OK;
-    if (!input || !output)
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_forward_f32: NULL pointer");
-    return cdx::launch_activation_f32(input, output, n, act, stream);
+    return act_impl("cdx_activation_forward_f32", input, output, n, act, stream,
+                    cdx::launch_activation_f32);
+}
+
+int cdx_activation_forward_f64(const double* input, double* output, int64_t n, int act,
+                               hipStream_t stream) {
+    return act_impl("cdx_activation_forward_f64", input, output, n, act, stream,
+                    cdx::launch_activation_f64);
 }
 
 int cdx_activation_backward_f32(const float* grad_output, const float* input, float* grad_input,
                                 int64_t n, int act, hipStream_t stream) {
-    if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: bad n");
-    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: act must be RELU or GELU");
-    if (n == 0) return CDX_OK;
-    if (!grad_output || !input || !grad_input)
-        return set_error(CDX_ERR_INVALID_ARG, "cdx_activation_backward_f32: NULL pointer");
-    return cdx::launch_activation_backward_f32(grad_output, input, grad_input, n, act, stream);
+    return act_bwd_impl("cdx_activation_backward_f32", grad_output, input, grad_input, n, act,
+                        stream, cdx::launch_activation_backward_f32);
+}
+
+int cdx_activation_backward_f64(const double* grad_output, const double* input,
+                                double* grad_input, int64_t n, int act, hipStream_t stream) {
+    return act_bwd_impl("cdx_activation_backward_f64", grad_output, input, grad_input, n, act,
+                        stream, cdx::launch_activation_backward_f64);
 }
 
 static bool bad_dtype(int dtype) { return dtype != CDX_DTYPE_F32 && dtype != CDX_DTYPE_F64; }

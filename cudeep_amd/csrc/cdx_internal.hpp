@@ -115,12 +115,21 @@ int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,
                       float* partials, int64_t partial_rows, hipStream_t stream);
 int64_t colsum_partial_rows(int64_t rows, int64_t cols);
 
+int launch_colsum_f64(const double* in, double* out, int64_t rows, int64_t cols,
+                      double* partials, int64_t partial_rows, hipStream_t stream);
 int launch_broadcast_add_row_f32(const float* m, const float* row, float* out,
+                                 int64_t rows, int64_t cols, hipStream_t stream);
+int launch_broadcast_add_row_f64(const double* m, const double* row, double* out,
                                  int64_t rows, int64_t cols, hipStream_t stream);
 int launch_activation_f32(const float* in, float* out, int64_t n, int act,
                           hipStream_t stream);
+int launch_activation_f64(const double* in, double* out, int64_t n, int act,
+                          hipStream_t stream);
 int launch_activation_backward_f32(const float* grad_out, const float* in,
                                    float* grad_in, int64_t n, int act,
+                                   hipStream_t stream);
+int launch_activation_backward_f64(const double* grad_out, const double* in,
+                                   double* grad_in, int64_t n, int act,
                                    hipStream_t stream);
 
 // GELU, tanh form 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3)
@@ -144,6 +153,22 @@ __device__ __forceinline__ float gelu_grad_f32(float x) {
     float one_minus_s = 1.0f / (1.0f + expf(2.0f * u));
     float du = c * (1.0f + 3.0f * k * x * x);
     return s + 2.0f * x * s * one_minus_s * du;
+}
+
+// fp64 GELU / GELU' with the same formulas in double precision.
+__device__ __forceinline__ double gelu_f64(double x) {
+    const double c = 0.7978845608, k = 0.044715;
+    double u = c * (x + k * x * x * x);
+    return x / (1.0 + exp(-2.0 * u));
+}
+
+__device__ __forceinline__ double gelu_grad_f64(double x) {
+    const double c = 0.7978845608, k = 0.044715;
+    double u = c * (x + k * x * x * x);
+    double s = 1.0 / (1.0 + exp(-2.0 * u));
+    double one_minus_s = 1.0 / (1.0 + exp(2.0 * u));
+    double du = c * (1.0 + 3.0 * k * x * x);
+    return s + 2.0 * x * s * one_minus_s * du;
 }
 
 __device__ __forceinline__ float apply_act(float v, int act) {

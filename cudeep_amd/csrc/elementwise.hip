@@ -17,16 +17,17 @@ namespace {
 constexpr int kColsumRows = 256;   // rows per pass-1 chunk
 constexpr int kColsumCols = 64;    // columns per pass-1 workgroup
 
+template <typename T>
 __global__ __launch_bounds__(256)
-void colsum_partial_kernel(const float* __restrict__ in, float* __restrict__ part,
+void colsum_partial_kernel(const T* __restrict__ in, T* __restrict__ part,
                            int64_t rows, int64_t cols) {
-    __shared__ float red[4][kColsumCols];
+    __shared__ T red[4][kColsumCols];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const int64_t c = (int64_t)blockIdx.x * kColsumCols + tx;
     const int64_t r0 = (int64_t)blockIdx.y * kColsumRows;
     int64_t r1 = r0 + kColsumRows;
     if (r1 > rows) r1 = rows;
-    float acc = 0.0f;
+    T acc = 0;
     if (c < cols)
         for (int64_t r = r0 + ty; r < r1; r += 4) acc += in[r * cols + c];
     red[ty][tx] = acc;
@@ -35,44 +36,58 @@ void colsum_partial_kernel(const float* __restrict__ in, float* __restrict__ par
         part[(int64_t)blockIdx.y * cols + c] = ((red[0][tx] + red[1][tx]) + red[2][tx]) + red[3][tx];
 }
 
+template <typename T>
 __global__ __launch_bounds__(256)
-void colsum_final_kernel(const float* __restrict__ part, float* __restrict__ out,
+void colsum_final_kernel(const T* __restrict__ part, T* __restrict__ out,
                          int64_t chunks, int64_t cols) {
     const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= cols) return;
-    float acc = 0.0f;
+    T acc = 0;
     for (int64_t i = 0; i < chunks; ++i) acc += part[i * cols + c];
     out[c] = acc;
 }
 
+template <typename T>
 __global__ __launch_bounds__(256)
-void bias_row_kernel(const float* __restrict__ m, const float* __restrict__ row,
-                     float* __restrict__ out, int64_t rows, int64_t cols) {
+void bias_row_kernel(const T* __restrict__ m, const T* __restrict__ row,
+                     T* __restrict__ out, int64_t rows, int64_t cols) {
     const int64_t n = rows * cols;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         out[i] = m[i] + row[i % cols];
 }
 
+__device__ __forceinline__ double apply_act(double v, int act) {
+    if (act == CDX_EPI_RELU) return v > 0.0 ? v : 0.0;
+    if (act == CDX_EPI_GELU) return gelu_f64(v);
+    return v;
+}
+
+template <typename T>
 __global__ __launch_bounds__(256)
-void act_fwd_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n, int act) {
+void act_fwd_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, int act) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         y[i] = apply_act(x[i], act);
 }
 
+__device__ __forceinline__ float gelu_grad(float v) { return gelu_grad_f32(v); }
+__device__ __forceinline__ double gelu_grad(double v) { return gelu_grad_f64(v); }
+
+template <typename T>
 __global__ __launch_bounds__(256)
-void act_bwd_kernel(const float* __restrict__ go, const float* __restrict__ x,
-                    float* __restrict__ gi, int64_t n, int act) {
+void act_bwd_kernel(const T* __restrict__ go, const T* __restrict__ x,
+                    T* __restrict__ gi, int64_t n, int act) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const float v = x[i];
-        gi[i] = act == CDX_EPI_RELU ? (v > 0.0f ? go[i] : 0.0f) : go[i] * gelu_grad_f32(v);
+        const T v = x[i];
+        gi[i] = act == CDX_EPI_RELU ? (v > T(0) ? go[i] : T(0)) : go[i] * gelu_grad(v);
     }
 }
 
+template <typename T>
 __global__ __launch_bounds__(256)
-void fill_kernel(float* __restrict__ y, int64_t n, float v) {
+void fill_kernel(T* __restrict__ y, int64_t n, T v) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
         y[i] = v;
@@ -118,42 +133,82 @@ int64_t colsum_partial_rows(int64_t rows, int64_t cols) {
     return ceil_div(rows, kColsumRows);
 }
 
-int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,
-                      float* partials, int64_t partial_rows, hipStream_t stream) {
+template <typename T>
+int colsum_t(const T* in, T* out, int64_t rows, int64_t cols, T* partials, int64_t partial_rows,
+             hipStream_t stream) {
     if (cols <= 0) return CDX_OK;
     if (partial_rows > 65535) return set_error(CDX_ERR_UNSUPPORTED, "sum_reduce_rows: too many rows");
     if (rows <= 0) {   // empty sum: zeros (a fill kernel, capture-safe)
-        hipLaunchKernelGGL(fill_kernel, dim3(grid_for(cols)), dim3(256), 0, stream, out, cols, 0.0f);
+        hipLaunchKernelGGL(fill_kernel<T>, dim3(grid_for(cols)), dim3(256), 0, stream, out, cols, T(0));
         return hip_error(hipGetLastError(), "fill_kernel launch");
     }
     dim3 g1((unsigned)ceil_div(cols, kColsumCols), (unsigned)partial_rows);
-    hipLaunchKernelGGL(colsum_partial_kernel, g1, dim3(256), 0, stream, in, partials, rows, cols);
+    hipLaunchKernelGGL(colsum_partial_kernel<T>, g1, dim3(256), 0, stream, in, partials, rows, cols);
     int st = hip_error(hipGetLastError(), "colsum_partial_kernel launch");
     if (st) return st;
-    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0,
+    hipLaunchKernelGGL(colsum_final_kernel<T>, dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0,
                        stream, partials, out, partial_rows, cols);
     return hip_error(hipGetLastError(), "colsum_final_kernel launch");
 }
 
-int launch_broadcast_add_row_f32(const float* m, const float* row, float* out,
-                                 int64_t rows, int64_t cols, hipStream_t stream) {
+int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,
+                      float* partials, int64_t partial_rows, hipStream_t stream) {
+    return colsum_t(in, out, rows, cols, partials, partial_rows, stream);
+}
+
+int launch_colsum_f64(const double* in, double* out, int64_t rows, int64_t cols,
+                      double* partials, int64_t partial_rows, hipStream_t stream) {
+    return colsum_t(in, out, rows, cols, partials, partial_rows, stream);
+}
+
+template <typename T>
+int bias_row_t(const T* m, const T* row, T* out, int64_t rows, int64_t cols, hipStream_t stream) {
     if (rows * cols == 0) return CDX_OK;
-    hipLaunchKernelGGL(bias_row_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(bias_row_kernel<T>, dim3(grid_for(rows * cols)), dim3(256), 0, stream,
                        m, row, out, rows, cols);
     return hip_error(hipGetLastError(), "bias_row_kernel launch");
 }
 
-int launch_activation_f32(const float* in, float* out, int64_t n, int act, hipStream_t stream) {
+int launch_broadcast_add_row_f32(const float* m, const float* row, float* out,
+                                 int64_t rows, int64_t cols, hipStream_t stream) {
+    return bias_row_t(m, row, out, rows, cols, stream);
+}
+
+int launch_broadcast_add_row_f64(const double* m, const double* row, double* out,
+                                 int64_t rows, int64_t cols, hipStream_t stream) {
+    return bias_row_t(m, row, out, rows, cols, stream);
+}
+
+template <typename T>
+int act_t(const T* in, T* out, int64_t n, int act, hipStream_t stream) {
     if (n == 0) return CDX_OK;
-    hipLaunchKernelGGL(act_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n, act);
+    hipLaunchKernelGGL(act_fwd_kernel<T>, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n, act);
     return hip_error(hipGetLastError(), "act_fwd_kernel launch");
+}
+
+template <typename T>
+int act_bwd_t(const T* go, const T* in, T* gi, int64_t n, int act, hipStream_t stream) {
+    if (n == 0) return CDX_OK;
+    hipLaunchKernelGGL(act_bwd_kernel<T>, dim3(grid_for(n)), dim3(256), 0, stream, go, in, gi, n, act);
+    return hip_error(hipGetLastError(), "act_bwd_kernel launch");
+}
+
+int launch_activation_f32(const float* in, float* out, int64_t n, int act, hipStream_t stream) {
+    return act_t(in, out, n, act, stream);
+}
+
+int launch_activation_f64(const double* in, double* out, int64_t n, int act, hipStream_t stream) {
+    return act_t(in, out, n, act, stream);
 }
 
 int launch_activation_backward_f32(const float* go, const float* in, float* gi, int64_t n,
                                    int act, hipStream_t stream) {
-    if (n == 0) return CDX_OK;
-    hipLaunchKernelGGL(act_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, stream, go, in, gi, n, act);
-    return hip_error(hipGetLastError(), "act_bwd_kernel launch");
+    return act_bwd_t(go, in, gi, n, act, stream);
+}
+
+int launch_activation_backward_f64(const double* go, const double* in, double* gi, int64_t n,
+                                   int act, hipStream_t stream) {
+    return act_bwd_t(go, in, gi, n, act, stream);
 }
 
 }  // namespace cdx

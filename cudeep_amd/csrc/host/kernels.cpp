@@ -1,0 +1,258 @@
+// cudeep::kernels launchers (the reference's C++ operator API,
+// include/cudeep/kernels/*.cuh) implemented over the C-ABI of
+// libcudeep_amd.so.  Each template is explicitly instantiated for float and
+// double, as the reference does; combinations outside this build (fp64
+// conv, non-ReLU/GELU activations) throw.
+#include <atomic>
+#include <string>
+
+#include "../../../include/cudeep/error.hpp"
+#include "../../../include/cudeep/kernels/activation.hpp"
+#include "../../../include/cudeep/kernels/conv.hpp"
+#include "../../../include/cudeep/kernels/elementwise.hpp"
+#include "../../../include/cudeep/kernels/matmul.hpp"
+#include "../../../include/cudeep/kernels/reduce.hpp"
+#include "../../../include/cudeep/kernels/unary.hpp"
+
+namespace cudeep {
+namespace kernels {
+
+namespace {
+
+std::atomic<int> g_precision{CDX_PREC_TF32MODE};
+
+template <typename T>
+constexpr int dtype_code() {
+    return sizeof(T) == 4 ? CDX_DTYPE_F32 : CDX_DTYPE_F64;
+}
+
+int epi_code(GemmEpilogue e) {
+    switch (e) {
+        case GemmEpilogue::None: return CDX_EPI_NONE;
+        case GemmEpilogue::ReLU: return CDX_EPI_RELU;
+        case GemmEpilogue::GELU: return CDX_EPI_GELU;
+        default: throw std::runtime_error("GEMM epilogue not supported by this build (ReLU/GELU only)");
+    }
+}
+
+int act_code(ActivationType a) {
+    if (a == ActivationType::ReLU) return CDX_EPI_RELU;
+    if (a == ActivationType::GELU) return CDX_EPI_GELU;
+    throw std::runtime_error("activation not supported by this build (ReLU/GELU only)");
+}
+
+}  // namespace
+
+void set_matmul_precision(MatmulPrecision p) {
+    g_precision = p == MatmulPrecision::FP32 ? CDX_PREC_FP32 : CDX_PREC_TF32MODE;
+}
+
+MatmulPrecision get_matmul_precision() {
+    return g_precision.load() == CDX_PREC_FP32 ? MatmulPrecision::FP32 : MatmulPrecision::TF32Mode;
+}
+
+void launch_matmul_ex(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                      bool transA, bool transB, int64_t lda, int64_t ldb, int64_t ldc,
+                      const float* bias, bool bias_per_col, GemmEpilogue epilogue,
+                      hipStream_t stream, int precision) {
+    const int prec = precision >= 0 ? precision : g_precision.load();
+    const int bm = bias ? (bias_per_col ? CDX_BIAS_COL : CDX_BIAS_ROW) : CDX_BIAS_NONE;
+    CUDEEP_CHECK_CDX(cdx_gemm_ex(prec, transA ? CDX_OP_T : CDX_OP_N, transB ? CDX_OP_T : CDX_OP_N,
+                                 M, N, K, A, lda, B, ldb, C, ldc, bias, bm, epi_code(epilogue),
+                                 stream));
+}
+
+void launch_matmul_dgemm_ex(const double* A, const double* B, double* C, int64_t M, int64_t N,
+                            int64_t K, bool transA, bool transB, int64_t lda, int64_t ldb,
+                            int64_t ldc, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_dgemm(transA ? CDX_OP_T : CDX_OP_N, transB ? CDX_OP_T : CDX_OP_N, M, N, K,
+                               A, lda, B, ldb, C, ldc, stream));
+}
+
+template <>
+void launch_matmul_kernel<float>(const float* A, const float* B, float* C, int M, int N, int K,
+                                 hipStream_t stream) {
+    launch_matmul_ex(A, B, C, M, N, K, false, false, K > 1 ? K : 1, N > 1 ? N : 1, N, nullptr,
+                     true, GemmEpilogue::None, stream);
+}
+
+template <>
+void launch_matmul_kernel<double>(const double* A, const double* B, double* C, int M, int N,
+                                  int K, hipStream_t stream) {
+    launch_matmul_dgemm_ex(A, B, C, M, N, K, false, false, K > 1 ? K : 1, N > 1 ? N : 1, N,
+                           stream);
+}
+
+template <>
+void launch_matmul_kernel_fp32<float>(const float* A, const float* B, float* C, int M, int N,
+                                      int K, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_sgemm_f32(A, B, C, M, N, K, stream));
+}
+
+template <>
+void launch_matmul_kernel_fp32<double>(const double* A, const double* B, double* C, int M, int N,
+                                       int K, hipStream_t stream) {
+    launch_matmul_kernel<double>(A, B, C, M, N, K, stream);
+}
+
+template <typename T>
+void launch_matmul_tiled_kernel(const T* A, const T* B, T* C, int M, int N, int K, int,
+                                hipStream_t stream) {
+    launch_matmul_kernel<T>(A, B, C, M, N, K, stream);
+}
+template void launch_matmul_tiled_kernel<float>(const float*, const float*, float*, int, int, int,
+                                                int, hipStream_t);
+template void launch_matmul_tiled_kernel<double>(const double*, const double*, double*, int, int,
+                                                 int, int, hipStream_t);
+
+void launch_matmul_fused_act(const float* A, const float* B, float* C, int M, int N, int K,
+                             GemmEpilogue epilogue, hipStream_t stream) {
+    launch_matmul_ex(A, B, C, M, N, K, false, false, K > 1 ? K : 1, N > 1 ? N : 1, N, nullptr,
+                     true, epilogue, stream);
+}
+
+// ---- conv ------------------------------------------------------------------
+
+template <>
+void launch_conv2d_forward_kernel<float>(const float* input, const float* weight, const float* bias,
+                                         float* output, int batch, int IC, int OC, int IH, int IW,
+                                         int KH, int KW, int SH, int SW, int PH, int PW,
+                                         hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_forward_f32(input, weight, bias, output, batch, IC, OC, IH, IW,
+                                            KH, KW, SH, SW, PH, PW, g_precision.load(), nullptr,
+                                            0, stream));
+}
+
+template <>
+void launch_conv2d_forward_kernel<double>(const double*, const double*, const double*, double*,
+                                          int, int, int, int, int, int, int, int, int, int, int,
+                                          hipStream_t) {
+    throw std::runtime_error("conv2d: float64 is not supported by this build");
+}
+
+template <>
+void launch_conv2d_backward_data_kernel<float>(const float* grad_output, const float* weight,
+                                               float* grad_input, int batch, int IC, int OC,
+                                               int IH, int IW, int KH, int KW, int SH, int SW,
+                                               int PH, int PW, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_f32(grad_output, weight, grad_input, batch, IC, OC,
+                                                  IH, IW, KH, KW, SH, SW, PH, PW,
+                                                  g_precision.load(), nullptr, 0, stream));
+}
+
+template <>
+void launch_conv2d_backward_data_kernel<double>(const double*, const double*, double*, int, int,
+                                                int, int, int, int, int, int, int, int, int,
+                                                hipStream_t) {
+    throw std::runtime_error("conv2d backward: float64 is not supported by this build");
+}
+
+template <>
+void launch_conv2d_backward_weight_kernel<float>(const float* grad_output, const float* input,
+                                                 float* grad_weight, int batch, int IC, int OC,
+                                                 int IH, int IW, int KH, int KW, int SH, int SW,
+                                                 int PH, int PW, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_backward_weight_f32(grad_output, input, grad_weight, batch, IC,
+                                                    OC, IH, IW, KH, KW, SH, SW, PH, PW,
+                                                    g_precision.load(), nullptr, 0, stream));
+}
+
+template <>
+void launch_conv2d_backward_weight_kernel<double>(const double*, const double*, double*, int, int,
+                                                  int, int, int, int, int, int, int, int, int,
+                                                  hipStream_t) {
+    throw std::runtime_error("conv2d backward: float64 is not supported by this build");
+}
+
+void launch_conv2d_backward_bias_kernel(const float* grad_output, float* grad_bias, int batch,
+                                        int out_channels, int spatial, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_backward_bias_f32(grad_output, grad_bias, batch, out_channels,
+                                                  spatial, stream));
+}
+
+// ---- elementwise / reductions / activations ---------------------------------
+
+template <typename T>
+void launch_add_kernel(const T* a, const T* b, T* out, int64_t n, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_binary(CDX_BINARY_ADD, dtype_code<T>(), a, b, out, n, s));
+}
+template <typename T>
+void launch_sub_kernel(const T* a, const T* b, T* out, int64_t n, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_binary(CDX_BINARY_SUB, dtype_code<T>(), a, b, out, n, s));
+}
+template <typename T>
+void launch_mul_kernel(const T* a, const T* b, T* out, int64_t n, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_binary(CDX_BINARY_MUL, dtype_code<T>(), a, b, out, n, s));
+}
+template <typename T>
+void launch_fill_kernel(T* data, T value, int64_t n, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_fill(data, n, (double)value, dtype_code<T>(), s));
+}
+
+template <>
+void launch_broadcast_add_row_kernel<float>(const float* m, const float* row, float* out,
+                                            int64_t rows, int64_t cols, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_broadcast_add_row_f32(m, row, out, rows, cols, s));
+}
+
+template <>
+void launch_broadcast_add_row_kernel<double>(const double* m, const double* row, double* out,
+                                             int64_t rows, int64_t cols, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_broadcast_add_row_f64(m, row, out, rows, cols, s));
+}
+
+template <>
+void launch_sum_reduce_rows_kernel<float>(const float* in, float* out, int64_t rows, int64_t cols,
+                                          hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_sum_reduce_rows_f32(in, out, rows, cols, nullptr, 0, s));
+}
+
+template <>
+void launch_sum_reduce_rows_kernel<double>(const double* in, double* out, int64_t rows,
+                                           int64_t cols, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_sum_reduce_rows_f64(in, out, rows, cols, nullptr, 0, s));
+}
+
+template <typename T>
+void launch_sum_kernel(const T* input, T* output, int64_t n, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_sum(input, output, n, dtype_code<T>(), nullptr, 0, s));
+}
+
+template <>
+void launch_activation_forward_kernel<float>(const float* in, float* out, int64_t n,
+                                             ActivationType act, float, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_activation_forward_f32(in, out, n, act_code(act), s));
+}
+
+template <>
+void launch_activation_forward_kernel<double>(const double* in, double* out, int64_t n,
+                                              ActivationType act, float, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_activation_forward_f64(in, out, n, act_code(act), s));
+}
+
+template <>
+void launch_activation_backward_kernel<float>(const float* go, const float* in, float* gi,
+                                              int64_t n, ActivationType act, float,
+                                              hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_activation_backward_f32(go, in, gi, n, act_code(act), s));
+}
+
+template <>
+void launch_activation_backward_kernel<double>(const double* go, const double* in, double* gi,
+                                               int64_t n, ActivationType act, float,
+                                               hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_activation_backward_f64(go, in, gi, n, act_code(act), s));
+}
+
+#define CDX_INST(T)                                                                         \
+    template void launch_add_kernel<T>(const T*, const T*, T*, int64_t, hipStream_t);       \
+    template void launch_sub_kernel<T>(const T*, const T*, T*, int64_t, hipStream_t);       \
+    template void launch_mul_kernel<T>(const T*, const T*, T*, int64_t, hipStream_t);       \
+    template void launch_fill_kernel<T>(T*, T, int64_t, hipStream_t);                       \
+    template void launch_sum_kernel<T>(const T*, T*, int64_t, hipStream_t);
+CDX_INST(float)
+CDX_INST(double)
+#undef CDX_INST
+
+}  // namespace kernels
+}  // namespace cudeep

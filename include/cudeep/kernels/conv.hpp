@@ -1,0 +1,39 @@
+// Conv2d launchers of the C++ host API, same signatures as the reference's
+// include/cudeep/kernels/conv.cuh:8-36 (NCHW input, OIHW weight, bias may be
+// null), over the C-ABI.  Scratch is allocated stream-ordered, as the
+// reference does; float only (double throws: not part of this build).
+#pragma once
+
+#include "../common.hpp"
+
+namespace cudeep {
+namespace kernels {
+
+template <typename T>
+void launch_conv2d_forward_kernel(const T* input, const T* weight, const T* bias, T* output,
+                                  int batch, int in_channels, int out_channels, int in_h,
+                                  int in_w, int kernel_h, int kernel_w, int stride_h,
+                                  int stride_w, int pad_h, int pad_w,
+                                  hipStream_t stream = nullptr);
+
+template <typename T>
+void launch_conv2d_backward_data_kernel(const T* grad_output, const T* weight, T* grad_input,
+                                        int batch, int in_channels, int out_channels, int in_h,
+                                        int in_w, int kernel_h, int kernel_w, int stride_h,
+                                        int stride_w, int pad_h, int pad_w,
+                                        hipStream_t stream = nullptr);
+
+template <typename T>
+void launch_conv2d_backward_weight_kernel(const T* grad_output, const T* input, T* grad_weight,
+                                          int batch, int in_channels, int out_channels,
+                                          int in_h, int in_w, int kernel_h, int kernel_w,
+                                          int stride_h, int stride_w, int pad_h, int pad_w,
+                                          hipStream_t stream = nullptr);
+
+// grad_bias[c] = sum of grad_output[:, c, :, :] (on the GPU).
+void launch_conv2d_backward_bias_kernel(const float* grad_output, float* grad_bias, int batch,
+                                        int out_channels, int spatial,
+                                        hipStream_t stream = nullptr);
+
+}  // namespace kernels
+}  // namespace cudeep

@@ -203,7 +203,8 @@ int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias,
 /* out[j] = sum_i in[i][j] over a row-major [rows, cols] matrix.
  * Replaces cudeep::kernels::launch_sum_reduce_rows_kernel<float>
  * (include/cudeep/kernels/unary.cuh:32-35, src/kernels/unary_kernel.cu:204-245).
- * Deterministic two-pass reduction; workspace may be NULL. */
+ * Deterministic two-pass reduction; workspace may be NULL.  The size query
+ * covers both the f32 and the f64 entry point. */
 size_t cdx_sum_reduce_rows_workspace_size(int64_t rows, int64_t cols);
 int cdx_sum_reduce_rows_f32(const float* input, float* output,
                             int64_t rows, int64_t cols,
@@ -215,6 +216,14 @@ int cdx_sum_reduce_rows_f32(const float* input, float* output,
  * (include/cudeep/kernels/elementwise.cuh:26-29, elementwise_kernel.cu:186-204). */
 int cdx_broadcast_add_row_f32(const float* matrix, const float* row, float* out,
                               int64_t rows, int64_t cols, hipStream_t stream);
+/* fp64 variants of the Linear helpers (float64 Linear, the reference's
+ * double instantiations of the same launchers). */
+int cdx_broadcast_add_row_f64(const double* matrix, const double* row, double* out,
+                              int64_t rows, int64_t cols, hipStream_t stream);
+int cdx_sum_reduce_rows_f64(const double* input, double* output,
+                            int64_t rows, int64_t cols,
+                            void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
 
 /* ReLU / GELU forward and backward (act = CDX_EPI_RELU or CDX_EPI_GELU).
  * Replace launch_activation_forward_kernel / launch_activation_backward_kernel
@@ -224,6 +233,11 @@ int cdx_activation_forward_f32(const float* input, float* output, int64_t n,
                                int act, hipStream_t stream);
 int cdx_activation_backward_f32(const float* grad_output, const float* input,
                                 float* grad_input, int64_t n, int act,
+                                hipStream_t stream);
+int cdx_activation_forward_f64(const double* input, double* output, int64_t n,
+                               int act, hipStream_t stream);
+int cdx_activation_backward_f64(const double* grad_output, const double* input,
+                                double* grad_input, int64_t n, int act,
                                 hipStream_t stream);
 
 /* ---- tensor runtime ----------------------------------------------------- */

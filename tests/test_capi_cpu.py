@@ -80,7 +80,7 @@ def test_conv_argument_validation():
     # workspace size query = K_col * B * OH * OW * 4
     assert L.lib().cdx_conv2d_forward_workspace_size(32, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
         == 576 * 32 * 56 * 56 * 4
-    assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 32 * 256 * 4
+    assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 32 * 256 * 8  # fp64-sized
     assert _status("cdx_activation_forward_f32", fake, fake, 4, 0, None) == L.CDX_ERR_INVALID_ARG
     assert _status("cdx_sum_reduce_rows_f32", None, fake, 4, 4, None, 0, None) \
         == L.CDX_ERR_INVALID_ARG

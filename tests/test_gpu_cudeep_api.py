@@ -1,0 +1,275 @@
+"""The drop-in Python surface on the GPU: cuDeep.Tensor / nn / init over
+the native _cudeep_core module, written like the reference's own tests
+(tests/unit/test_tensor_ops.py:210-262, test_autograd.py:85-231,
+test_nn.py:29-118, test_layers.py:58-75) plus oracle gates on the fused
+Linear / Conv2d paths."""
+import numpy as np
+import pytest
+
+import oracle
+from tests.gpu_util import require_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cd():
+    require_gpu()
+    from cudeep_amd import cuDeep
+    return cuDeep
+
+
+@pytest.fixture(autouse=True)
+def _precision(cd):
+    prev = cd.get_matmul_precision()
+    yield
+    cd.set_matmul_precision(prev)
+
+
+# ---- Tensor basics ---------------------------------------------------------
+
+def test_tensor_factories_and_views(cd):
+    T = cd.Tensor
+    say("tensor basics")
+    assert np.array_equal(T.zeros([2, 3]).numpy(), np.zeros((2, 3), np.float32))
+    assert np.array_equal(T.ones([4]).numpy(), np.ones(4, np.float32))
+    assert T.full([2, 2], 3.5).numpy().tolist() == [[3.5, 3.5], [3.5, 3.5]]
+    x = np.arange(24, dtype=np.float32).reshape(2, 3, 4)
+    t = T.from_numpy(x)
+    assert t.shape() == [2, 3, 4] and t.dtype() == cd.DType.float32
+    assert np.array_equal(t.reshape(6, 4).numpy(), x.reshape(6, 4))
+    assert np.array_equal(t.reshape([4, -1]).numpy(), x.reshape(4, 6))
+    tt = t.transpose(0, 2)
+    assert not tt.is_contiguous()
+    assert np.array_equal(tt.numpy(), x.transpose(2, 1, 0))
+    assert np.array_equal(tt.contiguous().numpy(), x.transpose(2, 1, 0))
+    a = np.random.default_rng(0).standard_normal((5, 7)).astype(np.float32)
+    b = np.random.default_rng(1).standard_normal((5, 7)).astype(np.float32)
+    A, B = T.from_numpy(a), T.from_numpy(b)
+    assert np.array_equal((A + B).numpy(), a + b)
+    assert np.array_equal((A - B).numpy(), a - b)
+    assert np.array_equal((A * B).numpy(), a * b)
+    d = T.from_numpy(np.arange(6, dtype=np.float64))
+    assert d.dtype() == cd.DType.float64 and d.numpy().dtype == np.float64
+    r = T.randn([1000, 100]).numpy()
+    assert abs(r.mean()) < 0.02 and abs(r.std() - 1) < 0.02
+    assert T.from_numpy(np.array([[1.0, 2.0]], np.float32)).sum().item() == 3.0
+
+
+def test_memory_pool_and_events(cd):
+    say("pool/events")
+    pool = cd.MemoryPool.instance()
+    before = pool.allocated_bytes
+    t = cd.Tensor.zeros([1024, 1024])
+    assert pool.allocated_bytes >= before + 4 * 1024 * 1024
+    del t
+    assert pool.cached_bytes >= 4 * 1024 * 1024
+    s = cd.Stream()
+    e0, e1 = cd.Event(), cd.Event()
+    e0.record(s)
+    e1.record(s)
+    e1.synchronize()
+    assert e1.elapsed_ms(e0) >= 0.0
+    info = cd.device_info()
+    assert info["multiprocessors"] > 0 and "gfx950" in info["arch"]
+
+
+# ---- matmul (reference tests/unit/test_tensor_ops.py:210-262) --------------
+
+@pytest.mark.parametrize("prec", ["tf32", "fp32"])
+def test_matmul_reference_cases(cd, prec):
+    cd.set_matmul_precision(prec)
+    T = cd.Tensor
+    say("matmul cases", prec)
+    a = T.from_numpy(np.array([[1, 2], [3, 4]], np.float32))
+    b = T.from_numpy(np.array([[5, 6], [7, 8]], np.float32))
+    assert np.array_equal(a.matmul(b).numpy(), [[19, 22], [43, 50]])
+    x = np.random.randn(64, 64).astype(np.float32)
+    out = T.from_numpy(x).matmul(T.from_numpy(np.eye(64, dtype=np.float32))).numpy()
+    np.testing.assert_allclose(out, x, rtol=1e-5)
+    a = np.random.randn(3, 5).astype(np.float32)
+    b = np.random.randn(5, 7).astype(np.float32)
+    np.testing.assert_allclose((T.from_numpy(a) @ T.from_numpy(b)).numpy(), a @ b, rtol=1e-4,
+                               atol=1e-5)
+    a = np.random.randn(64, 128).astype(np.float32)
+    b = np.random.randn(128, 32).astype(np.float32)
+    np.testing.assert_allclose((T.from_numpy(a) @ T.from_numpy(b)).numpy(), a @ b, rtol=1e-3,
+                               atol=1e-3)
+
+
+def test_matmul_float64_and_transposed_views(cd):
+    T = cd.Tensor
+    say("matmul f64 / views")
+    a = np.random.randn(33, 17)
+    b = np.random.randn(17, 9)
+    np.testing.assert_allclose((T.from_numpy(a) @ T.from_numpy(b)).numpy(), a @ b, rtol=1e-12)
+    # transposed operands are consumed as views (no copy), results identical
+    cd.set_matmul_precision("fp32")
+    w = np.random.randn(40, 30).astype(np.float32)
+    x = np.random.randn(20, 30).astype(np.float32)
+    got = T.from_numpy(x).matmul(T.from_numpy(w).t()).numpy()
+    C64 = x.astype(np.float64) @ w.T.astype(np.float64)
+    e_ref = oracle.rel_fro(oracle.sgemm_seqfma(x, w, transB=True), C64)
+    assert oracle.rel_fro(got, C64) <= 2 * e_ref + 2.0 ** -24
+    got2 = T.from_numpy(w).t().matmul(T.from_numpy(x).t()).numpy()
+    assert oracle.rel_fro(got2, C64.T) <= 2 * e_ref + 2.0 ** -24
+
+
+# ---- autograd (reference tests/unit/test_autograd.py) ----------------------
+
+def test_matmul_grad_kat(cd, kats):
+    k = kats["autograd_sum_matmul"]
+    T = cd.Tensor
+    say("autograd kat")
+    a = T.from_numpy(np.array(k["A"], np.float32), requires_grad=True)
+    b = T.from_numpy(np.array(k["B"], np.float32), requires_grad=True)
+    a.matmul(b).sum().backward()
+    assert np.array_equal(a.grad.numpy(), np.array(k["dA"], np.float32))
+    assert np.array_equal(b.grad.numpy(), np.array(k["dB"], np.float32))
+
+
+def test_chain_rule_and_accumulation(cd):
+    T = cd.Tensor
+    say("chain rule")
+    a = T.from_numpy(np.array([2.0], np.float32), requires_grad=True)
+    (((a * 3.0) + 1.0) * 2.0).sum().backward()
+    np.testing.assert_allclose(a.grad.numpy(), [6.0])
+    w = T.from_numpy(np.array([[1.0, 2.0]], np.float32), requires_grad=True)
+    x1 = T.from_numpy(np.array([[1.0, 0.0]], np.float32))
+    w.matmul(x1.t()).sum().backward()
+    assert np.array_equal(w.grad.numpy(), [[1.0, 0.0]])
+    w.matmul(x1.t()).sum().backward()           # accumulates
+    assert np.array_equal(w.grad.numpy(), [[2.0, 0.0]])
+    with cd.no_grad():
+        y = w.matmul(x1.t())
+    assert y._grad_fn is None
+
+
+def test_broadcast_add_grad(cd):
+    T = cd.Tensor
+    say("broadcast add grad")
+    mat = T.from_numpy(np.zeros((3, 4), np.float32), requires_grad=True)
+    row = T.from_numpy(np.zeros(4, np.float32), requires_grad=True)
+    cd.broadcast_add(mat, row).sum().backward()
+    np.testing.assert_allclose(mat.grad.numpy(), np.ones((3, 4)))
+    np.testing.assert_allclose(row.grad.numpy(), [3, 3, 3, 3])
+
+
+# ---- nn.Linear / Sequential (reference tests/unit/test_nn.py) --------------
+
+def test_linear_reference_cases(cd, kats):
+    nn, T = cd.nn, cd.Tensor
+    say("linear cases")
+    layer = nn.Linear(10, 5)
+    assert len(layer.parameters()) == 2
+    assert layer._parameters["weight"].shape() == [5, 10]
+    assert len(nn.Linear(10, 5, bias=False).parameters()) == 1
+    assert nn.Linear(8, 4)(T.randn([2, 8])).shape() == [2, 4]
+    for name in ("linear_fixed_weight", "linear_identity_bias"):
+        k = kats[name]
+        layer = nn.Linear(len(k["W"][0]), len(k["W"]))
+        layer._parameters["weight"] = T.from_numpy(np.array(k["W"], np.float32))
+        layer._parameters["bias"] = T.from_numpy(np.array(k["b"], np.float32))
+        assert np.array_equal(layer(T.from_numpy(np.array(k["x"], np.float32))).numpy(),
+                              np.array(k["y"], np.float32))
+    l64 = nn.Linear(4, 3, dtype=cd.DType.float64)
+    out = l64(T.randn([1, 4], cd.DType.float64))
+    assert out.shape() == [1, 3] and out.dtype() == cd.DType.float64
+    model = nn.Sequential(nn.Linear(784, 256), nn.Linear(256, 128), nn.Linear(128, 10))
+    assert model(T.randn([8, 784])).shape() == [8, 10] and len(model.parameters()) == 6
+
+
+@pytest.mark.parametrize("prec", ["fp32", "tf32"])
+def test_mlp_c4_forward_backward_vs_oracle(cd, prec):
+    """C4 through the drop-in API: Sequential(Linear(784,256), ReLU,
+    Linear(256,10)), batch 8192, Xavier-uniform weights, loss = sum(y * g)
+    so dY = g.  Every gradient is gated against fp64 closed forms."""
+    nn, T, init = cd.nn, cd.Tensor, cd.init
+    cd.set_matmul_precision(prec)
+    np.random.seed(7)
+    model = nn.Sequential(nn.Linear(784, 256), nn.ReLU(), nn.Linear(256, 10))
+    init.xavier_uniform_(model[0]._parameters["weight"])
+    init.xavier_uniform_(model[2]._parameters["weight"])
+    b1 = (np.random.randn(256) * 0.1).astype(np.float32)
+    b2 = (np.random.randn(10) * 0.1).astype(np.float32)
+    model[0]._parameters["bias"] = nn.Parameter(T.from_numpy(b1))
+    model[2]._parameters["bias"] = nn.Parameter(T.from_numpy(b2))
+    W1 = model[0]._parameters["weight"].numpy()
+    W2 = model[2]._parameters["weight"].numpy()
+    bound1 = np.sqrt(6.0 / (784 + 256))
+    assert np.abs(W1).max() <= bound1 and np.abs(W1).max() > 0.95 * bound1
+    x = np.random.randn(8192, 784).astype(np.float32)
+    g = np.random.randn(8192, 10).astype(np.float32)
+    say("C4 via cuDeep.nn", prec)
+    X = T.from_numpy(x, requires_grad=True)
+    y = model(X)
+    (y * T.from_numpy(g)).sum().backward()
+    # fp64 closed forms
+    z1 = x.astype(np.float64) @ W1.T.astype(np.float64) + b1
+    h = np.maximum(z1, 0)
+    y64 = h @ W2.T.astype(np.float64) + b2
+    dh = g.astype(np.float64) @ W2.astype(np.float64)
+    dz1 = dh * (z1 > 0)
+    want = {"y": y64, "dW2": g.T.astype(np.float64) @ h, "db2": g.sum(0),
+            "dW1": dz1.T @ x.astype(np.float64), "db1": dz1.sum(0),
+            "dX": dz1 @ W1.astype(np.float64)}
+    got = {"y": y.numpy(), "dW2": model[2]._parameters["weight"].grad.numpy(),
+           "db2": model[2]._parameters["bias"].grad.numpy(),
+           "dW1": model[0]._parameters["weight"].grad.numpy(),
+           "db1": model[0]._parameters["bias"].grad.numpy(), "dX": X.grad.numpy()}
+    # tolerance: 2x the fp32 seq-FMA error of the same product class (K up
+    # to 8192) -- a few 1e-6; TF32 mode (bf16x3) stays well inside 1e-4.
+    tol = 2e-5 if prec == "fp32" else 1e-4
+    for kname in want:
+        e = oracle.rel_fro(got[kname], want[kname])
+        print(f"C4 api {prec} {kname}: relFro {e:.2e}")
+        assert e < tol, kname
+
+
+# ---- nn.Conv2d (reference tests/unit/test_layers.py:58-75) -----------------
+
+def test_conv2d_layer_shapes(cd):
+    nn, T = cd.nn, cd.Tensor
+    say("conv shapes")
+    assert nn.Conv2d(3, 16, kernel_size=3, padding=1)(T.randn([2, 3, 8, 8])).shape() == [2, 16, 8, 8]
+    assert nn.Conv2d(1, 4, kernel_size=3)(T.randn([1, 1, 6, 6])).shape() == [1, 4, 4, 4]
+    assert nn.Conv2d(1, 1, kernel_size=3, stride=2, padding=1)(T.randn([1, 1, 8, 8])).shape() == [1, 1, 4, 4]
+
+
+@pytest.mark.parametrize("prec", ["fp32", "tf32"])
+def test_conv2d_layer_forward_backward_vs_oracle(cd, prec):
+    nn, T = cd.nn, cd.Tensor
+    cd.set_matmul_precision(prec)
+    rng = np.random.default_rng(3)
+    layer = nn.Conv2d(8, 12, kernel_size=3, stride=1, padding=1)
+    w = (rng.standard_normal((12, 8, 3, 3)) * np.sqrt(2 / 72)).astype(np.float32)
+    b = (rng.standard_normal(12) * 0.1).astype(np.float32)
+    layer._parameters["weight"] = nn.Parameter(T.from_numpy(w))
+    layer._parameters["bias"] = nn.Parameter(T.from_numpy(b))
+    x = rng.standard_normal((4, 8, 14, 14)).astype(np.float32)
+    g = rng.standard_normal((4, 12, 14, 14)).astype(np.float32)
+    say("conv layer", prec)
+    X = T.from_numpy(x, requires_grad=True)
+    y = layer(X)
+    (y * T.from_numpy(g)).sum().backward()
+    tol = 1e-5 if prec == "fp32" else 1e-4
+    assert oracle.rel_fro(y.numpy(), oracle.conv2d_direct64(x, w, b, (1, 1), (1, 1))) < tol
+    assert oracle.rel_fro(X.grad.numpy(),
+                          oracle.conv2d_backward_data64(g, w, x.shape, (1, 1), (1, 1))) < tol
+    assert oracle.rel_fro(layer._parameters["weight"].grad.numpy(),
+                          oracle.conv2d_backward_weight64(g, x, w.shape, (1, 1), (1, 1))) < tol
+    assert oracle.rel_fro(layer._parameters["bias"].grad.numpy(),
+                          g.astype(np.float64).sum(axis=(0, 2, 3))) < 1e-5
+
+
+def test_init_distributions(cd):
+    T, init = cd.Tensor, cd.init
+    say("init")
+    np.random.seed(0)
+    w = init.kaiming_normal_(T.zeros([64, 64, 3, 3]))
+    std = w.numpy().std()
+    assert abs(std - np.sqrt(2.0 / 576)) < 0.002     # He-normal, C5 weights
+    w = init.xavier_uniform_(T.zeros([256, 784])).numpy()
+    bound = np.sqrt(6.0 / (784 + 256))
+    assert np.abs(w).max() <= bound and abs(w.std() - bound / np.sqrt(3)) < 0.002
+    assert np.array_equal(init.constant_(T.zeros([3]), 2.5).numpy(), [2.5, 2.5, 2.5])
