@@ -111,8 +111,11 @@ def test_matmul_float64_and_transposed_views(cd):
     C64 = x.astype(np.float64) @ w.T.astype(np.float64)
     e_ref = oracle.rel_fro(oracle.sgemm_seqfma(x, w, transB=True), C64)
     assert oracle.rel_fro(got, C64) <= 2 * e_ref + 2.0 ** -24
-    got2 = T.from_numpy(w).t().matmul(T.from_numpy(x).t()).numpy()
+    got2 = T.from_numpy(w).matmul(T.from_numpy(x).t()).numpy()          # W x^T
     assert oracle.rel_fro(got2, C64.T) <= 2 * e_ref + 2.0 ** -24
+    xt = T.from_numpy(np.ascontiguousarray(x.T))                          # A as a view
+    got3 = xt.t().matmul(T.from_numpy(w).t()).numpy()
+    assert oracle.rel_fro(got3, C64) <= 2 * e_ref + 2.0 ** -24
 
 
 # ---- autograd (reference tests/unit/test_autograd.py) ----------------------
