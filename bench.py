@@ -245,6 +245,14 @@ def main():
         log("cpu:", cpu)
 
     achieved = 2.0 * 4096 ** 3 / (head["kernel_ms_mean"] * 1e-3) / 1e12
+    # HBM bytes per launch of the headline kernel, measured offline with two
+    # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a plain-copy
+    # calibration; see profiles/gemm_f32_4096_pmc_traffic.md.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_f32_4096_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = round(json.load(f)["traffic_bytes"])
     out = {
         "metric": "FP32 GEMM TFLOP/s at 4096^3 (+% of FP32 MFMA peak); TF32-mode TFLOP/s",
         "value": round(head["tflops"], 3),
@@ -263,7 +271,7 @@ def main():
         "pct_of_fp32_mfma_peak": round(100 * head["tflops"] / FP32_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": traffic},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -8,9 +8,10 @@
 // split once, while it is staged into LDS, into
 //     hi = bf16_rne(x),   lo = bf16_rne(x - hi)        (x - hi is exact)
 // and every product is formed as  hi*hi + hi*lo + lo*hi  with fp32
-// accumulation.  |x - hi - lo| <= 2^-16 |x|, and the dropped lo*lo term is
-// <= 2^-16 |ab|, so each product carries a relative error of at most about
-// 3 * 2^-16 ~= 4.6e-5 -- against ~1e-3 for TF32 operand truncation.
+// accumulation.  |x - hi| <= 2^-8 |x| and |x - hi - lo| <= 2^-17 |x|; the
+// dropped lo*lo term is <= 2^-16 |ab|, so each product carries a relative
+// error of at most 2^-15 ~= 3.1e-5 -- against up to ~2e-3 for TF32 operand
+// truncation.
 //
 // Structure: BM x BN output tile per workgroup; fp32 global loads into VGPRs
 // (double-buffered against the MFMAs of the current k-tile), split in

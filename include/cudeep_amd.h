@@ -56,7 +56,7 @@ extern "C" {
 #define CDX_BIAS_COL  2            /* C[m][n] += bias[n]  (Linear)            */
 
 #define CDX_PREC_FP32     0        /* true-FP32 MFMA (v_mfma_f32_16x16x4_f32) */
-#define CDX_PREC_TF32MODE 1        /* bf16x3 split MFMA, |rel err| <= ~3*2^-16 per product */
+#define CDX_PREC_TF32MODE 1        /* bf16x3 split MFMA, |rel err| <= 2^-15 per product */
 
 #define CDX_DTYPE_F32 0
 #define CDX_DTYPE_F64 1
