@@ -52,6 +52,18 @@ struct SplitLoader {
     static_assert(NB % NT == 0 || NB < NT, "tile not divisible by thread count");
     float4 v[NV][4];  // v[blk][q]: KCONTIG -> mn row q, 4 k;  else k row q, 4 mn
 
+    // 4x4 block -> (bc, br).  k-contiguous: consecutive threads walk k
+    // (bc), so a wavefront reads 128 contiguous bytes per row and its
+    // 8-byte LDS stores land on consecutive banks.  m/n-contiguous: the
+    // 8 k-blocks of a column group go to 8 consecutive threads (br fastest),
+    // so each global row is still read as 128 contiguous bytes (8 threads x
+    // 16 B) while the transposed LDS stores of 8 consecutive threads fill 16
+    // consecutive banks instead of striding 4 rows apart (an 8-way conflict).
+    __device__ __forceinline__ static void block_coords(int blk, int& bc, int& br) {
+        if (KCONTIG) { bc = blk % (BK / 4); br = blk / (BK / 4); }
+        else         { br = blk % (BK / 4); bc = blk / (BK / 4); }
+    }
+
     __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld,
                                          int64_t mn0, int64_t k0, int64_t mnmax,
                                          int64_t kmax, bool vec, int tid) {
@@ -59,10 +71,8 @@ struct SplitLoader {
         for (int b = 0; b < NV; ++b) {
             int blk = tid + b * NT;
             if (NB < NT && blk >= NB) break;
-            // blocks ordered so consecutive threads walk the contiguous dim
-            int bc, br;   // block index along contiguous / strided dimension
-            if (KCONTIG) { bc = blk % (BK / 4); br = blk / (BK / 4); }
-            else         { bc = blk % (BMN / 4); br = blk / (BMN / 4); }
+            int bc, br;   // block index along the contiguous / strided dimension
+            block_coords(blk, bc, br);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 int64_t gr, gc, rmax, cmax;
@@ -93,8 +103,7 @@ struct SplitLoader {
             int blk = tid + b * NT;
             if (NB < NT && blk >= NB) break;
             int bc, br;
-            if (KCONTIG) { bc = blk % (BK / 4); br = blk / (BK / 4); }
-            else         { bc = blk % (BMN / 4); br = blk / (BMN / 4); }
+            block_coords(blk, bc, br);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {       // r indexes mn within the block
                 float x[4];                     // 4 consecutive k at this mn
@@ -260,7 +269,17 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
             const int64_t n = bn + wn0 + jn * 16 + l16;
             if (n >= p.N) continue;
             int64_t col_off = n;
-            if (SPLITN) col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
+            if (SPLITN) {
+                // NCHW map; 32-bit quotient when it fits (a 64-bit divide is
+                // a long instruction sequence per output column)
+                if (p.N <= (int64_t)UINT32_MAX) {
+                    const uint32_t nn = (uint32_t)n, ns = (uint32_t)p.n_split;
+                    const uint32_t q = nn / ns;
+                    col_off = (int64_t)q * p.ldc_split + (int64_t)(nn - q * ns);
+                } else {
+                    col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
+                }
+            }
             float bias_n = 0.0f;
             if (p.bias_mode == CDX_BIAS_COL) bias_n = p.bias[n];
 #pragma unroll
@@ -321,14 +340,19 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 //  * Small: 64x64x32, 4 waves of 32x32, for small / narrow problems.
 //  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x32, 4 waves of
 //    32x32 (~108 logical TFLOP/s on 64 x 100352 x 576).
+//  * NarrowN / NarrowM: one dimension <= 16 (the MLP's 10-class layer).
 using CfgHuge = Cfg<256, 256, 32, 128, 64, 8>;
 using CfgLarge = Cfg<128, 128, 64, 32, 64, 8>;
 using CfgSkinnyM = Cfg<64, 64, 32, 32, 32, 1>;
 using CfgSmall = Cfg<64, 64, 32, 32, 32, 8>;
+using CfgNarrowN = Cfg<64, 16, 32, 16, 16, 8>;
+using CfgNarrowM = Cfg<16, 64, 32, 16, 16, 1>;
 
 }  // namespace
 
 int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream) {
+    if (g.N <= 16) return launch_ops<CfgNarrowN>(g, stream);
+    if (g.M <= 16) return launch_ops<CfgNarrowM>(g, stream);
     if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
     if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_ops<CfgHuge>(g, stream);
     if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge>(g, stream);

@@ -240,7 +240,17 @@ void gemm_f32_mfma_kernel(KParams p) {
             const int64_t n = bn + wn0 + jn * 16 + l16;
             if (n >= p.N) continue;
             int64_t col_off = n;
-            if (SPLITN) col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
+            if (SPLITN) {
+                // NCHW map; 32-bit quotient when it fits (a 64-bit divide is
+                // a long instruction sequence per output column)
+                if (p.N <= (int64_t)UINT32_MAX) {
+                    const uint32_t nn = (uint32_t)n, ns = (uint32_t)p.n_split;
+                    const uint32_t q = nn / ns;
+                    col_off = (int64_t)q * p.ldc_split + (int64_t)(nn - q * ns);
+                } else {
+                    col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
+                }
+            }
             float bias_n = 0.0f;
             if (p.bias_mode == CDX_BIAS_COL) bias_n = p.bias[n];
 #pragma unroll
@@ -308,13 +318,19 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
 //    64x64x16, 4 waves of 32x32 (~86 TFLOP/s on 64 x 100352 x 576, against
 //    49 with 64x256 tiles).
+//  * NarrowN / NarrowM: one operand dimension <= 16 (the MLP's 10-class
+//    layer and its gradients): 16-wide tiles instead of mostly-empty 64-wide.
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8>;
 using CfgMedium = Cfg<64, 64, 16, 16, 32, 8>;
 using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1>;
+using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8>;
+using CfgNarrowM = Cfg<16, 64, 16, 16, 16, 1>;
 
 }  // namespace
 
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
+    if (g.N <= 16) return launch_ops<CfgNarrowN>(g, stream);
+    if (g.M <= 16) return launch_ops<CfgNarrowM>(g, stream);
     if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
     // Large tiles once there are at least two per CU (256 CUs).
     int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);
