@@ -86,8 +86,13 @@ def bench_gemm(n, precision, steps, warmup, seed):
     A = torch.randn((n, n), device="cuda", generator=g)
     B = torch.randn((n, n), device="cuda", generator=g)
     C = torch.empty((n, n), device="cuda")
-    f = ops.sgemm if precision == cd.PREC_FP32 else ops.gemm_tf32mode
-    ms, per = time_launches(lambda: f(A, B, out=C), steps, warmup)
+    if precision == cd.PREC_FP32:
+        def f():
+            ops.sgemm(A, B, out=C)           # cdx_sgemm_f32
+    else:
+        def f():
+            ops.gemm(A, B, precision=precision, out=C)
+    ms, per = time_launches(f, steps, warmup)
     flops = 2.0 * n ** 3
     return {"n": n, "ms_per_step": ms, "kernel_ms_mean": statistics.mean(per),
             "kernel_ms_median": statistics.median(per),
@@ -231,6 +236,10 @@ def main():
             r["frac_of_bf16x3_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 3)
             extra[f"tf32mode_{n}"] = r
             log(f"tf32mode {n}^3:", r)
+        r = bench_gemm(4096, cd.PREC_TF32MODE4, args.steps, args.warmup, seed=3)
+        r["frac_of_bf16x4_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 4)
+        extra["tf32mode4_4096"] = r
+        log("tf32mode4 (bf16x4) 4096^3:", r)
         for prec, name in ((cd.PREC_FP32, "fp32"), (cd.PREC_TF32MODE, "tf32mode")):
             extra[f"mlp_c4_{name}"] = bench_mlp(args.steps, args.warmup, prec)
             log(f"mlp {name}:", extra[f"mlp_c4_{name}"])
@@ -269,6 +278,8 @@ def main():
         "config": {"workload": "C2: FP32 SGEMM C=A*B, M=N=K=4096, row-major, beta=0",
                    "M": 4096, "N": 4096, "K": 4096, "entry_point": "cdx_sgemm_f32"},
         "pct_of_fp32_mfma_peak": round(100 * head["tflops"] / FP32_PEAK_TFLOPS, 2),
+        "tf32mode_4096_tflops": (round(extra["tf32mode_4096"]["tflops"], 3)
+                                 if "tf32mode_4096" in extra else None),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                      "traffic": traffic},

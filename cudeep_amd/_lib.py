@@ -19,9 +19,9 @@ CDX_ERR_HIP = 3
 CDX_ERR_WORKSPACE = 4
 
 OP_N, OP_T = 0, 1
-EPI_NONE, EPI_RELU, EPI_GELU = 0, 1, 2
+EPI_NONE, EPI_RELU, EPI_GELU, EPI_SILU, EPI_SIGMOID = 0, 1, 2, 3, 4
 BIAS_NONE, BIAS_ROW, BIAS_COL = 0, 1, 2
-PREC_FP32, PREC_TF32MODE = 0, 1
+PREC_FP32, PREC_TF32MODE, PREC_TF32MODE4 = 0, 1, 2
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int

@@ -1,7 +1,7 @@
 // pybind11 module `_cudeep_core`: the Python surface of the reference's
 // src/bindings/module.cpp:75-981, restricted to the dense-contraction path
 // (Tensor + matmul, conv2d forward / backward, broadcast_add,
-// sum_reduce_rows, sum, relu / gelu / activation_backward, Stream / Event /
+// sum_reduce_rows, sum, relu / gelu / sigmoid / silu / activation_backward, Stream / Event /
 // MemoryPool, device_info), with the same names, argument names and
 // defaults, plus the entry points this build adds: linear_forward (one
 // fused GEMM for x W^T + b with an activation), matmul_ex (transposed
@@ -40,7 +40,9 @@ void require_f32(const Tensor& t, const char* fn) {
 kernels::ActivationType parse_act(const std::string& name) {
     if (name == "relu") return kernels::ActivationType::ReLU;
     if (name == "gelu") return kernels::ActivationType::GELU;
-    if (name == "sigmoid" || name == "tanh" || name == "silu" || name == "leaky_relu")
+    if (name == "silu") return kernels::ActivationType::SiLU;
+    if (name == "sigmoid") return kernels::ActivationType::Sigmoid;
+    if (name == "tanh" || name == "leaky_relu")
         throw std::runtime_error("activation '" + name + "' is not part of this build");
     throw std::runtime_error("Unknown activation: " + name);
 }
@@ -93,7 +95,9 @@ kernels::GemmEpilogue parse_epi(const std::string& a) {
     if (a == "none" || a.empty()) return kernels::GemmEpilogue::None;
     if (a == "relu") return kernels::GemmEpilogue::ReLU;
     if (a == "gelu") return kernels::GemmEpilogue::GELU;
-    throw std::runtime_error("linear_forward: activation must be none, relu or gelu");
+    if (a == "silu") return kernels::GemmEpilogue::SiLU;
+    if (a == "sigmoid") return kernels::GemmEpilogue::Sigmoid;
+    throw std::runtime_error("linear_forward: activation must be none, relu, gelu, silu or sigmoid");
 }
 
 int64_t leading_dim(const Tensor& t) {
@@ -193,6 +197,10 @@ PYBIND11_MODULE(_cudeep_core, m) {
     m.def("relu", [](const Tensor& t) { return activation(t, kernels::ActivationType::ReLU); },
           py::arg("input"));
     m.def("gelu", [](const Tensor& t) { return activation(t, kernels::ActivationType::GELU); },
+          py::arg("input"));
+    m.def("sigmoid", [](const Tensor& t) { return activation(t, kernels::ActivationType::Sigmoid); },
+          py::arg("input"));
+    m.def("silu", [](const Tensor& t) { return activation(t, kernels::ActivationType::SiLU); },
           py::arg("input"));
     m.def("activation_backward",
           [](const Tensor& grad_output, const Tensor& input, const std::string& act_name,
@@ -331,10 +339,14 @@ PYBIND11_MODULE(_cudeep_core, m) {
     m.def("set_matmul_precision", [](const std::string& p) {
         if (p == "fp32") kernels::set_matmul_precision(kernels::MatmulPrecision::FP32);
         else if (p == "tf32") kernels::set_matmul_precision(kernels::MatmulPrecision::TF32Mode);
-        else throw std::runtime_error("set_matmul_precision: 'fp32' or 'tf32'");
+        else if (p == "tf32x4") kernels::set_matmul_precision(kernels::MatmulPrecision::TF32Mode4);
+        else throw std::runtime_error("set_matmul_precision: 'fp32', 'tf32' or 'tf32x4'");
     }, py::arg("precision"));
     m.def("get_matmul_precision", []() {
-        return kernels::get_matmul_precision() == kernels::MatmulPrecision::FP32 ? "fp32" : "tf32";
+        const auto p = kernels::get_matmul_precision();
+        return p == kernels::MatmulPrecision::FP32        ? "fp32"
+               : p == kernels::MatmulPrecision::TF32Mode4 ? "tf32x4"
+                                                          : "tf32";
     });
 
     // ---- conv ----

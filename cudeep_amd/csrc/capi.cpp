@@ -52,10 +52,17 @@ int check_gemm(const char* fn, int opA, int opB, int64_t M, int64_t N, int64_t K
     return CDX_OK;
 }
 
+bool valid_precision(int p) {
+    return p == CDX_PREC_FP32 || p == CDX_PREC_TF32MODE || p == CDX_PREC_TF32MODE4;
+}
+
+bool valid_epilogue(int e) { return e >= CDX_EPI_NONE && e <= CDX_EPI_SIGMOID; }
+
 int run_gemm(int precision, cdx::GemmArgs g, hipStream_t stream) {
     if (g.M == 0 || g.N == 0) return CDX_OK;
     if (precision == CDX_PREC_FP32) return cdx::launch_gemm_f32(g, stream);
-    if (precision == CDX_PREC_TF32MODE) return cdx::launch_gemm_bf16x3(g, stream);
+    if (precision == CDX_PREC_TF32MODE) return cdx::launch_gemm_bf16x3(g, 3, stream);
+    if (precision == CDX_PREC_TF32MODE4) return cdx::launch_gemm_bf16x3(g, 4, stream);
     return set_error(CDX_ERR_INVALID_ARG, "gemm: unknown precision");
 }
 
@@ -110,13 +117,13 @@ int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K
                 const float* bias, int bias_mode, int epilogue, hipStream_t stream) {
     int st = check_gemm("cdx_gemm_ex", opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
     if (st) return st;
-    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+    if (!valid_precision(precision))
         return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad precision");
     if (bias_mode != CDX_BIAS_NONE && bias_mode != CDX_BIAS_ROW && bias_mode != CDX_BIAS_COL)
         return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad bias_mode");
     if (bias_mode != CDX_BIAS_NONE && !bias && M > 0 && N > 0)
         return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bias is NULL");
-    if (epilogue != CDX_EPI_NONE && epilogue != CDX_EPI_RELU && epilogue != CDX_EPI_GELU)
+    if (!valid_epilogue(epilogue))
         return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad epilogue");
     cdx::GemmArgs g{opA, opB, M, N, K, A, lda, B, ldb, C, ldc, 0, 0, bias, bias_mode, epilogue};
     return run_gemm(precision, g, stream);
@@ -170,7 +177,7 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight, const float*
     int st = check_conv("cdx_conv2d_forward_f32", batch, in_channels, out_channels, in_h, in_w,
                         kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w);
     if (st) return st;
-    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+    if (!valid_precision(precision))
         return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: bad precision");
     const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
     const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
@@ -293,7 +300,7 @@ int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight, 
     int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
                         stride_h, stride_w, pad_h, pad_w);
     if (st) return st;
-    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+    if (!valid_precision(precision))
         return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
     if (batch * in_channels * in_h * in_w == 0) return CDX_OK;
     if (!grad_input || (out_channels > 0 && (!grad_output || !weight)))
@@ -350,7 +357,7 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
     int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
                         stride_h, stride_w, pad_h, pad_w);
     if (st) return st;
-    if (precision != CDX_PREC_FP32 && precision != CDX_PREC_TF32MODE)
+    if (!valid_precision(precision))
         return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
     ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
                              stride_w, pad_h, pad_w);
@@ -460,8 +467,8 @@ template <typename T, typename Launch>
 static int act_impl(const char* fn, const T* input, T* output, int64_t n, int act,
                     hipStream_t stream, Launch launch) {
     if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad n");
-    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
-        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU or GELU");
+    if (act == CDX_EPI_NONE || !valid_epilogue(act))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU, GELU, SILU or SIGMOID");
     if (n == 0) return CDX_OK;
     if (!input || !output) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
     return launch(input, output, n, act, stream);
@@ -473,8 +480,8 @@ template <typename T, typename Launch>
 static int act_bwd_impl(const char* fn, const T* go, const T* input, T* gi, int64_t n, int act,
                         hipStream_t stream, Launch launch) {
     if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad n");
-    if (act != CDX_EPI_RELU && act != CDX_EPI_GELU)
-        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU or GELU");
+    if (act == CDX_EPI_NONE || !valid_epilogue(act))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU, GELU, SILU or SIGMOID");
     if (n == 0) return CDX_OK;
     if (!go || !input || !gi) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
     return launch(go, input, gi, n, act, stream);

@@ -41,7 +41,8 @@ struct GemmArgs {
 
 // Launchers (no argument validation: the C-ABI validates first).
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream);
-int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream);
+// terms = 3 (bf16x3: hi*hi + hi*lo + lo*hi) or 4 (adds lo*lo).
+int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream);
 int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
                  const double* A, int64_t lda, const double* B, int64_t ldb,
                  double* C, int64_t ldc, hipStream_t stream);
@@ -171,9 +172,33 @@ __device__ __forceinline__ double gelu_grad_f64(double x) {
     return s + 2.0 * x * s * one_minus_s * du;
 }
 
+__device__ __forceinline__ float exp_t(float x) { return expf(x); }
+__device__ __forceinline__ double exp_t(double x) { return exp(x); }
+
+// Sigmoid 1 / (1 + exp(-x)) and SiLU x * sigmoid(x) (the reference's
+// epilogue definitions, matmul_kernel.cu:1538-1550).  For x -> -inf,
+// exp(-x) overflows to inf and both go to (-)0 without a NaN.
+template <typename T>
+__device__ __forceinline__ T sigmoid_t(T x) { return T(1) / (T(1) + exp_t(-x)); }
+template <typename T>
+__device__ __forceinline__ T silu_t(T x) { return x / (T(1) + exp_t(-x)); }
+// sigmoid' = s (1 - s);  silu' = s + x s (1 - s), with 1 - s = 1 / (1 + e^x)
+// computed directly (no cancellation for large x).
+template <typename T>
+__device__ __forceinline__ T sigmoid_grad_t(T x) {
+    return T(1) / (T(1) + exp_t(-x)) * (T(1) / (T(1) + exp_t(x)));
+}
+template <typename T>
+__device__ __forceinline__ T silu_grad_t(T x) {
+    const T s = T(1) / (T(1) + exp_t(-x)), one_minus_s = T(1) / (T(1) + exp_t(x));
+    return s + x * s * one_minus_s;
+}
+
 __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == CDX_EPI_RELU) return v > 0.0f ? v : 0.0f;
     if (act == CDX_EPI_GELU) return gelu_f32(v);
+    if (act == CDX_EPI_SILU) return silu_t(v);
+    if (act == CDX_EPI_SIGMOID) return sigmoid_t(v);
     return v;
 }
 

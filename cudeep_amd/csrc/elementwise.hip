@@ -60,6 +60,8 @@ void bias_row_kernel(const T* __restrict__ m, const T* __restrict__ row,
 __device__ __forceinline__ double apply_act(double v, int act) {
     if (act == CDX_EPI_RELU) return v > 0.0 ? v : 0.0;
     if (act == CDX_EPI_GELU) return gelu_f64(v);
+    if (act == CDX_EPI_SILU) return silu_t(v);
+    if (act == CDX_EPI_SIGMOID) return sigmoid_t(v);
     return v;
 }
 
@@ -74,6 +76,14 @@ void act_fwd_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, int a
 __device__ __forceinline__ float gelu_grad(float v) { return gelu_grad_f32(v); }
 __device__ __forceinline__ double gelu_grad(double v) { return gelu_grad_f64(v); }
 
+// d act / dx at the pre-activation input x (ReLU: the mask x > 0)
+template <typename T>
+__device__ __forceinline__ T act_grad(T x, int act) {
+    if (act == CDX_EPI_GELU) return gelu_grad(x);
+    if (act == CDX_EPI_SILU) return silu_grad_t(x);
+    return sigmoid_grad_t(x);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256)
 void act_bwd_kernel(const T* __restrict__ go, const T* __restrict__ x,
@@ -81,7 +91,7 @@ void act_bwd_kernel(const T* __restrict__ go, const T* __restrict__ x,
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
         const T v = x[i];
-        gi[i] = act == CDX_EPI_RELU ? (v > T(0) ? go[i] : T(0)) : go[i] * gelu_grad(v);
+        gi[i] = act == CDX_EPI_RELU ? (v > T(0) ? go[i] : T(0)) : go[i] * act_grad(v, act);
     }
 }
 

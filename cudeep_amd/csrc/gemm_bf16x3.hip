@@ -11,7 +11,10 @@
 // accumulation.  |x - hi| <= 2^-8 |x| and |x - hi - lo| <= 2^-17 |x|; the
 // dropped lo*lo term is <= 2^-16 |ab|, so each product carries a relative
 // error of at most 2^-15 ~= 3.1e-5 -- against up to ~2e-3 for TF32 operand
-// truncation.
+// truncation.  The four-term variant (TERMS = 4) adds lo*lo: then only the
+// split residual remains (<= 2^-16 per product), and operands with at most
+// 16 significant bits -- TF32-rounded inputs among them -- multiply exactly,
+// leaving fp32 accumulation as the only error.
 //
 // Structure: BM x BN output tile per workgroup; fp32 global loads into VGPRs
 // (double-buffered against the MFMAs of the current k-tile), split in
@@ -133,10 +136,14 @@ struct SplitLoader {
     }
 };
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_>
+// ALIGNED_ONLY: the configuration is only instantiated without bounds
+// checks (its checked variant would not fit the register file); the
+// dispatcher sends it aligned problems only.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_, bool ALIGNED_ONLY_ = false>
 struct Cfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int GROUP_M = GROUP_M_;
+    static constexpr bool ALIGNED_ONLY = ALIGNED_ONLY_;
     static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
     static constexpr int NT = WAVES_M * WAVES_N * 64;
     static constexpr int FM = WM / 16, FN = WN / 16;
@@ -156,7 +163,7 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int grou
     tn = in_g / gsize;
 }
 
-template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN>
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS>
 __global__ __launch_bounds__(CF::NT)
 void gemm_bf16x3_kernel(KParams p, int vec) {
     constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
@@ -240,6 +247,33 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
                 bh[j] = *reinterpret_cast<const bf16x8*>(sBh + off);
                 bl[j] = *reinterpret_cast<const bf16x8*>(sBl + off);
             }
+            if (TERMS == 4) {
+                // Two-level accumulation: the four products of this 32-k
+                // step (small terms first) are summed from zero, so the
+                // MFMA's internal roundings act on a 32-term partial sum
+                // and only the one add below rounds at the size of C.  One
+                // row of tiles at a time keeps the partials to FN registers.
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    floatx4 t[FN];
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            al[i], bl[j], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], t[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], t[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], t[j], 0, 0, 0);
+                        acc[i][j] += t[j];
+                    }
+                }
+                continue;
+            }
             // small cross terms first, then the dominant hi*hi term
 #pragma unroll
             for (int i = 0; i < FM; ++i)
@@ -296,16 +330,16 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     }
 }
 
-template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN>
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS>
 int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
-    hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN>),
+    hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN, TERMS>),
                        dim3((unsigned)tiles, (unsigned)splits), dim3(CF::NT), 0, stream, kp, vec);
     return hip_error(hipGetLastError(), "gemm_bf16x3_kernel launch");
 }
 
-template <class CF, int OPA, int OPB>
+template <class CF, int OPA, int OPB, int TERMS>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
@@ -315,21 +349,25 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned)
-        return split ? launch_cfg<CF, OPA, OPB, false, true>(kp, 1, splits, stream)
-                     : launch_cfg<CF, OPA, OPB, false, false>(kp, 1, splits, stream);
-    return split ? launch_cfg<CF, OPA, OPB, true, true>(kp, vec, splits, stream)
-                 : launch_cfg<CF, OPA, OPB, true, false>(kp, vec, splits, stream);
+        return split ? launch_cfg<CF, OPA, OPB, false, true, TERMS>(kp, 1, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, false, false, TERMS>(kp, 1, splits, stream);
+    if constexpr (CF::ALIGNED_ONLY) {
+        return set_error(CDX_ERR_UNSUPPORTED, "gemm_bf16x3: unaligned problem sent to an aligned-only tile");
+    } else {
+        return split ? launch_cfg<CF, OPA, OPB, true, true, TERMS>(kp, vec, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, true, false, TERMS>(kp, vec, splits, stream);
+    }
 }
 
-template <class CF>
+template <class CF, int TERMS = 3>
 int launch_ops(const GemmArgs& g0, hipStream_t stream) {
     const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
     return with_splitk(g0, tiles, CF::BK, stream,
                        [&](const GemmArgs& g, int splits, int64_t k_chunk) {
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, splits, k_chunk, stream);
-        return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N, TERMS>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T, TERMS>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N, TERMS>(g, splits, k_chunk, stream);
+        return launch_mode<CF, CDX_OP_T, CDX_OP_T, TERMS>(g, splits, k_chunk, stream);
     });
 }
 
@@ -337,26 +375,42 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 //  * Huge: 256x256x32, 8 waves of 128x64; 160 KiB of LDS (one workgroup
 //    per CU); ~366 logical TFLOP/s at 4096^3.
 //  * Large: 128x128x64, 8 waves of 32x64; ~215 at 2048^3.
-//  * Small: 64x64x32, 4 waves of 32x32, for small / narrow problems.
+//  * Small: 64x64x64, 4 waves of 32x32, for small / narrow problems.  The
+//    deeper k-tile halves the k-iterations of short-K problems, which are
+//    bound by per-iteration latency (8192 x 256 x 784: 48 us against 76
+//    with BK = 32); 16-wide tiles for N or M <= 16 measured no faster.
 //  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x32, 4 waves of
 //    32x32 (~108 logical TFLOP/s on 64 x 100352 x 576).
-//  * NarrowN / NarrowM: one dimension <= 16 (the MLP's 10-class layer).
-using CfgHuge = Cfg<256, 256, 32, 128, 64, 8>;
+using CfgHuge = Cfg<256, 256, 32, 128, 64, 8, true>;
 using CfgLarge = Cfg<128, 128, 64, 32, 64, 8>;
 using CfgSkinnyM = Cfg<64, 64, 32, 32, 32, 1>;
-using CfgSmall = Cfg<64, 64, 32, 32, 32, 8>;
-using CfgNarrowN = Cfg<64, 16, 32, 16, 16, 8>;
-using CfgNarrowM = Cfg<16, 64, 32, 16, 16, 1>;
+using CfgSmall = Cfg<64, 64, 64, 32, 32, 8>;
+
+// True when launch_mode would run CF without bounds checks (no split-K).
+template <class CF>
+bool aligned_for(const GemmArgs& g) {
+    return ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
+           g.ldb % 4 == 0 && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
+           g.K % CF::BK == 0;
+}
+
+template <int TERMS>
+int dispatch(const GemmArgs& g, hipStream_t stream) {
+    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM, TERMS>(g, stream);
+    // Huge holds 128 accumulators per lane: only its unchecked three-term
+    // form fits in 256 registers without spilling.
+    if constexpr (TERMS == 3) {
+        if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<CfgHuge>(g))
+            return launch_ops<CfgHuge, TERMS>(g, stream);
+    }
+    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge, TERMS>(g, stream);
+    return launch_ops<CfgSmall, TERMS>(g, stream);
+}
 
 }  // namespace
 
-int launch_gemm_bf16x3(const GemmArgs& g, hipStream_t stream) {
-    if (g.N <= 16) return launch_ops<CfgNarrowN>(g, stream);
-    if (g.M <= 16) return launch_ops<CfgNarrowM>(g, stream);
-    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
-    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256) return launch_ops<CfgHuge>(g, stream);
-    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge>(g, stream);
-    return launch_ops<CfgSmall>(g, stream);
+int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream) {
+    return terms == 4 ? dispatch<4>(g, stream) : dispatch<3>(g, stream);
 }
 
 }  // namespace cdx

@@ -318,19 +318,18 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
 //    64x64x16, 4 waves of 32x32 (~86 TFLOP/s on 64 x 100352 x 576, against
 //    49 with 64x256 tiles).
-//  * NarrowN / NarrowM: one operand dimension <= 16 (the MLP's 10-class
-//    layer and its gradients): 16-wide tiles instead of mostly-empty 64-wide.
+//  * NarrowN: N <= 16 (the MLP's 10-class layer): 64x16 tiles instead of
+//    mostly-empty 64x64 ones (8192 x 10 x 256: 10.8 us against 14.6).  A
+//    16-row tile for M <= 16 measured no faster than Medium.
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8>;
 using CfgMedium = Cfg<64, 64, 16, 16, 32, 8>;
 using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1>;
 using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8>;
-using CfgNarrowM = Cfg<16, 64, 16, 16, 16, 1>;
 
 }  // namespace
 
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
     if (g.N <= 16) return launch_ops<CfgNarrowN>(g, stream);
-    if (g.M <= 16) return launch_ops<CfgNarrowM>(g, stream);
     if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
     // Large tiles once there are at least two per CU (256 CUs).
     int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);

@@ -31,24 +31,33 @@ int epi_code(GemmEpilogue e) {
         case GemmEpilogue::None: return CDX_EPI_NONE;
         case GemmEpilogue::ReLU: return CDX_EPI_RELU;
         case GemmEpilogue::GELU: return CDX_EPI_GELU;
-        default: throw std::runtime_error("GEMM epilogue not supported by this build (ReLU/GELU only)");
+        case GemmEpilogue::SiLU: return CDX_EPI_SILU;
+        case GemmEpilogue::Sigmoid: return CDX_EPI_SIGMOID;
     }
+    throw std::runtime_error("unknown GEMM epilogue");
 }
 
 int act_code(ActivationType a) {
     if (a == ActivationType::ReLU) return CDX_EPI_RELU;
     if (a == ActivationType::GELU) return CDX_EPI_GELU;
-    throw std::runtime_error("activation not supported by this build (ReLU/GELU only)");
+    if (a == ActivationType::SiLU) return CDX_EPI_SILU;
+    if (a == ActivationType::Sigmoid) return CDX_EPI_SIGMOID;
+    throw std::runtime_error("activation not supported by this build (ReLU, GELU, SiLU, Sigmoid)");
 }
 
 }  // namespace
 
 void set_matmul_precision(MatmulPrecision p) {
-    g_precision = p == MatmulPrecision::FP32 ? CDX_PREC_FP32 : CDX_PREC_TF32MODE;
+    g_precision = p == MatmulPrecision::FP32       ? CDX_PREC_FP32
+                  : p == MatmulPrecision::TF32Mode4 ? CDX_PREC_TF32MODE4
+                                                    : CDX_PREC_TF32MODE;
 }
 
 MatmulPrecision get_matmul_precision() {
-    return g_precision.load() == CDX_PREC_FP32 ? MatmulPrecision::FP32 : MatmulPrecision::TF32Mode;
+    const int p = g_precision.load();
+    return p == CDX_PREC_FP32        ? MatmulPrecision::FP32
+           : p == CDX_PREC_TF32MODE4 ? MatmulPrecision::TF32Mode4
+                                     : MatmulPrecision::TF32Mode;
 }
 
 void launch_matmul_ex(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,

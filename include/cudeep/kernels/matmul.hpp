@@ -18,7 +18,10 @@
 namespace cudeep {
 namespace kernels {
 
-enum class MatmulPrecision { FP32, TF32Mode };
+// FP32: true-FP32 MFMA.  TF32Mode: bf16x3 split MFMA (per-product relative
+// error <= 2^-15).  TF32Mode4: bf16x4 (<= 2^-16; exact products for
+// TF32-rounded operands).
+enum class MatmulPrecision { FP32, TF32Mode, TF32Mode4 };
 
 // Process-wide precision of launch_matmul_kernel<float> and everything
 // built on it (Tensor::matmul, conv, Linear).  Default: TF32Mode.
@@ -41,7 +44,6 @@ void launch_matmul_tiled_kernel(const T* A, const T* B, T* C, int M, int N, int 
 
 enum class GemmEpilogue { None, ReLU, GELU, SiLU, Sigmoid };
 
-// SiLU / Sigmoid epilogues are not part of this build and throw.
 void launch_matmul_fused_act(const float* A, const float* B, float* C, int M, int N, int K,
                              GemmEpilogue epilogue, hipStream_t stream = nullptr);
 

@@ -45,18 +45,25 @@ extern "C" {
 #define CDX_OP_N 0                 /* use the operand as stored             */
 #define CDX_OP_T 1                 /* use its transpose                     */
 
-/* Epilogues; values follow cudeep::kernels::GemmEpilogue
- * (include/cudeep/kernels/matmul.cuh:32-38) for the ones implemented. */
-#define CDX_EPI_NONE 0
-#define CDX_EPI_RELU 1
-#define CDX_EPI_GELU 2
+/* Epilogues / activations; values follow cudeep::kernels::GemmEpilogue
+ * (include/cudeep/kernels/matmul.cuh:32-38).  GELU is the tanh form,
+ * SiLU = x * sigmoid(x), Sigmoid = 1 / (1 + exp(-x))
+ * (src/kernels/matmul_kernel.cu:1538-1550). */
+#define CDX_EPI_NONE    0
+#define CDX_EPI_RELU    1
+#define CDX_EPI_GELU    2
+#define CDX_EPI_SILU    3
+#define CDX_EPI_SIGMOID 4
 
 #define CDX_BIAS_NONE 0
 #define CDX_BIAS_ROW  1            /* C[m][n] += bias[m]  (conv: per channel) */
 #define CDX_BIAS_COL  2            /* C[m][n] += bias[n]  (Linear)            */
 
-#define CDX_PREC_FP32     0        /* true-FP32 MFMA (v_mfma_f32_16x16x4_f32) */
-#define CDX_PREC_TF32MODE 1        /* bf16x3 split MFMA, |rel err| <= 2^-15 per product */
+#define CDX_PREC_FP32      0       /* true-FP32 MFMA (v_mfma_f32_16x16x4_f32) */
+#define CDX_PREC_TF32MODE  1       /* bf16x3 split MFMA, |rel err| <= 2^-15 per product */
+#define CDX_PREC_TF32MODE4 2       /* bf16x4 split MFMA, |rel err| <= 2^-16 per product;
+                                      exact products for operands of <= 16 significant
+                                      bits (TF32-rounded inputs) */
 
 #define CDX_DTYPE_F32 0
 #define CDX_DTYPE_F64 1
@@ -225,10 +232,11 @@ int cdx_sum_reduce_rows_f64(const double* input, double* output,
                             void* workspace, size_t workspace_bytes,
                             hipStream_t stream);
 
-/* ReLU / GELU forward and backward (act = CDX_EPI_RELU or CDX_EPI_GELU).
- * Replace launch_activation_forward_kernel / launch_activation_backward_kernel
- * for those two activations (include/cudeep/kernels/activation.cuh:17-31,
- * src/kernels/activation_kernel.cu:19-52, :256-319). */
+/* Activation forward and backward, act = CDX_EPI_RELU, _GELU, _SILU or
+ * _SIGMOID.  Replace launch_activation_forward_kernel /
+ * launch_activation_backward_kernel for those activations
+ * (include/cudeep/kernels/activation.cuh:17-31,
+ * src/kernels/activation_kernel.cu:19-66, :206-330). */
 int cdx_activation_forward_f32(const float* input, float* output, int64_t n,
                                int act, hipStream_t stream);
 int cdx_activation_backward_f32(const float* grad_output, const float* input,

@@ -321,6 +321,46 @@ def relu_grad(x):
     return (np.asarray(x) > 0).astype(np.float64)
 
 
+def sigmoid(x):
+    """1 / (1 + exp(-x)) in fp64 (reference act_sigmoid,
+    src/kernels/activation_kernel.cu:24-31; GEMM epilogue
+    src/kernels/matmul_kernel.cu:1541).  Evaluated as exp(min(x,0)) /
+    (1 + exp(-|x|)) so neither tail overflows."""
+    x = np.asarray(x, dtype=np.float64)
+    e = np.exp(-np.abs(x))
+    return np.where(x >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+
+
+def sigmoid_grad(x):
+    """s (1 - s) (reference backward, activation_kernel.cu:268-274)."""
+    s = sigmoid(x)
+    return s * sigmoid(-np.asarray(x, dtype=np.float64))
+
+
+def silu(x):
+    """x * sigmoid(x) (reference act_silu, activation_kernel.cu:55-62)."""
+    x = np.asarray(x, dtype=np.float64)
+    return x * sigmoid(x)
+
+
+def silu_grad(x):
+    """s (1 + x (1 - s)) (reference backward, activation_kernel.cu:297-303)."""
+    x = np.asarray(x, dtype=np.float64)
+    s = sigmoid(x)
+    return s * (1.0 + x * sigmoid(-x))
+
+
+def activation(x, name):
+    """Forward activation by name: relu / gelu / silu / sigmoid."""
+    return {"relu": relu, "gelu": gelu, "silu": silu, "sigmoid": sigmoid}[name](x)
+
+
+def activation_grad(x, name):
+    """d activation / dx at the pre-activation input x."""
+    return {"relu": relu_grad, "gelu": gelu_grad, "silu": silu_grad,
+            "sigmoid": sigmoid_grad}[name](x)
+
+
 def rel_fro(C, Cref) -> float:
     """Relative Frobenius error ||C - Cref||_F / ||Cref||_F (in fp64)."""
     C = np.asarray(C, dtype=np.float64)

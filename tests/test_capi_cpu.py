@@ -53,8 +53,9 @@ def test_gemm_argument_validation():
         == L.CDX_ERR_INVALID_ARG          # lda < K
     assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, None, 4, fake, 4, fake, 4, None, 0, 0, None) \
         == L.CDX_ERR_INVALID_ARG          # NULL A
-    assert _status("cdx_gemm_ex", 9, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 0, None) \
-        == L.CDX_ERR_INVALID_ARG          # precision
+    for prec in (9, 3, -1):
+        assert _status("cdx_gemm_ex", prec, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 0,
+                       None) == L.CDX_ERR_INVALID_ARG          # precision
     assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 2, 0, None) \
         == L.CDX_ERR_INVALID_ARG          # bias mode without bias
     assert _status("cdx_gemm_ex", 0, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4, None, 0, 5, None) \
@@ -82,6 +83,9 @@ def test_conv_argument_validation():
         == 576 * 32 * 56 * 56 * 4
     assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 32 * 256 * 8  # fp64-sized
     assert _status("cdx_activation_forward_f32", fake, fake, 4, 0, None) == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_activation_forward_f32", fake, fake, 4, 5, None) == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_activation_backward_f64", fake, fake, fake, 4, 5, None) \
+        == L.CDX_ERR_INVALID_ARG
     assert _status("cdx_sum_reduce_rows_f32", None, fake, 4, 4, None, 0, None) \
         == L.CDX_ERR_INVALID_ARG
 

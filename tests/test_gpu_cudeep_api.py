@@ -76,7 +76,7 @@ def test_memory_pool_and_events(cd):
 
 # ---- matmul (reference tests/unit/test_tensor_ops.py:210-262) --------------
 
-@pytest.mark.parametrize("prec", ["tf32", "fp32"])
+@pytest.mark.parametrize("prec", ["tf32", "fp32", "tf32x4"])
 def test_matmul_reference_cases(cd, prec):
     cd.set_matmul_precision(prec)
     T = cd.Tensor
@@ -95,6 +95,29 @@ def test_matmul_reference_cases(cd, prec):
     b = np.random.randn(128, 32).astype(np.float32)
     np.testing.assert_allclose((T.from_numpy(a) @ T.from_numpy(b)).numpy(), a @ b, rtol=1e-3,
                                atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_core_activations_vs_oracle(cd, dtype):
+    """_cudeep_core relu / gelu / sigmoid / silu and activation_backward
+    (reference module.cpp:185-207, :837-872) against the fp64 oracle."""
+    from cudeep_amd.cuDeep import _core
+    x = np.linspace(-12, 12, 4099).astype(dtype)
+    go = np.random.default_rng(3).standard_normal(x.shape).astype(dtype)
+    # fp64: the oracle's GELU is the reference's 0.5 x (1 + tanh(u)), whose
+    # 1 + tanh(u) cancels for x << 0 (absolute error ~ |x| 2^-53), so the
+    # gate is a few 1e-12 against the 1e-3 floor
+    tol = 2e-6 if dtype == np.float32 else 5e-12
+    for name in ("relu", "gelu", "sigmoid", "silu"):
+        say("core activation", name, dtype.__name__)
+        y = getattr(_core, name)(_core.Tensor.from_numpy(x)).numpy()
+        want = oracle.activation(x, name)
+        assert y.dtype == dtype
+        assert np.max(np.abs(y - want) / np.maximum(np.abs(want), 1e-3)) < tol, name
+        g = _core.activation_backward(_core.Tensor.from_numpy(go), _core.Tensor.from_numpy(x),
+                                      name).numpy()
+        wg = go * oracle.activation_grad(x, name)
+        assert np.max(np.abs(g - wg)) < 5 * tol * max(1.0, np.abs(wg).max()), name
 
 
 def test_matmul_float64_and_transposed_views(cd):

@@ -40,16 +40,25 @@ def _ref_errors(A, B, tA=False, tB=False, rows=None):
 # reference known answers (tests/golden/kats.json)
 # ---------------------------------------------------------------------------
 
+def _gemm_fn(mode):
+    """NN GEMM entry for a precision mode name."""
+    import cudeep_amd as cd
+    if mode == "fp32":
+        return ops().sgemm
+    if mode == "tf32":
+        return ops().gemm_tf32mode
+    return lambda A, B: ops().gemm(A, B, precision=cd.PREC_TF32MODE4)
+
+
 @pytest.mark.parametrize("name", ["matmul_2x2", "matmul_diag_identity", "mma_identity",
                                   "mma_integer_pattern"])
-@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+@pytest.mark.parametrize("mode", ["fp32", "tf32", "tf32x4"])
 def test_gemm_kats_exact(kats, name, mode):
     k = kats[name]
     A = np.array(k["A"], np.float32)
     B = np.array(k["B"], np.float32)
     say("kat", name, mode)
-    f = ops().sgemm if mode == "fp32" else ops().gemm_tf32mode
-    C = host(f(dev(A), dev(B)))
+    C = host(_gemm_fn(mode)(dev(A), dev(B)))
     assert np.array_equal(C, np.array(k["C"], np.float32))
 
 
@@ -75,15 +84,14 @@ def test_randn_times_identity_rtol_1e5():
         assert np.allclose(C, A, rtol=1e-5, atol=0)
 
 
-@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+@pytest.mark.parametrize("mode", ["fp32", "tf32", "tf32x4"])
 def test_integer_inputs_exact_any_shape(mode):
     rng = np.random.default_rng(22)
     for (M, N, K) in [(16, 8, 8), (130, 70, 200), (256, 256, 64)]:
         A = rng.integers(-8, 9, (M, K)).astype(np.float32)
         B = rng.integers(-8, 9, (K, N)).astype(np.float32)
         say("integer", mode, M, N, K)
-        f = ops().sgemm if mode == "fp32" else ops().gemm_tf32mode
-        assert np.array_equal(host(f(dev(A), dev(B))), A.astype(np.float64) @ B)
+        assert np.array_equal(host(_gemm_fn(mode)(dev(A), dev(B))), A.astype(np.float64) @ B)
 
 
 # ---------------------------------------------------------------------------
@@ -150,31 +158,68 @@ def test_fp32_c2_4096_sampled_rows_and_checksum():
 
 
 @pytest.mark.parametrize("n", [2048, 4096])
-def test_tf32mode_c3(n):
-    """C3: TF32 mode at 2048^3 / 4096^3, inputs N(0,1): raw fp32 (the bits
-    the reference feeds its MMA) and pre-rounded to TF32 (RNE)."""
+@pytest.mark.parametrize("terms", [3, 4])
+def test_tf32mode_c3(n, terms):
+    """C3: TF32 mode (bf16x3 / bf16x4) at 2048^3 / 4096^3, inputs N(0,1),
+    read as raw fp32 (the bits the reference feeds its MMA): the error must
+    not exceed the emulated reference TF32 error under either operand
+    rounding (RZ / RNE)."""
+    import cudeep_amd as cd
     rng = np.random.default_rng(303 + n)
     A = normal(rng, (n, n))
     B = normal(rng, (n, n))
-    say("C3 tf32mode", n)
-    C = host(ops().gemm_tf32mode(dev(A), dev(B)))
+    say("C3 tf32mode raw", n, terms)
+    prec = cd.PREC_TF32MODE if terms == 3 else cd.PREC_TF32MODE4
+    C = host(ops().gemm(dev(A), dev(B), precision=prec))
     rows = (n // 2, n // 2 + 96)
     C64 = oracle.dgemm(A, B, rows=rows)
     e = oracle.rel_fro(C[rows[0]:rows[1]], C64)
     e_rz = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rz", rows=rows), C64)
     e_rne = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rne", rows=rows), C64)
-    print(f"C3 n={n} raw: bf16x3={e:.3e} tf32(rz)={e_rz:.3e} tf32(rne)={e_rne:.3e}")
+    print(f"C3 n={n} raw: bf16x{terms}={e:.3e} tf32(rz)={e_rz:.3e} tf32(rne)={e_rne:.3e}")
     assert e <= min(e_rz, e_rne)
     assert _checksum_identity(A, B, C) < 1e-4
 
 
-def test_tf32mode_parity_shapes():
+@pytest.mark.parametrize("n", [2048, 4096])
+def test_tf32mode_c3_prerounded(n):
+    """C3 under the second reading: operands pre-rounded to TF32 (RNE), so
+    the reference's TF32 products are exact and its error is fp32
+    accumulation only.  bf16x4 splits such operands exactly (hi + lo has 16
+    significant bits) and sums each 32-k step from zero before one add into
+    C, so its error must not exceed the emulated reference's (an ideal MMA:
+    exact 8-term chunks, one fp32 rounding each).  bf16x3 drops lo*lo, which is at most
+    2^-18 |a b| here (|lo| <= 2^-9 |x|), so per element its error is bounded
+    by 2^-18 sum_k |a_ik b_kj| on top of accumulation."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(313 + n)
+    A = oracle.tf32_round(normal(rng, (n, n)), "rne")
+    B = oracle.tf32_round(normal(rng, (n, n)), "rne")
+    rows = (n // 3, n // 3 + 96)
+    C64 = oracle.dgemm(A, B, rows=rows)
+    e_ref = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rne", rows=rows), C64)
+    absAB = np.abs(A[rows[0]:rows[1]]).astype(np.float64) @ np.abs(B).astype(np.float64)
+    bound3 = 2.0 ** -18 * np.linalg.norm(absAB) / np.linalg.norm(C64) + 2 * e_ref
+    res = {}
+    for terms, prec in ((3, cd.PREC_TF32MODE), (4, cd.PREC_TF32MODE4)):
+        say("C3 tf32mode pre-rounded", n, terms)
+        C = host(ops().gemm(dev(A), dev(B), precision=prec))
+        res[terms] = oracle.rel_fro(C[rows[0]:rows[1]], C64)
+    print(f"C3 n={n} pre-rounded: bf16x3={res[3]:.3e} bf16x4={res[4]:.3e} "
+          f"tf32 ideal={e_ref:.3e} bf16x3 bound={bound3:.3e}")
+    assert res[4] <= e_ref
+    assert res[3] <= bound3
+
+
+@pytest.mark.parametrize("mode", ["tf32", "tf32x4"])
+def test_tf32mode_parity_shapes(mode):
     rng = np.random.default_rng(304)
-    for (M, N, K) in [(17, 33, 65), (300, 200, 784), (8192, 10, 256), (64, 1000, 576)]:
+    for (M, N, K) in [(17, 33, 65), (300, 200, 784), (8192, 10, 256), (64, 1000, 576),
+                      (8192, 256, 784), (10, 256, 8192)]:
         A = normal(rng, (M, K))
         B = normal(rng, (K, N))
-        say("tf32 shape", M, N, K)
-        C = host(ops().gemm_tf32mode(dev(A), dev(B)))
+        say("tf32 shape", mode, M, N, K)
+        C = host(_gemm_fn(mode)(dev(A), dev(B)))
         C64 = oracle.dgemm(A, B)
         e = oracle.rel_fro(C, C64)
         e_rne = oracle.rel_fro(oracle.gemm_tf32emu(A, B, "rne"), C64)
@@ -182,14 +227,15 @@ def test_tf32mode_parity_shapes():
 
 
 @pytest.mark.parametrize("tA,tB", [(False, True), (True, False), (True, True)])
-def test_tf32mode_transposes(tA, tB):
+@pytest.mark.parametrize("prec_name", ["PREC_TF32MODE", "PREC_TF32MODE4"])
+def test_tf32mode_transposes(tA, tB, prec_name):
     import cudeep_amd as cd
     rng = np.random.default_rng(305)
     M, N, K = 200, 300, 500
     A = normal(rng, (K, M) if tA else (M, K))
     B = normal(rng, (N, K) if tB else (K, N))
-    say("tf32 transposes", tA, tB)
-    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, precision=cd.PREC_TF32MODE))
+    say("tf32 transposes", tA, tB, prec_name)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, precision=getattr(cd, prec_name)))
     C64 = oracle.dgemm(A, B, tA, tB)
     opA = A.T if tA else A
     opB = B.T if tB else B
@@ -202,8 +248,8 @@ def test_tf32mode_transposes(tA, tB):
 # fused epilogues (bias per row / column, ReLU, GELU)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("mode", ["fp32", "tf32"])
-@pytest.mark.parametrize("epi", ["none", "relu", "gelu"])
+@pytest.mark.parametrize("mode", ["fp32", "tf32", "tf32x4"])
+@pytest.mark.parametrize("epi", ["none", "relu", "gelu", "silu", "sigmoid"])
 @pytest.mark.parametrize("bias_mode", ["none", "row", "col"])
 def test_fused_epilogue(mode, epi, bias_mode):
     import cudeep_amd as cd
@@ -213,8 +259,9 @@ def test_fused_epilogue(mode, epi, bias_mode):
     B = normal(rng, (K, N))
     bias = normal(rng, (M if bias_mode == "row" else N,))
     bm = {"none": cd.BIAS_NONE, "row": cd.BIAS_ROW, "col": cd.BIAS_COL}[bias_mode]
-    ep = {"none": cd.EPI_NONE, "relu": cd.EPI_RELU, "gelu": cd.EPI_GELU}[epi]
-    prec = cd.PREC_FP32 if mode == "fp32" else cd.PREC_TF32MODE
+    ep = {"none": cd.EPI_NONE, "relu": cd.EPI_RELU, "gelu": cd.EPI_GELU,
+          "silu": cd.EPI_SILU, "sigmoid": cd.EPI_SIGMOID}[epi]
+    prec = {"fp32": cd.PREC_FP32, "tf32": cd.PREC_TF32MODE, "tf32x4": cd.PREC_TF32MODE4}[mode]
     say("epilogue", mode, epi, bias_mode)
     C = host(ops().gemm(dev(A), dev(B), precision=prec, bias=dev(bias) if bm else None,
                         bias_mode=bm, epilogue=ep))
@@ -223,7 +270,7 @@ def test_fused_epilogue(mode, epi, bias_mode):
         Z = Z + bias[:, None]
     elif bias_mode == "col":
         Z = Z + bias[None, :]
-    want = {"none": Z, "relu": oracle.relu(Z), "gelu": oracle.gelu(Z)}[epi]
+    want = Z if epi == "none" else oracle.activation(Z, epi)
     scale = np.abs(Z).max()
     # GEMM error (<= ~1e-6 relative) plus the epilogue's own few-ulp error
     assert np.max(np.abs(C - want)) <= 2e-5 * scale + 1e-6
@@ -297,14 +344,14 @@ def test_leading_dimension_views():
 @pytest.mark.parametrize("M,N,K,tA", [(64, 64, 8192, False), (100, 50, 5000, False),
                                       (256, 784, 8192, True), (10, 256, 8192, True),
                                       (33, 17, 3001, True)])
-@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+@pytest.mark.parametrize("mode", ["fp32", "tf32", "tf32x4"])
 def test_split_k_parity(M, N, K, tA, mode):
     import cudeep_amd as cd
     rng = np.random.default_rng(M + N + K)
     A = normal(rng, (K, M) if tA else (M, K))
     B = normal(rng, (K, N))
     bias = normal(rng, (N,))
-    prec = cd.PREC_FP32 if mode == "fp32" else cd.PREC_TF32MODE
+    prec = {"fp32": cd.PREC_FP32, "tf32": cd.PREC_TF32MODE, "tf32x4": cd.PREC_TF32MODE4}[mode]
     say("split-K", mode, M, N, K, tA)
     C = host(ops().gemm(dev(A), dev(B), transA=tA, precision=prec, bias=dev(bias),
                         bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU))

@@ -154,10 +154,11 @@ def test_sum_reduce_rows(rows, cols):
         assert oracle.rel_fro(got, want) <= 2 * e_ref + 2.0 ** -24
 
 
-@pytest.mark.parametrize("act", ["relu", "gelu"])
+@pytest.mark.parametrize("act", ["relu", "gelu", "silu", "sigmoid"])
 def test_activations(act):
     import cudeep_amd as cd
-    a = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU}[act]
+    a = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU, "silu": cd.EPI_SILU,
+         "sigmoid": cd.EPI_SIGMOID}[act]
     x = np.linspace(-8, 8, 100003).astype(np.float32)
     go = np.random.default_rng(9).standard_normal(x.shape).astype(np.float32)
     say("activation", act)
@@ -167,9 +168,9 @@ def test_activations(act):
         assert np.array_equal(y, np.maximum(x, 0))
         assert np.array_equal(g, np.where(x > 0, go, 0).astype(np.float32))
     else:
-        want = oracle.gelu(x)
+        want = oracle.activation(x, act)
         assert np.max(np.abs(y - want) / np.maximum(np.abs(want), 1e-3)) < 2e-6
-        wg = go * oracle.gelu_grad(x)
+        wg = go * oracle.activation_grad(x, act)
         assert np.max(np.abs(g - wg)) < 1e-5 * max(1.0, np.abs(wg).max())
 
 

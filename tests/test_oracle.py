@@ -284,6 +284,28 @@ def test_gelu_against_torch_and_derivative():
     assert np.array_equal(oracle.relu_grad(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 1.0])
 
 
+def test_sigmoid_silu_against_tanh_torch_and_derivative():
+    """sigmoid against scipy's expit and, away from the cancelling tail, the
+    closed form (1 + tanh(x/2)) / 2; SiLU against torch's silu; both
+    derivatives against central differences; the tails stay finite."""
+    torch = pytest.importorskip("torch")
+    special = pytest.importorskip("scipy.special")
+    x = np.linspace(-30, 30, 2001)
+    assert np.allclose(oracle.sigmoid(x), special.expit(x), rtol=1e-14, atol=0)
+    xm = x[x > -8]
+    assert np.allclose(oracle.sigmoid(xm), 0.5 * (1.0 + np.tanh(0.5 * xm)), rtol=1e-11, atol=0)
+    assert oracle.sigmoid(np.array([0.0]))[0] == 0.5
+    assert np.allclose(oracle.silu(x), torch.nn.functional.silu(torch.from_numpy(x)).numpy(),
+                       rtol=1e-13, atol=1e-300)
+    h = 1e-6
+    for f, g in ((oracle.sigmoid, oracle.sigmoid_grad), (oracle.silu, oracle.silu_grad)):
+        num = (f(x + h) - f(x - h)) / (2 * h)
+        assert np.allclose(g(x), num, atol=1e-8)
+    big = np.array([-1000.0, 1000.0])
+    assert np.all(np.isfinite(oracle.sigmoid(big))) and np.all(np.isfinite(oracle.silu_grad(big)))
+    assert np.array_equal(oracle.sigmoid(big), [0.0, 1.0])
+
+
 # ---------------------------------------------------------------------------
 # col2im and the backward-conv routes (conv_kernel.cu:344-545)
 # ---------------------------------------------------------------------------
