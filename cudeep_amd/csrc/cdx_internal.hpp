@@ -202,4 +202,78 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     return v;
 }
 
+template <int ACT>
+__device__ __forceinline__ float act_fixed(float v) {
+    if constexpr (ACT == CDX_EPI_RELU) return v > 0.0f ? v : 0.0f;
+    if constexpr (ACT == CDX_EPI_GELU) return gelu_f32(v);
+    if constexpr (ACT == CDX_EPI_SILU) return silu_t(v);
+    if constexpr (ACT == CDX_EPI_SIGMOID) return sigmoid_t(v);
+    return v;
+}
+
+// Where a GEMM's output element (m, n) goes, with the bias and activation
+// of the epilogue (see GemmArgs for the output map).
+struct EpiArgs {
+    float* C; int64_t ldc, M, N, n_split, ldc_split;
+    const float* bias; int bias_mode, epilogue;
+};
+
+// Writes one wave's FM x FN grid of 16 x 16 MFMA accumulator tiles (D
+// layout of v_mfma_f32_16x16x*: register r of lane l is row 4 (l / 16) + r,
+// column l % 16), whose top-left element is (m0, n0).  The activation is a
+// template parameter so the per-element code is straight-line; CHECK adds
+// the M / N bounds tests that ragged tiles need.
+template <int FM, int FN, bool CHECK, bool SPLITN, int ACT>
+__device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], const EpiArgs& e,
+                                              int64_t m0, int64_t n0, int lane) {
+    const int l16 = lane & 15, lq = lane >> 4;
+    const bool bias_col = e.bias_mode == CDX_BIAS_COL, bias_row = e.bias_mode == CDX_BIAS_ROW;
+    int64_t col_off[FN];
+    float bcol[FN];
+#pragma unroll
+    for (int jn = 0; jn < FN; ++jn) {
+        const int64_t n = n0 + jn * 16 + l16;
+        col_off[jn] = n;
+        if (SPLITN) {
+            // NCHW map; 32-bit quotient when it fits (a 64-bit divide is a
+            // long instruction sequence)
+            if (e.N <= (int64_t)UINT32_MAX) {
+                const uint32_t nn = (uint32_t)n, ns = (uint32_t)e.n_split;
+                const uint32_t q = nn / ns;
+                col_off[jn] = (int64_t)q * e.ldc_split + (int64_t)(nn - q * ns);
+            } else {
+                col_off[jn] = (n / e.n_split) * e.ldc_split + (n % e.n_split);
+            }
+        }
+        bcol[jn] = (bias_col && (!CHECK || n < e.N)) ? e.bias[n] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = m0 + i * 16 + 4 * lq + r;
+            if (CHECK && m >= e.M) continue;
+            const float brow = bias_row ? e.bias[m] : 0.0f;
+            float* crow = e.C + m * e.ldc;
+#pragma unroll
+            for (int jn = 0; jn < FN; ++jn) {
+                if (CHECK && n0 + jn * 16 + l16 >= e.N) continue;
+                crow[col_off[jn]] = act_fixed<ACT>(acc[i][jn][r] + bcol[jn] + brow);
+            }
+        }
+    }
+}
+
+template <int FM, int FN, bool CHECK, bool SPLITN>
+__device__ __forceinline__ void write_acc(const floatx4 (&acc)[FM][FN], const EpiArgs& e,
+                                          int64_t m0, int64_t n0, int lane) {
+    switch (e.epilogue) {
+        case CDX_EPI_RELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_RELU>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_GELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_GELU>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_SILU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_SILU>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_SIGMOID: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_SIGMOID>(acc, e, m0, n0, lane); break;
+        default: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_NONE>(acc, e, m0, n0, lane); break;
+    }
+}
+
 }  // namespace cdx

@@ -139,11 +139,15 @@ struct SplitLoader {
 // ALIGNED_ONLY: the configuration is only instantiated without bounds
 // checks (its checked variant would not fit the register file); the
 // dispatcher sends it aligned problems only.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_, bool ALIGNED_ONLY_ = false>
+// PIPE: 1 = one register staging set, last k-tile peeled; 2 = two staging
+// sets (load k+2 while splitting k+1) with MFMA / VALU interleave hints.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_, bool ALIGNED_ONLY_ = false,
+          int PIPE_ = 1>
 struct Cfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int GROUP_M = GROUP_M_;
     static constexpr bool ALIGNED_ONLY = ALIGNED_ONLY_;
+    static constexpr int PIPE = PIPE_;
     static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
     static constexpr int NT = WAVES_M * WAVES_N * 64;
     static constexpr int FM = WM / 16, FN = WN / 16;
@@ -198,17 +202,19 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     }
     const bool v = vec != 0;
 
-    SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK> la;
-    SplitLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK> lb;
+    using LoaderA = SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>;
+    using LoaderB = SplitLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK>;
+    LoaderA la;
+    LoaderB lb;
 
-    auto load_tiles = [&](int64_t k0) {
-        la.load(p.A, p.lda, bm, k0, p.M, p.K, v, tid);
-        lb.load(p.B, p.ldb, bn, k0, p.N, p.K, v, tid);
+    auto load_into = [&](LoaderA& a, LoaderB& b, int64_t k0) {
+        a.load(p.A, p.lda, bm, k0, p.M, p.K, v, tid);
+        b.load(p.B, p.ldb, bn, k0, p.N, p.K, v, tid);
     };
-    auto store_tiles = [&](int buf) {
+    auto store_from = [&](const LoaderA& a, const LoaderB& b, int buf) {
         unsigned short* s = lds + buf * STAGE;
-        la.template store<STRIDE>(s, s + A_PLANE, tid);
-        lb.template store<STRIDE>(s + 2 * A_PLANE, s + 2 * A_PLANE + B_PLANE, tid);
+        a.template store<STRIDE>(s, s + A_PLANE, tid);
+        b.template store<STRIDE>(s + 2 * A_PLANE, s + 2 * A_PLANE + B_PLANE, tid);
     };
 
     floatx4 acc[FM][FN];
@@ -217,16 +223,8 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t nk = ceil_div(p.K, BK);
-    load_tiles(0);
-    store_tiles(0);
-    __syncthreads();
-
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int buf = (int)(kt & 1);
-        const bool has_next = kt + 1 < nk;
-        if (has_next) load_tiles((kt + 1) * BK);
-
+    // MFMAs over the k-tile held in LDS stage `buf`
+    auto compute = [&](int buf) {
         const unsigned short* s = lds + buf * STAGE;
         const unsigned short* sAh = s;
         const unsigned short* sAl = s + A_PLANE;
@@ -291,43 +289,81 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
         }
+    };
 
-        if (has_next) store_tiles(buf ^ 1);
+    const int64_t nk = ceil_div(p.K, BK);
+    // the two-set pipeline only where it fits the register file unchecked
+    constexpr int PIPE = (CF::PIPE == 2 && !CHECK && TERMS == 3) ? 2 : 1;
+    if (PIPE == 2 && nk >= 2) {
+        // Two register staging sets: tile k+2 is loaded while tile k+1 is
+        // split and stored from the set loaded one iteration earlier, so
+        // the split never waits on global memory; the scheduling hints
+        // interleave that VALU / LDS-write work with the MFMAs.
+        LoaderA la1;
+        LoaderB lb1;
+        auto hints = [&]() {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
+            }
+        };
+        load_into(la, lb, 0);
+        load_into(la1, lb1, BK);
+        store_from(la, lb, 0);
         __syncthreads();
+        int64_t kt = 0;
+        // loop invariant (kt even): stage 0 holds tile kt, set 1 tile kt+1
+        for (; kt + 3 < nk; kt += 2) {
+            load_into(la, lb, (kt + 2) * BK);
+            compute(0);
+            store_from(la1, lb1, 1);
+            hints();
+            __syncthreads();
+            load_into(la1, lb1, (kt + 3) * BK);
+            compute(1);
+            store_from(la, lb, 0);
+            hints();
+            __syncthreads();
+        }
+        if (kt + 2 < nk) {            // three tiles left
+            load_into(la, lb, (kt + 2) * BK);
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            compute(1);
+            store_from(la, lb, 0);
+            __syncthreads();
+            compute(0);
+        } else {                      // two tiles left
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            compute(1);
+        }
+    } else if (nk > 0) {
+        // One staging set, one barrier per k-tile; the last tile is peeled
+        // so the loop body has no branch around the load / store.
+        load_into(la, lb, 0);
+        store_from(la, lb, 0);
+        __syncthreads();
+        int64_t kt = 0;
+        for (; kt + 1 < nk; ++kt) {
+            const int buf = (int)(kt & 1);
+            load_into(la, lb, (kt + 1) * BK);
+            compute(buf);
+            store_from(la, lb, buf ^ 1);
+            __syncthreads();
+        }
+        compute((int)(kt & 1));
     }
 
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int jn = 0; jn < FN; ++jn) {
-            const int64_t n = bn + wn0 + jn * 16 + l16;
-            if (n >= p.N) continue;
-            int64_t col_off = n;
-            if (SPLITN) {
-                // NCHW map; 32-bit quotient when it fits (a 64-bit divide is
-                // a long instruction sequence per output column)
-                if (p.N <= (int64_t)UINT32_MAX) {
-                    const uint32_t nn = (uint32_t)n, ns = (uint32_t)p.n_split;
-                    const uint32_t q = nn / ns;
-                    col_off = (int64_t)q * p.ldc_split + (int64_t)(nn - q * ns);
-                } else {
-                    col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
-                }
-            }
-            float bias_n = 0.0f;
-            if (p.bias_mode == CDX_BIAS_COL) bias_n = p.bias[n];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t m = bm + wm0 + i * 16 + 4 * lq + r;
-                if (m >= p.M) continue;
-                float val = acc[i][jn][r];
-                if (p.bias_mode == CDX_BIAS_COL) val += bias_n;
-                else if (p.bias_mode == CDX_BIAS_ROW) val += p.bias[m];
-                val = apply_act(val, p.epilogue);
-                p.C[m * p.ldc + col_off] = val;
-            }
-        }
-    }
+    // epilogue: bias, activation and the output map, straight from the
+    // accumulators
+    const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
+                      p.bias, p.bias_mode, p.epilogue};
+    write_acc<FM, FN, CHECK, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
 }
 
 template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS>
@@ -382,7 +418,7 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 //  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x32, 4 waves of
 //    32x32 (~108 logical TFLOP/s on 64 x 100352 x 576).
 using CfgHuge = Cfg<256, 256, 32, 128, 64, 8, true>;
-using CfgLarge = Cfg<128, 128, 64, 32, 64, 8>;
+using CfgLarge = Cfg<128, 128, 64, 32, 64, 8, false, 2>;
 using CfgSkinnyM = Cfg<64, 64, 32, 32, 32, 1>;
 using CfgSmall = Cfg<64, 64, 64, 32, 32, 8>;
 

@@ -231,40 +231,11 @@ void gemm_f32_mfma_kernel(KParams p) {
         __syncthreads();
     }
 
-    // Epilogue.  MFMA 16x16 output layout: register r of lane l holds
-    // row 4*(l/16) + r, column l%16 of the block.
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int jn = 0; jn < FN; ++jn) {
-            const int64_t n = bn + wn0 + jn * 16 + l16;
-            if (n >= p.N) continue;
-            int64_t col_off = n;
-            if (SPLITN) {
-                // NCHW map; 32-bit quotient when it fits (a 64-bit divide is
-                // a long instruction sequence per output column)
-                if (p.N <= (int64_t)UINT32_MAX) {
-                    const uint32_t nn = (uint32_t)n, ns = (uint32_t)p.n_split;
-                    const uint32_t q = nn / ns;
-                    col_off = (int64_t)q * p.ldc_split + (int64_t)(nn - q * ns);
-                } else {
-                    col_off = (n / p.n_split) * p.ldc_split + (n % p.n_split);
-                }
-            }
-            float bias_n = 0.0f;
-            if (p.bias_mode == CDX_BIAS_COL) bias_n = p.bias[n];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t m = bm + wm0 + i * 16 + 4 * lq + r;
-                if (m >= p.M) continue;
-                float v = acc[i][jn][r];
-                if (p.bias_mode == CDX_BIAS_COL) v += bias_n;
-                else if (p.bias_mode == CDX_BIAS_ROW) v += p.bias[m];
-                v = apply_act(v, p.epilogue);
-                p.C[m * p.ldc + col_off] = v;
-            }
-        }
-    }
+    // epilogue: bias, activation and the output map, straight from the
+    // accumulators
+    const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
+                      p.bias, p.bias_mode, p.epilogue};
+    write_acc<FM, FN, MODE != kLoadAlignedVec, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
 }
 
 template <class CF, int OPA, int OPB, int MODE, bool SPLITN>
