@@ -409,18 +409,21 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 
 // Tile configurations (measured on MI355X, NN):
 //  * Huge: 256x256x32, 8 waves of 128x64; 160 KiB of LDS (one workgroup
-//    per CU); ~366 logical TFLOP/s at 4096^3.
-//  * Large: 128x128x64, 8 waves of 32x64; ~215 at 2048^3.
+//    per CU); one staging set (two do not fit 256 registers); ~410-430
+//    logical TFLOP/s at 4096^3 in a back-to-back loop.
+//  * Large: 128x128x64, 8 waves of 32x64, two staging sets; ~260 at 2048^3
+//    (one set: ~237).
 //  * Small: 64x64x64, 4 waves of 32x32, for small / narrow problems.  The
 //    deeper k-tile halves the k-iterations of short-K problems, which are
-//    bound by per-iteration latency (8192 x 256 x 784: 48 us against 76
+//    bound by per-iteration latency (8192 x 256 x 784: 30 us against 75
 //    with BK = 32); 16-wide tiles for N or M <= 16 measured no faster.
-//  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x32, 4 waves of
-//    32x32 (~108 logical TFLOP/s on 64 x 100352 x 576).
+//  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x64, 4 waves of
+//    32x32, two staging sets (64 x 100352 x 576: 68 us = 109 logical
+//    TFLOP/s, against 76 with BK = 32 and one set).
 using CfgHuge = Cfg<256, 256, 32, 128, 64, 8, true>;
 using CfgLarge = Cfg<128, 128, 64, 32, 64, 8, false, 2>;
-using CfgSkinnyM = Cfg<64, 64, 32, 32, 32, 1>;
-using CfgSmall = Cfg<64, 64, 64, 32, 32, 8>;
+using CfgSkinnyM = Cfg<64, 64, 64, 32, 32, 1, false, 2>;
+using CfgSmall = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
 
 // True when launch_mode would run CF without bounds checks (no split-K).
 template <class CF>

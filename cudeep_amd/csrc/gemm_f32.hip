@@ -92,10 +92,13 @@ struct TileLoader {
     }
 };
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_>
+// PIPE: 1 = one register staging set; 2 = two sets (tile k+2 loads while
+// tile k+1 is written to LDS).
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_, int PIPE_ = 1>
 struct Cfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr int GROUP_M = GROUP_M_;
+    static constexpr int PIPE = PIPE_;
     static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
     static constexpr int NT = WAVES_M * WAVES_N * 64;
     static constexpr int FM = WM / 16, FN = WN / 16;
@@ -161,17 +164,17 @@ void gemm_f32_mfma_kernel(KParams p) {
     LA la;
     LB lb;
 
-    auto load_tiles = [&](int64_t k0) {
-        if (OPA == CDX_OP_N) la.load(p.A, p.lda, bm, k0, p.M, p.K, tid);
-        else                 la.load(p.A, p.lda, k0, bm, p.K, p.M, tid);
-        if (OPB == CDX_OP_N) lb.load(p.B, p.ldb, k0, bn, p.K, p.N, tid);
-        else                 lb.load(p.B, p.ldb, bn, k0, p.N, p.K, tid);
+    auto load_into = [&](LA& a, LB& b, int64_t k0) {
+        if (OPA == CDX_OP_N) a.load(p.A, p.lda, bm, k0, p.M, p.K, tid);
+        else                 a.load(p.A, p.lda, k0, bm, p.K, p.M, tid);
+        if (OPB == CDX_OP_N) b.load(p.B, p.ldb, k0, bn, p.K, p.N, tid);
+        else                 b.load(p.B, p.ldb, bn, k0, p.N, p.K, tid);
     };
-    auto store_tiles = [&](int buf) {
+    auto store_from = [&](const LA& a, const LB& b, int buf) {
         float* sA = lds + buf * (A_ELEMS + B_ELEMS);
         float* sB = sA + A_ELEMS;
-        la.template store<A_STRIDE>(sA, tid);
-        lb.template store<B_STRIDE>(sB, tid);
+        a.template store<A_STRIDE>(sA, tid);
+        b.template store<B_STRIDE>(sB, tid);
     };
 
     floatx4 acc[FM][FN];
@@ -180,16 +183,8 @@ void gemm_f32_mfma_kernel(KParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t nk = ceil_div(p.K, BK);
-    load_tiles(0);
-    store_tiles(0);
-    __syncthreads();
-
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        const int buf = (int)(kt & 1);
-        const bool has_next = kt + 1 < nk;
-        if (has_next) load_tiles((kt + 1) * BK);
-
+    // MFMAs over the k-tile held in LDS stage `buf`
+    auto compute = [&](int buf) {
         const float* sA = lds + buf * (A_ELEMS + B_ELEMS);
         const float* sB = sA + A_ELEMS;
 #pragma unroll
@@ -226,9 +221,59 @@ void gemm_f32_mfma_kernel(KParams p) {
                         acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[jn][j],
                                                                          acc[i][jn], 0, 0, 0);
         }
+    };
 
-        if (has_next) store_tiles(buf ^ 1);
+    const int64_t nk = ceil_div(p.K, BK);
+    if (CF::PIPE == 2 && nk >= 2) {
+        // Two register staging sets: tile k+2 is loaded while tile k+1 is
+        // written to LDS from the set loaded one iteration earlier, so the
+        // LDS stores never wait on global memory.
+        LA la1;
+        LB lb1;
+        load_into(la, lb, 0);
+        load_into(la1, lb1, BK);
+        store_from(la, lb, 0);
         __syncthreads();
+        int64_t kt = 0;
+        // loop invariant (kt even): stage 0 holds tile kt, set 1 tile kt+1
+        for (; kt + 3 < nk; kt += 2) {
+            load_into(la, lb, (kt + 2) * BK);
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            load_into(la1, lb1, (kt + 3) * BK);
+            compute(1);
+            store_from(la, lb, 0);
+            __syncthreads();
+        }
+        if (kt + 2 < nk) {            // three tiles left
+            load_into(la, lb, (kt + 2) * BK);
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            compute(1);
+            store_from(la, lb, 0);
+            __syncthreads();
+            compute(0);
+        } else {                      // two tiles left
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            compute(1);
+        }
+    } else {
+        // One staging set: tile k+1 is in flight during the MFMAs of tile k.
+        load_into(la, lb, 0);
+        store_from(la, lb, 0);
+        __syncthreads();
+        for (int64_t kt = 0; kt < nk; ++kt) {
+            const int buf = (int)(kt & 1);
+            const bool has_next = kt + 1 < nk;
+            if (has_next) load_into(la, lb, (kt + 1) * BK);
+            compute(buf);
+            if (has_next) store_from(la, lb, buf ^ 1);
+            __syncthreads();
+        }
     }
 
     // epilogue: bias, activation and the output map, straight from the
@@ -281,21 +326,23 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
     });
 }
 
-// Tile configurations (chosen by measurement on MI355X; 4096^3 NN):
+// Tile configurations (chosen by measurement on MI355X; 4096^3 NN).  All use
+// the two-set register pipeline, which measured 4-12 % faster everywhere
+// (4096^3: 138 against 133 TFLOP/s; 2048^3: 130 against 114).
 //  * Large: 128x128x16, 8 waves of 32x64 -> 2 waves per SIMD, 64 fp32
-//    accumulators per lane; ~132 TFLOP/s at 4096^3, ~112 at 2048^3.
+//    accumulators per lane.
 //  * Medium: 64x64x16, 8 waves of 16x32, for problems with too few large
 //    tiles to fill 256 CUs (~67 TFLOP/s at 1024^3 vs 27 with Large).
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
-//    64x64x16, 4 waves of 32x32 (~86 TFLOP/s on 64 x 100352 x 576, against
+//    64x64x16, 4 waves of 32x32 (~85 TFLOP/s on 64 x 100352 x 576, against
 //    49 with 64x256 tiles).
 //  * NarrowN: N <= 16 (the MLP's 10-class layer): 64x16 tiles instead of
-//    mostly-empty 64x64 ones (8192 x 10 x 256: 10.8 us against 14.6).  A
+//    mostly-empty 64x64 ones (8192 x 10 x 256: 9.8 us against 13.4).  A
 //    16-row tile for M <= 16 measured no faster than Medium.
-using CfgLarge = Cfg<128, 128, 16, 32, 64, 8>;
-using CfgMedium = Cfg<64, 64, 16, 16, 32, 8>;
-using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1>;
-using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8>;
+using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
+using CfgMedium = Cfg<64, 64, 16, 16, 32, 8, 2>;
+using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1, 2>;
+using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8, 2>;
 
 }  // namespace
 
