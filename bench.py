@@ -100,6 +100,22 @@ def bench_gemm(n, precision, steps, warmup, seed):
             "tflops_kernel_median": flops / (statistics.median(per) * 1e-3) / 1e12}
 
 
+def bench_gemm16(n, dtype, steps, warmup, seed):
+    """16-bit-operand GEMM (cdx_gemm16_ex): fp16 / bf16 A, B, fp32 C."""
+    import torch
+    import cudeep_amd.ops as ops
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    td = torch.float16 if dtype == "f16" else torch.bfloat16
+    A = torch.randn((n, n), device="cuda", generator=g).to(td)
+    B = torch.randn((n, n), device="cuda", generator=g).to(td)
+    C = torch.empty((n, n), device="cuda")
+    ms, per = time_launches(lambda: ops.gemm16(A, B, out=C), steps, warmup)
+    flops = 2.0 * n ** 3
+    return {"n": n, "ms_per_step": ms, "kernel_ms_median": statistics.median(per),
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "frac_of_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+
+
 def bench_mlp(steps, warmup, precision):
     """C4: 784 -> 256 -> 10, batch 8192: fused forward (bias+ReLU epilogue)
     and backward GEMMs (dX, dW per layer) + bias-grad column sums."""
@@ -240,6 +256,10 @@ def main():
         r["frac_of_bf16x4_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 4)
         extra["tf32mode4_4096"] = r
         log("tf32mode4 (bf16x4) 4096^3:", r)
+        for dt in ("f16", "bf16"):
+            r = bench_gemm16(4096, dt, args.steps, args.warmup, seed=6)
+            extra[f"{dt}_gemm_4096"] = r
+            log(f"{dt} GEMM 4096^3:", r)
         for prec, name in ((cd.PREC_FP32, "fp32"), (cd.PREC_TF32MODE, "tf32mode")):
             extra[f"mlp_c4_{name}"] = bench_mlp(args.steps, args.warmup, prec)
             log(f"mlp {name}:", extra[f"mlp_c4_{name}"])

@@ -37,6 +37,9 @@ SIGNATURES = {
     "cdx_gemm_ex": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                            _vp, _i64, _vp, _int, _int, _vp]),
     "cdx_matmul_fused_act": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "cdx_hgemm_f16": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "cdx_gemm16_ex": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
+                             _vp, _i64, _vp, _int, _int, _vp]),
     "cdx_dgemm": (_int, [_int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "cdx_im2col_f32": (_int, [_vp, _vp] + [_i64] * 10 + [_vp]),
     "cdx_conv2d_forward_workspace_size": (_sz, [_i64] * 10),
@@ -64,7 +67,7 @@ SIGNATURES = {
     "cdx_activation_backward_f64": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
 }
 
-DTYPE_F32, DTYPE_F64 = 0, 1
+DTYPE_F32, DTYPE_F64, DTYPE_F16, DTYPE_BF16 = 0, 1, 2, 3
 BINARY_ADD, BINARY_SUB, BINARY_MUL = 0, 1, 2
 
 _lib = None

@@ -129,6 +129,30 @@ int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K
     return run_gemm(precision, g, stream);
 }
 
+int cdx_gemm16_ex(int in_dtype, int opA, int opB, int64_t M, int64_t N, int64_t K,
+                  const void* A, int64_t lda, const void* B, int64_t ldb, float* C, int64_t ldc,
+                  const float* bias, int bias_mode, int epilogue, hipStream_t stream) {
+    int st = check_gemm("cdx_gemm16_ex", opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
+    if (st) return st;
+    if (in_dtype != CDX_DTYPE_F16 && in_dtype != CDX_DTYPE_BF16)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm16_ex: in_dtype must be F16 or BF16");
+    if (bias_mode != CDX_BIAS_NONE && bias_mode != CDX_BIAS_ROW && bias_mode != CDX_BIAS_COL)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm16_ex: bad bias_mode");
+    if (bias_mode != CDX_BIAS_NONE && !bias && M > 0 && N > 0)
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm16_ex: bias is NULL");
+    if (!valid_epilogue(epilogue))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm16_ex: bad epilogue");
+    if (M == 0 || N == 0) return CDX_OK;
+    cdx::GemmArgs g{opA, opB, M, N, K, A, lda, B, ldb, C, ldc, 0, 0, bias, bias_mode, epilogue};
+    return cdx::launch_gemm_16(g, in_dtype, stream);
+}
+
+int cdx_hgemm_f16(const void* A, const void* B, float* C, int64_t M, int64_t N, int64_t K,
+                  hipStream_t stream) {
+    return cdx_gemm16_ex(CDX_DTYPE_F16, CDX_OP_N, CDX_OP_N, M, N, K, A, K > 1 ? K : 1, B,
+                         N > 1 ? N : 1, C, N, nullptr, CDX_BIAS_NONE, CDX_EPI_NONE, stream);
+}
+
 int cdx_matmul_fused_act(const float* A, const float* B, float* C, int64_t M, int64_t N,
                          int64_t K, int epilogue, hipStream_t stream) {
     return cdx_gemm_ex(CDX_PREC_TF32MODE, CDX_OP_N, CDX_OP_N, M, N, K, A, K > 1 ? K : 1, B,

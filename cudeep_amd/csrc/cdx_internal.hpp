@@ -28,11 +28,12 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 //   addr(m, n) = m * ldc + (n / n_split) * ldc_split + (n % n_split)
 // n_split = 0 means the plain row-major map addr = m * ldc + n.  The split
 // map writes the conv GEMM's [OC, B*S] result straight into NCHW.
+// A and B point at fp32 elements, or at 16-bit ones for launch_gemm_16.
 struct GemmArgs {
     int opA, opB;
     int64_t M, N, K;
-    const float* A; int64_t lda;
-    const float* B; int64_t ldb;
+    const void* A; int64_t lda;
+    const void* B; int64_t ldb;
     float* C; int64_t ldc;
     int64_t n_split, ldc_split;
     const float* bias; int bias_mode;   // CDX_BIAS_*
@@ -43,6 +44,8 @@ struct GemmArgs {
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream);
 // terms = 3 (bf16x3: hi*hi + hi*lo + lo*hi) or 4 (adds lo*lo).
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream);
+// 16-bit operands (in_dtype CDX_DTYPE_F16 or CDX_DTYPE_BF16), fp32 accumulation and C.
+int launch_gemm_16(const GemmArgs& g, int in_dtype, hipStream_t stream);
 int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
                  const double* A, int64_t lda, const double* B, int64_t ldb,
                  double* C, int64_t ldc, hipStream_t stream);

@@ -22,14 +22,29 @@
 // so every MFMA operand is one 16-byte LDS read (8 consecutive k).
 // m/n-contiguous operands are transposed in registers on the way in (each
 // thread loads a 4x4 block and writes four k-runs).  Epilogue as in the
-// FP32 kernel (bias per row/column, ReLU/GELU, plain or NCHW output map).
+// FP32 kernel (bias per row/column, activation, plain or NCHW output map).
+//
+// The same kernel, instantiated for 16-bit inputs (IN = f16 or bf16), is the
+// FP16 / BF16 GEMM (the reference's hgemm_tc_kernel, matmul_kernel.cu:745-930):
+// the operands are copied into a single k-contiguous plane and multiplied
+// with one v_mfma_f32_16x16x32_{f16,bf16} per fragment pair, accumulating
+// and writing fp32.
+#include <type_traits>
+
 #include "cdx_internal.hpp"
 
 namespace cdx {
 namespace {
 
+// Operand element types of the kernel (IN template parameter).
+constexpr int kInF32 = 0;   // fp32, split into bf16 hi / lo on the way into LDS
+constexpr int kInF16 = 1;   // fp16, used as is
+constexpr int kInBF16 = 2;  // bf16, used as is
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
 struct KParams {
-    const float* A; const float* B; float* C; const float* bias;
+    const void* A; const void* B; float* C; const float* bias;
     int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
     int bias_mode, epilogue;
     int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
@@ -67,9 +82,10 @@ struct SplitLoader {
         else         { br = blk % (BK / 4); bc = blk / (BK / 4); }
     }
 
-    __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld,
+    __device__ __forceinline__ void load(const void* __restrict__ Xv, int64_t ld,
                                          int64_t mn0, int64_t k0, int64_t mnmax,
                                          int64_t kmax, bool vec, int tid) {
+        const float* __restrict__ X = static_cast<const float*>(Xv);
 #pragma unroll
         for (int b = 0; b < NV; ++b) {
             int blk = tid + b * NT;
@@ -136,6 +152,83 @@ struct SplitLoader {
     }
 };
 
+// 16-bit operands: the same 4x4-block walk as SplitLoader (same global
+// coalescing and LDS bank pattern), 8-byte loads of four 16-bit values,
+// copied unchanged into one k-contiguous plane.
+template <int BMN, int BK, int NT, bool KCONTIG, bool CHECK>
+struct HalfLoader {
+    static constexpr int NB = (BMN / 4) * (BK / 4);
+    static constexpr int NV = (NB + NT - 1) / NT;
+    static_assert(NB % NT == 0 || NB < NT, "tile not divisible by thread count");
+    uint2 v[NV][4];   // four 16-bit values each: KCONTIG -> mn row q, 4 k; else k row q, 4 mn
+
+    __device__ __forceinline__ static void block_coords(int blk, int& bc, int& br) {
+        SplitLoader<BMN, BK, NT, KCONTIG, CHECK>::block_coords(blk, bc, br);
+    }
+
+    __device__ __forceinline__ void load(const void* __restrict__ Xv, int64_t ld,
+                                         int64_t mn0, int64_t k0, int64_t mnmax,
+                                         int64_t kmax, bool vec, int tid) {
+        const unsigned short* __restrict__ X = static_cast<const unsigned short*>(Xv);
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;
+            block_coords(blk, bc, br);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int64_t gr, gc, rmax, cmax;
+                if (KCONTIG) { gr = mn0 + br * 4 + q; gc = k0 + bc * 4; rmax = mnmax; cmax = kmax; }
+                else         { gr = k0 + br * 4 + q;  gc = mn0 + bc * 4; rmax = kmax; cmax = mnmax; }
+                const unsigned short* p = X + gr * ld + gc;
+                if (!CHECK || (vec && gr < rmax && gc + 3 < cmax)) {
+                    v[b][q] = *reinterpret_cast<const uint2*>(p);
+                } else {
+                    const bool rok = gr < rmax;
+                    uint32_t e[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) e[t] = (rok && gc + t < cmax) ? p[t] : 0u;
+                    v[b][q].x = e[0] | (e[1] << 16);
+                    v[b][q].y = e[2] | (e[3] << 16);
+                }
+            }
+        }
+    }
+
+    // Writes the plane, layout [mn][STRIDE] (k contiguous), ushort units.
+    template <int STRIDE>
+    __device__ __forceinline__ void store(unsigned short* __restrict__ plane, int tid) const {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;
+            block_coords(blk, bc, br);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {       // r indexes mn within the block
+                uint2 hv;
+                if (KCONTIG) {
+                    hv = v[b][r];
+                } else {
+                    // v[b][q] holds k row q; take its 16-bit element r
+                    uint32_t x[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t w = r < 2 ? v[b][q].x : v[b][q].y;
+                        x[q] = (r & 1) ? (w >> 16) : (w & 0xFFFFu);
+                    }
+                    hv.x = x[0] | (x[1] << 16);
+                    hv.y = x[2] | (x[3] << 16);
+                }
+                const int mn = (KCONTIG ? br : bc) * 4 + r;
+                const int kk = (KCONTIG ? bc : br) * 4;
+                *reinterpret_cast<uint2*>(plane + mn * STRIDE + kk) = hv;
+            }
+        }
+    }
+};
+
 // ALIGNED_ONLY: the configuration is only instantiated without bounds
 // checks (its checked variant would not fit the register file); the
 // dispatcher sends it aligned problems only.
@@ -167,15 +260,19 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int grou
     tn = in_g / gsize;
 }
 
-template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS>
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN>
 __global__ __launch_bounds__(CF::NT)
 void gemm_bf16x3_kernel(KParams p, int vec) {
     constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
     constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
     static_assert(BK % 32 == 0, "BK must be a multiple of 32");
+    constexpr bool H16 = IN != kInF32;             // 16-bit operands: one plane
+    constexpr int NPL = H16 ? 1 : 2;               // planes per operand
+    constexpr int ES = H16 ? 2 : 4;                // operand element bytes
     constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
     constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
-    constexpr int STAGE = 2 * A_PLANE + 2 * B_PLANE;
+    constexpr int B_OFF = NPL * A_PLANE;           // stage layout: A hi [, A lo], B hi [, B lo]
+    constexpr int STAGE = NPL * (A_PLANE + B_PLANE);
     __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
 
     const int tid = threadIdx.x;
@@ -195,15 +292,17 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     // and writes a plain [M, N] partial (the reduction applies the epilogue).
     if (gridDim.y > 1) {
         const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
-        p.A += OPA == CDX_OP_N ? k0 : k0 * p.lda;
-        p.B += OPB == CDX_OP_N ? k0 * p.ldb : k0;
+        p.A = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? k0 : k0 * p.lda);
+        p.B = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? k0 * p.ldb : k0);
         p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
         p.C += (int64_t)blockIdx.y * p.M * p.N;
     }
     const bool v = vec != 0;
 
-    using LoaderA = SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>;
-    using LoaderB = SplitLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK>;
+    using LoaderA = std::conditional_t<H16, HalfLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>,
+                                       SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>>;
+    using LoaderB = std::conditional_t<H16, HalfLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK>,
+                                       SplitLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK>>;
     LoaderA la;
     LoaderB lb;
 
@@ -213,8 +312,13 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     };
     auto store_from = [&](const LoaderA& a, const LoaderB& b, int buf) {
         unsigned short* s = lds + buf * STAGE;
-        a.template store<STRIDE>(s, s + A_PLANE, tid);
-        b.template store<STRIDE>(s + 2 * A_PLANE, s + 2 * A_PLANE + B_PLANE, tid);
+        if constexpr (H16) {
+            a.template store<STRIDE>(s, tid);
+            b.template store<STRIDE>(s + B_OFF, tid);
+        } else {
+            a.template store<STRIDE>(s, s + A_PLANE, tid);
+            b.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, tid);
+        }
     };
 
     floatx4 acc[FM][FN];
@@ -227,11 +331,37 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     auto compute = [&](int buf) {
         const unsigned short* s = lds + buf * STAGE;
         const unsigned short* sAh = s;
-        const unsigned short* sAl = s + A_PLANE;
-        const unsigned short* sBh = s + 2 * A_PLANE;
-        const unsigned short* sBl = sBh + B_PLANE;
+        const unsigned short* sAl = s + A_PLANE;       // fp32 operands only
+        const unsigned short* sBh = s + B_OFF;
+        const unsigned short* sBl = sBh + B_PLANE;     // fp32 operands only
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
+            if constexpr (H16) {
+                // 16-bit operands: one MFMA per fragment pair
+                shortx8 a16[FM], b16[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    a16[i] = *reinterpret_cast<const shortx8*>(
+                        sAh + (wm0 + i * 16 + l16) * STRIDE + kk + 8 * lq);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    b16[j] = *reinterpret_cast<const shortx8*>(
+                        sBh + (wn0 + j * 16 + l16) * STRIDE + kk + 8 * lq);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        if constexpr (IN == kInF16)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                __builtin_bit_cast(halfx8, a16[i]), __builtin_bit_cast(halfx8, b16[j]),
+                                acc[i][j], 0, 0, 0);
+                        else
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(bf16x8, a16[i]), __builtin_bit_cast(bf16x8, b16[j]),
+                                acc[i][j], 0, 0, 0);
+                    }
+                continue;
+            }
             bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
@@ -293,7 +423,7 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
 
     const int64_t nk = ceil_div(p.K, BK);
     // the two-set pipeline only where it fits the register file unchecked
-    constexpr int PIPE = (CF::PIPE == 2 && !CHECK && TERMS == 3) ? 2 : 1;
+    constexpr int PIPE = (CF::PIPE == 2 && !CHECK && (TERMS == 3 || H16)) ? 2 : 1;
     if (PIPE == 2 && nk >= 2) {
         // Two register staging sets: tile k+2 is loaded while tile k+1 is
         // split and stored from the set loaded one iteration earlier, so
@@ -366,44 +496,46 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     write_acc<FM, FN, CHECK, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
 }
 
-template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS>
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN = kInF32>
 int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
-    hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN, TERMS>),
+    hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN, TERMS, IN>),
                        dim3((unsigned)tiles, (unsigned)splits), dim3(CF::NT), 0, stream, kp, vec);
     return hip_error(hipGetLastError(), "gemm_bf16x3_kernel launch");
 }
 
-template <class CF, int OPA, int OPB, int TERMS>
+template <class CF, int OPA, int OPB, int TERMS, int IN>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
-    bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&
+    // vector loads of four elements need 4-element-aligned bases and strides
+    constexpr unsigned VB = IN == kInF32 ? 16 : 8;
+    bool vec = ((uintptr_t)g.A % VB == 0) && ((uintptr_t)g.B % VB == 0) &&
                g.lda % 4 == 0 && g.ldb % 4 == 0;
     bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned)
-        return split ? launch_cfg<CF, OPA, OPB, false, true, TERMS>(kp, 1, splits, stream)
-                     : launch_cfg<CF, OPA, OPB, false, false, TERMS>(kp, 1, splits, stream);
+        return split ? launch_cfg<CF, OPA, OPB, false, true, TERMS, IN>(kp, 1, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, false, false, TERMS, IN>(kp, 1, splits, stream);
     if constexpr (CF::ALIGNED_ONLY) {
         return set_error(CDX_ERR_UNSUPPORTED, "gemm_bf16x3: unaligned problem sent to an aligned-only tile");
     } else {
-        return split ? launch_cfg<CF, OPA, OPB, true, true, TERMS>(kp, vec, splits, stream)
-                     : launch_cfg<CF, OPA, OPB, true, false, TERMS>(kp, vec, splits, stream);
+        return split ? launch_cfg<CF, OPA, OPB, true, true, TERMS, IN>(kp, vec, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, true, false, TERMS, IN>(kp, vec, splits, stream);
     }
 }
 
-template <class CF, int TERMS = 3>
+template <class CF, int TERMS = 3, int IN = kInF32>
 int launch_ops(const GemmArgs& g0, hipStream_t stream) {
     const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
     return with_splitk(g0, tiles, CF::BK, stream,
                        [&](const GemmArgs& g, int splits, int64_t k_chunk) {
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N, TERMS>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T, TERMS>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N, TERMS>(g, splits, k_chunk, stream);
-        return launch_mode<CF, CDX_OP_T, CDX_OP_T, TERMS>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N, TERMS, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T, TERMS, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N, TERMS, IN>(g, splits, k_chunk, stream);
+        return launch_mode<CF, CDX_OP_T, CDX_OP_T, TERMS, IN>(g, splits, k_chunk, stream);
     });
 }
 
@@ -450,6 +582,28 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
 
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream) {
     return terms == 4 ? dispatch<4>(g, stream) : dispatch<3>(g, stream);
+}
+
+namespace {
+
+// 16-bit operands: one plane and one MFMA per fragment pair, so a k-tile of
+// 64 costs the LDS of the split kernel's 32.
+using Cfg16Huge = Cfg<256, 256, 64, 128, 64, 8, true, 1>;
+using Cfg16Large = Cfg<128, 128, 64, 32, 64, 8, false, 2>;
+using Cfg16Small = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
+
+template <int IN>
+int dispatch16(const GemmArgs& g, hipStream_t stream) {
+    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<Cfg16Huge>(g))
+        return launch_ops<Cfg16Huge, 1, IN>(g, stream);
+    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<Cfg16Large, 1, IN>(g, stream);
+    return launch_ops<Cfg16Small, 1, IN>(g, stream);
+}
+
+}  // namespace
+
+int launch_gemm_16(const GemmArgs& g, int in_dtype, hipStream_t stream) {
+    return in_dtype == CDX_DTYPE_BF16 ? dispatch16<kInBF16>(g, stream) : dispatch16<kInF16>(g, stream);
 }
 
 }  // namespace cdx

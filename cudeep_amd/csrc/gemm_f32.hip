@@ -294,7 +294,8 @@ int launch_cfg(const KParams& kp, int splits, hipStream_t stream) {
 
 template <class CF, int OPA, int OPB>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
-    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+    KParams kp{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
+               g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
     // 16-byte loads need 16-byte aligned bases and leading dimensions.
     bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&

@@ -98,6 +98,11 @@ void launch_matmul_kernel_fp32<float>(const float* A, const float* B, float* C, 
     CUDEEP_CHECK_CDX(cdx_sgemm_f32(A, B, C, M, N, K, stream));
 }
 
+void launch_matmul_kernel_fp16(const __half* A, const __half* B, float* C, int M, int N, int K,
+                               hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_hgemm_f16(A, B, C, M, N, K, stream));
+}
+
 template <>
 void launch_matmul_kernel_fp32<double>(const double* A, const double* B, double* C, int M, int N,
                                        int K, hipStream_t stream) {

@@ -71,6 +71,57 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, precision: int = L.PREC_FP32,
     return out
 
 
+def gemm16(A: torch.Tensor, B: torch.Tensor, *, transA: bool = False, transB: bool = False,
+           bias: torch.Tensor | None = None, bias_mode: int = L.BIAS_NONE,
+           epilogue: int = L.EPI_NONE, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = epi(op(A) @ op(B) + bias) for float16 or bfloat16 A, B (both the
+    same type), fp32 accumulation and fp32 C (cdx_gemm16_ex)."""
+    if not isinstance(A, torch.Tensor) or A.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("A must be a float16 or bfloat16 tensor")
+    _need(A, "A", A.dtype)
+    _need(B, "B", A.dtype)
+    dt = L.DTYPE_F16 if A.dtype == torch.float16 else L.DTYPE_BF16
+    M, K = (A.shape[1], A.shape[0]) if transA else (A.shape[0], A.shape[1])
+    K2, N = (B.shape[1], B.shape[0]) if transB else (B.shape[0], B.shape[1])
+    if K != K2:
+        raise ValueError(f"inner dimensions differ: {K} vs {K2}")
+    if out is None:
+        out = torch.empty((M, N), device=A.device, dtype=torch.float32)
+    _need(out, "out")
+    if tuple(out.shape) != (M, N):
+        raise ValueError("out has the wrong shape")
+    bptr = None
+    if bias_mode != L.BIAS_NONE:
+        if bias is None:
+            raise ValueError("bias_mode set but bias is None")
+        _need(bias, "bias")
+        want = M if bias_mode == L.BIAS_ROW else N
+        if bias.numel() != want or not bias.is_contiguous():
+            raise ValueError("bias has the wrong size or is not contiguous")
+        bptr = bias.data_ptr()
+    L.call("cdx_gemm16_ex", dt, int(transA), int(transB), M, N, K,
+           A.data_ptr(), _ld(A, "A"), B.data_ptr(), _ld(B, "B"),
+           out.data_ptr(), _ld(out, "out"), bptr, bias_mode, epilogue, _stream())
+    return out
+
+
+def hgemm(A, B, out=None):
+    """C = A @ B for contiguous float16 A, B, fp32 C (cdx_hgemm_f16)."""
+    _need(A, "A", torch.float16)
+    _need(B, "B", torch.float16)
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0]:
+        raise ValueError("hgemm: shape mismatch")
+    if not (A.is_contiguous() and B.is_contiguous()):
+        raise ValueError("hgemm: operands must be contiguous")
+    M, K = A.shape
+    N = B.shape[1]
+    if out is None:
+        out = torch.empty((M, N), device=A.device, dtype=torch.float32)
+    _need(out, "out")
+    L.call("cdx_hgemm_f16", A.data_ptr(), B.data_ptr(), out.data_ptr(), M, N, K, _stream())
+    return out
+
+
 def sgemm(A, B, out=None):
     """C = A @ B, FP32 MFMA (cdx_sgemm_f32); A, B contiguous row-major."""
     _need(A, "A")

@@ -8,10 +8,14 @@
 //    (src/kernels/matmul_kernel.cu:1785-1841).  <double> is the fp64 GEMM.
 //  * launch_matmul_kernel_fp32<float>: always FP32 MFMA (the reference's
 //    "SGEMM", matmul_kernel.cu:1851-1863).
+//  * launch_matmul_kernel_fp16: fp16 A, B -> fp32 C (the reference's
+//    hgemm_tc_kernel, matmul_kernel.cu:745-930, :1926-1943).
 //  * launch_matmul_fused_act: GEMM + activation epilogue.
 //  * launch_matmul_ex: transposes, leading dimensions, bias, epilogue.
 // Errors throw std::runtime_error.
 #pragma once
+
+#include <hip/hip_fp16.h>
 
 #include "../common.hpp"
 
@@ -34,6 +38,9 @@ void launch_matmul_kernel(const T* A, const T* B, T* C, int M, int N, int K,
 
 template <typename T>
 void launch_matmul_kernel_fp32(const T* A, const T* B, T* C, int M, int N, int K,
+                               hipStream_t stream = nullptr);
+
+void launch_matmul_kernel_fp16(const __half* A, const __half* B, float* C, int M, int N, int K,
                                hipStream_t stream = nullptr);
 
 // tile_size is accepted for interface compatibility and ignored (as in the

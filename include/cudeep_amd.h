@@ -65,8 +65,10 @@ extern "C" {
                                       exact products for operands of <= 16 significant
                                       bits (TF32-rounded inputs) */
 
-#define CDX_DTYPE_F32 0
-#define CDX_DTYPE_F64 1
+#define CDX_DTYPE_F32  0
+#define CDX_DTYPE_F64  1
+#define CDX_DTYPE_F16  2           /* IEEE binary16 (GEMM operands only) */
+#define CDX_DTYPE_BF16 3           /* bfloat16 (GEMM operands only)      */
 
 #define CDX_BINARY_ADD 0
 #define CDX_BINARY_SUB 1
@@ -111,6 +113,25 @@ int cdx_gemm_ex(int precision, int opA, int opB,
 int cdx_matmul_fused_act(const float* A, const float* B, float* C,
                          int64_t M, int64_t N, int64_t K, int epilogue,
                          hipStream_t stream);
+
+/* C[M,N] = A * B with fp16 A [M,K] and B [K,N] (row-major), fp32
+ * accumulation and fp32 C (v_mfma_f32_16x16x32_f16).
+ * Replaces cudeep::kernels::launch_matmul_kernel_fp16
+ * (matmul.cuh:27-30, matmul_kernel.cu:745-930, :1926-1943). */
+int cdx_hgemm_f16(const void* A, const void* B, float* C,
+                  int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* General 16-bit-operand form: in_dtype is CDX_DTYPE_F16 or CDX_DTYPE_BF16;
+ * transposes, leading dimensions, bias and epilogue as in cdx_gemm_ex; fp32
+ * accumulation and C.  No counterpart in the reference beyond
+ * launch_matmul_kernel_fp16 (the bf16 / transposed / fused forms). */
+int cdx_gemm16_ex(int in_dtype, int opA, int opB,
+                  int64_t M, int64_t N, int64_t K,
+                  const void* A, int64_t lda,
+                  const void* B, int64_t ldb,
+                  float* C, int64_t ldc,
+                  const float* bias, int bias_mode, int epilogue,
+                  hipStream_t stream);
 
 /* C[M,N] = op(A) * op(B) in fp64 (v_mfma_f64_16x16x4_f64).
  * Replaces cudeep::kernels::launch_matmul_kernel<double>

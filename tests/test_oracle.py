@@ -284,6 +284,24 @@ def test_gelu_against_torch_and_derivative():
     assert np.array_equal(oracle.relu_grad(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 1.0])
 
 
+def test_tf32_round_is_identity_on_16bit_values():
+    """fp16 and bf16 values have at most 11 significant bits, so TF32 rounding
+    (either mode) leaves them unchanged: gemm_tf32emu on fp32-converted 16-bit
+    operands is the exact-product, 8-term-chunk ideal MMA used as the FP16 /
+    BF16 GEMM yardstick."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.uniform(-4, 4, 20000)
+    for td in (torch.float16, torch.bfloat16):
+        v = torch.from_numpy(x.astype(np.float32)).to(td).float().numpy()
+        v = v[np.isfinite(v)]
+        for mode in ("rz", "rne"):
+            assert np.array_equal(oracle.tf32_round(v, mode), v)
+    # and a value with 12 significant bits is changed (the check has teeth)
+    y = np.float32(1 + 2.0 ** -11)
+    assert oracle.tf32_round(np.array([y]), "rz")[0] != y
+
+
 def test_sigmoid_silu_against_tanh_torch_and_derivative():
     """sigmoid against scipy's expit and, away from the cancelling tail, the
     closed form (1 + tanh(x/2)) / 2; SiLU against torch's silu; both
