@@ -186,10 +186,17 @@ def bench_conv(steps, warmup, precision):
     im_ms, _ = time_launches(lambda: ops.im2col(x, 3, 3, (1, 1), (1, 1), out=col), steps, warmup)
     flops = 2.0 * 32 * 64 * 56 * 56 * 64 * 9
     im2col_bytes = 576 * 100352 * 4 + 32 * 64 * 56 * 56 * 4
+    # Winograd F(4x4, 3x3) route (the reference's route for this layer); TFLOP/s
+    # counted with the direct-convolution FLOPs, as for the im2col route
+    wws = torch.empty(ops.conv2d_winograd_workspace_bytes(x.shape, 64, (1, 1)) // 4,
+                      device="cuda")
+    wino_ms, _ = time_launches(lambda: ops.conv2d_winograd(x, w, b, (1, 1), precision,
+                                                           workspace=wws, out=y), steps, warmup)
     return {"conv_ms": conv_ms, "conv_tflops": flops / (conv_ms * 1e-3) / 1e12,
             "im2col_ms": im_ms, "im2col_gbs": im2col_bytes / (im_ms * 1e-3) / 1e9,
             "gemm_ms_est": conv_ms - im_ms,
-            "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12}
+            "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12,
+            "winograd_ms": wino_ms, "winograd_tflops_equiv": flops / (wino_ms * 1e-3) / 1e12}
 
 
 def cpu_baseline(n=4096):

@@ -49,6 +49,8 @@ SIGNATURES = {
     "cdx_broadcast_add_row_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "cdx_activation_forward_f32": (_int, [_vp, _vp, _i64, _int, _vp]),
     "cdx_activation_backward_f32": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
+    "cdx_conv2d_winograd_workspace_size": (_sz, [_i64] * 7),
+    "cdx_conv2d_forward_winograd_f32": (_int, [_vp, _vp, _vp, _vp] + [_i64] * 7 + [_int, _vp, _sz, _vp]),
     "cdx_col2im_f32": (_int, [_vp, _vp] + [_i64] * 10 + [_vp]),
     "cdx_conv2d_backward_data_workspace_size": (_sz, [_i64] * 11),
     "cdx_conv2d_backward_data_f32": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),

@@ -239,6 +239,56 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight, const float*
     return st;
 }
 
+size_t cdx_conv2d_winograd_workspace_size(int64_t batch, int64_t in_channels,
+                                          int64_t out_channels, int64_t in_h, int64_t in_w,
+                                          int64_t pad_h, int64_t pad_w) {
+    if (check_conv("cdx_conv2d_winograd_workspace_size", batch, in_channels, out_channels, in_h,
+                   in_w, 3, 3, 1, 1, pad_h, pad_w))
+        return 0;
+    return cdx::winograd_workspace_floats(batch, in_channels, out_channels, in_h + 2 * pad_h - 2,
+                                          in_w + 2 * pad_w - 2) * sizeof(float);
+}
+
+int cdx_conv2d_forward_winograd_f32(const float* input, const float* weight, const float* bias,
+                                    float* output, int64_t batch, int64_t in_channels,
+                                    int64_t out_channels, int64_t in_h, int64_t in_w,
+                                    int64_t pad_h, int64_t pad_w, int precision, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+    const char* fn = "cdx_conv2d_forward_winograd_f32";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, 3, 3, 1, 1, pad_h, pad_w);
+    if (st) return st;
+    if (!valid_precision(precision)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
+    const int64_t OH = in_h + 2 * pad_h - 2, OW = in_w + 2 * pad_w - 2;
+    if (batch == 0 || out_channels == 0 || OH * OW == 0) return CDX_OK;
+    if (!output || !weight || (in_channels > 0 && !input))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    if (in_channels == 0) {   // empty sum: the output is the bias
+        return cdx_conv2d_forward_f32(input, weight, bias, output, batch, 0, out_channels, in_h,
+                                      in_w, 3, 3, 1, 1, pad_h, pad_w, precision, nullptr, 0, stream);
+    }
+    const size_t need =
+        cdx::winograd_workspace_floats(batch, in_channels, out_channels, OH, OW) * sizeof(float);
+    float* ws = static_cast<float*>(workspace);
+    bool owned = false;
+    if (workspace) {
+        if (workspace_bytes < need)
+            return set_error(CDX_ERR_WORKSPACE, std::string(fn) + ": workspace too small");
+    } else {
+        st = cdx::hip_error(hipMallocAsync(reinterpret_cast<void**>(&ws), need, stream),
+                            "cdx_conv2d_forward_winograd_f32: hipMallocAsync");
+        if (st) return st;
+        owned = true;
+    }
+    st = cdx::launch_conv2d_winograd_f32(input, weight, bias, output, batch, in_channels,
+                                         out_channels, in_h, in_w, pad_h, pad_w, precision, ws,
+                                         stream);
+    if (owned) {
+        int st2 = cdx::hip_error(hipFreeAsync(ws, stream), "cdx_conv2d_forward_winograd_f32: hipFreeAsync");
+        if (!st) st = st2;
+    }
+    return st;
+}
+
 int cdx_col2im_f32(const float* col, float* grad_input, int64_t batch, int64_t in_channels,
                    int64_t in_h, int64_t in_w, int64_t kernel_h, int64_t kernel_w,
                    int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,

@@ -38,6 +38,9 @@ struct GemmArgs {
     int64_t n_split, ldc_split;
     const float* bias; int bias_mode;   // CDX_BIAS_*
     int epilogue;                       // CDX_EPI_*
+    // Batched form: `batch` independent problems, problem z at A + z*stride_a,
+    // B + z*stride_b, C + z*stride_c (elements); bias shared.
+    int64_t batch = 1, stride_a = 0, stride_b = 0, stride_c = 0;
 };
 
 // Launchers (no argument validation: the C-ABI validates first).
@@ -75,7 +78,7 @@ inline int choose_splitk(int64_t tiles, int64_t K, int bk, int64_t* k_chunk) {
 template <class LaunchFn>
 int with_splitk(const GemmArgs& g, int64_t tiles, int bk, hipStream_t stream, LaunchFn launch) {
     int64_t k_chunk;
-    const int splits = choose_splitk(tiles, g.K, bk, &k_chunk);
+    const int splits = g.batch > 1 ? (k_chunk = g.K, 1) : choose_splitk(tiles, g.K, bk, &k_chunk);
     if (splits == 1) return launch(g, 1, g.K);
     float* part = nullptr;
     const size_t bytes = (size_t)splits * (size_t)g.M * (size_t)g.N * sizeof(float);
@@ -95,6 +98,14 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,
                       int64_t SH, int64_t SW, int64_t PH, int64_t PW,
                       hipStream_t stream);
+
+// Winograd F(4x4, 3x3) forward for 3x3 stride-1 convolution; ws holds
+// winograd_workspace_floats(...) floats (U, V and M).
+size_t winograd_workspace_floats(int64_t batch, int64_t IC, int64_t OC, int64_t OH, int64_t OW);
+int launch_conv2d_winograd_f32(const float* input, const float* weight, const float* bias,
+                               float* output, int64_t batch, int64_t IC, int64_t OC,
+                               int64_t IH, int64_t IW, int64_t PH, int64_t PW, int precision,
+                               float* ws, hipStream_t stream);
 
 int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,

@@ -48,6 +48,8 @@ struct KParams {
     int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
     int bias_mode, epilogue;
     int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
+    int64_t sa, sb, sc; // batch strides (elements) for blockIdx.z
+    int64_t batch;      // gridDim.z
 };
 
 __device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
@@ -297,6 +299,11 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
         p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
         p.C += (int64_t)blockIdx.y * p.M * p.N;
     }
+    if (gridDim.z > 1) {
+        p.A = static_cast<const char*>(p.A) + ES * (int64_t)blockIdx.z * p.sa;
+        p.B = static_cast<const char*>(p.B) + ES * (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
+    }
     const bool v = vec != 0;
 
     using LoaderA = std::conditional_t<H16, HalfLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>,
@@ -500,19 +507,22 @@ template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN
 int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
     hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN, TERMS, IN>),
-                       dim3((unsigned)tiles, (unsigned)splits), dim3(CF::NT), 0, stream, kp, vec);
+                       dim3((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch), dim3(CF::NT), 0, stream, kp, vec);
     return hip_error(hipGetLastError(), "gemm_bf16x3_kernel launch");
 }
 
 template <class CF, int OPA, int OPB, int TERMS, int IN>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
-               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
+               g.stride_a, g.stride_b, g.stride_c, g.batch};
     // vector loads of four elements need 4-element-aligned bases and strides
     constexpr unsigned VB = IN == kInF32 ? 16 : 8;
     bool vec = ((uintptr_t)g.A % VB == 0) && ((uintptr_t)g.B % VB == 0) &&
-               g.lda % 4 == 0 && g.ldb % 4 == 0;
+               g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+               g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
     bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
@@ -561,8 +571,8 @@ using CfgSmall = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
 template <class CF>
 bool aligned_for(const GemmArgs& g) {
     return ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
-           g.ldb % 4 == 0 && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
-           g.K % CF::BK == 0;
+           g.ldb % 4 == 0 && g.stride_a % 4 == 0 && g.stride_b % 4 == 0 && g.K > 0 &&
+           g.M % CF::BM == 0 && g.N % CF::BN == 0 && g.K % CF::BK == 0;
 }
 
 template <int TERMS>

@@ -43,6 +43,8 @@ struct KParams {
     int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
     int bias_mode, epilogue;
     int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
+    int64_t sa, sb, sc; // batch strides (elements) for blockIdx.z
+    int64_t batch;      // gridDim.z
 };
 
 // Loads a ROWS x COLS tile (COLS contiguous in memory) starting at (r0, c0)
@@ -156,6 +158,11 @@ void gemm_f32_mfma_kernel(KParams p) {
         p.B += OPB == CDX_OP_N ? k0 * p.ldb : k0;
         p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
         p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
+    if (gridDim.z > 1) {
+        p.A += (int64_t)blockIdx.z * p.sa;
+        p.B += (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
     }
 
     // Global tile loaders in memory orientation.
@@ -287,8 +294,9 @@ template <class CF, int OPA, int OPB, int MODE, bool SPLITN>
 int launch_cfg(const KParams& kp, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
     hipLaunchKernelGGL((gemm_f32_mfma_kernel<CF, OPA, OPB, MODE, SPLITN>),
-                       dim3((unsigned)tiles, (unsigned)splits), dim3(CF::NT), 0, stream, kp);
+                       dim3((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch), dim3(CF::NT), 0, stream, kp);
     return hip_error(hipGetLastError(), "gemm_f32_mfma_kernel launch");
 }
 
@@ -296,10 +304,12 @@ template <class CF, int OPA, int OPB>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
                g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
-               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk};
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
+               g.stride_a, g.stride_b, g.stride_c, g.batch};
     // 16-byte loads need 16-byte aligned bases and leading dimensions.
     bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&
-               g.lda % 4 == 0 && g.ldb % 4 == 0;
+               g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+               g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
     bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;

@@ -220,6 +220,42 @@ def conv2d_forward(x, w, bias=None, stride=(1, 1), padding=(0, 0),
     return out
 
 
+def conv2d_winograd(x, w, bias=None, padding=(0, 0), precision=L.PREC_FP32, workspace=None,
+                    out=None):
+    """3x3 stride-1 NCHW convolution by Winograd F(4x4, 3x3)
+    (cdx_conv2d_forward_winograd_f32)."""
+    _need(x, "input")
+    _need(w, "weight")
+    if x.dim() != 4 or w.dim() != 4 or not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("conv2d_winograd: input / weight must be contiguous NCHW / OIHW")
+    Bn, C, H, W = x.shape
+    OC, C2, KH, KW = w.shape
+    if C != C2 or KH != 3 or KW != 3:
+        raise ValueError("conv2d_winograd: needs a 3x3 kernel and matching channels")
+    OH, OW = H + 2 * padding[0] - 2, W + 2 * padding[1] - 2
+    if OH <= 0 or OW <= 0:
+        raise ValueError("conv2d_winograd: kernel larger than padded input")
+    if bias is not None:
+        _need(bias, "bias")
+        if bias.numel() != OC or not bias.is_contiguous():
+            raise ValueError("conv2d_winograd: bias must have out_channels elements")
+    if out is None:
+        out = torch.empty((Bn, OC, OH, OW), device=x.device, dtype=torch.float32)
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    L.call("cdx_conv2d_forward_winograd_f32", x.data_ptr(), w.data_ptr(),
+           None if bias is None else bias.data_ptr(), out.data_ptr(), Bn, C, OC, H, W,
+           padding[0], padding[1], precision, ws_ptr, ws_bytes, _stream())
+    return out
+
+
+def conv2d_winograd_workspace_bytes(x_shape, out_channels, padding=(0, 0)) -> int:
+    Bn, C, H, W = x_shape
+    return int(L.lib().cdx_conv2d_winograd_workspace_size(Bn, C, out_channels, H, W,
+                                                          padding[0], padding[1]))
+
+
 def conv2d_workspace_bytes(x_shape, w_shape, stride=(1, 1), padding=(0, 0)) -> int:
     Bn, C, H, W = x_shape
     _, _, KH, KW = w_shape

@@ -171,6 +171,27 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight,
                            void* workspace, size_t workspace_bytes,
                            hipStream_t stream);
 
+/* Bytes of workspace cdx_conv2d_forward_winograd_f32 needs:
+ * 36 * (OC*IC + IC*T + OC*T) floats, T = batch * ceil(OH/4) * ceil(OW/4). */
+size_t cdx_conv2d_winograd_workspace_size(
+    int64_t batch, int64_t in_channels, int64_t out_channels,
+    int64_t in_h, int64_t in_w, int64_t pad_h, int64_t pad_w);
+
+/* NCHW 3x3 stride-1 conv forward by Winograd F(4x4, 3x3): filter / input
+ * transforms, one batched GEMM over the 36 transform points, output
+ * transform + bias.  Replaces launch_conv2d_winograd_f43
+ * (src/kernels/conv_kernel.cu:557-789), the reference's route for 3x3
+ * stride-1 layers (:242-248).  Winograd adds transform rounding: expect
+ * errors several times those of the im2col route.  precision is CDX_PREC_*
+ * (the GEMM's); workspace may be NULL. */
+int cdx_conv2d_forward_winograd_f32(const float* input, const float* weight,
+                                    const float* bias, float* output,
+                                    int64_t batch, int64_t in_channels,
+                                    int64_t out_channels, int64_t in_h, int64_t in_w,
+                                    int64_t pad_h, int64_t pad_w, int precision,
+                                    void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
+
 /* grad_input[B, IC, IH, IW] from grad_col[K_col, B*OH*OW]: sums, per input
  * element, every column entry it was copied to (kh then kw ascending, fp32);
  * bit-exact with col2im_kernel (src/kernels/conv_kernel.cu:344-380). */

@@ -77,6 +77,8 @@ def lib():
         L.orc_colsum.argtypes = [_vp, _vp, _i64, _i64]
         L.orc_col2im.argtypes = [_vp, _vp] + [_i64] * 10
         L.orc_col2im64.argtypes = [_vp, _vp] + [_i64] * 10
+        L.orc_winograd_f43.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 7 + [_int]
+        L.orc_winograd_f43_64.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 7 + [_int]
         L.orc_gelu_vec.argtypes = [_vp, _vp, _i64]
         L.orc_gelu_grad_vec.argtypes = [_vp, _vp, _i64]
         L.orc_num_threads.restype = _int
@@ -223,6 +225,27 @@ def conv2d_ref_im2col(x, w, bias=None, stride=(1, 1), padding=(0, 0)):
     OW = conv_out_size(x.shape[3], KW, stride[1], padding[1])
     out = transpose_bias(flat, OC, Bn, OH * OW, bias)
     return out.reshape(Bn, OC, OH, OW)
+
+
+def conv2d_winograd(x, w, bias=None, padding=(0, 0), double=False, tf32=None):
+    """The reference's Winograd F(4x4, 3x3) route for 3x3 stride-1 convolution
+    (conv_kernel.cu:557-789) restated on the CPU: weight / input transforms,
+    36 seq-FMA GEMMs over input channels, output transform + bias, in fp32
+    (``double=True``: the same algorithm in fp64, equal to direct convolution
+    up to rounding).  ``tf32="rz" | "rne"`` rounds the GEMM operands to TF32
+    first, as the reference's default TF32 GEMM sees them."""
+    x, w = _c32(x), _c32(w)
+    Bn, IC, IH, IW = x.shape
+    OC, IC2, KH, KW = w.shape
+    assert IC == IC2 and KH == 3 and KW == 3
+    PH, PW = padding
+    OH, OW = IH + 2 * PH - 2, IW + 2 * PW - 2
+    out = np.empty((Bn, OC, OH, OW), np.float64 if double else np.float32)
+    b = None if bias is None else _c32(bias)
+    f = lib().orc_winograd_f43_64 if double else lib().orc_winograd_f43
+    mode = {None: 0, "rz": 1, "rne": 2}[tf32]
+    f(_p(x), _p(w), None if b is None else _p(b), _p(out), Bn, IC, OC, IH, IW, PH, PW, mode)
+    return out
 
 
 def col2im(col, x_shape, KH, KW, SH=1, SW=1, PH=0, PW=0):

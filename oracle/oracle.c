@@ -25,6 +25,8 @@
  *                       down each column).
  *   orc_gelu / relu     src/kernels/activation_kernel.cu:19-52 (forward) and
  *                       :256-319 (backward), written in double.
+ *   orc_winograd_f43    src/kernels/conv_kernel.cu:557-789 (Winograd F(4,3) route
+ *                       for 3x3 stride-1 convolution), fp32; _64: in double.
  *
  * Build: oracle/Makefile (gcc -O3 -march=x86-64-v3 -ffp-contract=off -fopenmp).
  * -ffp-contract=off keeps every fma explicit (fmaf) and forbids the compiler
@@ -398,3 +400,135 @@ void orc_gelu_vec(const double* x, double* y, int64_t n) {
 void orc_gelu_grad_vec(const double* x, double* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = orc_gelu_grad(x[i]);
 }
+
+/*
+ * Winograd F(4x4, 3x3) convolution, the reference's route for 3x3 stride-1
+ * convolutions (conv_kernel.cu:242-248, :557-789), with the transform
+ * matrices of Lavin & Gray (2016) for the interpolation points 0, +-1, +-2:
+ *   U = G g G^T   (3x3 filter  -> 6x6),   G   = [1/4 0 0; -1/6 -1/6 -1/6;
+ *                                                -1/6 1/6 -1/6; 1/24 1/12 1/6;
+ *                                                1/24 -1/12 1/6; 0 0 1]
+ *   V = B^T d B   (6x6 input patch at (4 th - PH, 4 tw - PW), zero padded),
+ *                 B^T rows: [4 0 -5 0 1 0] [0 -4 -4 1 1 0] [0 4 -4 -1 1 0]
+ *                           [0 -2 -1 2 1 0] [0 2 -1 -2 1 0] [0 4 0 -5 0 1]
+ *   M_a = U_a V_a  for each of the 36 points a (a GEMM over input channels),
+ *   Y = A^T m A + bias (6x6 -> 4x4 output tile),
+ *                 A^T rows: [1 1 1 1 1 0] [0 1 -1 2 -2 0] [0 1 1 4 4 0]
+ *                           [0 1 -1 8 -8 1]
+ * Each 2-D transform applies the 1-D transform to the columns, then to the
+ * rows of the result (conv_kernel.cu:611-617, :656-670, :709-728).  The
+ * fp32 form sums the 36 GEMMs by sequential fmaf over ic ascending (the
+ * reference's FP32 GEMM, matmul_kernel.cu:499-520); the double form is the
+ * same algorithm in fp64, which equals direct convolution up to rounding.
+ */
+#define WINO_BODY(T, NAME, FMA, ROUND)                                                   \
+static void NAME##_wcol(T g0, T g1, T g2, T* u) {                                       \
+    u[0] = (T)0.25 * g0;                                                                \
+    u[1] = -((T)1 / (T)6) * (g0 + g1 + g2);                                             \
+    u[2] = -((T)1 / (T)6) * (g0 - g1 + g2);                                             \
+    u[3] = ((T)1 / (T)24) * g0 + ((T)1 / (T)12) * g1 + ((T)1 / (T)6) * g2;              \
+    u[4] = ((T)1 / (T)24) * g0 - ((T)1 / (T)12) * g1 + ((T)1 / (T)6) * g2;              \
+    u[5] = g2;                                                                          \
+}                                                                                       \
+static void NAME##_icol(const T* d, T* t) {                                             \
+    t[0] = (T)4 * d[0] - (T)5 * d[2] + d[4];                                            \
+    t[1] = -(T)4 * d[1] - (T)4 * d[2] + d[3] + d[4];                                    \
+    t[2] = (T)4 * d[1] - (T)4 * d[2] - d[3] + d[4];                                     \
+    t[3] = -(T)2 * d[1] - d[2] + (T)2 * d[3] + d[4];                                    \
+    t[4] = (T)2 * d[1] - d[2] - (T)2 * d[3] + d[4];                                     \
+    t[5] = (T)4 * d[1] - (T)5 * d[3] + d[5];                                            \
+}                                                                                       \
+static void NAME##_ocol(const T* m, T* o) {                                             \
+    o[0] = m[0] + m[1] + m[2] + m[3] + m[4];                                            \
+    o[1] = m[1] - m[2] + (T)2 * m[3] - (T)2 * m[4];                                     \
+    o[2] = m[1] + m[2] + (T)4 * m[3] + (T)4 * m[4];                                     \
+    o[3] = m[1] - m[2] + (T)8 * m[3] - (T)8 * m[4] + m[5];                              \
+}                                                                                       \
+void NAME(const float* input, const float* weight, const float* bias, T* out,           \
+          int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,                \
+          int64_t PH, int64_t PW, int tf32_mode) {                                      \
+    const int64_t OH = IH + 2 * PH - 2, OW = IW + 2 * PW - 2;                           \
+    const int64_t TH = (OH + 3) / 4, TW = (OW + 3) / 4, NT = batch * TH * TW;           \
+    T* U = (T*)malloc(sizeof(T) * 36 * OC * IC);                                        \
+    T* V = (T*)malloc(sizeof(T) * 36 * IC * NT);                                        \
+    T* Mm = (T*)malloc(sizeof(T) * 36 * OC * NT);                                       \
+    _Pragma("omp parallel for schedule(static)")                                        \
+    for (int64_t p = 0; p < OC * IC; ++p) {                                             \
+        const float* g = weight + p * 9;                                                \
+        T tmp[6][3], u[6];                                                              \
+        for (int j = 0; j < 3; ++j) {                                                   \
+            NAME##_wcol((T)g[j], (T)g[3 + j], (T)g[6 + j], u);                          \
+            for (int i = 0; i < 6; ++i) tmp[i][j] = u[i];                               \
+        }                                                                               \
+        for (int i = 0; i < 6; ++i) {                                                   \
+            NAME##_wcol(tmp[i][0], tmp[i][1], tmp[i][2], u);                            \
+            for (int j = 0; j < 6; ++j)                                                 \
+                U[(int64_t)(i * 6 + j) * OC * IC + p] = ROUND(u[j], tf32_mode);         \
+        }                                                                               \
+    }                                                                                   \
+    _Pragma("omp parallel for schedule(static)")                                        \
+    for (int64_t q = 0; q < IC * NT; ++q) {                                             \
+        const int64_t ic = q / NT, tile = q % NT;                                       \
+        const int64_t b = tile / (TH * TW), th = (tile / TW) % TH, tw = tile % TW;      \
+        const float* src = input + (b * IC + ic) * IH * IW;                             \
+        T d[6][6], tmp[6][6], col[6], t[6];                                             \
+        for (int i = 0; i < 6; ++i)                                                     \
+            for (int j = 0; j < 6; ++j) {                                               \
+                const int64_t ih = th * 4 - PH + i, iw = tw * 4 - PW + j;               \
+                d[i][j] = (ih >= 0 && ih < IH && iw >= 0 && iw < IW)                    \
+                              ? (T)src[ih * IW + iw] : (T)0;                            \
+            }                                                                           \
+        for (int j = 0; j < 6; ++j) {                                                   \
+            for (int i = 0; i < 6; ++i) col[i] = d[i][j];                               \
+            NAME##_icol(col, t);                                                        \
+            for (int i = 0; i < 6; ++i) tmp[i][j] = t[i];                               \
+        }                                                                               \
+        for (int i = 0; i < 6; ++i) {                                                   \
+            NAME##_icol(tmp[i], t);                                                     \
+            for (int j = 0; j < 6; ++j)                                                 \
+                V[((int64_t)(i * 6 + j) * IC + ic) * NT + tile] = ROUND(t[j], tf32_mode); \
+        }                                                                               \
+    }                                                                                   \
+    _Pragma("omp parallel for collapse(2) schedule(static)")                            \
+    for (int64_t a = 0; a < 36; ++a)                                                    \
+        for (int64_t oc = 0; oc < OC; ++oc) {                                           \
+            T* mrow = Mm + (a * OC + oc) * NT;                                          \
+            for (int64_t n = 0; n < NT; ++n) mrow[n] = (T)0;                            \
+            for (int64_t ic = 0; ic < IC; ++ic) {                                       \
+                const T u = U[(a * OC + oc) * IC + ic];                                 \
+                const T* vrow = V + (a * IC + ic) * NT;                                 \
+                for (int64_t n = 0; n < NT; ++n) mrow[n] = FMA(u, vrow[n], mrow[n]);    \
+            }                                                                           \
+        }                                                                               \
+    _Pragma("omp parallel for schedule(static)")                                        \
+    for (int64_t q = 0; q < OC * NT; ++q) {                                             \
+        const int64_t oc = q / NT, tile = q % NT;                                       \
+        const int64_t b = tile / (TH * TW), th = (tile / TW) % TH, tw = tile % TW;      \
+        T m[6][6], tmp[4][6], col[6], o[4];                                             \
+        for (int i = 0; i < 6; ++i)                                                     \
+            for (int j = 0; j < 6; ++j) m[i][j] = Mm[((int64_t)(i * 6 + j) * OC + oc) * NT + tile]; \
+        for (int j = 0; j < 6; ++j) {                                                   \
+            for (int i = 0; i < 6; ++i) col[i] = m[i][j];                               \
+            NAME##_ocol(col, o);                                                        \
+            for (int i = 0; i < 4; ++i) tmp[i][j] = o[i];                               \
+        }                                                                               \
+        const T bv = bias ? (T)bias[oc] : (T)0;                                         \
+        for (int i = 0; i < 4; ++i) {                                                   \
+            NAME##_ocol(tmp[i], o);                                                     \
+            const int64_t oh = th * 4 + i;                                              \
+            if (oh >= OH) break;                                                        \
+            for (int j = 0; j < 4; ++j) {                                               \
+                const int64_t ow = tw * 4 + j;                                          \
+                if (ow < OW) out[((b * OC + oc) * OH + oh) * OW + ow] = o[j] + bv;      \
+            }                                                                           \
+        }                                                                               \
+    }                                                                                   \
+    free(U); free(V); free(Mm);                                                         \
+}
+
+/* tf32_mode 0: GEMM operands as computed; 1 = RZ, 2 = RNE: rounded to TF32
+ * first, as the reference's default (TF32 tensor-core) GEMM sees them. */
+static inline float wino_round_f(float x, int mode) { return mode ? tf32_round(x, mode - 1) : x; }
+static inline double wino_round_d(double x, int mode) { (void)mode; return x; }
+WINO_BODY(float, orc_winograd_f43, fmaf, wino_round_f)
+WINO_BODY(double, orc_winograd_f43_64, fma, wino_round_d)

@@ -382,3 +382,44 @@ def test_conv_backward_vs_torch_fp64(geom):
     dx32 = oracle.conv2d_backward_data_ref(dy, w, x.shape, (SH, SW), (PH, PW))
     dw32 = oracle.conv2d_backward_weight_ref(dy, x, w.shape, (SH, SW), (PH, PW))
     assert oracle.rel_fro(dx32, dx64) < 1e-6 and oracle.rel_fro(dw32, dw64) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Winograd F(4x4, 3x3) route (conv_kernel.cu:557-789)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,IC,OC,H,W,P", [(2, 3, 4, 9, 11, 1), (1, 5, 2, 6, 6, 0),
+                                           (2, 8, 8, 16, 16, 1), (1, 1, 1, 7, 5, 2),
+                                           (1, 4, 3, 3, 3, 0), (1, 2, 2, 13, 4, 1)])
+def test_winograd_double_equals_direct_conv(B, IC, OC, H, W, P):
+    """In exact arithmetic F(4x4, 3x3) is the 3x3 cross-correlation, so the
+    fp64 form must match the fp64 direct convolution to rounding: a wrong
+    transform coefficient, sign or tile offset breaks this at O(1)."""
+    rng = np.random.default_rng(B * 100 + IC * 10 + H + P)
+    x = rng.standard_normal((B, IC, H, W)).astype(np.float32)
+    w = rng.standard_normal((OC, IC, 3, 3)).astype(np.float32)
+    b = rng.standard_normal(OC).astype(np.float32)
+    d = oracle.conv2d_direct64(x, w, b, padding=(P, P))
+    w64 = oracle.conv2d_winograd(x, w, b, padding=(P, P), double=True)
+    assert w64.shape == d.shape
+    assert np.abs(w64 - d).max() <= 1e-12 * np.abs(d).max()
+    # fp32: transform rounding, bounded well below the data scale
+    w32 = oracle.conv2d_winograd(x, w, b, padding=(P, P))
+    assert oracle.rel_fro(w32, d) < 1e-5
+    # TF32 operand rounding costs about 2^-11 relative, more than fp32
+    wt = oracle.conv2d_winograd(x, w, b, padding=(P, P), tf32="rne")
+    assert oracle.rel_fro(w32, d) < oracle.rel_fro(wt, d) < 1e-2
+
+
+def test_winograd_reference_conv_kats(kats):
+    """The reference's 3x3 conv known answers (test_kernels.cu:352-425) through
+    the Winograd route: all-ones -> 9, bias 10 -> 19, pad 1 -> 4 / 6 / 9."""
+    for name in ("conv_3x3_ones", "conv_3x3_bias", "conv_3x3_pad1"):
+        k = kats[name]
+        x = np.array(k["x"], np.float32).reshape(k["x_shape"])
+        w = np.array(k["w"], np.float32).reshape(k["w_shape"])
+        b = np.array(k["bias"], np.float32) if k.get("bias") is not None else None
+        assert tuple(k["stride"]) == (1, 1)
+        y = oracle.conv2d_winograd(x, w, b, padding=tuple(k["padding"]))
+        want = np.array(k["y"], np.float32).reshape(y.shape)
+        assert np.allclose(y, want, rtol=0, atol=1e-5), name
