@@ -349,6 +349,19 @@ PYBIND11_MODULE(_cudeep_core, m) {
                                                           : "tf32";
     });
 
+    m.def("set_conv_algorithm", [](const std::string& a) {
+        if (a == "auto") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Auto);
+        else if (a == "im2col") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Im2col);
+        else if (a == "winograd") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Winograd);
+        else throw std::runtime_error("set_conv_algorithm: 'auto', 'im2col' or 'winograd'");
+    }, py::arg("algorithm"));
+    m.def("get_conv_algorithm", []() {
+        const auto a = kernels::get_conv_algorithm();
+        return a == kernels::ConvAlgorithm::Im2col     ? "im2col"
+               : a == kernels::ConvAlgorithm::Winograd ? "winograd"
+                                                       : "auto";
+    });
+
     // ---- conv ----
     m.def("conv2d_forward",
           [](const Tensor& input, const Tensor& weight, py::object bias_obj,

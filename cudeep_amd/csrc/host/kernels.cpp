@@ -20,6 +20,7 @@ namespace kernels {
 namespace {
 
 std::atomic<int> g_precision{CDX_PREC_TF32MODE};
+std::atomic<int> g_conv_algo{(int)ConvAlgorithm::Auto};
 
 template <typename T>
 constexpr int dtype_code() {
@@ -46,6 +47,10 @@ int act_code(ActivationType a) {
 }
 
 }  // namespace
+
+void set_conv_algorithm(ConvAlgorithm a) { g_conv_algo = (int)a; }
+
+ConvAlgorithm get_conv_algorithm() { return (ConvAlgorithm)g_conv_algo.load(); }
 
 void set_matmul_precision(MatmulPrecision p) {
     g_precision = p == MatmulPrecision::FP32       ? CDX_PREC_FP32
@@ -132,9 +137,23 @@ void launch_conv2d_forward_kernel<float>(const float* input, const float* weight
                                          float* output, int batch, int IC, int OC, int IH, int IW,
                                          int KH, int KW, int SH, int SW, int PH, int PW,
                                          hipStream_t stream) {
-    CUDEEP_CHECK_CDX(cdx_conv2d_forward_f32(input, weight, bias, output, batch, IC, OC, IH, IW,
-                                            KH, KW, SH, SW, PH, PW, g_precision.load(), nullptr,
-                                            0, stream));
+    const int64_t OH = ((int64_t)IH + 2 * PH - KH) / SH + 1;
+    const int64_t OW = ((int64_t)IW + 2 * PW - KW) / SW + 1;
+    const bool wino_ok = KH == 3 && KW == 3 && SH == 1 && SW == 1;
+    const ConvAlgorithm algo = get_conv_algorithm();
+    if (algo == ConvAlgorithm::Winograd && !wino_ok)
+        throw std::runtime_error("conv2d: Winograd needs a 3x3 kernel with stride 1");
+    const bool wino = algo == ConvAlgorithm::Winograd ||
+                      (algo == ConvAlgorithm::Auto && wino_ok && OH * OW >= 16);
+    if (wino) {
+        CUDEEP_CHECK_CDX(cdx_conv2d_forward_winograd_f32(input, weight, bias, output, batch, IC,
+                                                         OC, IH, IW, PH, PW, g_precision.load(),
+                                                         nullptr, 0, stream));
+    } else {
+        CUDEEP_CHECK_CDX(cdx_conv2d_forward_f32(input, weight, bias, output, batch, IC, OC, IH, IW,
+                                                KH, KW, SH, SW, PH, PW, g_precision.load(),
+                                                nullptr, 0, stream));
+    }
 }
 
 template <>

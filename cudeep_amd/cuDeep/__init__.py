@@ -10,7 +10,8 @@ native ``_cudeep_core`` module; there is no CPU fallback.
 __version__ = "0.1.0"
 
 from ._core import (DType, Event, Layout, MemoryPool, Stream, device_info,  # noqa: F401
-                    get_matmul_precision, set_matmul_precision)
+                    get_conv_algorithm, get_matmul_precision, set_conv_algorithm,
+                    set_matmul_precision)
 from .tensor import (Tensor, broadcast_add, conv2d, gelu, linear, ones_like,  # noqa: F401
                      randn_like, relu, zeros_like)
 from .autograd import no_grad  # noqa: F401
@@ -20,5 +21,5 @@ __all__ = [
     "Tensor", "DType", "Layout", "Stream", "Event", "MemoryPool", "device_info",
     "zeros_like", "ones_like", "randn_like", "relu", "gelu", "broadcast_add", "conv2d",
     "linear", "no_grad", "nn", "autograd", "init", "set_matmul_precision",
-    "get_matmul_precision",
+    "get_matmul_precision", "set_conv_algorithm", "get_conv_algorithm",
 ]

@@ -14,7 +14,7 @@ try:
         broadcast_add, sum_reduce_rows, sum,
         matmul_ex, linear_forward,
         conv2d_forward, conv2d_backward_data, conv2d_backward_weight, conv2d_backward_bias,
-        set_matmul_precision, get_matmul_precision,
+        set_matmul_precision, get_matmul_precision, set_conv_algorithm, get_conv_algorithm,
         device_info,
     )
 except ImportError as e:  # pragma: no cover - exercised when the build is missing

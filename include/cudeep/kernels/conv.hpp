@@ -9,6 +9,14 @@
 namespace cudeep {
 namespace kernels {
 
+// Forward algorithm of launch_conv2d_forward_kernel<float>.  Auto follows the
+// reference's routing (src/kernels/conv_kernel.cu:242-248): Winograd F(4x4,
+// 3x3) for 3x3 stride-1 layers with at least 16 output pixels per image,
+// im2col + GEMM otherwise.  Winograd on another geometry throws.
+enum class ConvAlgorithm { Auto, Im2col, Winograd };
+void set_conv_algorithm(ConvAlgorithm a);
+ConvAlgorithm get_conv_algorithm();
+
 template <typename T>
 void launch_conv2d_forward_kernel(const T* input, const T* weight, const T* bias, T* output,
                                   int batch, int in_channels, int out_channels, int in_h,

@@ -288,6 +288,42 @@ def test_conv2d_layer_forward_backward_vs_oracle(cd, prec):
                           g.astype(np.float64).sum(axis=(0, 2, 3))) < 1e-5
 
 
+def test_conv_algorithm_routing(cd):
+    """launch_conv2d_forward_kernel routes like the reference
+    (conv_kernel.cu:242-248): 3x3 stride-1 layers with >= 16 output pixels
+    go to Winograd F(4x4, 3x3), the rest to im2col + GEMM; both can be forced."""
+    from cudeep_amd.cuDeep import _core
+    prev = cd.get_conv_algorithm()
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((2, 8, 14, 14)).astype(np.float32)
+    w = (rng.standard_normal((12, 8, 3, 3)) * 0.15).astype(np.float32)
+    b = (rng.standard_normal(12) * 0.1).astype(np.float32)
+    X, W, Bv = (_core.Tensor.from_numpy(a) for a in (x, w, b))
+
+    def run(algo, stride=(1, 1), pad=(1, 1), xt=X):
+        cd.set_conv_algorithm(algo)
+        return _core.conv2d_forward(xt, W, Bv, list(stride), list(pad)).numpy()
+    try:
+        cd.set_matmul_precision("fp32")
+        say("conv routing")
+        y_auto, y_wino, y_i2c = run("auto"), run("winograd"), run("im2col")
+        assert np.array_equal(y_auto, y_wino)
+        y64 = oracle.conv2d_direct64(x, w, b, (1, 1), (1, 1))
+        e_w = oracle.rel_fro(oracle.conv2d_winograd(x, w, b, padding=(1, 1)), y64)
+        e_i = oracle.rel_fro(oracle.conv2d_ref_im2col(x, w, b, (1, 1), (1, 1)), y64)
+        assert oracle.rel_fro(y_wino, y64) <= 2 * e_w
+        assert oracle.rel_fro(y_i2c, y64) <= 2 * e_i
+        # stride 2: auto takes im2col, forcing Winograd is an error
+        assert np.array_equal(run("auto", (2, 2)), run("im2col", (2, 2)))
+        with pytest.raises(RuntimeError):
+            run("winograd", (2, 2))
+        # fewer than 16 output pixels per image: im2col
+        small = _core.Tensor.from_numpy(x[:, :, :5, :5].copy())
+        assert np.array_equal(run("auto", pad=(0, 0), xt=small), run("im2col", pad=(0, 0), xt=small))
+    finally:
+        cd.set_conv_algorithm(prev)
+
+
 def test_init_distributions(cd):
     T, init = cd.Tensor, cd.init
     say("init")
