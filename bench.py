@@ -192,7 +192,19 @@ def bench_conv(steps, warmup, precision):
                       device="cuda")
     wino_ms, _ = time_launches(lambda: ops.conv2d_winograd(x, w, b, (1, 1), precision,
                                                            workspace=wws, out=y), steps, warmup)
+    # backward: data (GEMM W^T dY + col2im), weight (im2col + GEMM dY col^T), bias
+    dy = torch.randn((32, 64, 56, 56), device="cuda", generator=g)
+    dx = torch.empty_like(x)
+    dw = torch.empty_like(w)
+    db = torch.empty_like(b)
+
+    def bwd():
+        ops.conv2d_backward_data(dy, w, x.shape, (1, 1), (1, 1), precision, out=dx)
+        ops.conv2d_backward_weight(dy, x, w.shape, (1, 1), (1, 1), precision, out=dw)
+        ops.conv2d_backward_bias(dy, out=db)
+    bwd_ms, _ = time_launches(bwd, steps, warmup)
     return {"conv_ms": conv_ms, "conv_tflops": flops / (conv_ms * 1e-3) / 1e12,
+            "bwd_ms": bwd_ms, "bwd_tflops": 2 * flops / (bwd_ms * 1e-3) / 1e12,
             "im2col_ms": im_ms, "im2col_gbs": im2col_bytes / (im_ms * 1e-3) / 1e9,
             "gemm_ms_est": conv_ms - im_ms,
             "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12,

@@ -120,6 +120,40 @@ void im2col_plane_kernel(const float* __restrict__ in, float* __restrict__ col, 
 // (src/kernels/conv_kernel.cu:344-380): one thread per input element,
 // fp32 sum over kh (outer) then kw (inner), both ascending, starting from
 // 0, of every column entry that element was copied to.
+//
+// Fast form (every index below 2^31, stride 1): 32-bit index arithmetic
+// and no division per tap -- the 64-bit form spends most of its time in
+// integer division.
+__global__ __launch_bounds__(256)
+void col2im_s1_kernel32(const float* __restrict__ col, float* __restrict__ grad_in,
+                        Im2colGeom g) {
+    const uint32_t IW = (uint32_t)g.IW, IH = (uint32_t)g.IH, IC = (uint32_t)g.IC;
+    const uint32_t KH = (uint32_t)g.KH, KW = (uint32_t)g.KW, OW = (uint32_t)g.OW;
+    const int32_t OH = (int32_t)g.OH, OWs = (int32_t)g.OW;
+    const int32_t PH = (int32_t)g.PH, PW = (int32_t)g.PW;
+    const uint32_t spatial = (uint32_t)g.spatial, BS = (uint32_t)(g.batch * g.spatial);
+    const uint32_t total = (uint32_t)(g.batch * g.IC * g.IH * g.IW);
+    for (uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        const uint32_t iw = idx % IW, t1 = idx / IW;
+        const uint32_t ih = t1 % IH, t2 = t1 / IH;
+        const uint32_t ic = t2 % IC, b = t2 / IC;
+        const float* cb = col + b * spatial;
+        float acc = 0.0f;
+        for (uint32_t kh = 0; kh < KH; ++kh) {
+            const int32_t oh = (int32_t)ih + PH - (int32_t)kh;
+            if (oh < 0 || oh >= OH) continue;
+            const float* crow = cb + (ic * KH + kh) * KW * BS + (uint32_t)oh * OW;
+            for (uint32_t kw = 0; kw < KW; ++kw) {
+                const int32_t ow = (int32_t)iw + PW - (int32_t)kw;
+                if (ow < 0 || ow >= OWs) continue;
+                acc += crow[kw * BS + (uint32_t)ow];
+            }
+        }
+        grad_in[idx] = acc;
+    }
+}
+
 __global__ __launch_bounds__(256)
 void col2im_kernel(const float* __restrict__ col, float* __restrict__ grad_in, Im2colGeom g) {
     const int64_t total = g.batch * g.IC * g.IH * g.IW;
@@ -150,8 +184,28 @@ void col2im_kernel(const float* __restrict__ col, float* __restrict__ grad_in, I
 }
 
 // [B, C, S] -> [C, B*S] (NCHW grad_output to the GEMM's channel-major
-// matrix), conv_kernel.cu:383-399.  Writes are coalesced along B*S; reads
-// walk contiguous s of one (b, c) plane.
+// matrix), conv_kernel.cu:383-399: a copy of B*C contiguous planes of S
+// floats, plane (b, c) -> dst + c*B*S + b*S.  blockIdx.y = plane, 16-byte
+// copies when S % 4 == 0 and both bases are 16-byte aligned.
+__global__ __launch_bounds__(256)
+void nchw_to_cm_planes_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                              int64_t batch, int64_t C, int64_t S, int vec) {
+    const int64_t plane = blockIdx.y;
+    const int64_t b = plane / C, c = plane - b * C;
+    const float* sp = src + plane * S;
+    float* dp = dst + (c * batch + b) * S;
+    if (vec) {
+        const int64_t n4 = S / 4;
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+             i += (int64_t)gridDim.x * blockDim.x)
+            reinterpret_cast<float4*>(dp)[i] = reinterpret_cast<const float4*>(sp)[i];
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < S;
+             i += (int64_t)gridDim.x * blockDim.x)
+            dp[i] = sp[i];
+    }
+}
+
 __global__ __launch_bounds__(256)
 void nchw_to_cm_kernel(const float* __restrict__ src, float* __restrict__ dst,
                        int64_t batch, int64_t C, int64_t S) {
@@ -164,26 +218,52 @@ void nchw_to_cm_kernel(const float* __restrict__ src, float* __restrict__ dst,
     }
 }
 
-// db[c] = sum over b, s of dy[b, c, s]: one workgroup per channel, fixed
-// per-thread order then a fixed LDS tree -- deterministic.  Replaces the
-// host-side NumPy sum of the reference's Conv2dOp (python/cuDeep/tensor.py:718-721).
-__global__ __launch_bounds__(256)
+// db[c] = sum over b, s of dy[b, c, s]: one 1024-thread workgroup per
+// channel, 16-byte loads where the planes allow, a fixed per-thread order
+// then a fixed LDS tree -- deterministic.  Replaces the host-side NumPy sum
+// of the reference's Conv2dOp (python/cuDeep/tensor.py:718-721).
+constexpr int kBiasThreads = 1024;
+
+__global__ __launch_bounds__(kBiasThreads)
 void conv_bias_grad_kernel(const float* __restrict__ dy, float* __restrict__ db,
-                           int64_t batch, int64_t C, int64_t S) {
-    __shared__ float red[256];
+                           int64_t batch, int64_t C, int64_t S, int vec) {
+    __shared__ float red[kBiasThreads];
     const int64_t c = blockIdx.x;
+    const int t = threadIdx.x;
     float acc = 0.0f;
-    for (int64_t b = 0; b < batch; ++b) {
-        const float* plane = dy + (b * C + c) * S;
-        for (int64_t s = threadIdx.x; s < S; s += blockDim.x) acc += plane[s];
+    if (vec) {
+        // this thread's float4 slots of every plane, 4 planes' loads in flight
+        // at a time, summed in (plane, slot) order
+        const int64_t n4 = S / 4;
+        const int64_t cs = C * S;
+        for (int64_t i = t; i < n4; i += kBiasThreads) {
+            const float4* p4 = reinterpret_cast<const float4*>(dy + c * S) + i;
+            int64_t b = 0;
+            for (; b + 3 < batch; b += 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = *(const float4*)((const float*)p4 + (b + u) * cs);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc += ((v[u].x + v[u].y) + v[u].z) + v[u].w;
+            }
+            for (; b < batch; ++b) {
+                const float4 v = *(const float4*)((const float*)p4 + b * cs);
+                acc += ((v.x + v.y) + v.z) + v.w;
+            }
+        }
+    } else {
+        for (int64_t b = 0; b < batch; ++b) {
+            const float* plane = dy + (b * C + c) * S;
+            for (int64_t s = t; s < S; s += kBiasThreads) acc += plane[s];
+        }
     }
-    red[threadIdx.x] = acc;
+    red[t] = acc;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    for (int w = kBiasThreads / 2; w > 0; w >>= 1) {
+        if (t < w) red[t] += red[t + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) db[c] = red[0];
+    if (t == 0) db[c] = red[0];
 }
 
 unsigned grid_for(int64_t n) {
@@ -213,6 +293,13 @@ int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t I
     Im2colGeom g = make_geom(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW);
     const int64_t total = batch * IC * IH * IW;
     if (total == 0) return CDX_OK;
+    const bool fits32 = total < ((int64_t)1 << 31) &&
+                        g.IC * g.KH * g.KW * g.batch * g.spatial < ((int64_t)1 << 31);
+    if (fits32 && g.SH == 1 && g.SW == 1) {
+        hipLaunchKernelGGL(col2im_s1_kernel32, dim3(grid_for(total)), dim3(256), 0, stream, col,
+                           grad_in, g);
+        return hip_error(hipGetLastError(), "col2im_s1_kernel32 launch");
+    }
     hipLaunchKernelGGL(col2im_kernel, dim3(grid_for(total)), dim3(256), 0, stream, col, grad_in, g);
     return hip_error(hipGetLastError(), "col2im_kernel launch");
 }
@@ -221,6 +308,15 @@ int launch_nchw_to_cm_f32(const float* src, float* dst, int64_t batch, int64_t C
                           hipStream_t stream) {
     const int64_t total = batch * C * S;
     if (total == 0) return CDX_OK;
+    if (batch * C <= 65535) {
+        const int vec = S % 4 == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0;
+        const int64_t per = vec ? S / 4 : S;
+        int64_t gx = ceil_div(per, 256);
+        if (gx > 64) gx = 64;
+        hipLaunchKernelGGL(nchw_to_cm_planes_kernel, dim3((unsigned)gx, (unsigned)(batch * C)),
+                           dim3(256), 0, stream, src, dst, batch, C, S, vec);
+        return hip_error(hipGetLastError(), "nchw_to_cm_planes_kernel launch");
+    }
     hipLaunchKernelGGL(nchw_to_cm_kernel, dim3(grid_for(total)), dim3(256), 0, stream,
                        src, dst, batch, C, S);
     return hip_error(hipGetLastError(), "nchw_to_cm_kernel launch");
@@ -230,8 +326,9 @@ int launch_conv_bias_grad_f32(const float* dy, float* db, int64_t batch, int64_t
                               hipStream_t stream) {
     if (C == 0) return CDX_OK;
     if (C > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "conv bias grad: too many channels");
-    hipLaunchKernelGGL(conv_bias_grad_kernel, dim3((unsigned)C), dim3(256), 0, stream,
-                       dy, db, batch, C, S);
+    const int vec = S % 4 == 0 && (uintptr_t)dy % 16 == 0;
+    hipLaunchKernelGGL(conv_bias_grad_kernel, dim3((unsigned)C), dim3(kBiasThreads), 0, stream,
+                       dy, db, batch, C, S, vec);
     return hip_error(hipGetLastError(), "conv_bias_grad_kernel launch");
 }
 

@@ -2,9 +2,11 @@
 //   * column sums (bias gradient), replacing sum_reduce_rows_kernel
 //     (src/kernels/unary_kernel.cu:204-238), which runs one thread per 4
 //     columns serially down all rows (64 active threads for 256 columns).
-//     Here: pass 1 splits the rows into chunks of kColsumRows, 4 row-lanes x
-//     64 columns per workgroup, fixed-order fp32 sums into a partials
-//     buffer; pass 2 adds the partials in chunk order.  Deterministic.
+//     Here: pass 1 splits the rows into up to kColsumMaxChunks chunks of at
+//     least kColsumMinRows rows (enough workgroups to fill the GPU), 4
+//     row-lanes x 64 columns per workgroup, fixed-order fp32 sums into a
+//     partials buffer; pass 2 reduces the partials of each column the same
+//     way.  Deterministic.
 //   * broadcast row add (elementwise_kernel.cu:186-204).
 //   * ReLU / GELU forward and backward (activation_kernel.cu:19-52,
 //     :256-319); the GELU is the tanh form written through exp
@@ -14,37 +16,47 @@
 namespace cdx {
 namespace {
 
-constexpr int kColsumRows = 256;   // rows per pass-1 chunk
-constexpr int kColsumCols = 64;    // columns per pass-1 workgroup
+constexpr int kColsumMinRows = 32;       // rows per pass-1 chunk, at least
+constexpr int kColsumMaxChunks = 1024;   // pass-1 chunks, at most
+constexpr int kColsumCols = 64;          // columns per workgroup
 
+// Sums rows [y * chunk, (y + 1) * chunk) of each column into part[y][c]:
+// 4 row-lanes stride down the chunk, then a fixed-order combine.
 template <typename T>
 __global__ __launch_bounds__(256)
 void colsum_partial_kernel(const T* __restrict__ in, T* __restrict__ part,
-                           int64_t rows, int64_t cols) {
+                           int64_t rows, int64_t cols, int64_t chunk) {
     __shared__ T red[4][kColsumCols];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const int64_t c = (int64_t)blockIdx.x * kColsumCols + tx;
-    const int64_t r0 = (int64_t)blockIdx.y * kColsumRows;
-    int64_t r1 = r0 + kColsumRows;
+    const int64_t r0 = (int64_t)blockIdx.y * chunk;
+    int64_t r1 = r0 + chunk;
     if (r1 > rows) r1 = rows;
     T acc = 0;
-    if (c < cols)
-        for (int64_t r = r0 + ty; r < r1; r += 4) acc += in[r * cols + c];
+    if (c < cols) {
+        // groups of 8 rows per lane: the 8 loads are issued together, then
+        // added in row order (a plain loop would wait on each load in turn)
+        int64_t r = r0 + ty;
+        for (; r + 28 < r1; r += 32) {
+            T v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = in[(r + 4 * u) * cols + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; r < r1; r += 4) acc += in[r * cols + c];
+    }
     red[ty][tx] = acc;
     __syncthreads();
     if (ty == 0 && c < cols)
         part[(int64_t)blockIdx.y * cols + c] = ((red[0][tx] + red[1][tx]) + red[2][tx]) + red[3][tx];
 }
 
-template <typename T>
-__global__ __launch_bounds__(256)
-void colsum_final_kernel(const T* __restrict__ part, T* __restrict__ out,
-                         int64_t chunks, int64_t cols) {
-    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
-    T acc = 0;
-    for (int64_t i = 0; i < chunks; ++i) acc += part[i * cols + c];
-    out[c] = acc;
+int64_t colsum_chunk_rows(int64_t rows) {
+    int64_t chunks = ceil_div(rows, kColsumMinRows);
+    if (chunks > kColsumMaxChunks) chunks = kColsumMaxChunks;
+    if (chunks < 1) chunks = 1;
+    return ceil_div(rows, chunks);
 }
 
 template <typename T>
@@ -113,7 +125,16 @@ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t M, in
          i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t m = i / N, n = i - m * N;
         float v = P[i];
-        for (int s = 1; s < splits; ++s) v += P[(int64_t)s * MN + i];
+        // slices in order; 8 loads in flight per group instead of one at a time
+        int s = 1;
+        for (; s + 7 < splits; s += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = P[(int64_t)(s + u) * MN + i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        for (; s < splits; ++s) v += P[(int64_t)s * MN + i];
         if (bias_mode == CDX_BIAS_COL) v += bias[n];
         else if (bias_mode == CDX_BIAS_ROW) v += bias[m];
         v = apply_act(v, act);
@@ -140,25 +161,29 @@ int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStrea
 
 int64_t colsum_partial_rows(int64_t rows, int64_t cols) {
     (void)cols;
-    return ceil_div(rows, kColsumRows);
+    return rows > 0 ? ceil_div(rows, colsum_chunk_rows(rows)) : 1;
 }
 
 template <typename T>
 int colsum_t(const T* in, T* out, int64_t rows, int64_t cols, T* partials, int64_t partial_rows,
              hipStream_t stream) {
     if (cols <= 0) return CDX_OK;
-    if (partial_rows > 65535) return set_error(CDX_ERR_UNSUPPORTED, "sum_reduce_rows: too many rows");
     if (rows <= 0) {   // empty sum: zeros (a fill kernel, capture-safe)
         hipLaunchKernelGGL(fill_kernel<T>, dim3(grid_for(cols)), dim3(256), 0, stream, out, cols, T(0));
         return hip_error(hipGetLastError(), "fill_kernel launch");
     }
-    dim3 g1((unsigned)ceil_div(cols, kColsumCols), (unsigned)partial_rows);
-    hipLaunchKernelGGL(colsum_partial_kernel<T>, g1, dim3(256), 0, stream, in, partials, rows, cols);
+    const int64_t chunk = colsum_chunk_rows(rows);
+    const int64_t chunks = ceil_div(rows, chunk);
+    if (chunks > partial_rows) return set_error(CDX_ERR_WORKSPACE, "sum_reduce_rows: partials too small");
+    const unsigned gx = (unsigned)ceil_div(cols, kColsumCols);
+    hipLaunchKernelGGL(colsum_partial_kernel<T>, dim3(gx, (unsigned)chunks), dim3(256), 0, stream,
+                       in, partials, rows, cols, chunk);
     int st = hip_error(hipGetLastError(), "colsum_partial_kernel launch");
     if (st) return st;
-    hipLaunchKernelGGL(colsum_final_kernel<T>, dim3((unsigned)ceil_div(cols, 256)), dim3(256), 0,
-                       stream, partials, out, partial_rows, cols);
-    return hip_error(hipGetLastError(), "colsum_final_kernel launch");
+    // pass 2: the same kernel over the [chunks, cols] partials, one chunk
+    hipLaunchKernelGGL(colsum_partial_kernel<T>, dim3(gx, 1u), dim3(256), 0, stream,
+                       partials, out, chunks, cols, chunks);
+    return hip_error(hipGetLastError(), "colsum_partial_kernel launch");
 }
 
 int launch_colsum_f32(const float* in, float* out, int64_t rows, int64_t cols,

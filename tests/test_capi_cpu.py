@@ -81,7 +81,9 @@ def test_conv_argument_validation():
     # workspace size query = K_col * B * OH * OW * 4
     assert L.lib().cdx_conv2d_forward_workspace_size(32, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
         == 576 * 32 * 56 * 56 * 4
-    assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 32 * 256 * 8  # fp64-sized
+    # 8192 rows -> 256 chunks of 32 rows; partials sized for fp64
+    assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 256 * 256 * 8
+    assert L.lib().cdx_sum_reduce_rows_workspace_size(10 ** 7, 3) == 1024 * 3 * 8
     assert _status("cdx_activation_forward_f32", fake, fake, 4, 0, None) == L.CDX_ERR_INVALID_ARG
     assert _status("cdx_activation_forward_f32", fake, fake, 4, 5, None) == L.CDX_ERR_INVALID_ARG
     assert _status("cdx_activation_backward_f64", fake, fake, fake, 4, 5, None) \

@@ -138,8 +138,8 @@ def test_autograd_kat_via_gemms(kats):
     assert np.array_equal(dB, np.array(k["dB"], np.float32))
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 3), (8192, 256), (8192, 10), (1000, 1000),
-                                       (0, 5)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 3), (33, 65), (8192, 256), (8192, 10),
+                                       (1000, 1000), (100003, 7), (0, 5)])
 def test_sum_reduce_rows(rows, cols):
     rng = np.random.default_rng(rows + cols)
     x = rng.integers(-100, 100, (rows, cols)).astype(np.float32)
