@@ -192,19 +192,36 @@ def bench_conv(steps, warmup, precision):
                       device="cuda")
     wino_ms, _ = time_launches(lambda: ops.conv2d_winograd(x, w, b, (1, 1), precision,
                                                            workspace=wws, out=y), steps, warmup)
-    # backward: data (GEMM W^T dY + col2im), weight (im2col + GEMM dY col^T), bias
+    # backward: data (stride 1: im2col of dY + GEMM with the flipped filter;
+    # or Winograd on the transposed conv), weight (im2col + GEMM dY col^T), bias
     dy = torch.randn((32, 64, 56, 56), device="cuda", generator=g)
     dx = torch.empty_like(x)
     dw = torch.empty_like(w)
     db = torch.empty_like(b)
+    dws = torch.empty(ops.conv2d_backward_data_winograd_workspace_bytes(x.shape, 64, (1, 1)) // 4,
+                      device="cuda")
+
+    def bwd_data():
+        ops.conv2d_backward_data(dy, w, x.shape, (1, 1), (1, 1), precision, out=dx)
+
+    def bwd_data_wino():
+        ops.conv2d_backward_data_winograd(dy, w, x.shape, (1, 1), precision, workspace=dws, out=dx)
+
+    def bwd_weight():
+        ops.conv2d_backward_weight(dy, x, w.shape, (1, 1), (1, 1), precision, out=dw)
 
     def bwd():
-        ops.conv2d_backward_data(dy, w, x.shape, (1, 1), (1, 1), precision, out=dx)
-        ops.conv2d_backward_weight(dy, x, w.shape, (1, 1), (1, 1), precision, out=dw)
+        bwd_data_wino()
+        bwd_weight()
         ops.conv2d_backward_bias(dy, out=db)
     bwd_ms, _ = time_launches(bwd, steps, warmup)
+    bd_ms, _ = time_launches(bwd_data, steps, warmup)
+    bdw_ms, _ = time_launches(bwd_data_wino, steps, warmup)
+    bw_ms, _ = time_launches(bwd_weight, steps, warmup)
     return {"conv_ms": conv_ms, "conv_tflops": flops / (conv_ms * 1e-3) / 1e12,
             "bwd_ms": bwd_ms, "bwd_tflops": 2 * flops / (bwd_ms * 1e-3) / 1e12,
+            "bwd_data_im2col_ms": bd_ms, "bwd_data_winograd_ms": bdw_ms,
+            "bwd_weight_ms": bw_ms,
             "im2col_ms": im_ms, "im2col_gbs": im2col_bytes / (im_ms * 1e-3) / 1e9,
             "gemm_ms_est": conv_ms - im_ms,
             "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12,

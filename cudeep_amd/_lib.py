@@ -54,6 +54,8 @@ SIGNATURES = {
     "cdx_col2im_f32": (_int, [_vp, _vp] + [_i64] * 10 + [_vp]),
     "cdx_conv2d_backward_data_workspace_size": (_sz, [_i64] * 11),
     "cdx_conv2d_backward_data_f32": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),
+    "cdx_conv2d_backward_data_winograd_workspace_size": (_sz, [_i64] * 7),
+    "cdx_conv2d_backward_data_winograd_f32": (_int, [_vp, _vp, _vp] + [_i64] * 7 + [_int, _vp, _sz, _vp]),
     "cdx_conv2d_backward_weight_workspace_size": (_sz, [_i64] * 11),
     "cdx_conv2d_backward_weight_f32": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),
     "cdx_conv2d_backward_bias_f32": (_int, [_vp, _vp, _i64, _i64, _i64, _vp]),

@@ -192,12 +192,18 @@ size_t cdx_conv2d_forward_workspace_size(int64_t batch, int64_t in_channels, int
     return (size_t)(in_channels * kernel_h * kernel_w) * (size_t)(batch * OH * OW) * sizeof(float);
 }
 
-int cdx_conv2d_forward_f32(const float* input, const float* weight, const float* bias,
-                           float* output, int64_t batch, int64_t in_channels,
-                           int64_t out_channels, int64_t in_h, int64_t in_w, int64_t kernel_h,
-                           int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
-                           int64_t pad_w, int precision, void* workspace,
-                           size_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// im2col + one GEMM into NCHW; blocked_sum asks the FP32 GEMM for its
+// two-level k sum (see GemmArgs).
+int conv_forward_im2col(const float* input, const float* weight, const float* bias,
+                        float* output, int64_t batch, int64_t in_channels,
+                        int64_t out_channels, int64_t in_h, int64_t in_w, int64_t kernel_h,
+                        int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                        int64_t pad_w, int precision, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream, bool blocked_sum) {
     int st = check_conv("cdx_conv2d_forward_f32", batch, in_channels, out_channels, in_h, in_w,
                         kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w);
     if (st) return st;
@@ -230,6 +236,7 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight, const float*
         cdx::GemmArgs g{CDX_OP_N, CDX_OP_N, out_channels, BS, Kc, weight, Kc > 0 ? Kc : 1,
                         col, BS, output, S, S, out_channels * S,
                         bias, bias ? CDX_BIAS_ROW : CDX_BIAS_NONE, CDX_EPI_NONE};
+        g.blocked_sum = blocked_sum;
         st = run_gemm(precision, g, stream);
     }
     if (owned) {
@@ -237,6 +244,21 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight, const float*
         if (!st) st = st2;
     }
     return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cdx_conv2d_forward_f32(const float* input, const float* weight, const float* bias,
+                           float* output, int64_t batch, int64_t in_channels,
+                           int64_t out_channels, int64_t in_h, int64_t in_w, int64_t kernel_h,
+                           int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                           int64_t pad_w, int precision, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+    return conv_forward_im2col(input, weight, bias, output, batch, in_channels, out_channels,
+                               in_h, in_w, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w,
+                               precision, workspace, workspace_bytes, stream, false);
 }
 
 size_t cdx_conv2d_winograd_workspace_size(int64_t batch, int64_t in_channels,
@@ -319,6 +341,25 @@ ConvSizes conv_sizes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t 
     return z;
 }
 
+// Stride-1 backward data is the forward convolution of grad_output with the
+// filter channel-swapped and spatially reversed, padded KH-1-PH / KW-1-PW:
+//   dX[b,ic,ih,iw] = sum_{oc,kh,kw} dY[b,oc,ih+PH-kh,iw+PW-kw] W[oc,ic,kh,kw]
+// and with kh' = KH-1-kh the dY row is ih + kh' - (KH-1-PH).  Needs that
+// padding to be >= 0 (and OC > 0: an empty sum takes the GEMM route, which
+// writes zeros).
+bool bwd_data_as_forward(int64_t OC, int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                         int64_t PW) {
+    return OC > 0 && SH == 1 && SW == 1 && PH <= KH - 1 && PW <= KW - 1;
+}
+
+// Workspace of the implicit backward-weight kernel (0 when it does not apply).
+size_t wgrad_implicit_floats(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                             int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                             int64_t PW) {
+    if (!cdx::conv_wgrad_implicit_ok(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW)) return 0;
+    return cdx::conv_wgrad_implicit_floats(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+}
+
 // Stream-ordered scratch: the caller's workspace, or a hipMallocAsync block
 // freed on the same stream when the call ends.
 struct Scratch {
@@ -359,6 +400,12 @@ size_t cdx_conv2d_backward_data_workspace_size(int64_t batch, int64_t in_channel
         return 0;
     ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
                              stride_w, pad_h, pad_w);
+    if (bwd_data_as_forward(out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w)) {
+        // flipped filter [IC, OC, KH, KW] + im2col of grad_out [OC*KH*KW, B*IH*IW]
+        const size_t khw = (size_t)(kernel_h * kernel_w);
+        return ((size_t)in_channels * out_channels * khw +
+                (size_t)out_channels * khw * (size_t)(batch * in_h * in_w)) * sizeof(float);
+    }
     // grad_col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
     size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
     return n * sizeof(float);
@@ -387,6 +434,24 @@ int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight, 
     Scratch ws;
     st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
     if (st) return st;
+    if (bwd_data_as_forward(out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w)) {
+        // stride 1: grad_input = conv(grad_out, flipped filter, padding KH-1-PH, KW-1-PW),
+        // one im2col + one long-K GEMM straight into NCHW (no grad_col, no col2im)
+        float* wf = static_cast<float*>(ws.ptr);
+        const int64_t khw = kernel_h * kernel_w;
+        float* col = wf + in_channels * out_channels * khw;
+        st = cdx::launch_flip_filter_f32(weight, wf, out_channels, in_channels, khw, stream);
+        // The reference sums OC products per grad_col entry, then KH*KW entries
+        // in col2im; one K = OC*KH*KW running sum would be a ~KH*KW times
+        // longer rounding chain, so FP32 takes the GEMM's two-level sum.
+        if (!st)
+            st = conv_forward_im2col(grad_output, wf, nullptr, grad_input, batch, out_channels,
+                                     in_channels, z.OH, z.OW, kernel_h, kernel_w, 1, 1,
+                                     kernel_h - 1 - pad_h, kernel_w - 1 - pad_w, precision, col,
+                                     need - (size_t)in_channels * out_channels * khw * sizeof(float),
+                                     stream, true);
+        return ws.release(st);
+    }
     float* grad_col = static_cast<float*>(ws.ptr);
     const float* dy_cm = grad_output;                   // batch 1: NCHW is [OC, S] already
     if (batch > 1) {
@@ -406,6 +471,55 @@ int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight, 
     return ws.release(st);
 }
 
+size_t cdx_conv2d_backward_data_winograd_workspace_size(int64_t batch, int64_t in_channels,
+                                                        int64_t out_channels, int64_t in_h,
+                                                        int64_t in_w, int64_t pad_h,
+                                                        int64_t pad_w) {
+    const char* fn = "cdx_conv2d_backward_data_winograd_workspace_size";
+    if (check_conv(fn, batch, in_channels, out_channels, in_h, in_w, 3, 3, 1, 1, pad_h, pad_w))
+        return 0;
+    if (pad_h > 2 || pad_w > 2) {
+        set_error(CDX_ERR_UNSUPPORTED, std::string(fn) + ": padding above 2");
+        return 0;
+    }
+    // the transposed problem: OC input channels -> IC output channels, IH x IW out
+    return cdx::winograd_workspace_floats(batch, out_channels, in_channels, in_h, in_w) *
+           sizeof(float);
+}
+
+int cdx_conv2d_backward_data_winograd_f32(const float* grad_output, const float* weight,
+                                          float* grad_input, int64_t batch, int64_t in_channels,
+                                          int64_t out_channels, int64_t in_h, int64_t in_w,
+                                          int64_t pad_h, int64_t pad_w, int precision,
+                                          void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
+    const char* fn = "cdx_conv2d_backward_data_winograd_f32";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, 3, 3, 1, 1, pad_h, pad_w);
+    if (st) return st;
+    if (pad_h > 2 || pad_w > 2)
+        return set_error(CDX_ERR_UNSUPPORTED, std::string(fn) + ": padding above 2");
+    if (!valid_precision(precision))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
+    if (batch * in_channels * in_h * in_w == 0) return CDX_OK;
+    if (!grad_input || (out_channels > 0 && (!grad_output || !weight)))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    if (out_channels == 0)   // empty sum: zeros, through the GEMM route
+        return cdx_conv2d_backward_data_f32(grad_output, weight, grad_input, batch, in_channels,
+                                            0, in_h, in_w, 3, 3, 1, 1, pad_h, pad_w, precision,
+                                            nullptr, 0, stream);
+    const int64_t OH = in_h + 2 * pad_h - 2, OW = in_w + 2 * pad_w - 2;
+    const size_t need =
+        cdx::winograd_workspace_floats(batch, out_channels, in_channels, in_h, in_w) * sizeof(float);
+    Scratch ws;
+    st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
+    if (st) return st;
+    st = cdx::launch_conv2d_winograd_f32(grad_output, weight, nullptr, grad_input, batch,
+                                         out_channels, in_channels, OH, OW, 2 - pad_h, 2 - pad_w,
+                                         precision, static_cast<float*>(ws.ptr), stream,
+                                         /*flip_filter=*/true);
+    return ws.release(st);
+}
+
 size_t cdx_conv2d_backward_weight_workspace_size(int64_t batch, int64_t in_channels,
                                                  int64_t out_channels, int64_t in_h, int64_t in_w,
                                                  int64_t kernel_h, int64_t kernel_w,
@@ -416,9 +530,12 @@ size_t cdx_conv2d_backward_weight_workspace_size(int64_t batch, int64_t in_chann
         return 0;
     ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
                              stride_w, pad_h, pad_w);
-    // col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
+    // enough for either route: col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
+    // (GEMM route), or the implicit kernel's split partials
     size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
-    return n * sizeof(float);
+    const size_t imp = wgrad_implicit_floats(batch, in_channels, out_channels, in_h, in_w,
+                                             kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w);
+    return (n > imp ? n : imp) * sizeof(float);
 }
 
 int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
@@ -441,6 +558,25 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
     const size_t need = cdx_conv2d_backward_weight_workspace_size(
         batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
         pad_h, pad_w);
+    if (z.BS > 0 && cdx::conv_wgrad_implicit_ok(batch, in_channels, out_channels, in_h, in_w,
+                                                kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                                                pad_w)) {
+        // implicit GEMM from the NCHW tensors (no col buffer).  Its FP32 MFMA
+        // products are also what the TF32 modes get: exact products, faster
+        // here than im2col + the split-bf16 GEMM, within both error bounds.
+        Scratch ws;
+        st = ws.acquire(workspace, workspace_bytes,
+                        wgrad_implicit_floats(batch, in_channels, out_channels, in_h, in_w,
+                                              kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                                              pad_w) * sizeof(float),
+                        stream, fn);
+        if (st) return st;
+        st = cdx::launch_conv_wgrad_f32(grad_output, input, grad_weight,
+                                        static_cast<float*>(ws.ptr), batch, in_channels,
+                                        out_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                                        stride_w, pad_h, pad_w, stream);
+        return ws.release(st);
+    }
     Scratch ws;
     st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
     if (st) return st;

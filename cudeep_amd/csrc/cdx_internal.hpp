@@ -41,6 +41,10 @@ struct GemmArgs {
     // Batched form: `batch` independent problems, problem z at A + z*stride_a,
     // B + z*stride_b, C + z*stride_c (elements); bias shared.
     int64_t batch = 1, stride_a = 0, stride_b = 0, stride_c = 0;
+    // FP32 NN products only: sum k in two levels (32-k partial sums added to
+    // the running total) instead of one running sum -- a rounding-error
+    // chain of ~32 + K/32 additions instead of ~K.
+    bool blocked_sum = false;
 };
 
 // Launchers (no argument validation: the C-ABI validates first).
@@ -104,12 +108,32 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
                       hipStream_t stream);
 
 // Winograd F(4x4, 3x3) forward for 3x3 stride-1 convolution; ws holds
-// winograd_workspace_floats(...) floats (U, V and M).
+// winograd_workspace_floats(...) floats (U, V and M).  With flip_filter the
+// filter is read as the stride-1 transposed convolution's: weight is
+// [IC][OC][3][3] (the forward layer's OIHW with O = this call's IC) and is
+// used channel-swapped and spatially reversed (backward data).
 size_t winograd_workspace_floats(int64_t batch, int64_t IC, int64_t OC, int64_t OH, int64_t OW);
 int launch_conv2d_winograd_f32(const float* input, const float* weight, const float* bias,
                                float* output, int64_t batch, int64_t IC, int64_t OC,
                                int64_t IH, int64_t IW, int64_t PH, int64_t PW, int precision,
-                               float* ws, hipStream_t stream);
+                               float* ws, hipStream_t stream, bool flip_filter = false);
+
+// wf[ic][oc][k'] = w[oc][ic][KHW-1-k'] (stride-1 transposed-conv filter).
+int launch_flip_filter_f32(const float* w, float* wf, int64_t OC, int64_t IC, int64_t KHW,
+                           hipStream_t stream);
+
+// Conv backward weight as an implicit GEMM (FP32 MFMA; operands gathered
+// from NCHW dY and x, no column buffer).  `ws` holds
+// conv_wgrad_implicit_floats(...) floats (the split partials).
+bool conv_wgrad_implicit_ok(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                            int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                            int64_t PW);
+size_t conv_wgrad_implicit_floats(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                                  int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                                  int64_t PW);
+int launch_conv_wgrad_f32(const float* dy, const float* x, float* dw, float* ws, int64_t batch,
+                          int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                          int64_t SH, int64_t SW, int64_t PH, int64_t PW, hipStream_t stream);
 
 int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,

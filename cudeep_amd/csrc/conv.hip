@@ -266,6 +266,21 @@ void conv_bias_grad_kernel(const float* __restrict__ dy, float* __restrict__ db,
     if (t == 0) db[c] = red[0];
 }
 
+// wf[ic, oc, k'] = w[oc, ic, KHW-1-k']: the filter of the stride-1
+// transposed convolution (channels swapped, both spatial axes reversed; the
+// flattened kh*KW+kw index reverses as a whole).
+__global__ __launch_bounds__(256)
+void flip_filter_kernel(const float* __restrict__ w, float* __restrict__ wf, int64_t OC,
+                        int64_t IC, int64_t KHW) {
+    const int64_t total = OC * IC * KHW;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t k = i % KHW, p = i / KHW;      // p = oc * IC + ic
+        const int64_t oc = p / IC, ic = p - oc * IC;
+        wf[(ic * OC + oc) * KHW + (KHW - 1 - k)] = w[i];
+    }
+}
+
 unsigned grid_for(int64_t n) {
     int64_t b = ceil_div(n, 256);
     if (b > 65536) b = 65536;
@@ -320,6 +335,15 @@ int launch_nchw_to_cm_f32(const float* src, float* dst, int64_t batch, int64_t C
     hipLaunchKernelGGL(nchw_to_cm_kernel, dim3(grid_for(total)), dim3(256), 0, stream,
                        src, dst, batch, C, S);
     return hip_error(hipGetLastError(), "nchw_to_cm_kernel launch");
+}
+
+int launch_flip_filter_f32(const float* w, float* wf, int64_t OC, int64_t IC, int64_t KHW,
+                           hipStream_t stream) {
+    const int64_t total = OC * IC * KHW;
+    if (total == 0) return CDX_OK;
+    hipLaunchKernelGGL(flip_filter_kernel, dim3(grid_for(total)), dim3(256), 0, stream, w, wf,
+                       OC, IC, KHW);
+    return hip_error(hipGetLastError(), "flip_filter_kernel launch");
 }
 
 int launch_conv_bias_grad_f32(const float* dy, float* db, int64_t batch, int64_t C, int64_t S,

@@ -122,7 +122,9 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int grou
     tn = in_g / gsize;
 }
 
-template <class CF, int OPA, int OPB, int MODE, bool SPLITN>
+// BLK: two-level k sum -- each pair of k-tiles (32 k) is summed from zero in
+// `part`, then added to `acc` (a rounding chain of ~32 + K/32 additions).
+template <class CF, int OPA, int OPB, int MODE, bool SPLITN, bool BLK>
 __global__ __launch_bounds__(CF::NT)
 void gemm_f32_mfma_kernel(KParams p) {
     constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
@@ -184,13 +186,28 @@ void gemm_f32_mfma_kernel(KParams p) {
         b.template store<B_STRIDE>(sB, tid);
     };
 
-    floatx4 acc[FM][FN];
+    floatx4 acc[FM][FN], part[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FN; ++j) {
+            acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    floatx4 (&tgt)[FM][FN] = BLK ? part : acc;
+    // BLK: fold the partial sum into the total and restart it
+    auto flush = [&]() {
+        if (!BLK) return;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                acc[i][j] += part[i][j];
+                part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+    };
 
-    // MFMAs over the k-tile held in LDS stage `buf`
+    // MFMAs over the k-tile held in LDS stage `buf`, into `tgt`
     auto compute = [&](int buf) {
         const float* sA = lds + buf * (A_ELEMS + B_ELEMS);
         const float* sB = sA + A_ELEMS;
@@ -225,8 +242,8 @@ void gemm_f32_mfma_kernel(KParams p) {
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
                     for (int jn = 0; jn < FN; ++jn)
-                        acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[jn][j],
-                                                                         acc[i][jn], 0, 0, 0);
+                        tgt[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][j], b[jn][j],
+                                                                         tgt[i][jn], 0, 0, 0);
         }
     };
 
@@ -252,6 +269,7 @@ void gemm_f32_mfma_kernel(KParams p) {
             compute(1);
             store_from(la, lb, 0);
             __syncthreads();
+            flush();
         }
         if (kt + 2 < nk) {            // three tiles left
             load_into(la, lb, (kt + 2) * BK);
@@ -261,6 +279,7 @@ void gemm_f32_mfma_kernel(KParams p) {
             compute(1);
             store_from(la, lb, 0);
             __syncthreads();
+            flush();
             compute(0);
         } else {                      // two tiles left
             compute(0);
@@ -268,6 +287,7 @@ void gemm_f32_mfma_kernel(KParams p) {
             __syncthreads();
             compute(1);
         }
+        flush();
     } else {
         // One staging set: tile k+1 is in flight during the MFMAs of tile k.
         load_into(la, lb, 0);
@@ -280,7 +300,9 @@ void gemm_f32_mfma_kernel(KParams p) {
             compute(buf);
             if (has_next) store_from(la, lb, buf ^ 1);
             __syncthreads();
+            if (kt & 1) flush();
         }
+        flush();
     }
 
     // epilogue: bias, activation and the output map, straight from the
@@ -290,17 +312,17 @@ void gemm_f32_mfma_kernel(KParams p) {
     write_acc<FM, FN, MODE != kLoadAlignedVec, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
 }
 
-template <class CF, int OPA, int OPB, int MODE, bool SPLITN>
+template <class CF, int OPA, int OPB, int MODE, bool SPLITN, bool BLK>
 int launch_cfg(const KParams& kp, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
     if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
-    hipLaunchKernelGGL((gemm_f32_mfma_kernel<CF, OPA, OPB, MODE, SPLITN>),
+    hipLaunchKernelGGL((gemm_f32_mfma_kernel<CF, OPA, OPB, MODE, SPLITN, BLK>),
                        dim3((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch), dim3(CF::NT), 0, stream, kp);
     return hip_error(hipGetLastError(), "gemm_f32_mfma_kernel launch");
 }
 
-template <class CF, int OPA, int OPB>
+template <class CF, int OPA, int OPB, bool BLK>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
                g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
@@ -314,15 +336,15 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned) {
-        return split ? launch_cfg<CF, OPA, OPB, kLoadAlignedVec, true>(kp, splits, stream)
-                     : launch_cfg<CF, OPA, OPB, kLoadAlignedVec, false>(kp, splits, stream);
+        return split ? launch_cfg<CF, OPA, OPB, kLoadAlignedVec, true, BLK>(kp, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, kLoadAlignedVec, false, BLK>(kp, splits, stream);
     }
     if (vec) {
-        return split ? launch_cfg<CF, OPA, OPB, kLoadCheckedVec, true>(kp, splits, stream)
-                     : launch_cfg<CF, OPA, OPB, kLoadCheckedVec, false>(kp, splits, stream);
+        return split ? launch_cfg<CF, OPA, OPB, kLoadCheckedVec, true, BLK>(kp, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, kLoadCheckedVec, false, BLK>(kp, splits, stream);
     }
-    return split ? launch_cfg<CF, OPA, OPB, kLoadScalar, true>(kp, splits, stream)
-                 : launch_cfg<CF, OPA, OPB, kLoadScalar, false>(kp, splits, stream);
+    return split ? launch_cfg<CF, OPA, OPB, kLoadScalar, true, BLK>(kp, splits, stream)
+                 : launch_cfg<CF, OPA, OPB, kLoadScalar, false, BLK>(kp, splits, stream);
 }
 
 template <class CF>
@@ -330,11 +352,18 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
     const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
     return with_splitk(g0, tiles, CF::BK, stream,
                        [&](const GemmArgs& g, int splits, int64_t k_chunk) {
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N>(g, splits, k_chunk, stream);
-        return launch_mode<CF, CDX_OP_T, CDX_OP_T>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N, false>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T, false>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N, false>(g, splits, k_chunk, stream);
+        return launch_mode<CF, CDX_OP_T, CDX_OP_T, false>(g, splits, k_chunk, stream);
     });
+}
+
+// Two-level k sum (GemmArgs::blocked_sum), NN products only, no split-K
+// (a split already sums in two levels).
+template <class CF>
+int launch_blocked(const GemmArgs& g, hipStream_t stream) {
+    return launch_mode<CF, CDX_OP_N, CDX_OP_N, true>(g, 1, g.K, stream);
 }
 
 // Tile configurations (chosen by measurement on MI355X; 4096^3 NN).  All use
@@ -363,9 +392,15 @@ using CfgSplitK = Cfg<64, 64, 16, 32, 32, 8, 2>;
 }  // namespace
 
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
+    const bool split = g.batch == 1 && splitk_applies(ceil_div(g.M, 64) * ceil_div(g.N, 64), g.K);
+    if (g.blocked_sum && !split && g.opA == CDX_OP_N && g.opB == CDX_OP_N) {
+        if (g.N <= 16) return launch_blocked<CfgNarrowN>(g, stream);
+        if (g.M <= 64 && g.N >= 4096) return launch_blocked<CfgSkinnyM>(g, stream);
+        if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 512) return launch_blocked<CfgLarge>(g, stream);
+        return launch_blocked<CfgMedium>(g, stream);
+    }
     if (g.N <= 16) return launch_ops<CfgNarrowN>(g, stream);
-    if (g.batch == 1 && splitk_applies(ceil_div(g.M, 64) * ceil_div(g.N, 64), g.K))
-        return launch_ops<CfgSplitK>(g, stream);
+    if (split) return launch_ops<CfgSplitK>(g, stream);
     if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
     // Large tiles once there are at least two per CU (256 CUs).
     int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);

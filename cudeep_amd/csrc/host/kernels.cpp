@@ -168,9 +168,30 @@ void launch_conv2d_backward_data_kernel<float>(const float* grad_output, const f
                                                float* grad_input, int batch, int IC, int OC,
                                                int IH, int IW, int KH, int KW, int SH, int SW,
                                                int PH, int PW, hipStream_t stream) {
-    CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_f32(grad_output, weight, grad_input, batch, IC, OC,
-                                                  IH, IW, KH, KW, SH, SW, PH, PW,
-                                                  g_precision.load(), nullptr, 0, stream));
+    // The forward's rule, applied to the transposed convolution that
+    // produces grad_input (3x3, stride 1, padding 2 - P >= 0, IH*IW pixels),
+    // in the TF32 modes only: the reference's backward data is GEMM +
+    // col2im, and in FP32 the Winograd transforms' rounding (~10x that
+    // route's error) would not stay within twice its error, so Auto keeps
+    // the GEMM route there.
+    const int prec = g_precision.load();
+    const bool wino_ok = KH == 3 && KW == 3 && SH == 1 && SW == 1 && PH <= 2 && PW <= 2;
+    const ConvAlgorithm algo = get_conv_algorithm();
+    if (algo == ConvAlgorithm::Winograd && !wino_ok)
+        throw std::runtime_error(
+            "conv2d backward: Winograd needs a 3x3 kernel with stride 1 and padding <= 2");
+    const bool wino = algo == ConvAlgorithm::Winograd ||
+                      (algo == ConvAlgorithm::Auto && wino_ok && (int64_t)IH * IW >= 16 &&
+                       prec != CDX_PREC_FP32);
+    if (wino) {
+        CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_winograd_f32(grad_output, weight, grad_input,
+                                                               batch, IC, OC, IH, IW, PH, PW,
+                                                               prec, nullptr, 0, stream));
+    } else {
+        CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_f32(grad_output, weight, grad_input, batch, IC,
+                                                      OC, IH, IW, KH, KW, SH, SW, PH, PW, prec,
+                                                      nullptr, 0, stream));
+    }
 }
 
 template <>

@@ -15,6 +15,9 @@
 //   Y (NCHW)           output transform + bias, one thread per (oc, tile),
 //                      16-byte stores of the 4-wide output rows where the
 //                      tile is whole and aligned.
+// Backward data of a 3x3 stride-1 layer runs the same pipeline on the
+// transposed convolution (grad_output in, the filter read channel-swapped
+// and spatially reversed by the filter transform, padding 2 - P).
 // Compared with im2col + GEMM this moves ~2.3x fewer HBM bytes at C5
 // (V and M are 36/16 of the input / output size, against the 9x im2col
 // buffer) and does 4x fewer multiplies in the GEMM.
@@ -56,12 +59,25 @@ __device__ __forceinline__ void wino_at(const float* m, float* o) {
     o[3] = m[1] - m[2] + 8.0f * m[3] - 8.0f * m[4] + m[5];
 }
 
+// FLIP: w is [IC][OC][3][3] and filter (oc, ic) is w[ic][oc] with both
+// spatial axes reversed (tap t read from 8 - t): the stride-1 transposed
+// convolution's filter, for backward data.
+template <bool FLIP>
 __global__ __launch_bounds__(256)
 void wino_filter_kernel(const float* __restrict__ w, float* __restrict__ U, int64_t OC,
                         int64_t IC) {
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // oc * IC + ic
     if (p >= OC * IC) return;
-    const float* g = w + p * 9;
+    float g[9];
+    if (FLIP) {
+        const int64_t oc = p / IC, ic = p - oc * IC;
+        const float* src = w + (ic * OC + oc) * 9;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) g[t] = src[8 - t];
+    } else {
+#pragma unroll
+        for (int t = 0; t < 9; ++t) g[t] = w[p * 9 + t];
+    }
     float tmp[6][3], u[6];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
@@ -174,7 +190,7 @@ size_t winograd_workspace_floats(int64_t batch, int64_t IC, int64_t OC, int64_t 
 int launch_conv2d_winograd_f32(const float* input, const float* weight, const float* bias,
                                float* output, int64_t batch, int64_t IC, int64_t OC,
                                int64_t IH, int64_t IW, int64_t PH, int64_t PW, int precision,
-                               float* ws, hipStream_t stream) {
+                               float* ws, hipStream_t stream, bool flip_filter) {
     WinoGeom g;
     g.B = batch; g.IC = IC; g.OC = OC; g.IH = IH; g.IW = IW; g.PH = PH; g.PW = PW;
     g.OH = IH + 2 * PH - 2; g.OW = IW + 2 * PW - 2;
@@ -188,8 +204,12 @@ int launch_conv2d_winograd_f32(const float* input, const float* weight, const fl
     float* V = U + 36 * OC * IC;
     float* Mm = V + 36 * IC * g.NT;
 
-    hipLaunchKernelGGL(wino_filter_kernel, dim3(blocks_for(OC * IC)), dim3(256), 0, stream,
-                       weight, U, OC, IC);
+    if (flip_filter)
+        hipLaunchKernelGGL(wino_filter_kernel<true>, dim3(blocks_for(OC * IC)), dim3(256), 0,
+                           stream, weight, U, OC, IC);
+    else
+        hipLaunchKernelGGL(wino_filter_kernel<false>, dim3(blocks_for(OC * IC)), dim3(256), 0,
+                           stream, weight, U, OC, IC);
     int st = hip_error(hipGetLastError(), "wino_filter_kernel launch");
     if (st) return st;
     hipLaunchKernelGGL(wino_input_kernel, dim3(blocks_for(IC * g.NT)), dim3(256), 0, stream,

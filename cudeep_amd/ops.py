@@ -350,6 +350,34 @@ def conv2d_backward_data(grad_out, w, x_shape, stride=(1, 1), padding=(0, 0),
     return out
 
 
+def conv2d_backward_data_winograd(grad_out, w, x_shape, padding=(0, 0), precision=L.PREC_FP32,
+                                  workspace=None, out=None):
+    """grad_input of a 3x3 stride-1 conv by Winograd F(4x4, 3x3) on the
+    transposed convolution (cdx_conv2d_backward_data_winograd_f32)."""
+    _need(grad_out, "grad_output")
+    _need(w, "weight")
+    Bn, C, H, W, OC, KH, KW, OH, OW = _conv_geom(tuple(x_shape), tuple(w.shape), (1, 1), padding)
+    if (KH, KW) != (3, 3) or padding[0] > 2 or padding[1] > 2:
+        raise ValueError("conv2d_backward_data_winograd: needs a 3x3 kernel and padding <= 2")
+    if tuple(grad_out.shape) != (Bn, OC, OH, OW) or not grad_out.is_contiguous() \
+            or not w.is_contiguous():
+        raise ValueError("conv2d_backward_data_winograd: bad grad_output / weight")
+    if out is None:
+        out = torch.empty((Bn, C, H, W), device=w.device, dtype=torch.float32)
+    ws_ptr, ws_bytes = (0, 0) if workspace is None else (workspace.data_ptr(),
+                                                         workspace.numel() * workspace.element_size())
+    L.call("cdx_conv2d_backward_data_winograd_f32", grad_out.data_ptr(), w.data_ptr(),
+           out.data_ptr(), Bn, C, OC, H, W, padding[0], padding[1], precision,
+           ws_ptr or None, ws_bytes, _stream())
+    return out
+
+
+def conv2d_backward_data_winograd_workspace_bytes(x_shape, out_channels, padding=(0, 0)) -> int:
+    Bn, C, H, W = x_shape
+    return int(L.lib().cdx_conv2d_backward_data_winograd_workspace_size(
+        Bn, C, out_channels, H, W, padding[0], padding[1]))
+
+
 def conv2d_backward_weight(grad_out, x, w_shape, stride=(1, 1), padding=(0, 0),
                            precision=L.PREC_FP32, out=None):
     _need(grad_out, "grad_output")

@@ -9,10 +9,15 @@
 namespace cudeep {
 namespace kernels {
 
-// Forward algorithm of launch_conv2d_forward_kernel<float>.  Auto follows the
-// reference's routing (src/kernels/conv_kernel.cu:242-248): Winograd F(4x4,
+// Algorithm of launch_conv2d_forward_kernel<float> and
+// launch_conv2d_backward_data_kernel<float>.  Auto follows the reference's
+// forward routing (src/kernels/conv_kernel.cu:242-248): Winograd F(4x4,
 // 3x3) for 3x3 stride-1 layers with at least 16 output pixels per image,
-// im2col + GEMM otherwise.  Winograd on another geometry throws.
+// im2col + GEMM otherwise; backward data applies the same rule to the
+// transposed convolution it runs (3x3, stride 1, padding <= 2, at least 16
+// input pixels per image) in the TF32 modes, and keeps the GEMM route in
+// FP32 (whose error bound is twice the reference's GEMM + col2im route).
+// Winograd on another geometry throws.
 enum class ConvAlgorithm { Auto, Im2col, Winograd };
 void set_conv_algorithm(ConvAlgorithm a);
 ConvAlgorithm get_conv_algorithm();

@@ -201,10 +201,17 @@ int cdx_col2im_f32(const float* col, float* grad_input,
                    int64_t stride_h, int64_t stride_w,
                    int64_t pad_h, int64_t pad_w, hipStream_t stream);
 
-/* Conv backward data: grad_col = weight^T * grad_out[OC, B*S] (one GEMM with
- * a transposed operand, no weight transpose pass), then col2im.
+/* Conv backward data.  Stride 1 (with pad_h <= kernel_h - 1, pad_w <=
+ * kernel_w - 1): the forward convolution of grad_out with the filter
+ * channel-swapped and spatially reversed, padded kernel - 1 - pad (im2col of
+ * grad_out + one long-K GEMM written straight to NCHW; in FP32 the GEMM
+ * sums k in two levels, keeping the rounding chain no longer than the
+ * reference's OC-term dot products + KH*KW-term col2im sums).  Other strides:
+ * grad_col = weight^T * grad_out[OC, B*S] (one GEMM with a transposed
+ * operand, no weight transpose pass), then col2im.  Both compute the
+ * reference's sums (src/kernels/conv_kernel.cu:417-478) in another order.
  * Replaces cudeep::kernels::launch_conv2d_backward_data_kernel<float>
- * (include/cudeep/kernels/conv.cuh:18-26, src/kernels/conv_kernel.cu:417-478).
+ * (include/cudeep/kernels/conv.cuh:18-26).
  * grad_input is overwritten.  workspace may be NULL. */
 size_t cdx_conv2d_backward_data_workspace_size(
     int64_t batch, int64_t in_channels, int64_t out_channels, int64_t in_h, int64_t in_w,
@@ -220,9 +227,32 @@ int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight,
                                  void* workspace, size_t workspace_bytes,
                                  hipStream_t stream);
 
-/* Conv backward weight: grad_weight[OC, K_col] = grad_out[OC, B*S] * col^T
- * (the col buffer read transposed by the GEMM -- no col transpose pass; the
- * long K = B*S is split across workgroups and reduced in a fixed order).
+/* Conv backward data of a 3x3 stride-1 layer by Winograd F(4x4, 3x3): the
+ * forward Winograd convolution of grad_out with the channel-swapped,
+ * spatially reversed filter, padded 2 - pad (pad_h, pad_w <= 2).  Same
+ * arguments and meaning as cdx_conv2d_backward_data_f32 for kernel 3x3,
+ * stride 1; errors are those of the Winograd forward.  The reference has no
+ * Winograd backward (its backward data is conv_kernel.cu:417-478); this is
+ * the faster route to the same gradient for the layers whose forward it
+ * runs by Winograd (:242-248). */
+size_t cdx_conv2d_backward_data_winograd_workspace_size(
+    int64_t batch, int64_t in_channels, int64_t out_channels,
+    int64_t in_h, int64_t in_w, int64_t pad_h, int64_t pad_w);
+int cdx_conv2d_backward_data_winograd_f32(const float* grad_output, const float* weight,
+                                          float* grad_input,
+                                          int64_t batch, int64_t in_channels,
+                                          int64_t out_channels, int64_t in_h, int64_t in_w,
+                                          int64_t pad_h, int64_t pad_w, int precision,
+                                          void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream);
+
+/* Conv backward weight: grad_weight[OC, K_col] = grad_out[OC, B*S] * col^T,
+ * as an implicit FP32-MFMA GEMM that gathers both operands from the NCHW
+ * grad_out and input: no col buffer, no reshape.
+ * All precisions take it (exact fp32 products meet the TF32 bounds too);
+ * problems beyond its 32-bit index range fall back to im2col + a GEMM that
+ * reads col transposed.  The long K = B*S is split across workgroups and
+ * reduced in a fixed order.  The workspace size covers both routes.
  * Replaces cudeep::kernels::launch_conv2d_backward_weight_kernel<float>
  * (include/cudeep/kernels/conv.cuh:28-36, src/kernels/conv_kernel.cu:486-545).
  * grad_weight is overwritten.  workspace may be NULL. */

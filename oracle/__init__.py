@@ -292,6 +292,23 @@ def conv2d_backward_data64(dy, w, x_shape, stride=(1, 1), padding=(0, 0)):
     return col2im(gcol, x_shape, KH, KW, stride[0], stride[1], padding[0], padding[1])
 
 
+def flip_filter(w):
+    """The stride-1 transposed convolution's filter: wf[ic, oc] = w[oc, ic]
+    with both spatial axes reversed."""
+    return np.ascontiguousarray(np.asarray(w, np.float32)[:, :, ::-1, ::-1].transpose(1, 0, 2, 3))
+
+
+def conv2d_backward_data_winograd(dy, w, x_shape, padding=(0, 0), double=False, tf32=None):
+    """grad_input of a 3x3 stride-1 conv as the Winograd forward of grad_out
+    with the flipped filter, padded 2 - P (the reference's Winograd route,
+    conv_kernel.cu:557-789, applied to the transposed convolution)."""
+    PH, PW = padding
+    dx = conv2d_winograd(dy, flip_filter(w), None, padding=(2 - PH, 2 - PW), double=double,
+                         tf32=tf32)
+    assert dx.shape == tuple(x_shape)
+    return dx
+
+
 def conv2d_backward_weight_ref(dy, x, w_shape, stride=(1, 1), padding=(0, 0), mode="fp32"):
     """The reference's backward-weight route (conv_kernel.cu:486-545):
     dW [OC, Kc] = dY [OC, B*S] @ col^T (seq-FMA, or the TF32 emulation)."""

@@ -81,6 +81,27 @@ def test_conv_argument_validation():
     # workspace size query = K_col * B * OH * OW * 4
     assert L.lib().cdx_conv2d_forward_workspace_size(32, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
         == 576 * 32 * 56 * 56 * 4
+    # backward data, stride 1: flipped filter + im2col of grad_out [OC*9, B*IH*IW]
+    assert L.lib().cdx_conv2d_backward_data_workspace_size(32, 64, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
+        == (64 * 64 * 9 + 64 * 9 * 32 * 56 * 56) * 4
+    # stride 2: grad_col [K_col, B*S] + grad_out in [OC, B*S]
+    assert L.lib().cdx_conv2d_backward_data_workspace_size(2, 3, 4, 9, 9, 3, 3, 2, 2, 1, 1) \
+        == (27 * 2 * 25 + 4 * 2 * 25) * 4
+    # padding above kernel - 1 keeps the col2im route
+    assert L.lib().cdx_conv2d_backward_data_workspace_size(1, 3, 4, 5, 5, 3, 3, 1, 1, 3, 0) \
+        == 27 * 9 * 3 * 4
+    # backward weight: the larger of the GEMM route (col + reshaped grad_out)
+    # and the implicit route's split partials
+    assert L.lib().cdx_conv2d_backward_weight_workspace_size(32, 64, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
+        == (576 + 64) * 32 * 3136 * 4
+    # Winograd backward data: the transposed problem (OC in, IC out, IH x IW tiles)
+    assert L.lib().cdx_conv2d_backward_data_winograd_workspace_size(32, 64, 64, 56, 56, 1, 1) \
+        == 36 * (64 * 64 + 2 * 64 * 32 * 14 * 14) * 4
+    assert L.lib().cdx_conv2d_backward_data_winograd_workspace_size(1, 2, 2, 8, 8, 3, 3) == 0
+    assert _status("cdx_conv2d_backward_data_winograd_f32", fake, fake, fake, 1, 2, 2, 8, 8, 3, 0,
+                   0, None, 0, None) == L.CDX_ERR_UNSUPPORTED
+    assert _status("cdx_conv2d_backward_data_winograd_f32", fake, fake, fake, 1, 2, 2, 8, 8, 1, 1,
+                   0, fake, 4, None) == L.CDX_ERR_WORKSPACE
     # 8192 rows -> 256 chunks of 32 rows; partials sized for fp64
     assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 256 * 256 * 8
     assert L.lib().cdx_sum_reduce_rows_workspace_size(10 ** 7, 3) == 1024 * 3 * 8

@@ -183,6 +183,12 @@ BWD_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
     (3, 4, 6, 5, 5, 2, 2, 1, 1, 1, 0),
     (4, 16, 28, 28, 32, 3, 3, 1, 1, 1, 1),
     (2, 8, 15, 17, 6, 1, 1, 2, 2, 0, 0),
+    # stride 1: flipped-filter forward route, incl. padding = kernel - 1,
+    # 1x1, and padding above kernel - 1 (falls back to GEMM + col2im)
+    (2, 5, 9, 4, 3, 5, 3, 1, 1, 4, 1),
+    (1, 8, 15, 17, 6, 1, 1, 1, 1, 0, 0),
+    (2, 3, 6, 7, 4, 3, 3, 1, 1, 3, 0),
+    (2, 33, 10, 30, 65, 3, 3, 1, 1, 0, 2),
 ]
 
 

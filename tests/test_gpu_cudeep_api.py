@@ -295,7 +295,8 @@ def test_conv2d_layer_forward_backward_vs_oracle(cd, prec):
 def test_conv_algorithm_routing(cd):
     """launch_conv2d_forward_kernel routes like the reference
     (conv_kernel.cu:242-248): 3x3 stride-1 layers with >= 16 output pixels
-    go to Winograd F(4x4, 3x3), the rest to im2col + GEMM; both can be forced."""
+    go to Winograd F(4x4, 3x3), the rest to im2col + GEMM; both can be
+    forced.  Backward data follows the same rule on its transposed conv."""
     from cudeep_amd.cuDeep import _core
     prev = cd.get_conv_algorithm()
     rng = np.random.default_rng(12)
@@ -324,6 +325,30 @@ def test_conv_algorithm_routing(cd):
         # fewer than 16 output pixels per image: im2col
         small = _core.Tensor.from_numpy(x[:, :, :5, :5].copy())
         assert np.array_equal(run("auto", pad=(0, 0), xt=small), run("im2col", pad=(0, 0), xt=small))
+
+        # backward data: the same rule on the transposed convolution in the
+        # TF32 modes; FP32 keeps the GEMM route under auto
+        g = rng.standard_normal((2, 12, 14, 14)).astype(np.float32)
+        G = _core.Tensor.from_numpy(g)
+
+        def run_bwd(algo, stride=(1, 1), pad=(1, 1), gt=G, shape=(2, 8, 14, 14)):
+            cd.set_conv_algorithm(algo)
+            return _core.conv2d_backward_data(gt, W, list(shape), list(stride), list(pad)).numpy()
+        d_auto, d_wino, d_i2c = run_bwd("auto"), run_bwd("winograd"), run_bwd("im2col")
+        assert np.array_equal(d_auto, d_i2c)
+        d64 = oracle.conv2d_backward_data64(g, w, x.shape, (1, 1), (1, 1))
+        e_w = oracle.rel_fro(oracle.conv2d_backward_data_winograd(g, w, x.shape, (1, 1)), d64)
+        e_i = oracle.rel_fro(oracle.conv2d_backward_data_ref(g, w, x.shape, (1, 1), (1, 1)), d64)
+        assert oracle.rel_fro(d_wino, d64) <= 2 * e_w
+        assert oracle.rel_fro(d_i2c, d64) <= 2 * e_i
+        cd.set_matmul_precision("tf32")
+        assert np.array_equal(run_bwd("auto"), run_bwd("winograd"))
+        assert not np.array_equal(run_bwd("auto"), run_bwd("im2col"))
+        cd.set_matmul_precision("fp32")
+        g2 = _core.Tensor.from_numpy(rng.standard_normal((2, 12, 7, 7)).astype(np.float32))
+        assert np.array_equal(run_bwd("auto", (2, 2), gt=g2), run_bwd("im2col", (2, 2), gt=g2))
+        with pytest.raises(RuntimeError):
+            run_bwd("winograd", (2, 2), gt=g2)
     finally:
         cd.set_conv_algorithm(prev)
 

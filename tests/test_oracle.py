@@ -384,6 +384,28 @@ def test_conv_backward_vs_torch_fp64(geom):
     assert oracle.rel_fro(dx32, dx64) < 1e-6 and oracle.rel_fro(dw32, dw64) < 1e-6
 
 
+@pytest.mark.parametrize("geom", [(2, 3, 8, 9, 4, 3, 3, 1, 1), (1, 2, 7, 7, 3, 3, 5, 2, 0),
+                                  (3, 4, 6, 5, 2, 2, 2, 1, 0), (2, 3, 5, 6, 2, 1, 1, 0, 0),
+                                  (1, 2, 9, 4, 3, 5, 3, 4, 1)])
+def test_backward_data_is_flipped_forward(geom):
+    """Stride-1 backward data equals the forward convolution of dY with the
+    channel-swapped, spatially reversed filter padded K-1-P (the identity
+    the stride-1 backward-data route runs on).  A filter read unflipped,
+    unswapped or with the wrong padding fails at O(1)."""
+    Bn, IC, H, W, OC, KH, KW, PH, PW = geom
+    rng = np.random.default_rng(43 + sum(geom))
+    w = rng.standard_normal((OC, IC, KH, KW)).astype(np.float32)
+    OH, OW = oracle.conv_out_size(H, KH, 1, PH), oracle.conv_out_size(W, KW, 1, PW)
+    dy = rng.standard_normal((Bn, OC, OH, OW)).astype(np.float32)
+    want = oracle.conv2d_backward_data64(dy, w, (Bn, IC, H, W), (1, 1), (PH, PW))
+    got = oracle.conv2d_direct64(dy, oracle.flip_filter(w), None, (1, 1), (KH - 1 - PH, KW - 1 - PW))
+    assert got.shape == want.shape
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    if KH == 3 and KW == 3 and PH <= 2 and PW <= 2:
+        wino = oracle.conv2d_backward_data_winograd(dy, w, (Bn, IC, H, W), (PH, PW), double=True)
+        assert oracle.rel_fro(wino, want) < 1e-13
+
+
 # ---------------------------------------------------------------------------
 # Winograd F(4x4, 3x3) route (conv_kernel.cu:557-789)
 # ---------------------------------------------------------------------------
