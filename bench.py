@@ -170,8 +170,9 @@ def bench_mlp(steps, warmup, precision):
 
 def bench_conv(steps, warmup, precision):
     """C5: N=32, C=64, 56x56 -> 64, 3x3, s1, p1: im2col + GEMM (bias in the
-    epilogue, output written NCHW)."""
+    epilogue, output written NCHW), Winograd, and the backward routes."""
     import torch
+    import cudeep_amd as cd
     import cudeep_amd.ops as ops
     g = torch.Generator(device="cuda").manual_seed(5)
     x = torch.randn((32, 64, 56, 56), device="cuda", generator=g)
@@ -210,8 +211,12 @@ def bench_conv(steps, warmup, precision):
     def bwd_weight():
         ops.conv2d_backward_weight(dy, x, w.shape, (1, 1), (1, 1), precision, out=dw)
 
+    # the routes launch_conv2d_backward_data_kernel takes (Auto): Winograd in
+    # the TF32 modes, the flipped-filter GEMM route in FP32
+    bwd_data_auto = bwd_data if precision == cd.PREC_FP32 else bwd_data_wino
+
     def bwd():
-        bwd_data_wino()
+        bwd_data_auto()
         bwd_weight()
         ops.conv2d_backward_bias(dy, out=db)
     bwd_ms, _ = time_launches(bwd, steps, warmup)
