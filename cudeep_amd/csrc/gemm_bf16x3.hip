@@ -559,12 +559,13 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
 //    deeper k-tile halves the k-iterations of short-K problems, which are
 //    bound by per-iteration latency (8192 x 256 x 784: 30 us against 75
 //    with BK = 32); 16-wide tiles for N or M <= 16 measured no faster.
-//  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x64x64, 4 waves of
-//    32x32, two staging sets (64 x 100352 x 576: 68 us = 109 logical
-//    TFLOP/s, against 76 with BK = 32 and one set).
+//  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x128x32, 4 waves of
+//    32x64, two staging sets (64 x 100352 x 576 in a back-to-back loop:
+//    49.5 us = 149 logical TFLOP/s, against 55.5 with 64x64x64 tiles, 65.5
+//    with 64x128x64 and 57-58 with 64x256x32).
 using CfgHuge = Cfg<256, 256, 32, 128, 64, 8, true>;
 using CfgLarge = Cfg<128, 128, 64, 32, 64, 8, false, 2>;
-using CfgSkinnyM = Cfg<64, 64, 64, 32, 32, 1, false, 2>;
+using CfgSkinnyM = Cfg<64, 128, 32, 32, 64, 1, false, 2>;
 using CfgSmall = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
 
 // True when launch_mode would run CF without bounds checks (no split-K).
