@@ -157,6 +157,45 @@ def bench_mlp(steps, warmup, precision):
     bwd_ms, _ = time_launches(bwd, steps, warmup)
     fwd_flops = 2.0 * 8192 * (784 * 256 + 256 * 10)
     bwd_flops = 2 * fwd_flops
+
+    # The same step as one HIP graph: at this size the eager step is bound by
+    # per-launch host work (Python + ctypes), which replaying a captured
+    # graph removes.  Every launch takes its scratch from a preallocated
+    # workspace, so nothing is allocated under capture.
+    def wsp(nbytes):
+        return torch.empty(max(nbytes, 4) // 4 + 1, device="cuda")
+    ws_w2 = wsp(ops.gemm_workspace_bytes(10, 256, 8192, precision=precision, transA=True))
+    ws_w1 = wsp(ops.gemm_workspace_bytes(256, 784, 8192, precision=precision, transA=True))
+    ws_x = wsp(ops.gemm_workspace_bytes(8192, 784, 256, precision=precision))
+    ws_h = wsp(ops.gemm_workspace_bytes(8192, 256, 10, precision=precision))
+    ws_f1 = wsp(ops.gemm_workspace_bytes(8192, 256, 784, precision=precision, transB=True))
+    ws_f2 = wsp(ops.gemm_workspace_bytes(8192, 10, 256, precision=precision, transB=True))
+    ws_b2 = wsp(ops.sum_reduce_rows_workspace_bytes(8192, 10))
+    ws_b1 = wsp(ops.sum_reduce_rows_workspace_bytes(8192, 256))
+
+    def step():
+        ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
+                 precision=precision, out=H, workspace=ws_f1)
+        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y,
+                 workspace=ws_f2)
+        ops.gemm(dY2, W2, precision=precision, out=dH, workspace=ws_h)
+        ops.gemm(dY2, H, transA=True, precision=precision, out=gW2, workspace=ws_w2)
+        ops.sum_reduce_rows(dY2, out=gb2, workspace=ws_b2)
+        ops.activation_backward(dH, H, cd.EPI_RELU, out=dZ)
+        ops.gemm(dZ, W1, precision=precision, out=gX, workspace=ws_x)
+        ops.gemm(dZ, X, transA=True, precision=precision, out=gW1, workspace=ws_w1)
+        ops.sum_reduce_rows(dZ, out=gb1, workspace=ws_b1)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    graph_ms, _ = time_launches(graph.replay, steps, warmup)
     # per-GEMM timing of the big forward GEMM
     l1_ms, _ = time_launches(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
                                               epilogue=cd.EPI_RELU, precision=precision, out=H),
@@ -164,6 +203,8 @@ def bench_mlp(steps, warmup, precision):
     return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
             "fwd_tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12,
             "bwd_tflops": bwd_flops / (bwd_ms * 1e-3) / 1e12,
+            "step_graph_ms": graph_ms,
+            "step_graph_tflops": (fwd_flops + bwd_flops) / (graph_ms * 1e-3) / 1e12,
             "fwd1_fused_ms": l1_ms,
             "fwd1_fused_tflops": 2.0 * 8192 * 784 * 256 / (l1_ms * 1e-3) / 1e12}
 

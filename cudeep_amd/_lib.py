@@ -36,6 +36,9 @@ SIGNATURES = {
     "cdx_gemm_tf32mode": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cdx_gemm_ex": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                            _vp, _i64, _vp, _int, _int, _vp]),
+    "cdx_gemm_workspace_size": (_sz, [_int, _int, _int, _i64, _i64, _i64]),
+    "cdx_gemm_ex_ws": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
+                              _vp, _i64, _vp, _int, _int, _vp, _sz, _vp]),
     "cdx_matmul_fused_act": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "cdx_hgemm_f16": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cdx_gemm16_ex": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,

@@ -112,9 +112,23 @@ int cdx_gemm_tf32mode(const float* A, const float* B, float* C, int64_t M, int64
     return run_gemm(CDX_PREC_TF32MODE, g, stream);
 }
 
-int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K,
-                const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
-                const float* bias, int bias_mode, int epilogue, hipStream_t stream) {
+size_t cdx_gemm_workspace_size(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K) {
+    if (!valid_precision(precision) || (opA != CDX_OP_N && opA != CDX_OP_T) ||
+        (opB != CDX_OP_N && opB != CDX_OP_T) || bad_dim(M) || bad_dim(N) || bad_dim(K)) {
+        set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_workspace_size: bad arguments");
+        return 0;
+    }
+    if (M == 0 || N == 0) return 0;
+    cdx::GemmArgs g{opA, opB, M, N, K, nullptr, 1, nullptr, 1, nullptr, N, 0, 0,
+                    nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+    if (precision == CDX_PREC_FP32) return cdx::gemm_f32_workspace(g);
+    return cdx::gemm_bf16x3_workspace(g, precision == CDX_PREC_TF32MODE4 ? 4 : 3);
+}
+
+int cdx_gemm_ex_ws(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K,
+                   const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                   int64_t ldc, const float* bias, int bias_mode, int epilogue, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
     int st = check_gemm("cdx_gemm_ex", opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
     if (st) return st;
     if (!valid_precision(precision))
@@ -126,7 +140,16 @@ int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K
     if (!valid_epilogue(epilogue))
         return set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_ex: bad epilogue");
     cdx::GemmArgs g{opA, opB, M, N, K, A, lda, B, ldb, C, ldc, 0, 0, bias, bias_mode, epilogue};
+    g.ws = workspace;
+    g.ws_bytes = workspace ? workspace_bytes : 0;
     return run_gemm(precision, g, stream);
+}
+
+int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K,
+                const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
+                const float* bias, int bias_mode, int epilogue, hipStream_t stream) {
+    return cdx_gemm_ex_ws(precision, opA, opB, M, N, K, A, lda, B, ldb, C, ldc, bias, bias_mode,
+                          epilogue, nullptr, 0, stream);
 }
 
 int cdx_gemm16_ex(int in_dtype, int opA, int opB, int64_t M, int64_t N, int64_t K,

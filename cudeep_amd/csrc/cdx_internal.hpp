@@ -45,10 +45,19 @@ struct GemmArgs {
     // the running total) instead of one running sum -- a rounding-error
     // chain of ~32 + K/32 additions instead of ~K.
     bool blocked_sum = false;
+    // Caller scratch for split-K partials (the launchers allocate stream-
+    // ordered when it is null); gemm_*_workspace() gives the bytes needed.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
 };
 
-// Launchers (no argument validation: the C-ABI validates first).
+// Launchers (no argument validation: the C-ABI validates first).  The
+// *_workspace functions return the split-K partial bytes the same launch
+// would use (0 when it does not split); they follow the launchers' own
+// configuration choice.
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream);
+size_t gemm_f32_workspace(const GemmArgs& g);
+size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms);
 // terms = 3 (bf16x3: hi*hi + hi*lo + lo*hi) or 4 (adds lo*lo).
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream);
 // 16-bit operands (in_dtype CDX_DTYPE_F16 or CDX_DTYPE_BF16), fp32 accumulation and C.
@@ -80,26 +89,43 @@ inline int choose_splitk(int64_t tiles, int64_t K, int bk, int64_t* k_chunk) {
     return (int)ceil_div(K, kc);
 }
 
+// Split-K partial bytes of a GEMM whose tile grid is `tiles` (0: no split).
+inline size_t splitk_bytes(const GemmArgs& g, int64_t tiles, int bk) {
+    if (g.batch > 1) return 0;
+    int64_t k_chunk;
+    const int splits = choose_splitk(tiles, g.K, bk, &k_chunk);
+    return splits > 1 ? (size_t)splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0;
+}
+
 // Runs a GEMM whose tile grid is `tiles` through split-K when the policy
-// asks for it: allocates the partials stream-ordered, calls
-// launch(kparams-adjusted GemmArgs, splits, k_chunk) and reduces.
+// asks for it: takes the partials from g.ws (or allocates them stream-
+// ordered), calls launch(kparams-adjusted GemmArgs, splits, k_chunk) and
+// reduces.
 template <class LaunchFn>
 int with_splitk(const GemmArgs& g, int64_t tiles, int bk, hipStream_t stream, LaunchFn launch) {
     int64_t k_chunk;
     const int splits = g.batch > 1 ? (k_chunk = g.K, 1) : choose_splitk(tiles, g.K, bk, &k_chunk);
     if (splits == 1) return launch(g, 1, g.K);
-    float* part = nullptr;
+    float* part = static_cast<float*>(g.ws);
     const size_t bytes = (size_t)splits * (size_t)g.M * (size_t)g.N * sizeof(float);
-    int st = hip_error(hipMallocAsync(reinterpret_cast<void**>(&part), bytes, stream),
+    int st = CDX_OK;
+    if (part) {
+        if (g.ws_bytes < bytes) return set_error(CDX_ERR_WORKSPACE, "gemm: workspace too small");
+    } else {
+        st = hip_error(hipMallocAsync(reinterpret_cast<void**>(&part), bytes, stream),
                        "gemm split-K: hipMallocAsync");
-    if (st) return st;
+        if (st) return st;
+    }
     GemmArgs q = g;
     q.C = part; q.ldc = g.N; q.n_split = 0; q.ldc_split = 0;
     q.bias = nullptr; q.bias_mode = CDX_BIAS_NONE; q.epilogue = CDX_EPI_NONE;
     st = launch(q, splits, k_chunk);
     if (!st) st = launch_splitk_reduce(part, splits, g, stream);
-    int st2 = hip_error(hipFreeAsync(part, stream), "gemm split-K: hipFreeAsync");
-    return st ? st : st2;
+    if (!g.ws) {
+        int st2 = hip_error(hipFreeAsync(part, stream), "gemm split-K: hipFreeAsync");
+        if (!st) st = st2;
+    }
+    return st;
 }
 
 int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,

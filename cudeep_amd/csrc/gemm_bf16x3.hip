@@ -576,20 +576,46 @@ bool aligned_for(const GemmArgs& g) {
            g.M % CF::BM == 0 && g.N % CF::BN == 0 && g.K % CF::BK == 0;
 }
 
-template <int TERMS>
-int dispatch(const GemmArgs& g, hipStream_t stream) {
-    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM, TERMS>(g, stream);
+// Configuration choice, shared by the launcher and the workspace query.
+enum class BfCfg { SkinnyM, Huge, Large, Small };
+
+BfCfg choose_bf(const GemmArgs& g, int terms) {
+    if (g.M <= 64 && g.N >= 4096) return BfCfg::SkinnyM;
     // Huge holds 128 accumulators per lane: only its unchecked three-term
     // form fits in 256 registers without spilling.
-    if constexpr (TERMS == 3) {
-        if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<CfgHuge>(g))
-            return launch_ops<CfgHuge, TERMS>(g, stream);
+    if (terms == 3 && ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<CfgHuge>(g))
+        return BfCfg::Huge;
+    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return BfCfg::Large;
+    return BfCfg::Small;
+}
+
+template <class CF>
+size_t ws_of(const GemmArgs& g) {
+    return splitk_bytes(g, ceil_div(g.M, CF::BM) * ceil_div(g.N, CF::BN), CF::BK);
+}
+
+template <int TERMS>
+int dispatch(const GemmArgs& g, hipStream_t stream) {
+    switch (choose_bf(g, TERMS)) {
+        case BfCfg::SkinnyM: return launch_ops<CfgSkinnyM, TERMS>(g, stream);
+        case BfCfg::Huge:
+            if constexpr (TERMS == 3) return launch_ops<CfgHuge, TERMS>(g, stream);
+            return set_error(CDX_ERR_UNSUPPORTED, "gemm: no four-term Huge configuration");
+        case BfCfg::Large: return launch_ops<CfgLarge, TERMS>(g, stream);
+        default: return launch_ops<CfgSmall, TERMS>(g, stream);
     }
-    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<CfgLarge, TERMS>(g, stream);
-    return launch_ops<CfgSmall, TERMS>(g, stream);
 }
 
 }  // namespace
+
+size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms) {
+    switch (choose_bf(g, terms)) {
+        case BfCfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
+        case BfCfg::Huge: return ws_of<CfgHuge>(g);
+        case BfCfg::Large: return ws_of<CfgLarge>(g);
+        default: return ws_of<CfgSmall>(g);
+    }
+}
 
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream) {
     return terms == 4 ? dispatch<4>(g, stream) : dispatch<3>(g, stream);

@@ -389,23 +389,58 @@ using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8, 2>;
 //    784 x 8192: 53 us against 61 with Medium).
 using CfgSplitK = Cfg<64, 64, 16, 32, 32, 8, 2>;
 
+// Configuration choice, shared by the launcher and the workspace query.
+enum class F32Cfg { NarrowN, SplitK, SkinnyM, Large, Medium };
+
+F32Cfg choose_f32(const GemmArgs& g, bool& blocked) {
+    const bool split = g.batch == 1 && splitk_applies(ceil_div(g.M, 64) * ceil_div(g.N, 64), g.K);
+    blocked = g.blocked_sum && !split && g.opA == CDX_OP_N && g.opB == CDX_OP_N;
+    if (g.N <= 16) return F32Cfg::NarrowN;
+    if (split && !blocked) return F32Cfg::SplitK;
+    if (g.M <= 64 && g.N >= 4096) return F32Cfg::SkinnyM;
+    // Large tiles once there are at least two per CU (256 CUs).
+    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 512) return F32Cfg::Large;
+    return F32Cfg::Medium;
+}
+
+template <class CF>
+size_t ws_of(const GemmArgs& g) {
+    return splitk_bytes(g, ceil_div(g.M, CF::BM) * ceil_div(g.N, CF::BN), CF::BK);
+}
+
 }  // namespace
 
-int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
-    const bool split = g.batch == 1 && splitk_applies(ceil_div(g.M, 64) * ceil_div(g.N, 64), g.K);
-    if (g.blocked_sum && !split && g.opA == CDX_OP_N && g.opB == CDX_OP_N) {
-        if (g.N <= 16) return launch_blocked<CfgNarrowN>(g, stream);
-        if (g.M <= 64 && g.N >= 4096) return launch_blocked<CfgSkinnyM>(g, stream);
-        if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 512) return launch_blocked<CfgLarge>(g, stream);
-        return launch_blocked<CfgMedium>(g, stream);
+size_t gemm_f32_workspace(const GemmArgs& g) {
+    bool blocked;
+    const F32Cfg c = choose_f32(g, blocked);
+    if (blocked) return 0;
+    switch (c) {
+        case F32Cfg::NarrowN: return ws_of<CfgNarrowN>(g);
+        case F32Cfg::SplitK: return ws_of<CfgSplitK>(g);
+        case F32Cfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
+        case F32Cfg::Large: return ws_of<CfgLarge>(g);
+        default: return ws_of<CfgMedium>(g);
     }
-    if (g.N <= 16) return launch_ops<CfgNarrowN>(g, stream);
-    if (split) return launch_ops<CfgSplitK>(g, stream);
-    if (g.M <= 64 && g.N >= 4096) return launch_ops<CfgSkinnyM>(g, stream);
-    // Large tiles once there are at least two per CU (256 CUs).
-    int64_t large_tiles = ceil_div(g.M, 128) * ceil_div(g.N, 128);
-    if (large_tiles >= 512) return launch_ops<CfgLarge>(g, stream);
-    return launch_ops<CfgMedium>(g, stream);
+}
+
+int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
+    bool blocked;
+    const F32Cfg c = choose_f32(g, blocked);
+    if (blocked) {
+        switch (c) {
+            case F32Cfg::NarrowN: return launch_blocked<CfgNarrowN>(g, stream);
+            case F32Cfg::SkinnyM: return launch_blocked<CfgSkinnyM>(g, stream);
+            case F32Cfg::Large: return launch_blocked<CfgLarge>(g, stream);
+            default: return launch_blocked<CfgMedium>(g, stream);
+        }
+    }
+    switch (c) {
+        case F32Cfg::NarrowN: return launch_ops<CfgNarrowN>(g, stream);
+        case F32Cfg::SplitK: return launch_ops<CfgSplitK>(g, stream);
+        case F32Cfg::SkinnyM: return launch_ops<CfgSkinnyM>(g, stream);
+        case F32Cfg::Large: return launch_ops<CfgLarge>(g, stream);
+        default: return launch_ops<CfgMedium>(g, stream);
+    }
 }
 
 }  // namespace cdx

@@ -42,9 +42,12 @@ def _ld(t: torch.Tensor, name: str) -> int:
 def gemm(A: torch.Tensor, B: torch.Tensor, *, precision: int = L.PREC_FP32,
          transA: bool = False, transB: bool = False, bias: torch.Tensor | None = None,
          bias_mode: int = L.BIAS_NONE, epilogue: int = L.EPI_NONE,
-         out: torch.Tensor | None = None) -> torch.Tensor:
+         out: torch.Tensor | None = None,
+         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """C = epi(op(A) @ op(B) + bias).  A, B are row-major storage; transA /
-    transB select the transpose, so x @ W.T is gemm(x, W, transB=True)."""
+    transB select the transpose, so x @ W.T is gemm(x, W, transB=True).
+    `workspace` (at least gemm_workspace_bytes(...) bytes) makes the call
+    allocation-free (cdx_gemm_ex_ws)."""
     _need(A, "A")
     _need(B, "B")
     M, K = (A.shape[1], A.shape[0]) if transA else (A.shape[0], A.shape[1])
@@ -65,10 +68,21 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, precision: int = L.PREC_FP32,
         if bias.numel() != want or not bias.is_contiguous():
             raise ValueError("bias has the wrong size or is not contiguous")
         bptr = bias.data_ptr()
-    L.call("cdx_gemm_ex", precision, int(transA), int(transB), M, N, K,
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        _need(workspace, "workspace")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    L.call("cdx_gemm_ex_ws", precision, int(transA), int(transB), M, N, K,
            A.data_ptr(), _ld(A, "A"), B.data_ptr(), _ld(B, "B"),
-           out.data_ptr(), _ld(out, "out"), bptr, bias_mode, epilogue, _stream())
+           out.data_ptr(), _ld(out, "out"), bptr, bias_mode, epilogue, ws_ptr, ws_bytes,
+           _stream())
     return out
+
+
+def gemm_workspace_bytes(M: int, N: int, K: int, *, precision: int = L.PREC_FP32,
+                         transA: bool = False, transB: bool = False) -> int:
+    """Scratch bytes gemm(..., workspace=) needs for op(A) [M, K] @ op(B) [K, N]."""
+    return int(L.lib().cdx_gemm_workspace_size(precision, int(transA), int(transB), M, N, K))
 
 
 def gemm16(A: torch.Tensor, B: torch.Tensor, *, transA: bool = False, transB: bool = False,
@@ -263,15 +277,26 @@ def conv2d_workspace_bytes(x_shape, w_shape, stride=(1, 1), padding=(0, 0)) -> i
         Bn, C, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1]))
 
 
-def sum_reduce_rows(x, out=None):
+def sum_reduce_rows(x, out=None, workspace=None):
+    """Column sums of a contiguous 2-D tensor; `workspace` (at least
+    sum_reduce_rows_workspace_bytes(rows, cols)) makes the call allocation-free."""
     _need(x, "input")
     if x.dim() != 2 or not x.is_contiguous():
         raise ValueError("sum_reduce_rows: input must be contiguous 2-D")
     rows, cols = x.shape
     if out is None:
         out = torch.empty((cols,), device=x.device, dtype=torch.float32)
-    L.call("cdx_sum_reduce_rows_f32", x.data_ptr(), out.data_ptr(), rows, cols, None, 0, _stream())
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        _need(workspace, "workspace")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    L.call("cdx_sum_reduce_rows_f32", x.data_ptr(), out.data_ptr(), rows, cols, ws_ptr, ws_bytes,
+           _stream())
     return out
+
+
+def sum_reduce_rows_workspace_bytes(rows: int, cols: int) -> int:
+    return int(L.lib().cdx_sum_reduce_rows_workspace_size(rows, cols))
 
 
 def broadcast_add_row(m, row, out=None):

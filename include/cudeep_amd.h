@@ -107,6 +107,28 @@ int cdx_gemm_ex(int precision, int opA, int opB,
                 const float* bias, int bias_mode, int epilogue,
                 hipStream_t stream);
 
+/* Bytes of scratch cdx_gemm_ex_ws needs for this problem: the split-K
+ * partials of long-K problems with few output tiles (e.g. weight gradients),
+ * 0 when the launch does not split.  The same (precision, transposes, sizes)
+ * always give the same answer. */
+size_t cdx_gemm_workspace_size(int precision, int opA, int opB,
+                               int64_t M, int64_t N, int64_t K);
+
+/* cdx_gemm_ex with caller scratch: with a workspace of at least
+ * cdx_gemm_workspace_size bytes the call allocates nothing (safe inside HIP
+ * graph capture); NULL falls back to stream-ordered allocation.  The
+ * reference's GEMM launchers allocate nothing because they never split K
+ * (matmul_kernel.cu:1785-1841); this is the same contract for the split
+ * launches.  Too small a workspace is CDX_ERR_WORKSPACE. */
+int cdx_gemm_ex_ws(int precision, int opA, int opB,
+                   int64_t M, int64_t N, int64_t K,
+                   const float* A, int64_t lda,
+                   const float* B, int64_t ldb,
+                   float* C, int64_t ldc,
+                   const float* bias, int bias_mode, int epilogue,
+                   void* workspace, size_t workspace_bytes,
+                   hipStream_t stream);
+
 /* C = act(A * B), TF32 mode, no bias.
  * Replaces cudeep::kernels::launch_matmul_fused_act
  * (matmul.cuh:40-44, matmul_kernel.cu:1884-1924); epilogue is CDX_EPI_*. */

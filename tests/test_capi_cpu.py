@@ -102,6 +102,15 @@ def test_conv_argument_validation():
                    0, None, 0, None) == L.CDX_ERR_UNSUPPORTED
     assert _status("cdx_conv2d_backward_data_winograd_f32", fake, fake, fake, 1, 2, 2, 8, 8, 1, 1,
                    0, fake, 4, None) == L.CDX_ERR_WORKSPACE
+    # GEMM split-K scratch: C4's dW1 (256 x 784 x 8192, TN) in FP32 runs 15
+    # slices of 560 k on the 64x64 split-K tile; 4096^3 never splits
+    assert L.lib().cdx_gemm_workspace_size(0, 1, 0, 256, 784, 8192) == 15 * 256 * 784 * 4
+    assert L.lib().cdx_gemm_workspace_size(0, 0, 0, 4096, 4096, 4096) == 0
+    assert L.lib().cdx_gemm_workspace_size(1, 0, 0, 4096, 4096, 4096) == 0
+    assert L.lib().cdx_gemm_workspace_size(0, 0, 0, 0, 4096, 4096) == 0
+    assert L.lib().cdx_gemm_workspace_size(7, 0, 0, 16, 16, 16) == 0     # bad precision
+    assert _status("cdx_gemm_ex_ws", 0, 1, 0, 256, 784, 8192, fake, 256, fake, 784, fake, 784,
+                   None, 0, 0, fake, 4, None) == L.CDX_ERR_WORKSPACE
     # 8192 rows -> 256 chunks of 32 rows; partials sized for fp64
     assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 256 * 256 * 8
     assert L.lib().cdx_sum_reduce_rows_workspace_size(10 ** 7, 3) == 1024 * 3 * 8
