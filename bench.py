@@ -328,18 +328,23 @@ def main():
     head = bench_gemm(4096, cd.PREC_FP32, args.steps, args.warmup, seed=2)
     log("fp32 4096^3:", head)
     extra = {}
+    # The reduced-precision GEMMs run ~12 % slower for their first ~20 ms of
+    # back-to-back launches (the clock settles under the new load; measured
+    # 344 -> 300 us per 4096^3 TF32-mode launch), so their lines use at least
+    # 50 warmup launches and report the settled rate.
+    w_extra = max(args.warmup, 50)
     if not args.headline_only:
         for n in (4096, 2048):
-            r = bench_gemm(n, cd.PREC_TF32MODE, args.steps, args.warmup, seed=3)
+            r = bench_gemm(n, cd.PREC_TF32MODE, args.steps, w_extra, seed=3)
             r["frac_of_bf16x3_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 3)
             extra[f"tf32mode_{n}"] = r
             log(f"tf32mode {n}^3:", r)
-        r = bench_gemm(4096, cd.PREC_TF32MODE4, args.steps, args.warmup, seed=3)
+        r = bench_gemm(4096, cd.PREC_TF32MODE4, args.steps, w_extra, seed=3)
         r["frac_of_bf16x4_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 4)
         extra["tf32mode4_4096"] = r
         log("tf32mode4 (bf16x4) 4096^3:", r)
         for dt in ("f16", "bf16"):
-            r = bench_gemm16(4096, dt, args.steps, args.warmup, seed=6)
+            r = bench_gemm16(4096, dt, args.steps, w_extra, seed=6)
             extra[f"{dt}_gemm_4096"] = r
             log(f"{dt} GEMM 4096^3:", r)
         for prec, name in ((cd.PREC_FP32, "fp32"), (cd.PREC_TF32MODE, "tf32mode")):

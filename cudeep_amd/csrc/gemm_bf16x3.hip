@@ -115,6 +115,27 @@ struct SplitLoader {
         }
     }
 
+    // Unchecked load, address = wave-uniform tile base + 32-bit per-thread
+    // byte offset (one VGPR per block instead of a 64-bit pointer per row).
+    // `off` comes from tile_offsets(); the caller guarantees the tile is in
+    // bounds and that the offsets fit 32 bits.
+    __device__ __forceinline__ static void tile_offsets(uint32_t (&off)[NV], uint32_t ld_bytes, int tid) {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int bc, br;
+            block_coords(tid + b * NT, bc, br);
+            off[b] = (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 16);
+        }
+    }
+    __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
+                                            const uint32_t (&off)[NV]) {
+#pragma unroll
+        for (int b = 0; b < NV; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[b][q] = *reinterpret_cast<const float4*>(base + (uint64_t)(q * ld_bytes) + off[b]);
+    }
+
     // Writes hi / lo planes, layout [mn][STRIDE] (k contiguous), ushort units.
     template <int STRIDE>
     __device__ __forceinline__ void store(unsigned short* __restrict__ hi,
@@ -503,6 +524,185 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     write_acc<FM, FN, CHECK, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
 }
 
+// 256 x 256 tiles on a two-group ("ping-pong") schedule.  The eight waves
+// form two groups of four, one wave of each group per SIMD; group 0 owns
+// tile rows 0-127, group 1 rows 128-255, each wave a 128 x 64 sub-tile.
+// Every k-tile is worked in four slots separated by workgroup barriers:
+//     MEM_a  read the B fragments and A fragment rows 0-3 of this k-tile;
+//            split + store this thread's A block of the next k-tile (from
+//            registers) into the other LDS stage; load its A block of the
+//            k-tile after that from global memory
+//     MATH_a the MFMAs of A rows 0-3 (registers only)
+//     MEM_b  A fragment rows 4-7; the same store / load for the B block
+//     MATH_b the MFMAs of A rows 4-7
+// Group 1 runs one slot behind group 0 (one extra barrier at the start,
+// group 0 one at the end, so both execute 2 + 4 * nk barriers), so on each
+// SIMD one wave issues MFMAs while the other does its loads, splits and
+// LDS traffic.  Slot order keeps the two LDS stages safe: k-tile t+1 is
+// written in slots 4t..4t+3 (stage (t+1)&1, last read by k-tile t-1 in slot
+// 4t-1) and first read in slot 4t+4.  Global loads are consumed four slots
+// after they are issued.  Aligned problems only (M, N % 256, K % 32, 16-byte
+// operands).  fp32 operands, three terms, the same per-element term order as
+// gemm_bf16x3_kernel (so the same results); BK = 32, LDS 2 x 80 KiB.
+// Measured at 4096^3 against gemm_bf16x3_kernel's 256 x 256 configuration
+// (which runs the two waves of a SIMD in step): 0.310 against 0.361 ms.
+template <int OPA, int OPB, bool SPLITN>
+__global__ __launch_bounds__(512)
+void gemm_pingpong_kernel(KParams p) {
+    constexpr int BM = 256, BN = 256, NT = 512, GROUP_M = 8;
+    constexpr int BK = 32;
+    constexpr int ES = 4;                          // operand element bytes
+    constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
+    constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
+    constexpr int B_OFF = 2 * A_PLANE;             // stage: A hi, A lo, B hi, B lo
+    constexpr int STAGE = 2 * (A_PLANE + B_PLANE);
+    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int grp = wave >> 2;
+    const int wm0 = grp * 128;
+    const int wn0 = (wave & 3) * 64;
+    const int l16 = lane & 15;
+    const int lq = lane >> 4;
+
+    int tm, tn;
+    tile_of_block((int)(p.M / BM), (int)(p.N / BN), GROUP_M, tm, tn);
+    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? k0 : k0 * p.lda);
+        p.B = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? k0 * p.ldb : k0);
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
+    if (gridDim.z > 1) {
+        p.A = static_cast<const char*>(p.A) + ES * (int64_t)blockIdx.z * p.sa;
+        p.B = static_cast<const char*>(p.B) + ES * (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
+    }
+
+    using LoaderA = SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>;
+    using LoaderB = SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>;
+    static_assert(LoaderA::NB % NT == 0 && LoaderB::NB % NT == 0, "whole blocks per thread");
+    LoaderA la;
+    LoaderB lb;
+    auto store_a = [&](unsigned short* s) { la.template store<STRIDE>(s, s + A_PLANE, tid); };
+    auto store_b = [&](unsigned short* s) {
+        lb.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, tid);
+    };
+
+    floatx4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // fa: hi / lo fragments of four A rows (one half of the wave's rows);
+    // fb: hi / lo fragments of the wave's four B columns
+    bf16x8 fa[4][2], fb[4][2];
+    auto read_a = [&](const unsigned short* s, int half) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl)
+                fa[i][pl] = *reinterpret_cast<const bf16x8*>(
+                    s + pl * A_PLANE + (wm0 + (half * 4 + i) * 16 + l16) * STRIDE + 8 * lq);
+    };
+    auto read_b = [&](const unsigned short* s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl)
+                fb[j][pl] = *reinterpret_cast<const bf16x8*>(
+                    s + B_OFF + pl * B_PLANE + (wn0 + j * 16 + l16) * STRIDE + 8 * lq);
+    };
+    // MFMAs of fragment rows half*4 .. half*4+3: lo*hi and hi*lo first, then
+    // hi*hi (index 0 = hi, 1 = lo)
+    auto math = [&](int half) {
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[half * 4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    fa[i][1], fb[j][0], acc[half * 4 + i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[half * 4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    fa[i][0], fb[j][1], acc[half * 4 + i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[half * 4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    fa[i][0], fb[j][0], acc[half * 4 + i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // slot boundary: nothing moves across it
+    auto slot = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Global addressing: a wave-uniform base per k-tile plus 32-bit per-
+    // thread offsets (the launcher checks 256 rows of either operand span
+    // less than 4 GiB).  k-contiguous operands step ES*BK bytes per k-tile,
+    // m/n-contiguous ones BK rows.
+    const uint32_t lda_b = (uint32_t)(p.lda * ES), ldb_b = (uint32_t)(p.ldb * ES);
+    uint32_t offa[LoaderA::NV], offb[LoaderB::NV];
+    LoaderA::tile_offsets(offa, lda_b, tid);
+    LoaderB::tile_offsets(offb, ldb_b, tid);
+    const char* baseA = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? bm * p.lda : bm);
+    const char* baseB = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? bn : bn * p.ldb);
+    const int64_t stepA = OPA == CDX_OP_N ? (int64_t)ES * BK : (int64_t)BK * p.lda * ES;
+    const int64_t stepB = OPB == CDX_OP_N ? (int64_t)BK * p.ldb * ES : (int64_t)ES * BK;
+
+    const int64_t nk = p.K / BK;
+    la.load_at(baseA, lda_b, offa);
+    lb.load_at(baseB, ldb_b, offb);
+    store_a(lds);
+    store_b(lds);
+    if (nk > 1) {
+        la.load_at(baseA + stepA, lda_b, offa);
+        lb.load_at(baseB + stepB, ldb_b, offb);
+    }
+    __syncthreads();
+    if (grp == 1) slot();
+    // At the top of iteration t: stage t&1 holds k-tile t; la / lb hold (or
+    // are loading) k-tile t+1.
+    for (int64_t t = 0; t < nk; ++t) {
+        const unsigned short* s = lds + (t & 1) * STAGE;
+        unsigned short* sn = lds + ((t + 1) & 1) * STAGE;
+        read_b(s);
+        read_a(s, 0);
+        if (t + 1 < nk) {
+            store_a(sn);
+            if (t + 2 < nk) la.load_at(baseA + (t + 2) * stepA, lda_b, offa);
+        }
+        slot();
+        math(0);
+        slot();
+        read_a(s, 1);
+        if (t + 1 < nk) {
+            store_b(sn);
+            if (t + 2 < nk) lb.load_at(baseB + (t + 2) * stepB, ldb_b, offb);
+        }
+        slot();
+        math(1);
+        slot();
+    }
+    if (grp == 0) slot();
+
+    const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
+                      p.bias, p.bias_mode, p.epilogue};
+    write_acc<8, 4, false, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
+}
+
 template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN = kInF32>
 int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
@@ -535,6 +735,37 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
         return split ? launch_cfg<CF, OPA, OPB, true, true, TERMS, IN>(kp, vec, splits, stream)
                      : launch_cfg<CF, OPA, OPB, true, false, TERMS, IN>(kp, vec, splits, stream);
     }
+}
+
+template <int OPA, int OPB>
+int launch_pingpong(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
+               g.stride_a, g.stride_b, g.stride_c, g.batch};
+    const int64_t tiles = (g.M / 256) * (g.N / 256);
+    if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
+    const dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch);
+    if (g.n_split > 0)
+        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, true>), grid, dim3(512), 0, stream, kp);
+    else
+        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, false>), grid, dim3(512), 0, stream, kp);
+    return hip_error(hipGetLastError(), "gemm_pingpong_kernel launch");
+}
+
+// The ping-pong kernel (three terms, fp32 operands); the dispatcher sends it
+// problems for which pingpong_fits() holds.
+int launch_pingpong_ops(const GemmArgs& g0, hipStream_t stream) {
+    const int64_t tiles = (g0.M / 256) * (g0.N / 256);
+    return with_splitk(g0, tiles, 32, stream,
+                       [&](const GemmArgs& g, int splits, int64_t k_chunk) {
+        if (k_chunk % 32 != 0)
+            return set_error(CDX_ERR_UNSUPPORTED, "gemm: k slice not a multiple of 32");
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_N, CDX_OP_N>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_pingpong<CDX_OP_N, CDX_OP_T>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_T, CDX_OP_N>(g, splits, k_chunk, stream);
+        return launch_pingpong<CDX_OP_T, CDX_OP_T>(g, splits, k_chunk, stream);
+    });
 }
 
 template <class CF, int TERMS = 3, int IN = kInF32>
@@ -594,12 +825,21 @@ size_t ws_of(const GemmArgs& g) {
     return splitk_bytes(g, ceil_div(g.M, CF::BM) * ceil_div(g.N, CF::BN), CF::BK);
 }
 
+// The ping-pong kernel addresses a 256-row (or 32-k-row) operand panel with
+// 32-bit byte offsets.
+bool pingpong_fits(const GemmArgs& g) {
+    return g.lda < (int64_t(1) << 22) && g.ldb < (int64_t(1) << 22);
+}
+
 template <int TERMS>
 int dispatch(const GemmArgs& g, hipStream_t stream) {
     switch (choose_bf(g, TERMS)) {
         case BfCfg::SkinnyM: return launch_ops<CfgSkinnyM, TERMS>(g, stream);
         case BfCfg::Huge:
-            if constexpr (TERMS == 3) return launch_ops<CfgHuge, TERMS>(g, stream);
+            if constexpr (TERMS == 3) {
+                if (pingpong_fits(g)) return launch_pingpong_ops(g, stream);
+                return launch_ops<CfgHuge, TERMS>(g, stream);
+            }
             return set_error(CDX_ERR_UNSUPPORTED, "gemm: no four-term Huge configuration");
         case BfCfg::Large: return launch_ops<CfgLarge, TERMS>(g, stream);
         default: return launch_ops<CfgSmall, TERMS>(g, stream);

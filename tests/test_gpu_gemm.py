@@ -226,6 +226,58 @@ def test_tf32mode_parity_shapes(mode):
         assert e <= e_rne, (M, N, K, e, e_rne)
 
 
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("K", [32, 64, 96, 544])
+def test_tf32mode_256_tile_path(tA, tB, K):
+    """The 256 x 256 two-group (ping-pong) TF32-mode kernel, which M = N =
+    4096 selects (256 tiles, aligned).  K = 32 / 64 / 96 give one, two and
+    three k-tiles (the prologue and the loop-tail branches), K = 544 a
+    longer loop.  Gate: relFro on sampled rows <= the emulated reference
+    TF32 error (either operand rounding), plus the column-checksum identity
+    on the whole output."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(1000 + K + 2 * tA + tB)
+    n = 4096
+    A = normal(rng, (K, n) if tA else (n, K))
+    B = normal(rng, (n, K) if tB else (K, n))
+    say("tf32 256-tile path", tA, tB, K)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, precision=cd.PREC_TF32MODE))
+    opA = np.ascontiguousarray(A.T if tA else A)
+    opB = np.ascontiguousarray(B.T if tB else B)
+    for rows in ((0, 48), (n // 2 - 16, n // 2 + 16), (n - 48, n)):
+        C64 = oracle.dgemm(opA, opB, rows=rows)
+        e = oracle.rel_fro(C[rows[0]:rows[1]], C64)
+        e_rz = oracle.rel_fro(oracle.gemm_tf32emu(opA, opB, "rz", rows=rows), C64)
+        e_rne = oracle.rel_fro(oracle.gemm_tf32emu(opA, opB, "rne", rows=rows), C64)
+        assert e <= min(e_rz, e_rne), (rows, e, e_rz, e_rne)
+    assert _checksum_identity(opA, opB, C) < 1e-4
+
+
+@pytest.mark.parametrize("epi,bias_mode", [("gelu", "col"), ("relu", "row"), ("silu", "none")])
+def test_tf32mode_256_tile_epilogue(epi, bias_mode):
+    """Bias + activation epilogue of the 256 x 256 TF32-mode kernel (the
+    fused Linear forward at a large batch: x @ W^T)."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(1100)
+    M, N, K = 4096, 4096, 128
+    A = normal(rng, (M, K))
+    W = normal(rng, (N, K))
+    bias = normal(rng, (M if bias_mode == "row" else N,))
+    bm = {"none": cd.BIAS_NONE, "row": cd.BIAS_ROW, "col": cd.BIAS_COL}[bias_mode]
+    ep = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU, "silu": cd.EPI_SILU}[epi]
+    say("tf32 256-tile epilogue", epi, bias_mode)
+    C = host(ops().gemm(dev(A), dev(W), transB=True, precision=cd.PREC_TF32MODE,
+                        bias=dev(bias) if bm else None, bias_mode=bm, epilogue=ep))
+    rows = (1000, 1064)
+    Z = oracle.dgemm(A, np.ascontiguousarray(W.T), rows=rows)
+    if bias_mode == "row":
+        Z = Z + bias[rows[0]:rows[1], None]
+    elif bias_mode == "col":
+        Z = Z + bias[None, :]
+    want = oracle.activation(Z, epi)
+    assert np.max(np.abs(C[rows[0]:rows[1]] - want)) <= 2e-5 * np.abs(Z).max() + 1e-6
+
+
 @pytest.mark.parametrize("tA,tB", [(False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("prec_name", ["PREC_TF32MODE", "PREC_TF32MODE4"])
 def test_tf32mode_transposes(tA, tB, prec_name):
