@@ -47,6 +47,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--headline-only", action="store_true",
                    help="time only the 4096^3 FP32 GEMM (for profiler runs)")
+    p.add_argument("--tf32-only", action="store_true",
+                   help="time only the 4096^3 TF32-mode GEMM (for profiler runs); prints "
+                        "its line to stderr and no JSON")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also run a plain 256 MiB device copy (reference point for "
@@ -324,6 +327,10 @@ def main():
         torch.cuda.synchronize()
         log("copy calibration: 3 x 256 MiB device copies (268435456 B read + written each)")
 
+    if args.tf32_only:
+        r = bench_gemm(4096, cd.PREC_TF32MODE, args.steps, max(args.warmup, 50), seed=3)
+        log("tf32mode 4096^3:", r)
+        return
     log("headline: fp32 4096^3")
     head = bench_gemm(4096, cd.PREC_FP32, args.steps, args.warmup, seed=2)
     log("fp32 4096^3:", head)
