@@ -302,7 +302,66 @@ def cpu_baseline(n=4096):
             "kind": "port",
             "sample": f"full {n}^3 FP32 GEMM, seq-FMA host reference (oracle/oracle.c), "
                       f"1 warmup + median of 3 ({t_med:.2f} s each)",
-            "numpy_f32_tflops": flops / t_np / 1e12}
+            "numpy_f32_tflops": flops / t_np / 1e12,
+            "configs": cpu_configs()}
+
+
+def _cpu_time(fn, reps=3):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts)
+
+
+def cpu_configs():
+    """The same host reference (oracle/: seq-FMA SGEMM, im2col + SGEMM conv)
+    on the other configs, bounded samples: C1 in full; C4 forward + backward
+    on 1024 of the 8192 batch rows; C5 forward on 2 of the 32 images.  Rates
+    are the sample's algorithmic FLOPs / median wall time (1 warmup + 3)."""
+    import numpy as np
+    import oracle
+    rng = np.random.default_rng(7)
+    out = {}
+    A = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    B = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    t = _cpu_time(lambda: oracle.sgemm_seqfma(A, B), reps=5)
+    out["c1_512"] = {"tflops": 2.0 * 512 ** 3 / t / 1e12, "ms": t * 1e3, "sample": "full 512^3"}
+
+    rows = 1024
+    X = rng.standard_normal((rows, 784)).astype(np.float32)
+    W1 = rng.uniform(-0.07596, 0.07596, (256, 784)).astype(np.float32)
+    W2 = rng.uniform(-0.1502, 0.1502, (10, 256)).astype(np.float32)
+    b1 = (rng.standard_normal(256) * 0.1).astype(np.float32)
+    b2 = (rng.standard_normal(10) * 0.1).astype(np.float32)
+    dY2 = rng.standard_normal((rows, 10)).astype(np.float32)
+
+    def mlp_step():
+        H = np.maximum(oracle.sgemm_seqfma(X, W1, transB=True) + b1, 0)
+        oracle.sgemm_seqfma(H, W2, transB=True) + b2
+        dH = oracle.sgemm_seqfma(dY2, W2)
+        oracle.sgemm_seqfma(dY2, H, transA=True)
+        dY2.sum(0)
+        dZ = dH * (H > 0)
+        oracle.sgemm_seqfma(dZ, W1)
+        oracle.sgemm_seqfma(dZ, X, transA=True)
+        dZ.sum(0)
+    t = _cpu_time(mlp_step)
+    fl = 3 * 2.0 * rows * (784 * 256 + 256 * 10)
+    out["c4_mlp_step"] = {"tflops": fl / t / 1e12, "ms": t * 1e3,
+                          "sample": f"forward + backward, {rows} of 8192 batch rows"}
+
+    imgs = 2
+    x = rng.standard_normal((imgs, 64, 56, 56)).astype(np.float32)
+    w = (rng.standard_normal((64, 64, 3, 3)) * (2.0 / 576) ** 0.5).astype(np.float32)
+    b = (rng.standard_normal(64) * 0.1).astype(np.float32)
+    t = _cpu_time(lambda: oracle.conv2d_ref_im2col(x, w, b, (1, 1), (1, 1)))
+    fl = 2.0 * imgs * 64 * 56 * 56 * 64 * 9
+    out["c5_conv_fwd"] = {"tflops": fl / t / 1e12, "ms": t * 1e3,
+                          "sample": f"im2col + seq-FMA GEMM + bias, {imgs} of 32 images"}
+    return out
 
 
 def main():
