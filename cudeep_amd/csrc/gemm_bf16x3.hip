@@ -115,25 +115,30 @@ struct SplitLoader {
         }
     }
 
-    // Unchecked load, address = wave-uniform tile base + 32-bit per-thread
-    // byte offset (one VGPR per block instead of a 64-bit pointer per row).
-    // `off` comes from tile_offsets(); the caller guarantees the tile is in
-    // bounds and that the offsets fit 32 bits.
-    __device__ __forceinline__ static void tile_offsets(uint32_t (&off)[NV], uint32_t ld_bytes, int tid) {
-#pragma unroll
-        for (int b = 0; b < NV; ++b) {
-            int bc, br;
-            block_coords(tid + b * NT, bc, br);
-            off[b] = (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 16);
-        }
+    // Unchecked load, address = wave-uniform base + one 32-bit per-thread
+    // byte offset (`off`, from tile_offset()).  A thread's later blocks sit a
+    // uniform distance from its first (NT blocks further on: NT / (BK/4)
+    // block rows), so only one VGPR of address is live per operand.  The
+    // caller guarantees the tile is in bounds and the offsets fit 32 bits.
+    static constexpr int ES = 4;
+    __device__ __forceinline__ static uint32_t tile_offset(uint32_t ld_bytes, int tid) {
+        int bc, br;
+        block_coords(tid, bc, br);
+        return (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 4 * ES);
+    }
+    __device__ __forceinline__ static uint64_t block_step(int b, uint32_t ld_bytes) {
+        constexpr int ROWS = NT / (BK / 4) * 4;   // block rows between a thread's blocks
+        return KCONTIG ? (uint64_t)b * ROWS * ld_bytes : (uint64_t)b * ROWS * ES;
     }
     __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
-                                            const uint32_t (&off)[NV]) {
+                                            uint32_t off) {
+        static_assert(NB % NT == 0, "whole blocks per thread");
 #pragma unroll
         for (int b = 0; b < NV; ++b)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                v[b][q] = *reinterpret_cast<const float4*>(base + (uint64_t)(q * ld_bytes) + off[b]);
+                v[b][q] = *reinterpret_cast<const float4*>(
+                    base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes) + off);
     }
 
     // Writes hi / lo planes, layout [mn][STRIDE] (k contiguous), ushort units.
@@ -217,6 +222,28 @@ struct HalfLoader {
                 }
             }
         }
+    }
+
+    // As SplitLoader::tile_offset / load_at (four 16-bit elements per load).
+    static constexpr int ES = 2;
+    __device__ __forceinline__ static uint32_t tile_offset(uint32_t ld_bytes, int tid) {
+        int bc, br;
+        block_coords(tid, bc, br);
+        return (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 4 * ES);
+    }
+    __device__ __forceinline__ static uint64_t block_step(int b, uint32_t ld_bytes) {
+        constexpr int ROWS = NT / (BK / 4) * 4;
+        return KCONTIG ? (uint64_t)b * ROWS * ld_bytes : (uint64_t)b * ROWS * ES;
+    }
+    __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
+                                            uint32_t off) {
+        static_assert(NB % NT == 0, "whole blocks per thread");
+#pragma unroll
+        for (int b = 0; b < NV; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[b][q] = *reinterpret_cast<const uint2*>(
+                    base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes) + off);
     }
 
     // Writes the plane, layout [mn][STRIDE] (k contiguous), ushort units.
@@ -541,21 +568,26 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
 // LDS traffic.  Slot order keeps the two LDS stages safe: k-tile t+1 is
 // written in slots 4t..4t+3 (stage (t+1)&1, last read by k-tile t-1 in slot
 // 4t-1) and first read in slot 4t+4.  Global loads are consumed four slots
-// after they are issued.  Aligned problems only (M, N % 256, K % 32, 16-byte
-// operands).  fp32 operands, three terms, the same per-element term order as
-// gemm_bf16x3_kernel (so the same results); BK = 32, LDS 2 x 80 KiB.
-// Measured at 4096^3 against gemm_bf16x3_kernel's 256 x 256 configuration
-// (which runs the two waves of a SIMD in step): 0.310 against 0.361 ms.
-template <int OPA, int OPB, bool SPLITN>
+// after they are issued.  Aligned problems only (M, N % 256, K % BK, 16-byte
+// operands).  IN = fp32: three terms in gemm_bf16x3_kernel's per-element
+// order (so the same results), BK = 32, LDS 2 x 80 KiB; 16-bit operands: one
+// plane, BK = 64, one MFMA per fragment pair and 32-k step.  Measured at
+// 4096^3 against gemm_bf16x3_kernel's 256 x 256 configurations (the two
+// waves of a SIMD in step): 0.310 against 0.361 ms (bf16x3), 0.172 against
+// 0.234 ms (bf16).
+template <int OPA, int OPB, bool SPLITN, int IN = kInF32>
 __global__ __launch_bounds__(512)
 void gemm_pingpong_kernel(KParams p) {
     constexpr int BM = 256, BN = 256, NT = 512, GROUP_M = 8;
-    constexpr int BK = 32;
-    constexpr int ES = 4;                          // operand element bytes
+    constexpr bool H16 = IN != kInF32;
+    constexpr int BK = H16 ? 64 : 32;
+    constexpr int NK32 = BK / 32;                  // 32-k MFMA steps per k-tile
+    constexpr int NPL = H16 ? 1 : 2;               // planes per operand
+    constexpr int ES = H16 ? 2 : 4;                // operand element bytes
     constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
     constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
-    constexpr int B_OFF = 2 * A_PLANE;             // stage: A hi, A lo, B hi, B lo
-    constexpr int STAGE = 2 * (A_PLANE + B_PLANE);
+    constexpr int B_OFF = NPL * A_PLANE;           // stage: A planes, then B planes
+    constexpr int STAGE = NPL * (A_PLANE + B_PLANE);
     __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
 
     const int tid = threadIdx.x;
@@ -583,14 +615,20 @@ void gemm_pingpong_kernel(KParams p) {
         p.C += (int64_t)blockIdx.z * p.sc;
     }
 
-    using LoaderA = SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>;
-    using LoaderB = SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>;
+    using LoaderA = std::conditional_t<H16, HalfLoader<BM, BK, NT, OPA == CDX_OP_N, false>,
+                                       SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>>;
+    using LoaderB = std::conditional_t<H16, HalfLoader<BN, BK, NT, OPB == CDX_OP_T, false>,
+                                       SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>>;
     static_assert(LoaderA::NB % NT == 0 && LoaderB::NB % NT == 0, "whole blocks per thread");
     LoaderA la;
     LoaderB lb;
-    auto store_a = [&](unsigned short* s) { la.template store<STRIDE>(s, s + A_PLANE, tid); };
+    auto store_a = [&](unsigned short* s) {
+        if constexpr (H16) la.template store<STRIDE>(s, tid);
+        else la.template store<STRIDE>(s, s + A_PLANE, tid);
+    };
     auto store_b = [&](unsigned short* s) {
-        lb.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, tid);
+        if constexpr (H16) lb.template store<STRIDE>(s + B_OFF, tid);
+        else lb.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, tid);
     };
 
     floatx4 acc[8][4];
@@ -599,47 +637,67 @@ void gemm_pingpong_kernel(KParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // fa: hi / lo fragments of four A rows (one half of the wave's rows);
-    // fb: hi / lo fragments of the wave's four B columns
-    bf16x8 fa[4][2], fb[4][2];
+    // fa: fragments of four A rows (one half of the wave's rows), fb: of the
+    // wave's four B columns; [32-k step][plane], plane 0 = hi (or the 16-bit
+    // operand), 1 = lo
+    shortx8 fa[4][NK32][NPL], fb[4][NK32][NPL];
     auto read_a = [&](const unsigned short* s, int half) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int pl = 0; pl < 2; ++pl)
-                fa[i][pl] = *reinterpret_cast<const bf16x8*>(
-                    s + pl * A_PLANE + (wm0 + (half * 4 + i) * 16 + l16) * STRIDE + 8 * lq);
+            for (int kk = 0; kk < NK32; ++kk)
+#pragma unroll
+                for (int pl = 0; pl < NPL; ++pl)
+                    fa[i][kk][pl] = *reinterpret_cast<const shortx8*>(
+                        s + pl * A_PLANE + (wm0 + (half * 4 + i) * 16 + l16) * STRIDE + kk * 32 + 8 * lq);
     };
     auto read_b = [&](const unsigned short* s) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int pl = 0; pl < 2; ++pl)
-                fb[j][pl] = *reinterpret_cast<const bf16x8*>(
-                    s + B_OFF + pl * B_PLANE + (wn0 + j * 16 + l16) * STRIDE + 8 * lq);
+            for (int kk = 0; kk < NK32; ++kk)
+#pragma unroll
+                for (int pl = 0; pl < NPL; ++pl)
+                    fb[j][kk][pl] = *reinterpret_cast<const shortx8*>(
+                        s + B_OFF + pl * B_PLANE + (wn0 + j * 16 + l16) * STRIDE + kk * 32 + 8 * lq);
     };
-    // MFMAs of fragment rows half*4 .. half*4+3: lo*hi and hi*lo first, then
-    // hi*hi (index 0 = hi, 1 = lo)
+    auto mfma = [](const shortx8& a, const shortx8& b, const floatx4& c) {
+        if constexpr (IN == kInF16)
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, a),
+                                                          __builtin_bit_cast(halfx8, b), c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                           __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    };
+    // MFMAs of fragment rows half*4 .. half*4+3; fp32 operands: lo*hi and
+    // hi*lo first, then hi*hi
     auto math = [&](int half) {
         __builtin_amdgcn_s_setprio(1);
+        if constexpr (H16) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int kk = 0; kk < NK32; ++kk)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[half * 4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    fa[i][1], fb[j][0], acc[half * 4 + i][j], 0, 0, 0);
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                    for (int j = 0; j < 4; ++j)
+                        acc[half * 4 + i][j] = mfma(fa[i][kk][0], fb[j][kk][0], acc[half * 4 + i][j]);
+        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[half * 4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    fa[i][0], fb[j][1], acc[half * 4 + i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 4; ++j)
+                    acc[half * 4 + i][j] = mfma(fa[i][0][1], fb[j][0][0], acc[half * 4 + i][j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[half * 4 + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    fa[i][0], fb[j][0], acc[half * 4 + i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[half * 4 + i][j] = mfma(fa[i][0][0], fb[j][0][1], acc[half * 4 + i][j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[half * 4 + i][j] = mfma(fa[i][0][0], fb[j][0][0], acc[half * 4 + i][j]);
+        }
         __builtin_amdgcn_s_setprio(0);
     };
     // slot boundary: nothing moves across it
@@ -654,9 +712,8 @@ void gemm_pingpong_kernel(KParams p) {
     // less than 4 GiB).  k-contiguous operands step ES*BK bytes per k-tile,
     // m/n-contiguous ones BK rows.
     const uint32_t lda_b = (uint32_t)(p.lda * ES), ldb_b = (uint32_t)(p.ldb * ES);
-    uint32_t offa[LoaderA::NV], offb[LoaderB::NV];
-    LoaderA::tile_offsets(offa, lda_b, tid);
-    LoaderB::tile_offsets(offb, ldb_b, tid);
+    const uint32_t offa = LoaderA::tile_offset(lda_b, tid);
+    const uint32_t offb = LoaderB::tile_offset(ldb_b, tid);
     const char* baseA = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? bm * p.lda : bm);
     const char* baseB = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? bn : bn * p.ldb);
     const int64_t stepA = OPA == CDX_OP_N ? (int64_t)ES * BK : (int64_t)BK * p.lda * ES;
@@ -737,7 +794,7 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
     }
 }
 
-template <int OPA, int OPB>
+template <int OPA, int OPB, int IN>
 int launch_pingpong(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
@@ -747,24 +804,26 @@ int launch_pingpong(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t 
     if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
     const dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch);
     if (g.n_split > 0)
-        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, true>), grid, dim3(512), 0, stream, kp);
+        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, true, IN>), grid, dim3(512), 0, stream, kp);
     else
-        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, false>), grid, dim3(512), 0, stream, kp);
+        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, false, IN>), grid, dim3(512), 0, stream, kp);
     return hip_error(hipGetLastError(), "gemm_pingpong_kernel launch");
 }
 
-// The ping-pong kernel (three terms, fp32 operands); the dispatcher sends it
-// problems for which pingpong_fits() holds.
+// The ping-pong kernel for fp32 operands (three terms) or 16-bit ones; the
+// dispatcher sends it problems for which pingpong_fits() holds.
+template <int IN>
 int launch_pingpong_ops(const GemmArgs& g0, hipStream_t stream) {
+    constexpr int BK = IN == kInF32 ? 32 : 64;
     const int64_t tiles = (g0.M / 256) * (g0.N / 256);
-    return with_splitk(g0, tiles, 32, stream,
+    return with_splitk(g0, tiles, BK, stream,
                        [&](const GemmArgs& g, int splits, int64_t k_chunk) {
-        if (k_chunk % 32 != 0)
-            return set_error(CDX_ERR_UNSUPPORTED, "gemm: k slice not a multiple of 32");
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_N, CDX_OP_N>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_pingpong<CDX_OP_N, CDX_OP_T>(g, splits, k_chunk, stream);
-        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_T, CDX_OP_N>(g, splits, k_chunk, stream);
-        return launch_pingpong<CDX_OP_T, CDX_OP_T>(g, splits, k_chunk, stream);
+        if (k_chunk % BK != 0)
+            return set_error(CDX_ERR_UNSUPPORTED, "gemm: k slice not a multiple of the k-tile");
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_N, CDX_OP_N, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_pingpong<CDX_OP_N, CDX_OP_T, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_T, CDX_OP_N, IN>(g, splits, k_chunk, stream);
+        return launch_pingpong<CDX_OP_T, CDX_OP_T, IN>(g, splits, k_chunk, stream);
     });
 }
 
@@ -837,7 +896,7 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
         case BfCfg::SkinnyM: return launch_ops<CfgSkinnyM, TERMS>(g, stream);
         case BfCfg::Huge:
             if constexpr (TERMS == 3) {
-                if (pingpong_fits(g)) return launch_pingpong_ops(g, stream);
+                if (pingpong_fits(g)) return launch_pingpong_ops<kInF32>(g, stream);
                 return launch_ops<CfgHuge, TERMS>(g, stream);
             }
             return set_error(CDX_ERR_UNSUPPORTED, "gemm: no four-term Huge configuration");
@@ -871,8 +930,10 @@ using Cfg16Small = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
 
 template <int IN>
 int dispatch16(const GemmArgs& g, hipStream_t stream) {
-    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<Cfg16Huge>(g))
+    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<Cfg16Huge>(g)) {
+        if (pingpong_fits(g)) return launch_pingpong_ops<IN>(g, stream);
         return launch_ops<Cfg16Huge, 1, IN>(g, stream);
+    }
     if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<Cfg16Large, 1, IN>(g, stream);
     return launch_ops<Cfg16Small, 1, IN>(g, stream);
 }

@@ -107,6 +107,33 @@ def test_gemm16_4096_sampled_rows(dtype):
     assert np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs) < 1e-5
 
 
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("K", [64, 128, 192, 1088])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_gemm16_256_tile_path(tA, tB, K, dtype):
+    """The 256 x 256 two-group (ping-pong) kernel for 16-bit operands, which
+    M = N = 4096 selects: K = 64 / 128 / 192 give one, two and three k-tiles,
+    K = 1088 a longer loop; all four transposes.  Same gate as the other
+    16-bit tests on sampled rows, plus the column-checksum identity."""
+    rng = np.random.default_rng(2000 + K + 2 * tA + tB)
+    n = 4096
+    A, A32 = _operands(rng, (K, n) if tA else (n, K), dtype)
+    B, B32 = _operands(rng, (n, K) if tB else (K, n), dtype)
+    say("gemm16 256-tile path", dtype, tA, tB, K)
+    C = host(ops().gemm16(A, B, transA=tA, transB=tB))
+    opA = np.ascontiguousarray(A32.T if tA else A32)
+    opB = np.ascontiguousarray(B32.T if tB else B32)
+    for r0 in (0, 1500, n - 48):
+        rows = (r0, r0 + 48)
+        C64 = oracle.dgemm(opA, opB, rows=rows)
+        e = oracle.rel_fro(C[r0:r0 + 48], C64)
+        e_ideal = oracle.rel_fro(oracle.gemm_tf32emu(opA, opB, "rne", rows=rows), C64)
+        assert e <= 2 * e_ideal, (rows, e, e_ideal)
+    lhs = C.astype(np.float64).sum(0)
+    rhs = opA.astype(np.float64).sum(0) @ opB.astype(np.float64)
+    assert np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs) < 1e-5
+
+
 def test_hgemm_entry_point_and_epilogue():
     import cudeep_amd as cd
     rng = np.random.default_rng(65)
