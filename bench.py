@@ -44,7 +44,10 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    # 100 warmup launches (0.1 s at 4096^3): the clock settles over the first
+    # ~10-40 ms of sustained MFMA work (4096^3 FP32: 1.037 ms per launch with
+    # 10 warmup launches, 1.016 ms with 100)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--headline-only", action="store_true",
                    help="time only the 4096^3 FP32 GEMM (for profiler runs)")
     p.add_argument("--tf32-only", action="store_true",
@@ -57,14 +60,20 @@ def parse():
     return p.parse_args()
 
 
-def time_launches(fn, steps, warmup):
-    """Runs fn() warmup times, then `steps` times with a HIP event pair
-    around each launch on the current stream.  Returns (mean ms per step
-    from the bracketing events, list of per-launch ms)."""
+def time_launches(fn, steps, warmup, min_warm_s=0.0):
+    """Runs fn() warmup times (and, with min_warm_s, keeps going in batches
+    of 10 until that much wall time has passed), then `steps` times with a
+    HIP event pair around each launch on the current stream.  Returns (mean
+    ms per step from the bracketing events, list of per-launch ms)."""
     import torch
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < min_warm_s:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
     outer0 = torch.cuda.Event(enable_timing=True)
@@ -81,7 +90,7 @@ def time_launches(fn, steps, warmup):
     return outer0.elapsed_time(outer1) / steps, per
 
 
-def bench_gemm(n, precision, steps, warmup, seed):
+def bench_gemm(n, precision, steps, warmup, seed, min_warm_s=0.0):
     import torch
     import cudeep_amd.ops as ops
     import cudeep_amd as cd
@@ -95,7 +104,7 @@ def bench_gemm(n, precision, steps, warmup, seed):
     else:
         def f():
             ops.gemm(A, B, precision=precision, out=C)
-    ms, per = time_launches(f, steps, warmup)
+    ms, per = time_launches(f, steps, warmup, min_warm_s)
     flops = 2.0 * n ** 3
     return {"n": n, "ms_per_step": ms, "kernel_ms_mean": statistics.mean(per),
             "kernel_ms_median": statistics.median(per),
@@ -103,7 +112,7 @@ def bench_gemm(n, precision, steps, warmup, seed):
             "tflops_kernel_median": flops / (statistics.median(per) * 1e-3) / 1e12}
 
 
-def bench_gemm16(n, dtype, steps, warmup, seed):
+def bench_gemm16(n, dtype, steps, warmup, seed, min_warm_s=0.0):
     """16-bit-operand GEMM (cdx_gemm16_ex): fp16 / bf16 A, B, fp32 C."""
     import torch
     import cudeep_amd.ops as ops
@@ -112,7 +121,7 @@ def bench_gemm16(n, dtype, steps, warmup, seed):
     A = torch.randn((n, n), device="cuda", generator=g).to(td)
     B = torch.randn((n, n), device="cuda", generator=g).to(td)
     C = torch.empty((n, n), device="cuda")
-    ms, per = time_launches(lambda: ops.gemm16(A, B, out=C), steps, warmup)
+    ms, per = time_launches(lambda: ops.gemm16(A, B, out=C), steps, warmup, min_warm_s)
     flops = 2.0 * n ** 3
     return {"n": n, "ms_per_step": ms, "kernel_ms_median": statistics.median(per),
             "tflops": flops / (ms * 1e-3) / 1e12,
@@ -387,7 +396,8 @@ def main():
         log("copy calibration: 3 x 256 MiB device copies (268435456 B read + written each)")
 
     if args.tf32_only:
-        r = bench_gemm(4096, cd.PREC_TF32MODE, args.steps, max(args.warmup, 50), seed=3)
+        r = bench_gemm(4096, cd.PREC_TF32MODE, args.steps, max(args.warmup, 50), seed=3,
+                       min_warm_s=0.1)
         log("tf32mode 4096^3:", r)
         return
     log("headline: fp32 4096^3")
@@ -396,21 +406,22 @@ def main():
     extra = {}
     # The reduced-precision GEMMs run ~12 % slower for their first ~20 ms of
     # back-to-back launches (the clock settles under the new load; measured
-    # 344 -> 300 us per 4096^3 TF32-mode launch), so their lines use at least
-    # 50 warmup launches and report the settled rate.
+    # 344 -> 300 us per 4096^3 TF32-mode launch), so these lines warm up for
+    # at least 50 launches and 0.1 s and report the settled rate.
     w_extra = max(args.warmup, 50)
+    warm_s = 0.1
     if not args.headline_only:
         for n in (4096, 2048):
-            r = bench_gemm(n, cd.PREC_TF32MODE, args.steps, w_extra, seed=3)
+            r = bench_gemm(n, cd.PREC_TF32MODE, args.steps, w_extra, seed=3, min_warm_s=warm_s)
             r["frac_of_bf16x3_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 3)
             extra[f"tf32mode_{n}"] = r
             log(f"tf32mode {n}^3:", r)
-        r = bench_gemm(4096, cd.PREC_TF32MODE4, args.steps, w_extra, seed=3)
+        r = bench_gemm(4096, cd.PREC_TF32MODE4, args.steps, w_extra, seed=3, min_warm_s=warm_s)
         r["frac_of_bf16x4_ceiling"] = r["tflops"] / (BF16_PEAK_TFLOPS / 4)
         extra["tf32mode4_4096"] = r
         log("tf32mode4 (bf16x4) 4096^3:", r)
         for dt in ("f16", "bf16"):
-            r = bench_gemm16(4096, dt, args.steps, w_extra, seed=6)
+            r = bench_gemm16(4096, dt, args.steps, w_extra, seed=6, min_warm_s=warm_s)
             extra[f"{dt}_gemm_4096"] = r
             log(f"{dt} GEMM 4096^3:", r)
         for prec, name in ((cd.PREC_FP32, "fp32"), (cd.PREC_TF32MODE, "tf32mode")):
