@@ -72,17 +72,19 @@ int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStrea
 
 // Split-K policy shared by the GEMM kernels: split only when the tile grid
 // cannot fill the GPU (fewer than 128 tiles) and K is long; aim at ~768
-// workgroups with at least 256 k per slice (measured on the MLP / conv
-// weight gradients: 10x256x8192 best at 32 slices, 256x784x8192 at ~16,
-// 64x576x100352 at ~64-128).  Returns the slice count and sets *k_chunk (a
-// multiple of bk).
+// workgroups with at least min_k k per slice.  FP32 (BK 16) uses min_k 256
+// (measured on the MLP / conv weight gradients: 10x256x8192 best at 32
+// slices, 256x784x8192 at ~16, 64x576x100352 at ~64-128); the bf16x3 kernels
+// (BK 32-64, a longer pipeline fill per slice) 1024 (256x784x8192: 8 slices
+// 47.6 us NN / 35.2 NT against 55.9 / 42.3 at 15).  Returns the slice count
+// and sets *k_chunk (a multiple of bk).
 inline bool splitk_applies(int64_t tiles, int64_t K) { return tiles < 128 && K >= 2048; }
 
-inline int choose_splitk(int64_t tiles, int64_t K, int bk, int64_t* k_chunk) {
+inline int choose_splitk(int64_t tiles, int64_t K, int bk, int64_t* k_chunk, int64_t min_k = 256) {
     *k_chunk = K;
     if (!splitk_applies(tiles, K)) return 1;
     int64_t s = (768 + tiles / 2) / tiles;
-    if (s > K / 256) s = K / 256;
+    if (s > K / min_k) s = K / min_k;
     if (s < 2) return 1;
     int64_t kc = ceil_div(ceil_div(K, s), bk) * bk;
     *k_chunk = kc;
@@ -90,10 +92,10 @@ inline int choose_splitk(int64_t tiles, int64_t K, int bk, int64_t* k_chunk) {
 }
 
 // Split-K partial bytes of a GEMM whose tile grid is `tiles` (0: no split).
-inline size_t splitk_bytes(const GemmArgs& g, int64_t tiles, int bk) {
+inline size_t splitk_bytes(const GemmArgs& g, int64_t tiles, int bk, int64_t min_k = 256) {
     if (g.batch > 1) return 0;
     int64_t k_chunk;
-    const int splits = choose_splitk(tiles, g.K, bk, &k_chunk);
+    const int splits = choose_splitk(tiles, g.K, bk, &k_chunk, min_k);
     return splits > 1 ? (size_t)splits * (size_t)g.M * (size_t)g.N * sizeof(float) : 0;
 }
 
@@ -102,9 +104,11 @@ inline size_t splitk_bytes(const GemmArgs& g, int64_t tiles, int bk) {
 // ordered), calls launch(kparams-adjusted GemmArgs, splits, k_chunk) and
 // reduces.
 template <class LaunchFn>
-int with_splitk(const GemmArgs& g, int64_t tiles, int bk, hipStream_t stream, LaunchFn launch) {
+int with_splitk(const GemmArgs& g, int64_t tiles, int bk, hipStream_t stream, LaunchFn launch,
+                int64_t min_k = 256) {
     int64_t k_chunk;
-    const int splits = g.batch > 1 ? (k_chunk = g.K, 1) : choose_splitk(tiles, g.K, bk, &k_chunk);
+    const int splits = g.batch > 1 ? (k_chunk = g.K, 1)
+                                   : choose_splitk(tiles, g.K, bk, &k_chunk, min_k);
     if (splits == 1) return launch(g, 1, g.K);
     float* part = static_cast<float*>(g.ws);
     const size_t bytes = (size_t)splits * (size_t)g.M * (size_t)g.N * sizeof(float);

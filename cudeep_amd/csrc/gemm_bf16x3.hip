@@ -827,6 +827,10 @@ int launch_pingpong_ops(const GemmArgs& g0, hipStream_t stream) {
     });
 }
 
+// Split-K slices of these kernels hold at least this much k (see
+// choose_splitk).
+constexpr int64_t kSplitMinK = 1024;
+
 template <class CF, int TERMS = 3, int IN = kInF32>
 int launch_ops(const GemmArgs& g0, hipStream_t stream) {
     const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
@@ -836,7 +840,7 @@ int launch_ops(const GemmArgs& g0, hipStream_t stream) {
         if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T, TERMS, IN>(g, splits, k_chunk, stream);
         if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N, TERMS, IN>(g, splits, k_chunk, stream);
         return launch_mode<CF, CDX_OP_T, CDX_OP_T, TERMS, IN>(g, splits, k_chunk, stream);
-    });
+    }, kSplitMinK);
 }
 
 // Tile configurations (measured on MI355X, NN):
@@ -881,7 +885,7 @@ BfCfg choose_bf(const GemmArgs& g, int terms) {
 
 template <class CF>
 size_t ws_of(const GemmArgs& g) {
-    return splitk_bytes(g, ceil_div(g.M, CF::BM) * ceil_div(g.N, CF::BN), CF::BK);
+    return splitk_bytes(g, ceil_div(g.M, CF::BM) * ceil_div(g.N, CF::BN), CF::BK, kSplitMinK);
 }
 
 // The ping-pong kernel addresses a 256-row (or 32-k-row) operand panel with
@@ -905,9 +909,21 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
     }
 }
 
+// Weight-gradient-shaped products -- A transposed, too few output tiles to
+// fill the GPU, long K (split-K) -- run on the FP32 kernel in the TF32
+// modes: there both bf16x3 operands would be transposed in registers on the
+// way into LDS over short k slices, and FP32 measured faster (256 x 784 x
+// 8192: 52 us against 66 us at bf16x3's best split) with exact products,
+// which is inside the TF32-mode error bar.
+bool tn_split_to_f32(const GemmArgs& g, int terms) {
+    return g.opA == CDX_OP_T && g.batch == 1 && choose_bf(g, terms) == BfCfg::Small &&
+           splitk_applies(ceil_div(g.M, CfgSmall::BM) * ceil_div(g.N, CfgSmall::BN), g.K);
+}
+
 }  // namespace
 
 size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms) {
+    if (tn_split_to_f32(g, terms)) return gemm_f32_workspace(g);
     switch (choose_bf(g, terms)) {
         case BfCfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case BfCfg::Huge: return ws_of<CfgHuge>(g);
@@ -917,6 +933,7 @@ size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms) {
 }
 
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream) {
+    if (tn_split_to_f32(g, terms)) return launch_gemm_f32(g, stream);
     return terms == 4 ? dispatch<4>(g, stream) : dispatch<3>(g, stream);
 }
 
