@@ -62,6 +62,16 @@ __device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned
 
 __device__ __forceinline__ float ld_guard(const float* p, bool ok) { return ok ? *p : 0.0f; }
 
+// A wave-uniform address made explicit (scalar registers): loads of the form
+// uniform(p) + 32-bit offset can then use the scalar-base global load and
+// keep one VGPR of address per load instead of a 64-bit VGPR pair.
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
 // Loads an operand tile for the k-range [k0, k0+BK) and mn-range
 // [mn0, mn0+BMN) into registers, as 4x4 blocks (4 mn x 4 k).  KCONTIG says
 // whether k is the contiguous dimension in memory.
@@ -130,6 +140,11 @@ struct SplitLoader {
         constexpr int ROWS = NT / (BK / 4) * 4;   // block rows between a thread's blocks
         return KCONTIG ? (uint64_t)b * ROWS * ld_bytes : (uint64_t)b * ROWS * ES;
     }
+    // k-contiguous operands: the four rows' bases in scalar registers (with
+    // both operands k-contiguous the 64-bit per-row addresses otherwise spill)
+    __device__ __forceinline__ static const char* row_base(const char* p) {
+        return KCONTIG ? uniform_ptr(p) : p;
+    }
     __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
                                             uint32_t off) {
         static_assert(NB % NT == 0, "whole blocks per thread");
@@ -138,7 +153,7 @@ struct SplitLoader {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 v[b][q] = *reinterpret_cast<const float4*>(
-                    base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes) + off);
+                    row_base(base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes)) + off);
     }
 
     // Writes hi / lo planes, layout [mn][STRIDE] (k contiguous), ushort units.
@@ -235,6 +250,11 @@ struct HalfLoader {
         constexpr int ROWS = NT / (BK / 4) * 4;
         return KCONTIG ? (uint64_t)b * ROWS * ld_bytes : (uint64_t)b * ROWS * ES;
     }
+    // k-contiguous operands: the four rows' bases in scalar registers (with
+    // both operands k-contiguous the 64-bit per-row addresses otherwise spill)
+    __device__ __forceinline__ static const char* row_base(const char* p) {
+        return KCONTIG ? uniform_ptr(p) : p;
+    }
     __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
                                             uint32_t off) {
         static_assert(NB % NT == 0, "whole blocks per thread");
@@ -243,7 +263,7 @@ struct HalfLoader {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 v[b][q] = *reinterpret_cast<const uint2*>(
-                    base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes) + off);
+                    row_base(base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes)) + off);
     }
 
     // Writes the plane, layout [mn][STRIDE] (k contiguous), ushort units.
