@@ -208,6 +208,42 @@ def bench_mlp(steps, warmup, precision):
     with torch.cuda.graph(graph):
         step()
     graph_ms, _ = time_launches(graph.replay, steps, warmup)
+
+    # The same step with the backward's independent branches on two side
+    # streams (dW2 + its bias sum beside dH and the ReLU mask; dW1 + its bias
+    # sum beside dX), each on its own workspaces: the graph runs them
+    # concurrently, overlapping the GEMMs' latency-bound phases and tails.
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def step_forked():
+        main = torch.cuda.current_stream()
+        ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
+                 precision=precision, out=H, workspace=ws_f1)
+        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y,
+                 workspace=ws_f2)
+        s1.wait_stream(main)
+        with torch.cuda.stream(s1):
+            ops.gemm(dY2, H, transA=True, precision=precision, out=gW2, workspace=ws_w2)
+            ops.sum_reduce_rows(dY2, out=gb2, workspace=ws_b2)
+        ops.gemm(dY2, W2, precision=precision, out=dH, workspace=ws_h)
+        ops.activation_backward(dH, H, cd.EPI_RELU, out=dZ)
+        s2.wait_stream(main)
+        with torch.cuda.stream(s2):
+            ops.gemm(dZ, X, transA=True, precision=precision, out=gW1, workspace=ws_w1)
+            ops.sum_reduce_rows(dZ, out=gb1, workspace=ws_b1)
+        ops.gemm(dZ, W1, precision=precision, out=gX, workspace=ws_x)
+        main.wait_stream(s1)
+        main.wait_stream(s2)
+
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step_forked()
+    torch.cuda.current_stream().wait_stream(side)
+    graph2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph2):
+        step_forked()
+    graph2_ms, _ = time_launches(graph2.replay, steps, warmup)
     # per-GEMM timing of the big forward GEMM
     l1_ms, _ = time_launches(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
                                               epilogue=cd.EPI_RELU, precision=precision, out=H),
@@ -217,6 +253,8 @@ def bench_mlp(steps, warmup, precision):
             "bwd_tflops": bwd_flops / (bwd_ms * 1e-3) / 1e12,
             "step_graph_ms": graph_ms,
             "step_graph_tflops": (fwd_flops + bwd_flops) / (graph_ms * 1e-3) / 1e12,
+            "step_graph_forked_ms": graph2_ms,
+            "step_graph_forked_tflops": (fwd_flops + bwd_flops) / (graph2_ms * 1e-3) / 1e12,
             "fwd1_fused_ms": l1_ms,
             "fwd1_fused_tflops": 2.0 * 8192 * 784 * 256 / (l1_ms * 1e-3) / 1e12}
 

@@ -61,8 +61,12 @@ def test_gemm_workspace_zero_when_no_split():
         assert ops.gemm_workspace_bytes(8192, 784, 256, precision=prec) == 0
 
 
+@pytest.mark.parametrize("forked", [False, True])
 @pytest.mark.parametrize("prec", [0, 1])
-def test_captured_step_replays_match_eager(prec):
+def test_captured_step_replays_match_eager(prec, forked):
+    """forked: the backward's independent branches (dW2 + its bias sum beside
+    dH and the ReLU mask; dW1 + its bias sum beside dX) captured on two side
+    streams, each branch on its own workspaces."""
     import torch
     import cudeep_amd as cd
     ops = _ops()
@@ -103,17 +107,40 @@ def test_captured_step_replays_match_eager(prec):
         ops.gemm(o["dZ"], X, transA=True, precision=prec, out=o["gW1"], workspace=ws["w1"])
         ops.sum_reduce_rows(o["dZ"], out=o["gb1"], workspace=ws["b1"])
 
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def step_forked(o):
+        main = torch.cuda.current_stream()
+        ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
+                 precision=prec, out=o["H"], workspace=ws["f1"])
+        ops.gemm(o["H"], W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=prec,
+                 out=o["Y"], workspace=ws["f2"])
+        s1.wait_stream(main)
+        with torch.cuda.stream(s1):
+            ops.gemm(dY2, o["H"], transA=True, precision=prec, out=o["gW2"], workspace=ws["w2"])
+            ops.sum_reduce_rows(dY2, out=o["gb2"], workspace=ws["b2"])
+        ops.gemm(dY2, W2, precision=prec, out=o["dH"], workspace=ws["h"])
+        ops.activation_backward(o["dH"], o["H"], cd.EPI_RELU, out=o["dZ"])
+        s2.wait_stream(main)
+        with torch.cuda.stream(s2):
+            ops.gemm(o["dZ"], X, transA=True, precision=prec, out=o["gW1"], workspace=ws["w1"])
+            ops.sum_reduce_rows(o["dZ"], out=o["gb1"], workspace=ws["b1"])
+        ops.gemm(o["dZ"], W1, precision=prec, out=o["gX"], workspace=ws["x"])
+        main.wait_stream(s1)
+        main.wait_stream(s2)
+
+    captured = step_forked if forked else step
     X.normal_(generator=g)
     dY2.normal_(generator=g)
-    say("graph capture", "prec", prec)
+    say("graph capture", "prec", prec, "forked", forked)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        step(outs)
+        captured(outs)
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        step(outs)
+        captured(outs)
     torch.cuda.synchronize()
     eager = {k: torch.empty_like(v) for k, v in outs.items()}
     for r in range(4):
