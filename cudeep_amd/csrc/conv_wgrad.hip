@@ -49,6 +49,9 @@ namespace {
 #ifndef CDX_WGRAD_TARGET_WGS
 #define CDX_WGRAD_TARGET_WGS 256
 #endif
+#ifndef CDX_WGRAD_ROWS_WGS
+#define CDX_WGRAD_ROWS_WGS 256
+#endif
 constexpr int WG_BM = 64, WG_BN = CDX_WGRAD_BN, WG_BK = CDX_WGRAD_BK;
 constexpr int WG_WAVES_N = WG_BN / 32;
 constexpr int WG_NT = 64 * 2 * WG_WAVES_N;
@@ -307,6 +310,338 @@ void conv_wgrad_f32_kernel(WgArgs p) {
         }
 }
 
+// ---- Row-window form for 3x3, stride-1 layers ---------------------------
+//
+// With stride 1 the im2col rows of one input channel ic and filter row kh are
+// shifts of a single input row: for the output-row segment (b, oh, ow0 ..
+// ow0 + BKP) the gathered element is
+//   col[(ic, kh, kw)][p] = x[b, ic, oh + kh - PH, ow0 + p + kw - PW].
+// So a k-tile here is one such segment of BKP pixels (BKP = 32, 56 or 64: the
+// output width rounded up, segments of 64 beyond that).  Per k-tile the
+// workgroup stages into LDS the 64 dY rows of its output channels and the 3
+// input rows of each of its 16 input channels -- whole-row 16-byte loads, no
+// per-element index math or bounds test beyond the row and its two halo
+// columns -- and a lane reads its B operand at row (ic, kh), column p + kw.
+//
+// Tile: 64 (OC) x 144 (16 channels x 9 taps) outputs, 12 waves of 16 x 48 (three
+// per SIMD: a 6-wave workgroup of 32 x 48 leaves two SIMDs with twice the
+// MFMA work of the other two, and measured slower).
+// MFMA step t of a k-tile: lane (l16, lq) feeds pixel KQ*lq + t (KQ = BKP/4),
+// for A and B alike, so the four lane groups together cover each pixel once.
+// In LDS each input row is split into four blocks, one per lane group: block
+// g holds row positions KQ*g .. KQ*g + KQ + 1 (its pixels plus the two
+// columns the kw shift reaches; those are stored twice), at a pitch XB of 16
+// floats (48 when KQ + 2 > 16).  Rows sit at a pitch of 3 (mod 32) floats.  A
+// B read for filter row n = (ic*3 + kh)*3 + kw then lands on bank
+// (n + XB*lq + t) mod 64: 16 consecutive filter rows hit 16 consecutive banks
+// and the four lane groups disjoint quarters.  (Rows kept whole, the groups
+// 14 pixels apart overlapped on two banks each: 48 % of LDS-active cycles
+// were bank conflicts, 25 % with the blocks -- the C5 time did not change.)
+// Two register staging sets keep tile k+2's loads in flight; one workgroup
+// per CU (about 256 in all; two per CU with twice the slices measured slower).
+// Measured on MI355X at C5 (32 x 64 x 56^2, OC 64): 84.5 us per launch plus
+// the slice reduction, against 100+ us for conv_wgrad_f32_kernel.
+constexpr int RW_BM = 64, RW_ICT = 16, RW_BN = RW_ICT * 9, RW_NT = 768;
+
+template <int BKP>
+struct RwShape {
+    static constexpr int KQ = BKP / 4;                       // MFMA steps per k-tile
+    static constexpr int A_STRIDE = BKP + 4;                 // dY row pitch (floats)
+    static constexpr int XB = KQ + 2 <= 16 ? 16 : 48;        // x block pitch per lane group
+    static constexpr int X_LEN = 3 * XB + KQ + 2;            // floats used per x row
+    static constexpr int X_RS = ((X_LEN - 3 + 31) / 32) * 32 + 3;   // >= X_LEN, = 3 mod 32
+    static constexpr int X_ROWS = RW_ICT * 3;
+    static constexpr int STAGE = RW_BM * A_STRIDE + X_ROWS * X_RS;
+    static constexpr int NA = (RW_BM * KQ + RW_NT - 1) / RW_NT;       // dY float4 per thread
+    static constexpr int NX = (X_ROWS * KQ + RW_NT - 1) / RW_NT;      // x float4 per thread
+    static_assert(KQ % 2 == 0 && X_RS >= X_LEN && X_RS % 32 == 3, "row-window shape");
+    // LDS column(s) of row position P (0 .. BKP+1): its own block, and the
+    // previous block too for the first two positions of a block (c2 = c1 when
+    // there is no second copy, so both stores can be made unconditionally)
+    __device__ __forceinline__ static void cols_of(int P, int& c1, int& c2) {
+        const int b = P / KQ < 3 ? P / KQ : 3;
+        c1 = XB * b + P - KQ * b;
+        c2 = (b >= 1 && P - KQ * (b - 1) < KQ + 2) ? XB * (b - 1) + P - KQ * (b - 1) : c1;
+    }
+};
+
+struct RwArgs {
+    const float* dy;   // [B][OC][OH][OW]
+    const float* x;    // [B][IC][IH][IW]
+    float* out;        // [splits][OC][Kc] partials (or dW when one slice)
+    int64_t OC, IC, Kc;
+    int IH, IW, OH, OW, PH, PW, nseg;
+    int rows_total, rows_chunk;    // k-tiles (row segments) in all / per slice
+    int vec_dy, vec_x;             // 16-byte loads allowed
+};
+
+template <int BKP>
+__global__ __launch_bounds__(RW_NT)
+void conv_wgrad_rows_kernel(RwArgs p) {
+    using SH_ = RwShape<BKP>;
+    constexpr int KQ = SH_::KQ, A_STRIDE = SH_::A_STRIDE, X_RS = SH_::X_RS;
+    constexpr int STAGE = SH_::STAGE, NA = SH_::NA, NX = SH_::NX;
+    __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int wm0 = (wave / 3) * 16, wn0 = (wave % 3) * 48;
+
+    const int tiles_n = (int)ceil_div(p.IC, RW_ICT);
+    const int64_t bm = (int64_t)(blockIdx.x / tiles_n) * RW_BM;
+    const int64_t bic = (int64_t)(blockIdx.x % tiles_n) * RW_ICT;
+    const int r_begin = blockIdx.y * p.rows_chunk;
+    const int r_end = min(p.rows_total, r_begin + p.rows_chunk);
+    const int nk = r_end - r_begin;
+
+    // the row segment the next load() reads (running counters in k order)
+    int ld_seg = r_begin % p.nseg;
+    int ld_oh = (r_begin / p.nseg) % p.OH;
+    int ld_b = r_begin / (p.nseg * p.OH);
+
+    // This thread's staging slots are the same for every k-tile: element
+    // offsets from a wave-uniform per-k-tile base, validity of the row, and
+    // the LDS destination.  dY slot u: row (output channel) idx / KQ, 4-pixel
+    // column q = idx % KQ; x slot u: row (channel, kh) idx / KQ, column q.
+    int a_src[NA], a_dst[NA], a_q4[NA];
+    bool a_ok[NA];
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+        const int idx = tid + u * RW_NT;
+        const int row = idx / KQ, q = idx - (idx / KQ) * KQ;
+        a_ok[u] = idx < RW_BM * KQ && bm + row < p.OC;
+        a_src[u] = a_ok[u] ? row * p.OH * p.OW + 4 * q : 0;   // within one image's dY block
+        a_dst[u] = row * A_STRIDE + 4 * q;
+        a_q4[u] = 4 * q;
+    }
+    int x_src[NX], x_row[NX], x_c1[NX][4], x_c2[NX][4], x_q4[NX], x_kh[NX];
+    bool x_ok[NX];
+#pragma unroll
+    for (int u = 0; u < NX; ++u) {
+        const int idx = tid + u * RW_NT;
+        const int row = idx / KQ, q = idx - (idx / KQ) * KQ;   // row = icl * 3 + kh
+        const int icl = row / 3, kh = row - (row / 3) * 3;
+        x_ok[u] = idx < SH_::X_ROWS * KQ && bic + icl < p.IC;
+        x_src[u] = x_ok[u] ? icl * p.IH * p.IW + kh * p.IW + 4 * q : 0;
+        x_row[u] = row * X_RS;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) SH_::cols_of(p.PW + 4 * q + j, x_c1[u][j], x_c2[u][j]);
+        x_q4[u] = 4 * q;
+        x_kh[u] = kh;
+    }
+    // halo column hp of row tid/2 (threads 0 .. 2*X_ROWS-1): LDS position hp
+    // (left of the segment) when hp < PW, else BKP + hp (right of it); input
+    // column ow0 - PW + pos
+    const bool h_thread = tid < 2 * SH_::X_ROWS;
+    int h_src = 0, h_row = 0, h_c1 = 0, h_c2 = 0, h_kh = 0, h_col = 0;
+    bool h_ok = false;
+    if (h_thread) {
+        const int row = tid >> 1, hp = tid & 1;
+        const int icl = row / 3, kh = row - (row / 3) * 3;
+        const int pos = hp < p.PW ? hp : BKP + hp;
+        h_ok = bic + icl < p.IC;
+        h_col = pos - p.PW;
+        h_src = h_ok ? icl * p.IH * p.IW + kh * p.IW + h_col : 0;
+        h_row = row * X_RS;
+        SH_::cols_of(pos, h_c1, h_c2);
+        h_kh = kh;
+    }
+    const float* dy_blk = p.dy + bm * p.OH * p.OW;            // this tile's first channel
+    const float* x_blk = p.x + bic * p.IH * p.IW;
+
+    // registers staging one k-tile
+    struct Stage {
+        floatx4 va[NA], vx[NX];
+        float vh;
+    };
+    auto load = [&](Stage& st) {
+        const int ow0 = ld_seg * BKP;
+        // wave-uniform bases: dY row (b, oc = bm, oh) at ow0; x row (b, ic = bic,
+        // ih = oh - PH) at ow0
+        const float* yk = dy_blk + (int64_t)ld_b * p.OC * p.OH * p.OW + (int64_t)ld_oh * p.OW + ow0;
+        const float* xk = x_blk + (int64_t)ld_b * p.IC * p.IH * p.IW +
+                          (int64_t)(ld_oh - p.PH) * p.IW + ow0;
+        if (p.vec_dy && p.vec_x && ow0 + BKP <= p.OW && ow0 + BKP <= p.IW) {
+            // whole segment inside both rows: 16-byte loads from addresses that
+            // are always valid (a skipped row reads the tile's first dY row or
+            // the input's first element), zeroed by a select -- no branches
+#pragma unroll
+            for (int u = 0; u < NA; ++u) {
+                const floatx4 v = *reinterpret_cast<const floatx4*>(yk + a_src[u]);
+                st.va[u] = a_ok[u] ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int u = 0; u < NX; ++u) {
+                const bool rok = x_ok[u] && (unsigned)(ld_oh - p.PH + x_kh[u]) < (unsigned)p.IH;
+                const float* src = rok ? xk + x_src[u] : p.x;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(src);
+                st.vx[u] = rok ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < NA; ++u) {
+                const float* src = yk + a_src[u];
+                const int ow = ow0 + a_q4[u];
+                if (a_ok[u] && p.vec_dy && ow + 3 < p.OW) {
+                    st.va[u] = *reinterpret_cast<const floatx4*>(src);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) st.va[u][j] = a_ok[u] && ow + j < p.OW ? src[j] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < NX; ++u) {
+                const float* src = xk + x_src[u];
+                const int iw = ow0 + x_q4[u];
+                const bool rok = x_ok[u] && (unsigned)(ld_oh - p.PH + x_kh[u]) < (unsigned)p.IH;
+                if (rok && p.vec_x && iw + 3 < p.IW) {
+                    st.vx[u] = *reinterpret_cast<const floatx4*>(src);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) st.vx[u][j] = rok && iw + j < p.IW ? src[j] : 0.0f;
+                }
+            }
+        }
+        if (h_thread) {
+            const int iw = ow0 + h_col;
+            const bool ok = h_ok && (unsigned)(ld_oh - p.PH + h_kh) < (unsigned)p.IH &&
+                            (unsigned)iw < (unsigned)p.IW;
+            st.vh = ok ? xk[h_src] : 0.0f;
+        }
+        if (++ld_seg == p.nseg) {
+            ld_seg = 0;
+            if (++ld_oh == p.OH) {
+                ld_oh = 0;
+                ++ld_b;
+            }
+        }
+    };
+    auto store = [&](const Stage& st, int buf) {
+        float* sA = lds + buf * STAGE;
+        float* sX = sA + RW_BM * A_STRIDE;
+#pragma unroll
+        for (int u = 0; u < NA; ++u)
+            if (tid + u * RW_NT < RW_BM * KQ)
+                *reinterpret_cast<floatx4*>(sA + a_dst[u]) = st.va[u];
+#pragma unroll
+        for (int u = 0; u < NX; ++u)
+            if (tid + u * RW_NT < SH_::X_ROWS * KQ) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    sX[x_row[u] + x_c1[u][j]] = st.vx[u][j];
+                    sX[x_row[u] + x_c2[u][j]] = st.vx[u][j];
+                }
+            }
+        if (h_thread) {
+            sX[h_row + h_c1] = st.vh;
+            sX[h_row + h_c2] = st.vh;
+        }
+    };
+
+    // this lane's B rows: filter row n -> (channel, kh, kw) -> LDS row and shift
+    int b_off[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int n = wn0 + j * 16 + l16;          // 0 .. 143
+        const int icl = n / 9, tap = n - (n / 9) * 9;
+        const int kh = tap / 3, kw = tap - (tap / 3) * 3;
+        b_off[j] = RW_BM * A_STRIDE + (icl * 3 + kh) * X_RS + SH_::XB * lq + kw;
+    }
+    const int a_off = (wm0 + l16) * A_STRIDE + KQ * lq;
+
+    floatx4 acc[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int buf) {
+        const float* s = lds + buf * STAGE;
+#pragma unroll
+        for (int t0 = 0; t0 < KQ; t0 += 2) {
+            const float2 a = *reinterpret_cast<const float2*>(s + a_off + t0);
+            float b[3][2];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                b[j][0] = s[b_off[j] + t0];
+                b[j][1] = s[b_off[j] + t0 + 1];
+            }
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b[j][0], acc[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b[j][1], acc[j], 0, 0, 0);
+        }
+    };
+
+    // Two register staging sets: tile k+2 is loaded while tile k is
+    // multiplied and tile k+1 (loaded an iteration earlier) is written to LDS.
+    if (nk > 0) {
+        Stage s0, s1;
+        s0.vh = s1.vh = 0.0f;
+        load(s0);
+        if (nk > 1) load(s1);
+        store(s0, 0);
+        __syncthreads();
+        int k = 0;
+        for (; k + 1 < nk; k += 2) {        // LDS stage 0: tile k; s1: tile k+1
+            if (k + 2 < nk) load(s0);       // tile k+2
+            compute(0);
+            store(s1, 1);
+            __syncthreads();
+            if (k + 3 < nk) load(s1);       // tile k+3
+            compute(1);
+            if (k + 2 < nk) store(s0, 0);
+            __syncthreads();
+        }
+        if (k < nk) compute(0);             // odd count: the last tile, in stage 0
+    }
+
+    // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
+    // column l % 16
+    float* out = p.out + (int64_t)blockIdx.y * p.OC * p.Kc;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int64_t nn = bic * 9 + wn0 + j * 16 + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t m = bm + wm0 + 4 * lq + r;
+            if (m < p.OC && nn < p.Kc) out[m * p.Kc + nn] = acc[j][r];
+        }
+    }
+}
+
+// Pixels per k-tile: the output width rounded up to 32 / 56 / 64, or 64-pixel
+// segments for wider rows.
+int rw_bkp(int64_t OW) { return OW <= 32 ? 32 : OW <= 56 ? 56 : 64; }
+
+bool rows_applies(const WgGeom& g) {
+    // per-thread element offsets span at most one tile's 64 dY planes or 16
+    // input planes: 32-bit
+    const int64_t lim = (int64_t)1 << 31;
+    return g.KH == 3 && g.KW == 3 && g.SH == 1 && g.SW == 1 && g.PW >= 0 && g.PW <= 2 &&
+           g.PH >= 0 && RW_BM * g.OH * g.OW < lim && RW_ICT * g.IH * g.IW < lim;
+}
+
+struct RwPlan {
+    int bkp, nseg, rows_total, tiles, splits, chunk;
+};
+
+RwPlan rw_plan(const WgGeom& g) {
+    RwPlan r;
+    r.bkp = rw_bkp(g.OW);
+    r.nseg = (int)ceil_div(g.OW, r.bkp);
+    r.rows_total = (int)(g.B * g.OH * r.nseg);
+    r.tiles = (int)(ceil_div(g.OC, RW_BM) * ceil_div(g.IC, RW_ICT));
+    // about CDX_WGRAD_ROWS_WGS workgroups, at least 4 row segments per slice
+    int64_t s = CDX_WGRAD_ROWS_WGS / r.tiles;
+    if (s > r.rows_total / 4) s = r.rows_total / 4;
+    if (s < 1) s = 1;
+    r.chunk = (int)ceil_div(r.rows_total, s);
+    r.splits = (int)ceil_div(r.rows_total, r.chunk);
+    return r;
+}
+
 }  // namespace
 
 bool conv_wgrad_implicit_ok(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
@@ -325,7 +660,7 @@ size_t conv_wgrad_implicit_floats(int64_t batch, int64_t IC, int64_t OC, int64_t
                                   int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
                                   int64_t PW) {
     const WgGeom g = make_geom(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
-    const int s = splits_for(g);
+    const int s = rows_applies(g) ? rw_plan(g).splits : splits_for(g);
     return s > 1 ? (size_t)s * (size_t)OC * (size_t)g.Kc() : 0;
 }
 
@@ -333,6 +668,30 @@ int launch_conv_wgrad_f32(const float* dy, const float* x, float* dw, float* ws,
                           int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
                           int64_t SH, int64_t SW, int64_t PH, int64_t PW, hipStream_t stream) {
     const WgGeom g = make_geom(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    if (rows_applies(g)) {
+        const RwPlan r = rw_plan(g);
+        RwArgs p;
+        p.dy = dy; p.x = x;
+        p.out = r.splits > 1 ? ws : dw;
+        p.OC = OC; p.IC = IC; p.Kc = g.Kc();
+        p.IH = (int)IH; p.IW = (int)IW; p.OH = (int)g.OH; p.OW = (int)g.OW;
+        p.PH = (int)PH; p.PW = (int)PW; p.nseg = r.nseg;
+        p.rows_total = r.rows_total; p.rows_chunk = r.chunk;
+        p.vec_dy = g.OW % 4 == 0 && (uintptr_t)dy % 16 == 0;
+        p.vec_x = IW % 4 == 0 && (uintptr_t)x % 16 == 0;
+        const dim3 grid((unsigned)r.tiles, (unsigned)r.splits);
+        if (r.bkp == 32)
+            hipLaunchKernelGGL(conv_wgrad_rows_kernel<32>, grid, dim3(RW_NT), 0, stream, p);
+        else if (r.bkp == 56)
+            hipLaunchKernelGGL(conv_wgrad_rows_kernel<56>, grid, dim3(RW_NT), 0, stream, p);
+        else
+            hipLaunchKernelGGL(conv_wgrad_rows_kernel<64>, grid, dim3(RW_NT), 0, stream, p);
+        int st = hip_error(hipGetLastError(), "conv_wgrad_rows_kernel launch");
+        if (st || r.splits == 1) return st;
+        GemmArgs red{CDX_OP_N, CDX_OP_N, OC, g.Kc(), 0, nullptr, 1, nullptr, 1, dw, g.Kc(), 0, 0,
+                     nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+        return launch_splitk_reduce(ws, r.splits, red, stream);
+    }
     const int splits = splits_for(g);
     WgArgs p;
     p.dy = dy; p.x = x;

@@ -189,6 +189,11 @@ BWD_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
     (1, 8, 15, 17, 6, 1, 1, 1, 1, 0, 0),
     (2, 3, 6, 7, 4, 3, 3, 1, 1, 3, 0),
     (2, 33, 10, 30, 65, 3, 3, 1, 1, 0, 2),
+    # 3x3 stride 1 row-window weight gradient: rows wider than 64 pixels (two
+    # segments), 61-pixel rows, pad 2 with partial channel tiles
+    (1, 4, 5, 70, 8, 3, 3, 1, 1, 1, 1),
+    (2, 16, 9, 61, 16, 3, 3, 1, 1, 1, 1),
+    (1, 20, 6, 33, 70, 3, 3, 1, 1, 2, 2),
 ]
 
 
