@@ -366,40 +366,51 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
     return launch_mode<CF, CDX_OP_N, CDX_OP_N, true>(g, 1, g.K, stream);
 }
 
-// Tile configurations (chosen by measurement on MI355X; 4096^3 NN).  All use
-// the two-set register pipeline, which measured 4-12 % faster everywhere
-// (4096^3: 138 against 133 TFLOP/s; 2048^3: 130 against 114).
-//  * Large: 128x128x16, 8 waves of 32x64 -> 2 waves per SIMD, 64 fp32
+// Tile configurations (chosen by measurement on MI355X).  All use the two-set
+// register pipeline, which measured 4-12 % faster everywhere (4096^3: 138
+// against 133 TFLOP/s; 2048^3: 130 against 114).
+//  * Large: 128x128x16, 8 waves of 32x64 -> 2 waves per SIMD, 32 fp32
 //    accumulators per lane.
-//  * Medium: 64x64x16, 8 waves of 16x32, for problems with too few large
-//    tiles to fill 256 CUs (~67 TFLOP/s at 1024^3 vs 27 with Large).
+//  * Medium: 64x64x16, 4 waves of 32x32, for problems whose 128x128 tiles
+//    would spread unevenly over the 256 CUs, for the split-K slices (few
+//    tiles, long K: the weight gradients) and for small problems.  Against
+//    8 waves of 16x32 on the same tile: 2048^3 141 against 157 us, 4096 x
+//    1024 x 1024 73 against 81, 8192 x 256 x 784 (NT) 32 against 36, 8192 x
+//    784 x 256 41 against 45; 1024^3 NT the one loss (26 against 24).
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
-//    64x64x16, 4 waves of 32x32 (~85 TFLOP/s on 64 x 100352 x 576, against
-//    49 with 64x256 tiles).
+//    64x64x16, 4 waves of 32x32, XCD groups of one tile row (~85 TFLOP/s on
+//    64 x 100352 x 576, against 49 with 64x256 tiles).
 //  * NarrowN: N <= 16 (the MLP's 10-class layer): 64x16 tiles instead of
 //    mostly-empty 64x64 ones (8192 x 10 x 256: 9.8 us against 13.4).  A
 //    16-row tile for M <= 16 measured no faster than Medium.
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
-using CfgMedium = Cfg<64, 64, 16, 16, 32, 8, 2>;
+using CfgMedium = Cfg<64, 64, 16, 32, 32, 8, 2>;
 using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1, 2>;
 using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8, 2>;
-//  * SplitK: problems the split-K policy slices (few tiles, long K; the
-//    weight gradients): 64x64x16, 4 waves of 32x32, whose fragment reads
-//    per MFMA suit the m/n-contiguous operands of those TN products (256 x
-//    784 x 8192: 53 us against 61 with Medium).
-using CfgSplitK = Cfg<64, 64, 16, 32, 32, 8, 2>;
 
 // Configuration choice, shared by the launcher and the workspace query.
-enum class F32Cfg { NarrowN, SplitK, SkinnyM, Large, Medium };
+enum class F32Cfg { NarrowN, SkinnyM, Large, Medium };
+
+// Large tiles are ~8 % faster per tile, but a CU's time is set by its largest
+// share of tiles: Large is taken when its busiest-CU share (rounded up to
+// whole tiles per CU over the 256 CUs) is within 5 % of Medium's.  (2048^3,
+// 256 tiles: 130 against 141 us; 3072^3, 576 tiles: 561 against 459.)
+bool large_balanced(int64_t M, int64_t N) {
+    const int64_t tl = ceil_div(M, 128) * ceil_div(N, 128);
+    const int64_t tm = ceil_div(M, 64) * ceil_div(N, 64);
+    const int64_t cus = 256;
+    if (tl < cus) return false;
+    // ceil(tl/cus)/(tl/cus) <= 1.05 * ceil(tm/cus)/(tm/cus)
+    return ceil_div(tl, cus) * tm * 100 <= 105 * ceil_div(tm, cus) * tl;
+}
 
 F32Cfg choose_f32(const GemmArgs& g, bool& blocked) {
     const bool split = g.batch == 1 && splitk_applies(ceil_div(g.M, 64) * ceil_div(g.N, 64), g.K);
     blocked = g.blocked_sum && !split && g.opA == CDX_OP_N && g.opB == CDX_OP_N;
     if (g.N <= 16) return F32Cfg::NarrowN;
-    if (split && !blocked) return F32Cfg::SplitK;
+    if (split && !blocked) return F32Cfg::Medium;
     if (g.M <= 64 && g.N >= 4096) return F32Cfg::SkinnyM;
-    // Large tiles once there are at least two per CU (256 CUs).
-    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 512) return F32Cfg::Large;
+    if (large_balanced(g.M, g.N)) return F32Cfg::Large;
     return F32Cfg::Medium;
 }
 
@@ -416,7 +427,6 @@ size_t gemm_f32_workspace(const GemmArgs& g) {
     if (blocked) return 0;
     switch (c) {
         case F32Cfg::NarrowN: return ws_of<CfgNarrowN>(g);
-        case F32Cfg::SplitK: return ws_of<CfgSplitK>(g);
         case F32Cfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case F32Cfg::Large: return ws_of<CfgLarge>(g);
         default: return ws_of<CfgMedium>(g);
@@ -436,7 +446,6 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
     }
     switch (c) {
         case F32Cfg::NarrowN: return launch_ops<CfgNarrowN>(g, stream);
-        case F32Cfg::SplitK: return launch_ops<CfgSplitK>(g, stream);
         case F32Cfg::SkinnyM: return launch_ops<CfgSkinnyM>(g, stream);
         case F32Cfg::Large: return launch_ops<CfgLarge>(g, stream);
         default: return launch_ops<CfgMedium>(g, stream);
