@@ -35,8 +35,8 @@ namespace cdx {
 namespace {
 
 constexpr int kLoadAlignedVec = 0;  // every tile in bounds, 16-byte loads
-constexpr int kLoadCheckedVec = 1;  // bounds-checked, 16-byte loads where whole
-constexpr int kLoadScalar = 2;      // bounds-checked scalar loads (unaligned ld)
+constexpr int kLoadChecked = 1;     // bounds-checked; 16-byte loads where whole and the
+                                    // operand allows them (per-operand flag), else scalar
 
 struct KParams {
     const float* A; const float* B; float* C; const float* bias;
@@ -45,6 +45,7 @@ struct KParams {
     int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
     int64_t sa, sb, sc; // batch strides (elements) for blockIdx.z
     int64_t batch;      // gridDim.z
+    int vec_a, vec_b;   // kLoadChecked: operand base, ld and batch stride allow 16-byte loads
 };
 
 // Loads a ROWS x COLS tile (COLS contiguous in memory) starting at (r0, c0)
@@ -60,7 +61,7 @@ struct TileLoader {
 
     __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld,
                                          int64_t r0, int64_t c0, int64_t rmax,
-                                         int64_t cmax, int tid) {
+                                         int64_t cmax, bool vec, int tid) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             int idx = tid + i * NT;
@@ -70,7 +71,7 @@ struct TileLoader {
             const float* p = X + gr * ld + gc;
             if (MODE == kLoadAlignedVec) {
                 v[i] = *reinterpret_cast<const float4*>(p);
-            } else if (MODE == kLoadCheckedVec && gr < rmax && gc + 3 < cmax) {
+            } else if (vec && gr < rmax && gc + 3 < cmax) {
                 v[i] = *reinterpret_cast<const float4*>(p);
             } else {
                 bool rok = gr < rmax;
@@ -174,10 +175,10 @@ void gemm_f32_mfma_kernel(KParams p) {
     LB lb;
 
     auto load_into = [&](LA& a, LB& b, int64_t k0) {
-        if (OPA == CDX_OP_N) a.load(p.A, p.lda, bm, k0, p.M, p.K, tid);
-        else                 a.load(p.A, p.lda, k0, bm, p.K, p.M, tid);
-        if (OPB == CDX_OP_N) b.load(p.B, p.ldb, k0, bn, p.K, p.N, tid);
-        else                 b.load(p.B, p.ldb, bn, k0, p.N, p.K, tid);
+        if (OPA == CDX_OP_N) a.load(p.A, p.lda, bm, k0, p.M, p.K, p.vec_a, tid);
+        else                 a.load(p.A, p.lda, k0, bm, p.K, p.M, p.vec_a, tid);
+        if (OPB == CDX_OP_N) b.load(p.B, p.ldb, k0, bn, p.K, p.N, p.vec_b, tid);
+        else                 b.load(p.B, p.ldb, bn, k0, p.N, p.K, p.vec_b, tid);
     };
     auto store_from = [&](const LA& a, const LB& b, int buf) {
         float* sA = lds + buf * (A_ELEMS + B_ELEMS);
@@ -327,24 +328,22 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
     KParams kp{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
                g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
-               g.stride_a, g.stride_b, g.stride_c, g.batch};
-    // 16-byte loads need 16-byte aligned bases and leading dimensions.
-    bool vec = ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) &&
-               g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-               g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
-    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
+               g.stride_a, g.stride_b, g.stride_c, g.batch, 0, 0};
+    // 16-byte loads need 16-byte aligned bases, leading dimensions and batch
+    // strides, decided per operand (a 10-column operand no longer sends the
+    // other one down the scalar path: C4's dW2 = dY2^T H, 10 x 256 x 8192,
+    // 14 us with both operands scalar)
+    kp.vec_a = ((uintptr_t)g.A % 16 == 0) && g.lda % 4 == 0 && g.stride_a % 4 == 0;
+    kp.vec_b = ((uintptr_t)g.B % 16 == 0) && g.ldb % 4 == 0 && g.stride_b % 4 == 0;
+    bool aligned = kp.vec_a && kp.vec_b && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned) {
         return split ? launch_cfg<CF, OPA, OPB, kLoadAlignedVec, true, BLK>(kp, splits, stream)
                      : launch_cfg<CF, OPA, OPB, kLoadAlignedVec, false, BLK>(kp, splits, stream);
     }
-    if (vec) {
-        return split ? launch_cfg<CF, OPA, OPB, kLoadCheckedVec, true, BLK>(kp, splits, stream)
-                     : launch_cfg<CF, OPA, OPB, kLoadCheckedVec, false, BLK>(kp, splits, stream);
-    }
-    return split ? launch_cfg<CF, OPA, OPB, kLoadScalar, true, BLK>(kp, splits, stream)
-                 : launch_cfg<CF, OPA, OPB, kLoadScalar, false, BLK>(kp, splits, stream);
+    return split ? launch_cfg<CF, OPA, OPB, kLoadChecked, true, BLK>(kp, splits, stream)
+                 : launch_cfg<CF, OPA, OPB, kLoadChecked, false, BLK>(kp, splits, stream);
 }
 
 template <class CF>
