@@ -157,6 +157,26 @@ def test_fp32_c2_4096_sampled_rows_and_checksum():
     assert _checksum_identity(A, B, C) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (3072, 3072, 512), (4096, 1024, 1024)])
+@pytest.mark.parametrize("tA,tB", [(False, False), (True, True)])
+def test_fp32_mid_size_tile_choice(M, N, K, tA, tB):
+    """Mid-size problems on both sides of the 128x128 / 64x64 choice (128-tiles
+    that spread evenly over the CUs -- 256 of them at 2048^2 and 4096 x 1024 --
+    against 576 at 3072^2): sampled rows against the seq-FMA restatement and
+    the column-checksum identity over the whole product."""
+    rng = np.random.default_rng(M + 3 * N + 7 * K + 2 * tA + tB)
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (N, K) if tB else (K, N))
+    say("fp32 mid-size", M, N, K, tA, tB)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB))
+    for r0 in (0, M // 2 + 5, M - 64):
+        rows = (r0, r0 + 64)
+        C64, e_ref = _ref_errors(A, B, tA, tB, rows=rows)
+        e = oracle.rel_fro(C[r0:r0 + 64], C64)
+        assert e <= 2 * e_ref, (rows, e, e_ref)
+    assert _checksum_identity(A.T if tA else A, B.T if tB else B, C) < 1e-5
+
+
 @pytest.mark.parametrize("n", [2048, 4096])
 @pytest.mark.parametrize("terms", [3, 4])
 def test_tf32mode_c3(n, terms):
