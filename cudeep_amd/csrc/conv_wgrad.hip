@@ -617,10 +617,11 @@ int rw_bkp(int64_t OW) { return OW <= 32 ? 32 : OW <= 56 ? 56 : 64; }
 
 bool rows_applies(const WgGeom& g) {
     // per-thread element offsets span at most one tile's 64 dY planes or 16
-    // input planes: 32-bit
+    // input planes, and the row segments are counted in int: 32-bit
     const int64_t lim = (int64_t)1 << 31;
     return g.KH == 3 && g.KW == 3 && g.SH == 1 && g.SW == 1 && g.PW >= 0 && g.PW <= 2 &&
-           g.PH >= 0 && RW_BM * g.OH * g.OW < lim && RW_ICT * g.IH * g.IW < lim;
+           g.PH >= 0 && RW_BM * g.OH * g.OW < lim && RW_ICT * g.IH * g.IW < lim &&
+           g.B * g.OH * ceil_div(g.OW, rw_bkp(g.OW)) < lim;
 }
 
 struct RwPlan {
