@@ -438,3 +438,59 @@ def test_split_k_parity(M, N, K, tA, mode):
         Zt = oracle.gemm_tf32emu(opA, B, "rne") + bias[None, :]
         e_ref = oracle.rel_fro(oracle.relu(Zt.astype(np.float32)), want)
         assert oracle.rel_fro(C, want) <= e_ref
+
+
+# ---------------------------------------------------------------------------
+# special values
+# ---------------------------------------------------------------------------
+
+def _special_operands(M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    A = normal(rng, (M, K))
+    B = normal(rng, (K, N))
+    A[3, 5] = np.inf
+    A[7, 1] = -np.inf
+    A[11, 2] = np.nan
+    return A, B
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (300, 200, 784), (4096, 4096, 64)])
+def test_fp32_special_values_follow_ieee(M, N, K):
+    """FP32 mode: +-Inf and NaN operands propagate as in IEEE fp64 arithmetic on the
+    same operands (each output is one sum of products): the same Inf / NaN pattern and
+    signs, and the finite outputs within the usual FP32 gate."""
+    A, B = _special_operands(M, N, K, 808 + M)
+    say("fp32 special values", M, N, K)
+    C = host(ops().gemm(dev(A), dev(B)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        C64 = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(np.isnan(C), np.isnan(C64))
+    assert np.array_equal(np.isinf(C), np.isinf(C64))
+    inf = np.isinf(C64)
+    assert np.array_equal(np.sign(C[inf]), np.sign(C64[inf]))
+    fin = np.isfinite(C64).all(axis=1)
+    Af = A[fin]
+    Cs = oracle.sgemm_seqfma(Af, B)
+    e_ref = oracle.rel_fro(Cs, C64[fin])
+    assert oracle.rel_fro(C[fin], C64[fin]) <= 2 * e_ref + (F32_FLOOR if K < 64 else 0.0)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (4096, 4096, 64)])
+def test_tf32mode_special_values_stay_in_their_rows(M, N, K):
+    """TF32 modes: an infinite operand element makes the outputs it touches
+    non-finite (NaN where the reference's TF32 path gives +-Inf -- the split's
+    cross terms; documented), NaN stays NaN, and every output row without a
+    special operand is finite and inside the TF32-mode gate."""
+    import cudeep_amd as cd
+    A, B = _special_operands(M, N, K, 909 + M)
+    bad = ~np.isfinite(A).all(axis=1)
+    say("tf32 special values", M, N, K)
+    for prec in (cd.PREC_TF32MODE, cd.PREC_TF32MODE4):
+        C = host(ops().gemm(dev(A), dev(B), precision=prec))
+        assert not np.isfinite(C[bad]).any()
+        assert np.isfinite(C[~bad]).all()
+        Ag = A[~bad]
+        C64 = oracle.dgemm(Ag, B)
+        e = oracle.rel_fro(C[~bad], C64)
+        e_ref = min(oracle.rel_fro(oracle.gemm_tf32emu(Ag, B, m), C64) for m in ("rz", "rne"))
+        assert e <= e_ref, (prec, e, e_ref)
