@@ -367,20 +367,30 @@ PYBIND11_MODULE(_cudeep_core, m) {
           [](const Tensor& input, const Tensor& weight, py::object bias_obj,
              std::vector<int> stride, std::vector<int> padding) {
               Tensor in = ensure_contiguous(input), w = ensure_contiguous(weight);
-              require_f32(in, "conv2d_forward");
+              require_f32_or_f64(in, "conv2d_forward");
+              if (w.dtype() != in.dtype())
+                  throw std::runtime_error("conv2d_forward: input and weight dtypes differ");
               ConvGeom g = conv_geom(in.shape(), w.shape(), stride, padding);
               Tensor out({g.B, g.OC, g.OH, g.OW}, in.dtype());
               Tensor b;
-              const float* bptr = nullptr;
+              const void* bptr = nullptr;
               if (!bias_obj.is_none()) {
                   b = ensure_contiguous(bias_obj.cast<Tensor>());
                   if (b.numel() != g.OC) throw std::runtime_error("conv2d_forward: bias size");
-                  bptr = static_cast<const float*>(b.data());
+                  if (b.dtype() != in.dtype())
+                      throw std::runtime_error("conv2d_forward: bias dtype differs");
+                  bptr = b.data();
               }
-              kernels::launch_conv2d_forward_kernel<float>(
-                  static_cast<const float*>(in.data()), static_cast<const float*>(w.data()), bptr,
-                  static_cast<float*>(out.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW, g.SH,
-                  g.SW, g.PH, g.PW, in.stream());
+              if (in.dtype() == DType::Float64)
+                  kernels::launch_conv2d_forward_kernel<double>(
+                      static_cast<const double*>(in.data()), static_cast<const double*>(w.data()),
+                      static_cast<const double*>(bptr), static_cast<double*>(out.data()), g.B,
+                      g.IC, g.OC, g.IH, g.IW, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, in.stream());
+              else
+                  kernels::launch_conv2d_forward_kernel<float>(
+                      static_cast<const float*>(in.data()), static_cast<const float*>(w.data()),
+                      static_cast<const float*>(bptr), static_cast<float*>(out.data()), g.B,
+                      g.IC, g.OC, g.IH, g.IW, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, in.stream());
               return out;
           },
           py::arg("input"), py::arg("weight"), py::arg("bias") = py::none(),
@@ -390,15 +400,23 @@ PYBIND11_MODULE(_cudeep_core, m) {
           [](const Tensor& grad_output, const Tensor& weight, std::vector<int64_t> input_shape,
              std::vector<int> stride, std::vector<int> padding) {
               Tensor go = ensure_contiguous(grad_output), w = ensure_contiguous(weight);
-              require_f32(go, "conv2d_backward_data");
+              require_f32_or_f64(go, "conv2d_backward_data");
+              if (w.dtype() != go.dtype())
+                  throw std::runtime_error("conv2d_backward_data: grad_output and weight dtypes differ");
               ConvGeom g = conv_geom(input_shape, w.shape(), stride, padding);
               if (go.shape() != std::vector<int64_t>{g.B, g.OC, g.OH, g.OW})
                   throw std::runtime_error("conv2d_backward_data: grad_output shape mismatch");
               Tensor gi(input_shape, go.dtype());
-              kernels::launch_conv2d_backward_data_kernel<float>(
-                  static_cast<const float*>(go.data()), static_cast<const float*>(w.data()),
-                  static_cast<float*>(gi.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW, g.SH,
-                  g.SW, g.PH, g.PW, go.stream());
+              if (go.dtype() == DType::Float64)
+                  kernels::launch_conv2d_backward_data_kernel<double>(
+                      static_cast<const double*>(go.data()), static_cast<const double*>(w.data()),
+                      static_cast<double*>(gi.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW,
+                      g.SH, g.SW, g.PH, g.PW, go.stream());
+              else
+                  kernels::launch_conv2d_backward_data_kernel<float>(
+                      static_cast<const float*>(go.data()), static_cast<const float*>(w.data()),
+                      static_cast<float*>(gi.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW,
+                      g.SH, g.SW, g.PH, g.PW, go.stream());
               return gi;
           },
           py::arg("grad_output"), py::arg("weight"), py::arg("input_shape"), py::arg("stride"),
@@ -408,15 +426,23 @@ PYBIND11_MODULE(_cudeep_core, m) {
           [](const Tensor& grad_output, const Tensor& input, std::vector<int64_t> weight_shape,
              std::vector<int> stride, std::vector<int> padding) {
               Tensor go = ensure_contiguous(grad_output), in = ensure_contiguous(input);
-              require_f32(go, "conv2d_backward_weight");
+              require_f32_or_f64(go, "conv2d_backward_weight");
+              if (in.dtype() != go.dtype())
+                  throw std::runtime_error("conv2d_backward_weight: grad_output and input dtypes differ");
               ConvGeom g = conv_geom(in.shape(), weight_shape, stride, padding);
               if (go.shape() != std::vector<int64_t>{g.B, g.OC, g.OH, g.OW})
                   throw std::runtime_error("conv2d_backward_weight: grad_output shape mismatch");
               Tensor gw(weight_shape, go.dtype());
-              kernels::launch_conv2d_backward_weight_kernel<float>(
-                  static_cast<const float*>(go.data()), static_cast<const float*>(in.data()),
-                  static_cast<float*>(gw.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW, g.SH,
-                  g.SW, g.PH, g.PW, go.stream());
+              if (go.dtype() == DType::Float64)
+                  kernels::launch_conv2d_backward_weight_kernel<double>(
+                      static_cast<const double*>(go.data()), static_cast<const double*>(in.data()),
+                      static_cast<double*>(gw.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW,
+                      g.SH, g.SW, g.PH, g.PW, go.stream());
+              else
+                  kernels::launch_conv2d_backward_weight_kernel<float>(
+                      static_cast<const float*>(go.data()), static_cast<const float*>(in.data()),
+                      static_cast<float*>(gw.data()), g.B, g.IC, g.OC, g.IH, g.IW, g.KH, g.KW,
+                      g.SH, g.SW, g.PH, g.PW, go.stream());
               return gw;
           },
           py::arg("grad_output"), py::arg("input"), py::arg("weight_shape"), py::arg("stride"),
@@ -424,13 +450,18 @@ PYBIND11_MODULE(_cudeep_core, m) {
 
     m.def("conv2d_backward_bias", [](const Tensor& grad_output) {
         Tensor go = ensure_contiguous(grad_output);
-        require_f32(go, "conv2d_backward_bias");
+        require_f32_or_f64(go, "conv2d_backward_bias");
         if (go.ndim() != 4) throw std::runtime_error("conv2d_backward_bias: NCHW grad_output");
         const auto& s = go.shape();
         Tensor gb({s[1]}, go.dtype());
-        kernels::launch_conv2d_backward_bias_kernel(static_cast<const float*>(go.data()),
-                                                    static_cast<float*>(gb.data()), (int)s[0],
-                                                    (int)s[1], (int)(s[2] * s[3]), go.stream());
+        if (go.dtype() == DType::Float64)
+            kernels::launch_conv2d_backward_bias_kernel(static_cast<const double*>(go.data()),
+                                                        static_cast<double*>(gb.data()), (int)s[0],
+                                                        (int)s[1], (int)(s[2] * s[3]), go.stream());
+        else
+            kernels::launch_conv2d_backward_bias_kernel(static_cast<const float*>(go.data()),
+                                                        static_cast<float*>(gb.data()), (int)s[0],
+                                                        (int)s[1], (int)(s[2] * s[3]), go.stream());
         return gb;
     }, py::arg("grad_output"));
 

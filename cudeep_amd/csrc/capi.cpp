@@ -634,6 +634,76 @@ int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias, int
                                           stream);
 }
 
+int cdx_conv2d_forward_f64(const double* input, const double* weight, const double* bias,
+                           double* output, int64_t batch, int64_t in_channels,
+                           int64_t out_channels, int64_t in_h, int64_t in_w,
+                           int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                           int64_t stride_w, int64_t pad_h, int64_t pad_w, hipStream_t stream) {
+    const char* fn = "cdx_conv2d_forward_f64";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
+    const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
+    if (batch * out_channels * OH * OW == 0) return CDX_OK;
+    if (!output || !weight || (in_channels > 0 && !input))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    return cdx::launch_conv2d_forward_f64(input, weight, bias, output, batch, in_channels,
+                                          out_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                                          stride_w, pad_h, pad_w, stream);
+}
+
+int cdx_conv2d_backward_data_f64(const double* grad_output, const double* weight,
+                                 double* grad_input, int64_t batch, int64_t in_channels,
+                                 int64_t out_channels, int64_t in_h, int64_t in_w,
+                                 int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                 int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                 hipStream_t stream) {
+    const char* fn = "cdx_conv2d_backward_data_f64";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (batch * in_channels * in_h * in_w == 0) return CDX_OK;
+    if (!grad_input || (out_channels > 0 && (!grad_output || !weight)))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    return cdx::launch_conv2d_backward_data_f64(grad_output, weight, grad_input, batch,
+                                                in_channels, out_channels, in_h, in_w, kernel_h,
+                                                kernel_w, stride_h, stride_w, pad_h, pad_w,
+                                                stream);
+}
+
+int cdx_conv2d_backward_weight_f64(const double* grad_output, const double* input,
+                                   double* grad_weight, int64_t batch, int64_t in_channels,
+                                   int64_t out_channels, int64_t in_h, int64_t in_w,
+                                   int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                   int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                   hipStream_t stream) {
+    const char* fn = "cdx_conv2d_backward_weight_f64";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (out_channels * in_channels * kernel_h * kernel_w == 0) return CDX_OK;
+    const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
+    const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
+    if (!grad_weight || (batch * OH * OW > 0 && (!grad_output || !input)))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    return cdx::launch_conv2d_backward_weight_f64(grad_output, input, grad_weight, batch,
+                                                  in_channels, out_channels, in_h, in_w,
+                                                  kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                                                  pad_w, stream);
+}
+
+int cdx_conv2d_backward_bias_f64(const double* grad_output, double* grad_bias, int64_t batch,
+                                 int64_t out_channels, int64_t spatial, hipStream_t stream) {
+    if (bad_dim(batch) || bad_dim(out_channels) || bad_dim(spatial))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_backward_bias_f64: bad dims");
+    if (out_channels == 0) return CDX_OK;
+    if (!grad_bias || (batch * spatial > 0 && !grad_output))
+        return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_backward_bias_f64: NULL pointer");
+    return cdx::launch_conv_bias_grad_f64(grad_output, grad_bias, batch, out_channels, spatial,
+                                          stream);
+}
+
 size_t cdx_sum_reduce_rows_workspace_size(int64_t rows, int64_t cols) {
     if (bad_dim(rows) || bad_dim(cols)) return 0;
     // sized for fp64 partials so one query serves both dtypes

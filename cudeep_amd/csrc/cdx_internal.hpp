@@ -173,6 +173,22 @@ int launch_nchw_to_cm_f32(const float* src, float* dst, int64_t batch, int64_t C
 int launch_conv_bias_grad_f32(const float* dy, float* db, int64_t batch, int64_t C, int64_t S,
                               hipStream_t stream);
 
+// float64 conv (conv_f64.hip): direct fp64 sums, one chain per output.
+int launch_conv2d_forward_f64(const double* x, const double* w, const double* bias, double* out,
+                              int64_t B, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                              int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                              int64_t PW, hipStream_t stream);
+int launch_conv2d_backward_data_f64(const double* dy, const double* w, double* dx, int64_t B,
+                                    int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                                    int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                                    hipStream_t stream);
+int launch_conv2d_backward_weight_f64(const double* dy, const double* x, double* dw, int64_t B,
+                                      int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                                      int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                                      hipStream_t stream);
+int launch_conv_bias_grad_f64(const double* dy, double* db, int64_t B, int64_t C, int64_t S,
+                              hipStream_t stream);
+
 int launch_strided_copy(const void* src, void* dst, int ndim, const int64_t* shape,
                         const int64_t* strides, int dtype, hipStream_t stream);
 int launch_fill(void* dst, int64_t n, double v, int dtype, hipStream_t stream);

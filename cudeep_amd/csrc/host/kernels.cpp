@@ -1,8 +1,8 @@
 // cudeep::kernels launchers (the reference's C++ operator API,
 // include/cudeep/kernels/*.cuh) implemented over the C-ABI of
 // libcudeep_amd.so.  Each template is explicitly instantiated for float and
-// double, as the reference does; combinations outside this build (fp64
-// conv, non-ReLU/GELU activations) throw.
+// double, as the reference does; combinations outside this build (activations
+// other than ReLU / GELU / SiLU / Sigmoid) throw.
 #include <atomic>
 #include <string>
 
@@ -157,10 +157,12 @@ void launch_conv2d_forward_kernel<float>(const float* input, const float* weight
 }
 
 template <>
-void launch_conv2d_forward_kernel<double>(const double*, const double*, const double*, double*,
-                                          int, int, int, int, int, int, int, int, int, int, int,
-                                          hipStream_t) {
-    throw std::runtime_error("conv2d: float64 is not supported by this build");
+void launch_conv2d_forward_kernel<double>(const double* input, const double* weight,
+                                          const double* bias, double* output, int batch, int IC,
+                                          int OC, int IH, int IW, int KH, int KW, int SH, int SW,
+                                          int PH, int PW, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_forward_f64(input, weight, bias, output, batch, IC, OC, IH, IW,
+                                            KH, KW, SH, SW, PH, PW, stream));
 }
 
 template <>
@@ -195,10 +197,12 @@ void launch_conv2d_backward_data_kernel<float>(const float* grad_output, const f
 }
 
 template <>
-void launch_conv2d_backward_data_kernel<double>(const double*, const double*, double*, int, int,
-                                                int, int, int, int, int, int, int, int, int,
-                                                hipStream_t) {
-    throw std::runtime_error("conv2d backward: float64 is not supported by this build");
+void launch_conv2d_backward_data_kernel<double>(const double* grad_output, const double* weight,
+                                                double* grad_input, int batch, int IC, int OC,
+                                                int IH, int IW, int KH, int KW, int SH, int SW,
+                                                int PH, int PW, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_f64(grad_output, weight, grad_input, batch, IC, OC,
+                                                  IH, IW, KH, KW, SH, SW, PH, PW, stream));
 }
 
 template <>
@@ -212,15 +216,23 @@ void launch_conv2d_backward_weight_kernel<float>(const float* grad_output, const
 }
 
 template <>
-void launch_conv2d_backward_weight_kernel<double>(const double*, const double*, double*, int, int,
-                                                  int, int, int, int, int, int, int, int, int,
-                                                  hipStream_t) {
-    throw std::runtime_error("conv2d backward: float64 is not supported by this build");
+void launch_conv2d_backward_weight_kernel<double>(const double* grad_output, const double* input,
+                                                  double* grad_weight, int batch, int IC, int OC,
+                                                  int IH, int IW, int KH, int KW, int SH, int SW,
+                                                  int PH, int PW, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_backward_weight_f64(grad_output, input, grad_weight, batch, IC,
+                                                    OC, IH, IW, KH, KW, SH, SW, PH, PW, stream));
 }
 
 void launch_conv2d_backward_bias_kernel(const float* grad_output, float* grad_bias, int batch,
                                         int out_channels, int spatial, hipStream_t stream) {
     CUDEEP_CHECK_CDX(cdx_conv2d_backward_bias_f32(grad_output, grad_bias, batch, out_channels,
+                                                  spatial, stream));
+}
+
+void launch_conv2d_backward_bias_kernel(const double* grad_output, double* grad_bias, int batch,
+                                        int out_channels, int spatial, hipStream_t stream) {
+    CUDEEP_CHECK_CDX(cdx_conv2d_backward_bias_f64(grad_output, grad_bias, batch, out_channels,
                                                   spatial, stream));
 }
 

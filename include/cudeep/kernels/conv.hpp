@@ -1,7 +1,8 @@
 // Conv2d launchers of the C++ host API, same signatures as the reference's
 // include/cudeep/kernels/conv.cuh:8-36 (NCHW input, OIHW weight, bias may be
 // null), over the C-ABI.  Scratch is allocated stream-ordered, as the
-// reference does; float only (double throws: not part of this build).
+// reference does.  float and double, as the reference instantiates them
+// (src/kernels/conv_kernel.cu:793-798); double runs direct fp64 sums.
 #pragma once
 
 #include "../common.hpp"
@@ -45,6 +46,9 @@ void launch_conv2d_backward_weight_kernel(const T* grad_output, const T* input, 
 
 // grad_bias[c] = sum of grad_output[:, c, :, :] (on the GPU).
 void launch_conv2d_backward_bias_kernel(const float* grad_output, float* grad_bias, int batch,
+                                        int out_channels, int spatial,
+                                        hipStream_t stream = nullptr);
+void launch_conv2d_backward_bias_kernel(const double* grad_output, double* grad_bias, int batch,
                                         int out_channels, int spatial,
                                         hipStream_t stream = nullptr);
 

@@ -299,6 +299,37 @@ int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias,
                                  int64_t batch, int64_t out_channels, int64_t spatial,
                                  hipStream_t stream);
 
+/* float64 conv (no workspace).  Forward: each output the reference's fp64
+ * explicit-route chain -- sum over k = (ic*KH + kh)*KW + kw ascending of
+ * weight * input (zero padded), one FMA per term, then + bias[oc] (bias may
+ * be NULL).  Backward data / weight: the adjoint sums, one fp64 chain per
+ * output element.  Replace the double instantiations of
+ * cudeep::kernels::launch_conv2d_forward_kernel / _backward_data_kernel /
+ * _backward_weight_kernel (src/kernels/conv_kernel.cu:793-798; the explicit
+ * route :225-335, :417-545 with the double GEMM matmul_kernel.cu:691-743). */
+int cdx_conv2d_forward_f64(const double* input, const double* weight, const double* bias,
+                           double* output, int64_t batch, int64_t in_channels,
+                           int64_t out_channels, int64_t in_h, int64_t in_w,
+                           int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                           int64_t stride_w, int64_t pad_h, int64_t pad_w, hipStream_t stream);
+int cdx_conv2d_backward_data_f64(const double* grad_output, const double* weight,
+                                 double* grad_input, int64_t batch, int64_t in_channels,
+                                 int64_t out_channels, int64_t in_h, int64_t in_w,
+                                 int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                 int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                 hipStream_t stream);
+int cdx_conv2d_backward_weight_f64(const double* grad_output, const double* input,
+                                   double* grad_weight, int64_t batch, int64_t in_channels,
+                                   int64_t out_channels, int64_t in_h, int64_t in_w,
+                                   int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                   int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                   hipStream_t stream);
+/* grad_bias[c] = sum over b, s of grad_output[b, c, s] in fp64 (the
+ * reference's float64 Conv2dOp.backward, python/cuDeep/tensor.py:718-721). */
+int cdx_conv2d_backward_bias_f64(const double* grad_output, double* grad_bias,
+                                 int64_t batch, int64_t out_channels, int64_t spatial,
+                                 hipStream_t stream);
+
 /* ---- Linear helpers ---------------------------------------------------- */
 
 /* out[j] = sum_i in[i][j] over a row-major [rows, cols] matrix.

@@ -254,3 +254,102 @@ def test_conv_backward_c5_full():
         e_ref = oracle.rel_fro(oracle.conv2d_backward_data_ref(dy[i:i + 1], w, (1, 64, 56, 56),
                                                                (1, 1), (1, 1)), d64)
         assert oracle.rel_fro(dx[i:i + 1], d64) <= 2 * e_ref
+
+
+# ---------------------------------------------------------------------------
+# float64 conv (the reference's double instantiations)
+# ---------------------------------------------------------------------------
+
+def _conv64_calls(x, w, b, dy, stride, padding):
+    """The four fp64 C-ABI entry points on device copies of the operands."""
+    import torch
+    from cudeep_amd import _lib as L
+    Bn, C, H, W = x.shape
+    OC, _, KH, KW = w.shape
+    SH, SW = stride
+    PH, PW = padding
+    X, Wt, Y = dev(x), dev(w), dev(dy)
+    Bt = dev(b) if b is not None else None
+    geo = (Bn, C, OC, H, W, KH, KW, SH, SW, PH, PW)
+    out = torch.empty(dy.shape, dtype=torch.float64, device="cuda")
+    dx = torch.empty(x.shape, dtype=torch.float64, device="cuda")
+    dw = torch.empty(w.shape, dtype=torch.float64, device="cuda")
+    db = torch.empty((OC,), dtype=torch.float64, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    L.call("cdx_conv2d_forward_f64", X.data_ptr(), Wt.data_ptr(),
+           Bt.data_ptr() if Bt is not None else None, out.data_ptr(), *geo, s)
+    L.call("cdx_conv2d_backward_data_f64", Y.data_ptr(), Wt.data_ptr(), dx.data_ptr(), *geo, s)
+    L.call("cdx_conv2d_backward_weight_f64", Y.data_ptr(), X.data_ptr(), dw.data_ptr(), *geo, s)
+    L.call("cdx_conv2d_backward_bias_f64", Y.data_ptr(), db.data_ptr(), Bn, OC,
+           dy.shape[2] * dy.shape[3], s)
+    return host(out), host(dx), host(dw), host(db)
+
+
+F64_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
+    (2, 3, 8, 9, 4, 3, 3, 1, 1, 1, 1),
+    (1, 2, 7, 7, 3, 3, 5, 2, 1, 2, 0),
+    (3, 4, 6, 5, 5, 2, 2, 1, 1, 1, 0),
+    (2, 8, 15, 17, 6, 1, 1, 2, 2, 0, 0),
+    (2, 16, 28, 28, 32, 3, 3, 1, 1, 1, 1),
+]
+
+
+@pytest.mark.parametrize("g", F64_GEOMS)
+def test_conv_f64_parity(g):
+    """fp64 forward / backward data / backward weight / bias gradient against the
+    fp64 oracles.  Operands are fp32 values held in fp64 (the oracles read fp32),
+    so every product is exact and only the summation order differs."""
+    Bn, C, H, W, OC, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(640 + sum(g))
+    x = normal(rng, (Bn, C, H, W)).astype(np.float64)
+    w = normal(rng, (OC, C, KH, KW), std=np.sqrt(2.0 / (C * KH * KW))).astype(np.float64)
+    b = normal(rng, (OC,), std=0.1).astype(np.float64)
+    OH = oracle.conv_out_size(H, KH, SH, PH)
+    OW = oracle.conv_out_size(W, KW, SW, PW)
+    dy = normal(rng, (Bn, OC, OH, OW)).astype(np.float64)
+    st, pd = (SH, SW), (PH, PW)
+    say("conv f64", g)
+    out, dx, dw, db = _conv64_calls(x, w, b, dy, st, pd)
+    assert out.dtype == np.float64
+    assert oracle.rel_fro(out, oracle.conv2d_direct64(x, w, b, st, pd)) < 1e-14
+    assert oracle.rel_fro(dx, oracle.conv2d_backward_data64(dy, w, x.shape, st, pd)) < 1e-14
+    assert oracle.rel_fro(dw, oracle.conv2d_backward_weight64(dy, x, w.shape, st, pd)) < 1e-14
+    assert oracle.rel_fro(db, dy.sum(axis=(0, 2, 3))) < 1e-14
+
+
+def _conv_fwd_numpy64(x, w, b, stride, padding):
+    """Independent fp64 cross-correlation: zero-pad, then one tensor contraction
+    per filter tap."""
+    SH, SW = stride
+    PH, PW = padding
+    Bn, C, H, W = x.shape
+    OC, _, KH, KW = w.shape
+    OH, OW = (H + 2 * PH - KH) // SH + 1, (W + 2 * PW - KW) // SW + 1
+    xp = np.zeros((Bn, C, H + 2 * PH, W + 2 * PW))
+    xp[:, :, PH:PH + H, PW:PW + W] = x
+    out = np.zeros((Bn, OC, OH, OW))
+    for kh in range(KH):
+        for kw in range(KW):
+            win = xp[:, :, kh:kh + SH * (OH - 1) + 1:SH, kw:kw + SW * (OW - 1) + 1:SW]
+            out += np.einsum("oc,bchw->bohw", w[:, :, kh, kw], win)
+    return out + b[None, :, None, None]
+
+
+def test_conv_f64_full_precision_operands():
+    """Full 53-bit operands (not fp32 values): forward against an independent
+    NumPy fp64 contraction, backward through the adjoint identity
+    <conv(x), dy> = <x, dX(dy)> = <w, dW(dy, x)>, all in fp64."""
+    rng = np.random.default_rng(6464)
+    x = rng.standard_normal((2, 5, 11, 13))
+    w = rng.standard_normal((7, 5, 3, 3)) / 6.0
+    b = rng.standard_normal(7)
+    st, pd = (2, 1), (1, 2)
+    ref = _conv_fwd_numpy64(x, w, b, st, pd)
+    dy = rng.standard_normal(ref.shape)
+    say("conv f64 full precision")
+    out, dx, dw, db = _conv64_calls(x, w, b, dy, st, pd)
+    assert oracle.rel_fro(out, ref) < 1e-14
+    lin = float(np.sum((ref - b[None, :, None, None]) * dy))   # <conv without bias, dy>
+    assert abs(float(np.sum(x * dx)) - lin) <= 1e-12 * abs(lin)
+    assert abs(float(np.sum(w * dw)) - lin) <= 1e-12 * abs(lin)
+    assert np.allclose(db, dy.sum(axis=(0, 2, 3)), rtol=1e-14, atol=0)

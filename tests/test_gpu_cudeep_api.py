@@ -292,6 +292,32 @@ def test_conv2d_layer_forward_backward_vs_oracle(cd, prec):
                           g.astype(np.float64).sum(axis=(0, 2, 3))) < 1e-5
 
 
+def test_conv2d_layer_float64(cd):
+    """nn.Conv2d on float64 tensors (the reference instantiates its conv
+    launchers for double): forward and backward against the fp64 oracles on
+    fp32-valued operands."""
+    nn, T = cd.nn, cd.Tensor
+    rng = np.random.default_rng(64)
+    layer = nn.Conv2d(6, 10, kernel_size=3, stride=2, padding=1, dtype=cd.DType.float64)
+    w = (rng.standard_normal((10, 6, 3, 3)) * np.sqrt(2 / 54)).astype(np.float32).astype(np.float64)
+    b = (rng.standard_normal(10) * 0.1).astype(np.float32).astype(np.float64)
+    layer._parameters["weight"] = nn.Parameter(T.from_numpy(w))
+    layer._parameters["bias"] = nn.Parameter(T.from_numpy(b))
+    x = rng.standard_normal((3, 6, 13, 12)).astype(np.float32).astype(np.float64)
+    say("conv layer f64")
+    X = T.from_numpy(x, requires_grad=True)
+    y = layer(X)
+    assert y.dtype() == cd.DType.float64
+    g = rng.standard_normal(tuple(y.shape())).astype(np.float32).astype(np.float64)
+    (y * T.from_numpy(g)).sum().backward()
+    assert oracle.rel_fro(y.numpy(), oracle.conv2d_direct64(x, w, b, (2, 2), (1, 1))) < 1e-14
+    assert oracle.rel_fro(X.grad.numpy(),
+                          oracle.conv2d_backward_data64(g, w, x.shape, (2, 2), (1, 1))) < 1e-14
+    assert oracle.rel_fro(layer._parameters["weight"].grad.numpy(),
+                          oracle.conv2d_backward_weight64(g, x, w.shape, (2, 2), (1, 1))) < 1e-14
+    assert oracle.rel_fro(layer._parameters["bias"].grad.numpy(), g.sum(axis=(0, 2, 3))) < 1e-14
+
+
 def test_conv_algorithm_routing(cd):
     """launch_conv2d_forward_kernel routes like the reference
     (conv_kernel.cu:242-248): 3x3 stride-1 layers with >= 16 output pixels
