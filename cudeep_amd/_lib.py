@@ -20,11 +20,13 @@ CDX_ERR_WORKSPACE = 4
 
 OP_N, OP_T = 0, 1
 EPI_NONE, EPI_RELU, EPI_GELU, EPI_SILU, EPI_SIGMOID = 0, 1, 2, 3, 4
+ACT_TANH, ACT_LEAKY_RELU = 5, 6   # elementwise activations only
 BIAS_NONE, BIAS_ROW, BIAS_COL = 0, 1, 2
 PREC_FP32, PREC_TF32MODE, PREC_TF32MODE4 = 0, 1, 2
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
+_f32 = ctypes.c_float
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 
@@ -50,8 +52,8 @@ SIGNATURES = {
     "cdx_sum_reduce_rows_workspace_size": (_sz, [_i64, _i64]),
     "cdx_sum_reduce_rows_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _sz, _vp]),
     "cdx_broadcast_add_row_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
-    "cdx_activation_forward_f32": (_int, [_vp, _vp, _i64, _int, _vp]),
-    "cdx_activation_backward_f32": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
+    "cdx_activation_forward_f32": (_int, [_vp, _vp, _i64, _int, _f32, _vp]),
+    "cdx_activation_backward_f32": (_int, [_vp, _vp, _vp, _i64, _int, _f32, _vp]),
     "cdx_conv2d_winograd_workspace_size": (_sz, [_i64] * 7),
     "cdx_conv2d_forward_winograd_f32": (_int, [_vp, _vp, _vp, _vp] + [_i64] * 7 + [_int, _vp, _sz, _vp]),
     "cdx_col2im_f32": (_int, [_vp, _vp] + [_i64] * 10 + [_vp]),
@@ -74,8 +76,8 @@ SIGNATURES = {
     "cdx_sum": (_int, [_vp, _vp, _i64, _int, _vp, _sz, _vp]),
     "cdx_broadcast_add_row_f64": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "cdx_sum_reduce_rows_f64": (_int, [_vp, _vp, _i64, _i64, _vp, _sz, _vp]),
-    "cdx_activation_forward_f64": (_int, [_vp, _vp, _i64, _int, _vp]),
-    "cdx_activation_backward_f64": (_int, [_vp, _vp, _vp, _i64, _int, _vp]),
+    "cdx_activation_forward_f64": (_int, [_vp, _vp, _i64, _int, _f32, _vp]),
+    "cdx_activation_backward_f64": (_int, [_vp, _vp, _vp, _i64, _int, _f32, _vp]),
 }
 
 DTYPE_F32, DTYPE_F64, DTYPE_F16, DTYPE_BF16 = 0, 1, 2, 3

@@ -42,8 +42,8 @@ kernels::ActivationType parse_act(const std::string& name) {
     if (name == "gelu") return kernels::ActivationType::GELU;
     if (name == "silu") return kernels::ActivationType::SiLU;
     if (name == "sigmoid") return kernels::ActivationType::Sigmoid;
-    if (name == "tanh" || name == "leaky_relu")
-        throw std::runtime_error("activation '" + name + "' is not part of this build");
+    if (name == "tanh") return kernels::ActivationType::Tanh;
+    if (name == "leaky_relu") return kernels::ActivationType::LeakyReLU;
     throw std::runtime_error("Unknown activation: " + name);
 }
 
@@ -52,18 +52,18 @@ void require_f32_or_f64(const Tensor& t, const char* fn) {
         throw std::runtime_error(std::string(fn) + ": float32 or float64 required");
 }
 
-Tensor activation(const Tensor& t, kernels::ActivationType act) {
+Tensor activation(const Tensor& t, kernels::ActivationType act, float alpha = 0.01f) {
     Tensor in = ensure_contiguous(t);
     require_f32_or_f64(in, "activation");
     Tensor out(in.shape(), in.dtype());
     if (in.dtype() == DType::Float64)
         kernels::launch_activation_forward_kernel<double>(static_cast<const double*>(in.data()),
                                                           static_cast<double*>(out.data()),
-                                                          in.numel(), act, 0.01f, in.stream());
+                                                          in.numel(), act, alpha, in.stream());
     else
         kernels::launch_activation_forward_kernel<float>(static_cast<const float*>(in.data()),
                                                          static_cast<float*>(out.data()),
-                                                         in.numel(), act, 0.01f, in.stream());
+                                                         in.numel(), act, alpha, in.stream());
     return out;
 }
 
@@ -202,6 +202,13 @@ PYBIND11_MODULE(_cudeep_core, m) {
           py::arg("input"));
     m.def("silu", [](const Tensor& t) { return activation(t, kernels::ActivationType::SiLU); },
           py::arg("input"));
+    m.def("tanh_act", [](const Tensor& t) { return activation(t, kernels::ActivationType::Tanh); },
+          py::arg("input"));
+    m.def("leaky_relu",
+          [](const Tensor& t, float alpha) {
+              return activation(t, kernels::ActivationType::LeakyReLU, alpha);
+          },
+          py::arg("input"), py::arg("alpha") = 0.01f);
     m.def("activation_backward",
           [](const Tensor& grad_output, const Tensor& input, const std::string& act_name,
              float alpha) {

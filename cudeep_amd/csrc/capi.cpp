@@ -766,53 +766,59 @@ int cdx_broadcast_add_row_f64(const double* matrix, const double* row, double* o
 }
 
 extern "C++" {
+static bool valid_activation(int act) {
+    return act == CDX_EPI_RELU || act == CDX_EPI_GELU || act == CDX_EPI_SILU ||
+           act == CDX_EPI_SIGMOID || act == CDX_ACT_TANH || act == CDX_ACT_LEAKY_RELU;
+}
+
 template <typename T, typename Launch>
-static int act_impl(const char* fn, const T* input, T* output, int64_t n, int act,
+static int act_impl(const char* fn, const T* input, T* output, int64_t n, int act, float alpha,
                     hipStream_t stream, Launch launch) {
     if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad n");
-    if (act == CDX_EPI_NONE || !valid_epilogue(act))
-        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU, GELU, SILU or SIGMOID");
+    if (!valid_activation(act))
+        return set_error(CDX_ERR_INVALID_ARG,
+                         std::string(fn) + ": act must be RELU, GELU, SILU, SIGMOID, TANH or LEAKY_RELU");
     if (n == 0) return CDX_OK;
     if (!input || !output) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
-    return launch(input, output, n, act, stream);
+    return launch(input, output, n, act, alpha, stream);
 }
-}  // extern "C++"
 
-extern "C++" {
 template <typename T, typename Launch>
 static int act_bwd_impl(const char* fn, const T* go, const T* input, T* gi, int64_t n, int act,
-                        hipStream_t stream, Launch launch) {
+                        float alpha, hipStream_t stream, Launch launch) {
     if (bad_dim(n)) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad n");
-    if (act == CDX_EPI_NONE || !valid_epilogue(act))
-        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": act must be RELU, GELU, SILU or SIGMOID");
+    if (!valid_activation(act))
+        return set_error(CDX_ERR_INVALID_ARG,
+                         std::string(fn) + ": act must be RELU, GELU, SILU, SIGMOID, TANH or LEAKY_RELU");
     if (n == 0) return CDX_OK;
     if (!go || !input || !gi) return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
-    return launch(go, input, gi, n, act, stream);
+    return launch(go, input, gi, n, act, alpha, stream);
 }
 }  // extern "C++"
 
-int cdx_activation_forward_f32(const float* input, float* output, int64_t n, int act,
+int cdx_activation_forward_f32(const float* input, float* output, int64_t n, int act, float alpha,
                                hipStream_t stream) {
-    return act_impl("cdx_activation_forward_f32", input, output, n, act, stream,
+    return act_impl("cdx_activation_forward_f32", input, output, n, act, alpha, stream,
                     cdx::launch_activation_f32);
 }
 
 int cdx_activation_forward_f64(const double* input, double* output, int64_t n, int act,
-                               hipStream_t stream) {
-    return act_impl("cdx_activation_forward_f64", input, output, n, act, stream,
+                               float alpha, hipStream_t stream) {
+    return act_impl("cdx_activation_forward_f64", input, output, n, act, alpha, stream,
                     cdx::launch_activation_f64);
 }
 
 int cdx_activation_backward_f32(const float* grad_output, const float* input, float* grad_input,
-                                int64_t n, int act, hipStream_t stream) {
+                                int64_t n, int act, float alpha, hipStream_t stream) {
     return act_bwd_impl("cdx_activation_backward_f32", grad_output, input, grad_input, n, act,
-                        stream, cdx::launch_activation_backward_f32);
+                        alpha, stream, cdx::launch_activation_backward_f32);
 }
 
 int cdx_activation_backward_f64(const double* grad_output, const double* input,
-                                double* grad_input, int64_t n, int act, hipStream_t stream) {
+                                double* grad_input, int64_t n, int act, float alpha,
+                                hipStream_t stream) {
     return act_bwd_impl("cdx_activation_backward_f64", grad_output, input, grad_input, n, act,
-                        stream, cdx::launch_activation_backward_f64);
+                        alpha, stream, cdx::launch_activation_backward_f64);
 }
 
 static bool bad_dtype(int dtype) { return dtype != CDX_DTYPE_F32 && dtype != CDX_DTYPE_F64; }

@@ -210,16 +210,14 @@ int launch_broadcast_add_row_f32(const float* m, const float* row, float* out,
                                  int64_t rows, int64_t cols, hipStream_t stream);
 int launch_broadcast_add_row_f64(const double* m, const double* row, double* out,
                                  int64_t rows, int64_t cols, hipStream_t stream);
-int launch_activation_f32(const float* in, float* out, int64_t n, int act,
+int launch_activation_f32(const float* in, float* out, int64_t n, int act, float alpha,
                           hipStream_t stream);
-int launch_activation_f64(const double* in, double* out, int64_t n, int act,
+int launch_activation_f64(const double* in, double* out, int64_t n, int act, float alpha,
                           hipStream_t stream);
-int launch_activation_backward_f32(const float* grad_out, const float* in,
-                                   float* grad_in, int64_t n, int act,
-                                   hipStream_t stream);
-int launch_activation_backward_f64(const double* grad_out, const double* in,
-                                   double* grad_in, int64_t n, int act,
-                                   hipStream_t stream);
+int launch_activation_backward_f32(const float* grad_out, const float* in, float* grad_in,
+                                   int64_t n, int act, float alpha, hipStream_t stream);
+int launch_activation_backward_f64(const double* grad_out, const double* in, double* grad_in,
+                                   int64_t n, int act, float alpha, hipStream_t stream);
 
 // GELU, tanh form 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3)
 // (Hendrycks & Gimpel 2016; the reference's constants 0.7978845608 and

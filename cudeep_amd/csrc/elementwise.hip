@@ -69,41 +69,53 @@ void bias_row_kernel(const T* __restrict__ m, const T* __restrict__ row,
         out[i] = m[i] + row[i % cols];
 }
 
-__device__ __forceinline__ double apply_act(double v, int act) {
+// alpha: the leaky ReLU's negative slope (as a float, as the reference
+// passes it); the product alpha * v of two floats is exact in double, so the
+// float result equals the reference's float multiply
+__device__ __forceinline__ double apply_act(double v, int act, double alpha) {
     if (act == CDX_EPI_RELU) return v > 0.0 ? v : 0.0;
     if (act == CDX_EPI_GELU) return gelu_f64(v);
     if (act == CDX_EPI_SILU) return silu_t(v);
     if (act == CDX_EPI_SIGMOID) return sigmoid_t(v);
+    if (act == CDX_ACT_TANH) return tanh(v);
+    if (act == CDX_ACT_LEAKY_RELU) return v > 0.0 ? v : alpha * v;
     return v;
 }
 
 template <typename T>
 __global__ __launch_bounds__(256)
-void act_fwd_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, int act) {
+void act_fwd_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t n, int act, float alpha) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)
-        y[i] = apply_act(x[i], act);
+        y[i] = apply_act(x[i], act, alpha);
 }
 
 __device__ __forceinline__ float gelu_grad(float v) { return gelu_grad_f32(v); }
 __device__ __forceinline__ double gelu_grad(double v) { return gelu_grad_f64(v); }
 
-// d act / dx at the pre-activation input x (ReLU: the mask x > 0)
+// d act / dx at the pre-activation input x (ReLU / leaky ReLU: the mask x > 0,
+// handled in the kernel); tanh' = 1 - tanh(x)^2, formed in double
 template <typename T>
 __device__ __forceinline__ T act_grad(T x, int act) {
     if (act == CDX_EPI_GELU) return gelu_grad(x);
     if (act == CDX_EPI_SILU) return silu_grad_t(x);
+    if (act == CDX_ACT_TANH) {
+        const double t = tanh((double)x);
+        return (T)(1.0 - t * t);
+    }
     return sigmoid_grad_t(x);
 }
 
 template <typename T>
 __global__ __launch_bounds__(256)
 void act_bwd_kernel(const T* __restrict__ go, const T* __restrict__ x,
-                    T* __restrict__ gi, int64_t n, int act) {
+                    T* __restrict__ gi, int64_t n, int act, float alpha) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
         const T v = x[i];
-        gi[i] = act == CDX_EPI_RELU ? (v > T(0) ? go[i] : T(0)) : go[i] * act_grad(v, act);
+        if (act == CDX_EPI_RELU) gi[i] = v > T(0) ? go[i] : T(0);
+        else if (act == CDX_ACT_LEAKY_RELU) gi[i] = v > T(0) ? go[i] : (T)alpha * go[i];
+        else gi[i] = go[i] * act_grad(v, act);
     }
 }
 
@@ -137,7 +149,7 @@ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t M, in
         for (; s < splits; ++s) v += P[(int64_t)s * MN + i];
         if (bias_mode == CDX_BIAS_COL) v += bias[n];
         else if (bias_mode == CDX_BIAS_ROW) v += bias[m];
-        v = apply_act(v, act);
+        v = apply_act(v, act, 0.0);   // GEMM epilogues: no slope
         const int64_t col = n_split > 0 ? (n / n_split) * ldc_split + n % n_split : n;
         C[m * ldc + col] = v;
     }
@@ -215,35 +227,40 @@ int launch_broadcast_add_row_f64(const double* m, const double* row, double* out
 }
 
 template <typename T>
-int act_t(const T* in, T* out, int64_t n, int act, hipStream_t stream) {
+int act_t(const T* in, T* out, int64_t n, int act, float alpha, hipStream_t stream) {
     if (n == 0) return CDX_OK;
-    hipLaunchKernelGGL(act_fwd_kernel<T>, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n, act);
+    hipLaunchKernelGGL(act_fwd_kernel<T>, dim3(grid_for(n)), dim3(256), 0, stream, in, out, n, act,
+                       alpha);
     return hip_error(hipGetLastError(), "act_fwd_kernel launch");
 }
 
 template <typename T>
-int act_bwd_t(const T* go, const T* in, T* gi, int64_t n, int act, hipStream_t stream) {
+int act_bwd_t(const T* go, const T* in, T* gi, int64_t n, int act, float alpha,
+              hipStream_t stream) {
     if (n == 0) return CDX_OK;
-    hipLaunchKernelGGL(act_bwd_kernel<T>, dim3(grid_for(n)), dim3(256), 0, stream, go, in, gi, n, act);
+    hipLaunchKernelGGL(act_bwd_kernel<T>, dim3(grid_for(n)), dim3(256), 0, stream, go, in, gi, n,
+                       act, alpha);
     return hip_error(hipGetLastError(), "act_bwd_kernel launch");
 }
 
-int launch_activation_f32(const float* in, float* out, int64_t n, int act, hipStream_t stream) {
-    return act_t(in, out, n, act, stream);
+int launch_activation_f32(const float* in, float* out, int64_t n, int act, float alpha,
+                          hipStream_t stream) {
+    return act_t(in, out, n, act, alpha, stream);
 }
 
-int launch_activation_f64(const double* in, double* out, int64_t n, int act, hipStream_t stream) {
-    return act_t(in, out, n, act, stream);
+int launch_activation_f64(const double* in, double* out, int64_t n, int act, float alpha,
+                          hipStream_t stream) {
+    return act_t(in, out, n, act, alpha, stream);
 }
 
 int launch_activation_backward_f32(const float* go, const float* in, float* gi, int64_t n,
-                                   int act, hipStream_t stream) {
-    return act_bwd_t(go, in, gi, n, act, stream);
+                                   int act, float alpha, hipStream_t stream) {
+    return act_bwd_t(go, in, gi, n, act, alpha, stream);
 }
 
 int launch_activation_backward_f64(const double* go, const double* in, double* gi, int64_t n,
-                                   int act, hipStream_t stream) {
-    return act_bwd_t(go, in, gi, n, act, stream);
+                                   int act, float alpha, hipStream_t stream) {
+    return act_bwd_t(go, in, gi, n, act, alpha, stream);
 }
 
 }  // namespace cdx

@@ -43,7 +43,9 @@ int act_code(ActivationType a) {
     if (a == ActivationType::GELU) return CDX_EPI_GELU;
     if (a == ActivationType::SiLU) return CDX_EPI_SILU;
     if (a == ActivationType::Sigmoid) return CDX_EPI_SIGMOID;
-    throw std::runtime_error("activation not supported by this build (ReLU, GELU, SiLU, Sigmoid)");
+    if (a == ActivationType::Tanh) return CDX_ACT_TANH;
+    if (a == ActivationType::LeakyReLU) return CDX_ACT_LEAKY_RELU;
+    throw std::runtime_error("unknown activation");
 }
 
 }  // namespace
@@ -286,28 +288,28 @@ void launch_sum_kernel(const T* input, T* output, int64_t n, hipStream_t s) {
 
 template <>
 void launch_activation_forward_kernel<float>(const float* in, float* out, int64_t n,
-                                             ActivationType act, float, hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_activation_forward_f32(in, out, n, act_code(act), s));
+                                             ActivationType act, float alpha, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_activation_forward_f32(in, out, n, act_code(act), alpha, s));
 }
 
 template <>
 void launch_activation_forward_kernel<double>(const double* in, double* out, int64_t n,
-                                              ActivationType act, float, hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_activation_forward_f64(in, out, n, act_code(act), s));
+                                              ActivationType act, float alpha, hipStream_t s) {
+    CUDEEP_CHECK_CDX(cdx_activation_forward_f64(in, out, n, act_code(act), alpha, s));
 }
 
 template <>
 void launch_activation_backward_kernel<float>(const float* go, const float* in, float* gi,
-                                              int64_t n, ActivationType act, float,
+                                              int64_t n, ActivationType act, float alpha,
                                               hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_activation_backward_f32(go, in, gi, n, act_code(act), s));
+    CUDEEP_CHECK_CDX(cdx_activation_backward_f32(go, in, gi, n, act_code(act), alpha, s));
 }
 
 template <>
 void launch_activation_backward_kernel<double>(const double* go, const double* in, double* gi,
-                                               int64_t n, ActivationType act, float,
+                                               int64_t n, ActivationType act, float alpha,
                                                hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_activation_backward_f64(go, in, gi, n, act_code(act), s));
+    CUDEEP_CHECK_CDX(cdx_activation_backward_f64(go, in, gi, n, act_code(act), alpha, s));
 }
 
 #define CDX_INST(T)                                                                         \

@@ -10,7 +10,7 @@ try:
         Stream,
         Event,
         MemoryPool,
-        relu, gelu, sigmoid, silu, activation_backward,
+        relu, gelu, sigmoid, silu, tanh_act, leaky_relu, activation_backward,
         broadcast_add, sum_reduce_rows, sum,
         matmul_ex, linear_forward,
         conv2d_forward, conv2d_backward_data, conv2d_backward_weight, conv2d_backward_bias,

@@ -311,17 +311,20 @@ def broadcast_add_row(m, row, out=None):
     return out
 
 
-def activation(x, act, out=None):
+def activation(x, act, out=None, alpha=0.01):
+    """act(x) elementwise; act is EPI_RELU / _GELU / _SILU / _SIGMOID, ACT_TANH or
+    ACT_LEAKY_RELU (negative slope alpha)."""
     _need(x, "input")
     if not x.is_contiguous():
         raise ValueError("activation: input must be contiguous")
     if out is None:
         out = torch.empty_like(x)
-    L.call("cdx_activation_forward_f32", x.data_ptr(), out.data_ptr(), x.numel(), act, _stream())
+    L.call("cdx_activation_forward_f32", x.data_ptr(), out.data_ptr(), x.numel(), act, alpha,
+           _stream())
     return out
 
 
-def activation_backward(grad_out, x, act, out=None):
+def activation_backward(grad_out, x, act, out=None, alpha=0.01):
     _need(grad_out, "grad_output")
     _need(x, "input")
     if grad_out.shape != x.shape or not (x.is_contiguous() and grad_out.is_contiguous()):
@@ -329,7 +332,7 @@ def activation_backward(grad_out, x, act, out=None):
     if out is None:
         out = torch.empty_like(x)
     L.call("cdx_activation_backward_f32", grad_out.data_ptr(), x.data_ptr(), out.data_ptr(),
-           x.numel(), act, _stream())
+           x.numel(), act, alpha, _stream())
     return out
 
 

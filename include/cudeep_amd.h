@@ -54,6 +54,9 @@ extern "C" {
 #define CDX_EPI_GELU    2
 #define CDX_EPI_SILU    3
 #define CDX_EPI_SIGMOID 4
+/* elementwise activations only (cdx_activation_*), not GEMM epilogues */
+#define CDX_ACT_TANH       5
+#define CDX_ACT_LEAKY_RELU 6
 
 #define CDX_BIAS_NONE 0
 #define CDX_BIAS_ROW  1            /* C[m][n] += bias[m]  (conv: per channel) */
@@ -357,20 +360,21 @@ int cdx_sum_reduce_rows_f64(const double* input, double* output,
                             void* workspace, size_t workspace_bytes,
                             hipStream_t stream);
 
-/* Activation forward and backward, act = CDX_EPI_RELU, _GELU, _SILU or
- * _SIGMOID.  Replace launch_activation_forward_kernel /
- * launch_activation_backward_kernel for those activations
+/* Activation forward and backward, act = CDX_EPI_RELU, _GELU, _SILU,
+ * _SIGMOID, CDX_ACT_TANH or CDX_ACT_LEAKY_RELU (alpha: its negative slope,
+ * ignored by the others); the backward takes the pre-activation input.
+ * Replace launch_activation_forward_kernel / launch_activation_backward_kernel
  * (include/cudeep/kernels/activation.cuh:17-31,
  * src/kernels/activation_kernel.cu:19-66, :206-330). */
 int cdx_activation_forward_f32(const float* input, float* output, int64_t n,
-                               int act, hipStream_t stream);
+                               int act, float alpha, hipStream_t stream);
 int cdx_activation_backward_f32(const float* grad_output, const float* input,
-                                float* grad_input, int64_t n, int act,
+                                float* grad_input, int64_t n, int act, float alpha,
                                 hipStream_t stream);
 int cdx_activation_forward_f64(const double* input, double* output, int64_t n,
-                               int act, hipStream_t stream);
+                               int act, float alpha, hipStream_t stream);
 int cdx_activation_backward_f64(const double* grad_output, const double* input,
-                                double* grad_input, int64_t n, int act,
+                                double* grad_input, int64_t n, int act, float alpha,
                                 hipStream_t stream);
 
 /* ---- tensor runtime ----------------------------------------------------- */

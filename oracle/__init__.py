@@ -390,15 +390,41 @@ def silu_grad(x):
     return s * (1.0 + x * sigmoid(-x))
 
 
+def tanh(x):
+    """tanh in fp64 (reference act_tanh, src/kernels/activation_kernel.cu:33-40)."""
+    return np.tanh(np.asarray(x, dtype=np.float64))
+
+
+def tanh_grad(x):
+    """1 - tanh(x)^2 (reference backward, activation_kernel.cu:168-171)."""
+    t = tanh(x)
+    return 1.0 - t * t
+
+
+def leaky_relu(x, alpha=0.01):
+    """x > 0 ? x : alpha * x (reference act_leaky_relu, activation_kernel.cu:63-66),
+    alpha rounded to fp32 as the reference passes it."""
+    x = np.asarray(x, dtype=np.float64)
+    return np.where(x > 0, x, float(np.float32(alpha)) * x)
+
+
+def leaky_relu_grad(x, alpha=0.01):
+    """1 for x > 0, alpha otherwise (reference backward, activation_kernel.cu:190-191)."""
+    return np.where(np.asarray(x) > 0, 1.0, float(np.float32(alpha)))
+
+
 def activation(x, name):
-    """Forward activation by name: relu / gelu / silu / sigmoid."""
-    return {"relu": relu, "gelu": gelu, "silu": silu, "sigmoid": sigmoid}[name](x)
+    """Forward activation by name: relu / gelu / silu / sigmoid / tanh / leaky_relu
+    (slope 0.01, the reference's default)."""
+    return {"relu": relu, "gelu": gelu, "silu": silu, "sigmoid": sigmoid, "tanh": tanh,
+            "leaky_relu": leaky_relu}[name](x)
 
 
 def activation_grad(x, name):
     """d activation / dx at the pre-activation input x."""
     return {"relu": relu_grad, "gelu": gelu_grad, "silu": silu_grad,
-            "sigmoid": sigmoid_grad}[name](x)
+            "sigmoid": sigmoid_grad, "tanh": tanh_grad,
+            "leaky_relu": leaky_relu_grad}[name](x)
 
 
 def rel_fro(C, Cref) -> float:

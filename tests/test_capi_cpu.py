@@ -114,9 +114,11 @@ def test_conv_argument_validation():
     # 8192 rows -> 256 chunks of 32 rows; partials sized for fp64
     assert L.lib().cdx_sum_reduce_rows_workspace_size(8192, 256) == 256 * 256 * 8
     assert L.lib().cdx_sum_reduce_rows_workspace_size(10 ** 7, 3) == 1024 * 3 * 8
-    assert _status("cdx_activation_forward_f32", fake, fake, 4, 0, None) == L.CDX_ERR_INVALID_ARG
-    assert _status("cdx_activation_forward_f32", fake, fake, 4, 5, None) == L.CDX_ERR_INVALID_ARG
-    assert _status("cdx_activation_backward_f64", fake, fake, fake, 4, 5, None) \
+    assert _status("cdx_activation_forward_f32", fake, fake, 4, 0, 0.01, None) == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_activation_forward_f32", fake, fake, 4, 7, 0.01, None) == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_activation_backward_f64", fake, fake, fake, 4, 7, 0.01, None) \
+        == L.CDX_ERR_INVALID_ARG
+    assert _status("cdx_activation_forward_f32", None, fake, 4, L.ACT_TANH, 0.01, None) \
         == L.CDX_ERR_INVALID_ARG
     assert _status("cdx_sum_reduce_rows_f32", None, fake, 4, 4, None, 0, None) \
         == L.CDX_ERR_INVALID_ARG

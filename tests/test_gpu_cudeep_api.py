@@ -103,8 +103,9 @@ def test_matmul_reference_cases(cd, prec):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_core_activations_vs_oracle(cd, dtype):
-    """_cudeep_core relu / gelu / sigmoid / silu and activation_backward
-    (reference module.cpp:185-207, :837-872) against the fp64 oracle."""
+    """_cudeep_core relu / gelu / sigmoid / silu / tanh_act / leaky_relu and
+    activation_backward (reference module.cpp:185-207, :837-872) against the
+    fp64 oracle."""
     from cudeep_amd.cuDeep import _core
     x = np.linspace(-12, 12, 4099).astype(dtype)
     go = np.random.default_rng(3).standard_normal(x.shape).astype(dtype)
@@ -112,9 +113,10 @@ def test_core_activations_vs_oracle(cd, dtype):
     # 1 + tanh(u) cancels for x << 0 (absolute error ~ |x| 2^-53), so the
     # gate is a few 1e-12 against the 1e-3 floor
     tol = 2e-6 if dtype == np.float32 else 5e-12
-    for name in ("relu", "gelu", "sigmoid", "silu"):
+    for name in ("relu", "gelu", "sigmoid", "silu", "tanh", "leaky_relu"):
         say("core activation", name, dtype.__name__)
-        y = getattr(_core, name)(_core.Tensor.from_numpy(x)).numpy()
+        fwd = _core.tanh_act if name == "tanh" else getattr(_core, name)
+        y = fwd(_core.Tensor.from_numpy(x)).numpy()
         want = oracle.activation(x, name)
         assert y.dtype == dtype
         assert np.max(np.abs(y - want) / np.maximum(np.abs(want), 1e-3)) < tol, name
@@ -390,3 +392,16 @@ def test_init_distributions(cd):
     bound = np.sqrt(6.0 / (784 + 256))
     assert np.abs(w).max() <= bound and abs(w.std() - bound / np.sqrt(3)) < 0.002
     assert np.array_equal(init.constant_(T.zeros([3]), 2.5).numpy(), [2.5, 2.5, 2.5])
+
+
+def test_core_leaky_relu_slope(cd):
+    """leaky_relu(x, alpha) and its backward with a non-default slope."""
+    from cudeep_amd.cuDeep import _core
+    x = np.linspace(-3, 3, 257).astype(np.float32)
+    go = np.random.default_rng(5).standard_normal(x.shape).astype(np.float32)
+    say("leaky relu slope")
+    y = _core.leaky_relu(_core.Tensor.from_numpy(x), 0.2).numpy()
+    assert np.array_equal(y, oracle.leaky_relu(x, 0.2).astype(np.float32))
+    g = _core.activation_backward(_core.Tensor.from_numpy(go), _core.Tensor.from_numpy(x),
+                                  "leaky_relu", 0.2).numpy()
+    assert np.array_equal(g, (go * oracle.leaky_relu_grad(x, 0.2)).astype(np.float32))

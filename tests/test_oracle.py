@@ -284,6 +284,21 @@ def test_gelu_against_torch_and_derivative():
     assert np.array_equal(oracle.relu_grad(np.array([-1.0, 0.0, 2.0])), [0.0, 0.0, 1.0])
 
 
+def test_tanh_and_leaky_relu_closed_forms():
+    """tanh against its exponential form and its derivative against central
+    differences; leaky ReLU at known points (slope 0.01 as fp32)."""
+    x = np.linspace(-8, 8, 801)
+    e = np.exp(-2 * np.abs(x))
+    assert np.allclose(oracle.tanh(x), np.sign(x) * (1 - e) / (1 + e), rtol=1e-13, atol=1e-15)
+    h = 1e-6
+    num = (oracle.tanh(x + h) - oracle.tanh(x - h)) / (2 * h)
+    assert np.allclose(oracle.tanh_grad(x), num, atol=1e-8)
+    a = float(np.float32(0.01))
+    assert np.array_equal(oracle.leaky_relu(np.array([-2.0, 0.0, 3.0])), [-2.0 * a, 0.0, 3.0])
+    assert np.array_equal(oracle.leaky_relu_grad(np.array([-2.0, 0.0, 3.0])), [a, a, 1.0])
+    assert np.array_equal(oracle.leaky_relu(np.array([-1.0]), 0.2), [-float(np.float32(0.2))])
+
+
 def test_tf32_round_is_identity_on_16bit_values():
     """fp16 and bf16 values have at most 11 significant bits, so TF32 rounding
     (either mode) leaves them unchanged: gemm_tf32emu on fp32-converted 16-bit
