@@ -272,8 +272,10 @@ int cdx_conv2d_backward_data_winograd_f32(const float* grad_output, const float*
                                           hipStream_t stream);
 
 /* Conv backward weight: grad_weight[OC, K_col] = grad_out[OC, B*S] * col^T,
- * as an implicit FP32-MFMA GEMM that gathers both operands from the NCHW
- * grad_out and input: no col buffer, no reshape.
+ * as an implicit FP32-MFMA GEMM that reads both operands from the NCHW
+ * grad_out and input: no col buffer, no reshape (3x3 stride-1 layers stage
+ * whole input rows and form each tap as a shifted window; other geometries
+ * gather per element).
  * All precisions take it (exact fp32 products meet the TF32 bounds too);
  * problems beyond its 32-bit index range fall back to im2col + a GEMM that
  * reads col transposed.  The long K = B*S is split across workgroups and
