@@ -292,6 +292,8 @@ PYBIND11_MODULE(_cudeep_core, m) {
               Tensor A = ensure_contiguous(a), B = ensure_contiguous(b);
               if (A.ndim() != 2 || B.ndim() != 2)
                   throw std::runtime_error("matmul_ex: operands must be 2-D");
+              require_f32_or_f64(A, "matmul_ex");
+              require_f32_or_f64(B, "matmul_ex");
               if (A.dtype() != B.dtype()) throw std::runtime_error("matmul_ex: dtype mismatch");
               const int64_t M = trans_a ? A.shape()[1] : A.shape()[0];
               const int64_t K = trans_a ? A.shape()[0] : A.shape()[1];
@@ -326,6 +328,7 @@ PYBIND11_MODULE(_cudeep_core, m) {
               const float* bptr = nullptr;
               if (!bias_obj.is_none()) {
                   b = ensure_contiguous(bias_obj.cast<Tensor>());
+                  require_f32(b, "linear_forward");
                   if (b.numel() != W.shape()[0])
                       throw std::runtime_error("linear_forward: bias must have out_features entries");
                   bptr = static_cast<const float*>(b.data());

@@ -411,6 +411,30 @@ struct Scratch {
     }
 };
 
+// Scratch of the backward-weight GEMM route (problems beyond the implicit
+// kernel's index range): col [Kc, BS], (batch > 1) grad_out as [OC, BS], then
+// the split-K partials of the [OC, Kc] x BS product (the largest any
+// precision's launch takes), 256-byte aligned.
+struct WgradGemmBytes {
+    size_t gemm_off, gemm, total;
+};
+
+WgradGemmBytes wgrad_gemm_route_bytes(int64_t batch, int64_t out_channels, const ConvSizes& z) {
+    const size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
+    cdx::GemmArgs g{CDX_OP_N, CDX_OP_T, out_channels, z.Kc, z.BS, nullptr, 1, nullptr, 1,
+                    nullptr, z.Kc, 0, 0, nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+    size_t gemm = 0;
+    if (out_channels * z.Kc > 0) {
+        gemm = cdx::gemm_f32_workspace(g);
+        for (int terms = 3; terms <= 4; ++terms) {
+            const size_t t = cdx::gemm_bf16x3_workspace(g, terms);
+            if (t > gemm) gemm = t;
+        }
+    }
+    const size_t off = (n * sizeof(float) + 255) / 256 * 256;
+    return {off, gemm, gemm > 0 ? off + gemm : n * sizeof(float)};
+}
+
 }  // namespace
 
 size_t cdx_conv2d_backward_data_workspace_size(int64_t batch, int64_t in_channels,
@@ -553,12 +577,13 @@ size_t cdx_conv2d_backward_weight_workspace_size(int64_t batch, int64_t in_chann
         return 0;
     ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
                              stride_w, pad_h, pad_w);
-    // enough for either route: col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
-    // (GEMM route), or the implicit kernel's split partials
-    size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
-    const size_t imp = wgrad_implicit_floats(batch, in_channels, out_channels, in_h, in_w,
-                                             kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w);
-    return (n > imp ? n : imp) * sizeof(float);
+    // exactly what the route the launch takes uses
+    if (z.BS > 0 && cdx::conv_wgrad_implicit_ok(batch, in_channels, out_channels, in_h, in_w,
+                                                kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                                                pad_w))
+        return wgrad_implicit_floats(batch, in_channels, out_channels, in_h, in_w, kernel_h,
+                                     kernel_w, stride_h, stride_w, pad_h, pad_w) * sizeof(float);
+    return wgrad_gemm_route_bytes(batch, out_channels, z).total;
 }
 
 int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
@@ -600,6 +625,7 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
                                         stride_w, pad_h, pad_w, stream);
         return ws.release(st);
     }
+    const WgradGemmBytes wb = wgrad_gemm_route_bytes(batch, out_channels, z);
     Scratch ws;
     st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
     if (st) return st;
@@ -618,6 +644,10 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
         cdx::GemmArgs g{CDX_OP_N, CDX_OP_T, out_channels, z.Kc, z.BS, dy_cm, z.BS > 0 ? z.BS : 1,
                         col, z.BS > 0 ? z.BS : 1, grad_weight, z.Kc, 0, 0, nullptr,
                         CDX_BIAS_NONE, CDX_EPI_NONE};
+        if (wb.gemm > 0) {   // split-K partials from the same workspace
+            g.ws = static_cast<char*>(ws.ptr) + wb.gemm_off;
+            g.ws_bytes = wb.gemm;
+        }
         st = run_gemm(precision, g, stream);
     }
     return ws.release(st);

@@ -17,9 +17,10 @@
 //  * generic kernel (larger planes): one thread per 4 consecutive s of one
 //    (k, b) row, gathering straight from global memory.
 // Index math is 32-bit where the value is bounded by one plane or one row
-// (s < spatial, k < K_col); flat offsets are 64-bit, so results agree with
-// the reference wherever its int indices do not overflow and stay correct
-// beyond that.
+// (s < spatial, k < K_col) and both bounds fit 32 bits (the generic kernel
+// switches to 64-bit arithmetic otherwise); flat offsets are 64-bit, so
+// results agree with the reference wherever its int indices do not overflow
+// and stay correct beyond that.
 #include "cdx_internal.hpp"
 
 namespace cdx {
@@ -29,7 +30,10 @@ struct Im2colGeom {
     int64_t batch, IC, IH, IW, KH, KW, SH, SW, PH, PW, OH, OW, spatial, runs;
 };
 
-template <int VS>
+// IDX: the integer type of the per-element index arithmetic -- int where the
+// output plane (spatial) and the column count K_col fit 32 bits (the
+// launcher checks), int64_t otherwise.
+template <int VS, typename IDX>
 __global__ __launch_bounds__(256)
 void im2col_kernel(const float* __restrict__ in, float* __restrict__ col, Im2colGeom g) {
     const int64_t per_run = (g.spatial + VS - 1) / VS;
@@ -37,18 +41,18 @@ void im2col_kernel(const float* __restrict__ in, float* __restrict__ col, Im2col
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
          t += (int64_t)gridDim.x * blockDim.x) {
         const int64_t run = t / per_run;               // run = k * batch + b
-        const int s0 = (int)(t - run * per_run) * VS;
-        const int b = (int)(run % g.batch);
-        const int k = (int)(run / g.batch);
-        const int kw = k % (int)g.KW;
-        const int kh = (k / (int)g.KW) % (int)g.KH;
-        const int ic = k / (int)(g.KW * g.KH);
-        const float* plane = in + ((int64_t)b * g.IC + ic) * g.IH * g.IW;
+        const IDX s0 = (IDX)(t - run * per_run) * VS;
+        const int64_t b = run % g.batch;
+        const IDX k = (IDX)(run / g.batch);
+        const IDX kw = k % (IDX)g.KW;
+        const IDX kh = (k / (IDX)g.KW) % (IDX)g.KH;
+        const IDX ic = k / (IDX)(g.KW * g.KH);
+        const float* plane = in + (b * g.IC + ic) * g.IH * g.IW;
         float v[VS];
 #pragma unroll
         for (int e = 0; e < VS; ++e) {
-            const int s = s0 + e;
-            const int oh = s / (int)g.OW, ow = s % (int)g.OW;
+            const IDX s = s0 + e;
+            const IDX oh = s / (IDX)g.OW, ow = s % (IDX)g.OW;
             const int64_t ih = (int64_t)oh * g.SH - g.PH + kh;
             const int64_t iw = (int64_t)ow * g.SW - g.PW + kw;
             v[e] = (s < g.spatial && ih >= 0 && ih < g.IH && iw >= 0 && iw < g.IW)
@@ -385,10 +389,15 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
     const int64_t threads = g.runs * ((g.spatial + VS - 1) / VS);
     int64_t blocks = ceil_div(threads, 256);
     if (blocks > (int64_t)1 << 30) blocks = (int64_t)1 << 30;
-    if (vec)
-        hipLaunchKernelGGL(im2col_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, stream, in, col, g);
+    const bool narrow = g.spatial + 4 <= INT32_MAX && IC * KH * KW <= INT32_MAX;
+    if (narrow && vec)
+        hipLaunchKernelGGL((im2col_kernel<4, int>), dim3((unsigned)blocks), dim3(256), 0, stream, in, col, g);
+    else if (narrow)
+        hipLaunchKernelGGL((im2col_kernel<1, int>), dim3((unsigned)blocks), dim3(256), 0, stream, in, col, g);
+    else if (vec)
+        hipLaunchKernelGGL((im2col_kernel<4, int64_t>), dim3((unsigned)blocks), dim3(256), 0, stream, in, col, g);
     else
-        hipLaunchKernelGGL(im2col_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, in, col, g);
+        hipLaunchKernelGGL((im2col_kernel<1, int64_t>), dim3((unsigned)blocks), dim3(256), 0, stream, in, col, g);
     return hip_error(hipGetLastError(), "im2col_kernel launch");
 }
 

@@ -2,11 +2,16 @@
 //
 // The reference instantiates its conv launchers for double too
 // (src/kernels/conv_kernel.cu:793-798; Python Conv2d on float64 tensors,
-// python/cuDeep/tensor.py:691-723).  Its double forward is the explicit
-// route -- im2col, the scalar double GEMM (sgemm_double_kernel,
-// matmul_kernel.cu:691-743: per output one FMA chain over k ascending), then
-// the bias add of transpose_bias_kernel (conv_kernel.cu:74-93) -- so here
-// each output is that same chain computed directly from the NCHW tensors:
+// python/cuDeep/tensor.py:691-723), and its double forward routes like the
+// float one (:241-275): 3x3 stride-1 layers to Winograd F(4,3), layers whose
+// column buffer exceeds 4 MiB to the direct loop kernel (:172-215), the rest
+// to the explicit route -- im2col, the scalar double GEMM
+// (sgemm_double_kernel, matmul_kernel.cu:691-743: per output one FMA chain
+// over k ascending), then the bias add of transpose_bias_kernel
+// (conv_kernel.cu:74-93).  This build runs one direct fp64 chain for all
+// three routes: each output is the explicit route's chain computed straight
+// from the NCHW tensors (in fp64 the routes differ only in rounding far
+// below any test's resolution):
 //   out[b, oc, oh, ow] = (sum over k = (ic*KH + kh)*KW + kw, ascending, of
 //                         w[oc, k] * x[b, ic, oh*SH - PH + kh, ow*SW - PW + kw]) + bias[oc]
 // with zero padding, one fused multiply-add per term.  Backward data and

@@ -183,7 +183,7 @@ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t M, in
         for (; s < splits; ++s) v += P[(int64_t)s * MN + i];
         if (bias_mode == CDX_BIAS_COL) v += bias[n];
         else if (bias_mode == CDX_BIAS_ROW) v += bias[m];
-        v = apply_act(v, act, 0.0);   // GEMM epilogues: no slope
+        v = cdx::apply_act(v, act);   // the GEMM kernels' float epilogue (same rounding)
         const int64_t col = n_split > 0 ? (n / n_split) * ldc_split + n % n_split : n;
         C[m * ldc + col] = v;
     }

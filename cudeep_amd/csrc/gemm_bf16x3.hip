@@ -299,6 +299,111 @@ struct HalfLoader {
     }
 };
 
+// Special operand values in the split kernels.  The reference's TF32 MMA
+// takes raw fp32 bits (matmul_kernel.cu:186-201), so an infinite operand
+// gives IEEE results: +-Inf, or NaN for Inf * 0 and Inf - Inf.  The split
+// cannot: for x = +-Inf, lo = bf16(x - hi) = bf16(Inf - Inf) = NaN; for a
+// finite x at or beyond bf16's rounding limit (|x| >= 0x7F7F8000), hi
+// rounds to +-Inf and lo = x - hi = -+Inf, so lo*hi(b) and hi*hi(b) are
+// infinities of opposite sign (or lo*0 = NaN).  Either way EVERY output the
+// element touches -- its whole row of C (A) or column (B) -- comes out NaN,
+// and no output untouched by such an element does (a NaN operand gives NaN
+// in both arithmetics; finite sums that overflow stay +-Inf).  So the
+// outputs to repair are exactly the NaN accumulators: after the main loop,
+// each wave tests its 16 x 16 accumulator blocks (one compare per value and
+// one ballot per block, no cost in the k-loop) and recomputes the blocks
+// holding a NaN with FP32 MFMAs straight from global memory (IEEE products,
+// as the reference's), replacing only the NaN values.  Runs in the same
+// k-range as the accumulators (a split-K slice recomputes its own slice).
+// In code: nan_bits() (before the epilogue) records which accumulator values
+// are NaN, one bit per value; the epilogue writes as usual; then, only when
+// some bit is set, repair_nan_outputs() walks the wave's 16 x 16 blocks (a
+// loop, not unrolled: nothing of it is live during the main loop), recomputes
+// each block holding a NaN with FP32 MFMAs straight from global memory and
+// rewrites just the NaN positions through the same epilogue.  The operands
+// are addressed relative to the workgroup tile: A0 = &op(A)(bm, 0),
+// B0 = &op(B)(0, bn).
+template <int FM, int FN>
+struct NanBits {
+    static constexpr int NW = (FM * FN + 7) / 8;   // 4 bits (values) per block
+    uint32_t w[NW];
+};
+
+template <int FM, int FN>
+__device__ __forceinline__ bool any_nan(const floatx4 (&acc)[FM][FN]) {
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nan |= acc[i][j][e] != acc[i][j][e];
+    return __builtin_amdgcn_ballot_w64(nan) != 0;     // wave-uniform
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void nan_bits(const floatx4 (&acc)[FM][FN], NanBits<FM, FN>& nb) {
+#pragma unroll
+    for (int w = 0; w < NanBits<FM, FN>::NW; ++w) nb.w[w] = 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int bit = (i * FN + j) * 4 + e;
+                if (acc[i][j][e] != acc[i][j][e]) nb.w[bit >> 5] |= 1u << (bit & 31);
+            }
+}
+
+// One output element through the epilogue: the same operations, in the same
+// order, as write_acc_act (acc + column bias + row bias, activation, output
+// map).
+__device__ __forceinline__ void store_one(const EpiArgs& e, int64_t m, int64_t n, float v) {
+    const float bcol = e.bias_mode == CDX_BIAS_COL ? e.bias[n] : 0.0f;
+    const float brow = e.bias_mode == CDX_BIAS_ROW ? e.bias[m] : 0.0f;
+    const int64_t col = e.n_split > 0 ? (n / e.n_split) * e.ldc_split + n % e.n_split : n;
+    e.C[m * e.ldc + col] = apply_act(v + bcol + brow, e.epilogue);
+}
+
+template <int FM, int FN, int OPA, int OPB>
+__device__ __forceinline__ void repair_nan_outputs(const NanBits<FM, FN>& nb, const EpiArgs& e,
+                                                   const float* A0, int64_t lda,
+                                                   const float* B0, int64_t ldb, int64_t K,
+                                                   int64_t bm, int64_t bn, int wm0, int wn0,
+                                                   int lane) {
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int64_t rows = e.M - bm, cols = e.N - bn;   // valid extent of this tile
+#pragma unroll 1
+    for (int blk = 0; blk < FM * FN; ++blk) {
+        uint32_t word = nb.w[0];
+#pragma unroll
+        for (int w = 1; w < NanBits<FM, FN>::NW; ++w)
+            if ((blk >> 3) == w) word = nb.w[w];
+        const uint32_t nib = (word >> ((blk & 7) * 4)) & 0xFu;
+        if (__builtin_amdgcn_ballot_w64(nib != 0) == 0) continue;   // wave-uniform
+        const int i = blk / FN, j = blk % FN;
+        // v_mfma_f32_16x16x4_f32: this lane feeds A(m, k0 + lq) and
+        // B(k0 + lq, n); rows, columns and k outside the problem read as 0
+        const int64_t m = wm0 + i * 16 + l16, n = wn0 + j * 16 + l16;
+        const bool mok = m < rows, nok = n < cols;
+        floatx4 r = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int64_t k0 = 0; k0 < K; k0 += 4) {
+            const int64_t k = k0 + lq;
+            const float a = (mok && k < K) ? (OPA == CDX_OP_N ? A0[m * lda + k] : A0[k * lda + m]) : 0.0f;
+            const float b = (nok && k < K) ? (OPB == CDX_OP_N ? B0[k * ldb + n] : B0[n * ldb + k]) : 0.0f;
+            r = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, r, 0, 0, 0);
+        }
+        const int64_t ncol = wn0 + j * 16 + l16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t mrow = wm0 + i * 16 + 4 * lq + q;
+            if (((nib >> q) & 1u) && mrow < rows && ncol < cols)
+                store_one(e, bm + mrow, bn + ncol, r[q]);
+        }
+    }
+}
+
 // ALIGNED_ONLY: the configuration is only instantiated without bounds
 // checks (its checked variant would not fit the register file); the
 // dispatcher sends it aligned problems only.
@@ -565,10 +670,22 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     }
 
     // epilogue: bias, activation and the output map, straight from the
-    // accumulators
+    // accumulators; then IEEE values for the outputs an infinite or out-of-
+    // range operand touched (split operands only)
     const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
                       p.bias, p.bias_mode, p.epilogue};
+    NanBits<FM, FN> nb;
+    const bool repair = !H16 && any_nan(acc);
+    if (repair) nan_bits(acc, nb);
     write_acc<FM, FN, CHECK, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
+    if constexpr (!H16) {
+        if (repair) {
+            const float* A0 = static_cast<const float*>(p.A) + (OPA == CDX_OP_N ? bm * p.lda : bm);
+            const float* B0 = static_cast<const float*>(p.B) + (OPB == CDX_OP_N ? bn : bn * p.ldb);
+            repair_nan_outputs<FM, FN, OPA, OPB>(nb, epi, A0, p.lda, B0, p.ldb, p.K, bm, bn,
+                                                 wm0, wn0, lane);
+        }
+    }
 }
 
 // 256 x 256 tiles on a two-group ("ping-pong") schedule.  The eight waves
@@ -777,7 +894,19 @@ void gemm_pingpong_kernel(KParams p) {
 
     const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
                       p.bias, p.bias_mode, p.epilogue};
+    NanBits<8, 4> nb;
+    const bool repair = !H16 && any_nan(acc);
+    if (repair) nan_bits(acc, nb);
     write_acc<8, 4, false, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
+    if constexpr (!H16) {
+        // operands through the loop's own live values: the tile bases and
+        // the byte strides (no other kernel argument is kept across the loop)
+        if (repair)
+            repair_nan_outputs<8, 4, OPA, OPB>(nb, epi, reinterpret_cast<const float*>(baseA),
+                                               (int64_t)(lda_b / 4),
+                                               reinterpret_cast<const float*>(baseB),
+                                               (int64_t)(ldb_b / 4), nk * BK, bm, bn, wm0, wn0, lane);
+    }
 }
 
 template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN = kInF32>

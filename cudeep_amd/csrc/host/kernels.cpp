@@ -1,8 +1,9 @@
 // cudeep::kernels launchers (the reference's C++ operator API,
 // include/cudeep/kernels/*.cuh) implemented over the C-ABI of
 // libcudeep_amd.so.  Each template is explicitly instantiated for float and
-// double, as the reference does; combinations outside this build (activations
-// other than ReLU / GELU / SiLU / Sigmoid) throw.
+// double, as the reference does.  GEMM epilogues are ReLU / GELU / SiLU /
+// Sigmoid (the reference's GemmEpilogue set); the elementwise activation
+// launchers take every ActivationType.
 #include <atomic>
 #include <string>
 

@@ -1,52 +1,90 @@
 """Reverse-mode automatic differentiation for cuDeep tensors.
 
-Same contract as the reference engine (python/cuDeep/autograd.py:54-143):
-``Function.apply`` records (function, context, parents) on the result when
-any input requires grad; ``backward`` walks the graph in reverse
-topological order and accumulates parent gradients with the native add.
+Public contract of the reference engine (python/cuDeep/autograd.py:54-143):
+``Function`` subclasses define static ``forward(ctx, *args)`` and
+``backward(ctx, grad_output)``; ``Function.apply`` runs the forward and, when
+gradients are being recorded and some Tensor argument requires them, links
+the result into the graph; ``backward(root, grad_output=None)`` propagates
+gradients to every tensor that requires them.  ``backward`` returns one
+gradient (or None) per Tensor argument of ``forward``, in argument order.
+
+Design.  Each recorded result carries a ``Node`` in ``_grad_fn``: the
+Function class, its Context and the input tensors (the graph's edges).  A
+backward pass first counts, for every node reachable from the root, how
+many recorded consumers feed gradient into it, then runs nodes in
+dependency order (Kahn's algorithm): a node runs once all of its
+consumers have contributed, from a gradient buffer private to this pass.
+Leaf tensors (no node) that require gradients accumulate into ``.grad``
+across passes; a recorded result's ``.grad`` is set to the total gradient
+it received in the latest pass.
 """
 from __future__ import annotations
 
-_grad_enabled = True
+from collections import deque
+
+
+class _GradMode:
+    """Whether Function.apply records graph nodes (process-wide)."""
+
+    enabled = True
 
 
 class no_grad:
-    """Context manager that disables graph recording."""
+    """Context manager: no graph is recorded inside the block."""
 
     def __enter__(self):
-        global _grad_enabled
-        self._prev = _grad_enabled
-        _grad_enabled = False
+        self._saved = _GradMode.enabled
+        _GradMode.enabled = False
         return self
 
-    def __exit__(self, *args):
-        global _grad_enabled
-        _grad_enabled = self._prev
+    def __exit__(self, *exc):
+        _GradMode.enabled = self._saved
+        return False
 
 
 def is_grad_enabled() -> bool:
-    return _grad_enabled
+    return _GradMode.enabled
 
 
 class Context:
-    """Holds what a Function's backward needs."""
+    """Per-call scratch of a Function: ``save_for_backward`` / ``saved_tensors``
+    for what its backward needs, ``needs_input_grad`` (one flag per Tensor
+    argument, set before forward runs), and free attributes for anything
+    else the backward wants (e.g. ``ctx.pre = z``)."""
 
-    __slots__ = ("saved_data", "extra")
+    def __init__(self, needs_input_grad=()):
+        self.needs_input_grad = tuple(needs_input_grad)
+        self._saved = ()
 
-    def __init__(self):
-        self.saved_data: list = []
-        self.extra: dict = {}
-
-    def save_for_backward(self, *args):
-        self.saved_data = list(args)
+    def save_for_backward(self, *values):
+        self._saved = values
 
     @property
-    def saved_tensors(self) -> list:
-        return self.saved_data
+    def saved_tensors(self):
+        return list(self._saved)
+
+
+class Node:
+    """One recorded Function call: how to turn the gradient of its result into
+    gradients of its Tensor inputs."""
+
+    __slots__ = ("fn", "ctx", "inputs")
+
+    def __init__(self, fn, ctx, inputs):
+        self.fn = fn            # the Function subclass
+        self.ctx = ctx          # its Context from the forward
+        self.inputs = inputs    # Tensor arguments, in argument order
+
+    @property
+    def __name__(self):         # repr of a tensor names its producer
+        return self.fn.__name__
+
+    def __repr__(self):
+        return f"<Node {self.fn.__name__}>"
 
 
 class Function:
-    """Base class of differentiable operations (static forward / backward)."""
+    """Base class of differentiable operations."""
 
     @staticmethod
     def forward(ctx: Context, *args, **kwargs):
@@ -60,58 +98,87 @@ class Function:
     def apply(cls, *args, **kwargs):
         from .tensor import Tensor
 
-        ctx = Context()
-        parents = tuple(a for a in args if isinstance(a, Tensor))
-        needs_grad = _grad_enabled and any(t.requires_grad for t in parents)
+        inputs = tuple(a for a in args if isinstance(a, Tensor))
+        flags = tuple(bool(t.requires_grad) for t in inputs)
+        ctx = Context(flags)
         result = cls.forward(ctx, *args, **kwargs)
-        outs = result if isinstance(result, tuple) else (result,)
-        if needs_grad:
-            for r in outs:
-                if isinstance(r, Tensor):
-                    r.requires_grad = True
-                    r._grad_fn = cls
-                    r._ctx = ctx
-                    r._prev = parents
+        if _GradMode.enabled and any(flags):
+            node = Node(cls, ctx, inputs)
+            for out in (result if isinstance(result, tuple) else (result,)):
+                if isinstance(out, Tensor):
+                    out.requires_grad = True
+                    out._grad_fn = node
         return result
 
 
-def _toposort(root) -> list:
-    order, seen = [], set()
-    stack = [(root, False)]
-    while stack:                       # iterative: deep graphs do not recurse
-        t, done = stack.pop()
-        if done:
-            order.append(t)
-            continue
-        if id(t) in seen:
-            continue
-        seen.add(id(t))
-        stack.append((t, True))
-        for p in t._prev:
-            if id(p) not in seen:
-                stack.append((p, False))
-    return order
+def _consumer_counts(root_node) -> dict:
+    """For every node reachable from root_node: how many edges from other
+    reachable nodes point at it (its number of gradient contributions)."""
+    counts = {root_node: 0}
+    todo = [root_node]
+    while todo:
+        node = todo.pop()
+        for t in node.inputs:
+            child = t._grad_fn
+            if child is None or not t.requires_grad:
+                continue
+            if child in counts:
+                counts[child] += 1
+            else:
+                counts[child] = 1
+                todo.append(child)
+    return counts
+
+
+def _accumulate(buffers: dict, key, grad):
+    prev = buffers.get(key)
+    buffers[key] = grad if prev is None else prev._plus(grad)
 
 
 def backward(root, grad_output=None):
-    """Reverse-mode AD from ``root`` (scalar, or with ``grad_output``)."""
-    from .tensor import Tensor, ones_like
+    """Propagate d(root) back through the recorded graph.  ``grad_output``
+    defaults to ones for a single-element root and is required otherwise."""
+    from .tensor import ones_like
 
     if grad_output is None:
-        if root._data.numel() != 1:
-            raise RuntimeError("backward() requires grad_output for non-scalar tensors")
+        if root.numel() != 1:
+            raise RuntimeError("backward(): grad_output is required for a tensor with "
+                               f"{root.numel()} elements")
         grad_output = ones_like(root)
     root.grad = grad_output
-    for t in reversed(_toposort(root)):
-        if t._grad_fn is None or t.grad is None:
-            continue
-        grads = t._grad_fn.backward(t._ctx, t.grad)
-        if not isinstance(grads, tuple):
-            grads = (grads,)
-        for parent, g in zip(t._prev, grads):
-            if g is None or not parent.requires_grad:
+    start = root._grad_fn
+    if start is None:
+        return
+    pending = _consumer_counts(start)
+    grads = {start: grad_output}       # gradient buffer per node, this pass only
+    outputs = {start: root}            # node -> a tensor it produced (for .grad)
+    ready = deque([start])
+    while ready:
+        node = ready.popleft()
+        g = grads.pop(node, None)
+        out = outputs.pop(node, None)
+        if g is None:
+            # every consumer passed None: nothing flows on, but the inputs'
+            # pending counts are still released
+            in_grads = ()
+        else:
+            if out is not None and out is not root:
+                out.grad = g
+            in_grads = node.fn.backward(node.ctx, g)
+            if not isinstance(in_grads, tuple):
+                in_grads = (in_grads,)
+        for i, t in enumerate(node.inputs):
+            if not t.requires_grad:
                 continue
-            if parent.grad is None:
-                parent.grad = g
-            else:
-                parent.grad = Tensor._wrap(parent.grad._data + g._data)
+            gi = in_grads[i] if i < len(in_grads) else None
+            child = t._grad_fn
+            if child is None:          # leaf: accumulates across passes
+                if gi is not None:
+                    t.grad = gi if t.grad is None else t.grad._plus(gi)
+                continue
+            if gi is not None:
+                _accumulate(grads, child, gi)
+                outputs.setdefault(child, t)
+            pending[child] -= 1
+            if pending[child] == 0:
+                ready.append(child)

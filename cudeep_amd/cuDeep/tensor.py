@@ -1,18 +1,23 @@
 """Autograd-aware Tensor over the native ``_cudeep_core.Tensor``.
 
-Public surface of the reference's python/cuDeep/tensor.py for the
-dense-contraction path: construction from numpy / lists / raw tensors,
-factories, shape queries, reshape / transpose, +, -, *, matmul (@), sum,
-relu / gelu, broadcast_add, conv2d, backward.  Differences in how the work
-is done (same results, fewer passes):
+The public surface of the reference's python/cuDeep/tensor.py:57-319 for the
+dense-contraction path -- construction from NumPy arrays, lists, scalars or
+raw tensors; the zeros / ones / randn / from_numpy / full factories; shape
+queries; reshape / transpose / t; +, -, * (tensors or scalars), @ / matmul;
+sum; relu / gelu; broadcast_add; conv2d; linear; backward -- over a design
+of this build:
 
-* ``MatMulOp.backward`` computes dA = dY B^T and dB = A^T dY with
-  transposed-operand GEMMs instead of materialising transposes
-  (reference tensor.py:430-443 copies both).
-* ``linear`` runs x W^T + b (and a ReLU / GELU epilogue) as one fused GEMM
-  launch; its backward uses the NN / TN GEMMs and the GPU column sum.
-* ``Conv2dOp.backward`` computes the bias gradient on the GPU (reference
-  tensor.py:718-721 copies grad_output to the host and sums in NumPy).
+* a Tensor is a thin handle: the native tensor (``_data``), ``grad``,
+  ``requires_grad`` and the graph node that produced it (``_grad_fn``, see
+  autograd.py);
+* operator overloads go through one table (``_BINARY``) and one scalar
+  promotion rule;
+* the differentiable operations work without materialised transposes:
+  ``MatMulOp.backward`` computes dA = dY B^T and dB = A^T dY with transposed-
+  operand GEMMs (reference tensor.py:430-443 copies both), ``linear`` runs
+  x W^T + b with its activation as one fused GEMM, and ``Conv2dOp.backward``
+  computes the bias gradient on the GPU (reference tensor.py:718-721 sums on
+  the host in NumPy).
 """
 from __future__ import annotations
 
@@ -36,45 +41,55 @@ from ._core import (
     sum as _sum,
     sum_reduce_rows as _sum_reduce_rows,
 )
-from .autograd import Function, backward as _backward
+from .autograd import Function, backward as _run_backward
+
+
+def _np_dtype(dtype) -> type:
+    return np.float64 if dtype == DType.float64 else np.float32
+
+
+def _to_raw(data, dtype) -> _RawTensor:
+    """Native tensor holding `data` (a native tensor is taken as is; NumPy
+    data is uploaded as float32 unless it is float64 or dtype asks)."""
+    if isinstance(data, _RawTensor):
+        return data
+    if isinstance(data, Tensor):
+        return data._data
+    if isinstance(data, np.ndarray):
+        if dtype is not None:
+            want = _np_dtype(dtype)
+        else:
+            want = data.dtype.type if data.dtype in (np.float32, np.float64) else np.float32
+        return _RawTensor.from_numpy(np.ascontiguousarray(data, dtype=want))
+    if isinstance(data, (list, tuple, int, float, np.floating, np.integer)):
+        return _RawTensor.from_numpy(np.asarray(data, dtype=_np_dtype(dtype)))
+    raise TypeError(f"Tensor(): unsupported data of type {type(data).__name__}")
 
 
 class Tensor:
-    """GPU tensor with reverse-mode autograd (reference tensor.py:57-307)."""
+    """GPU tensor with reverse-mode autograd."""
 
-    __slots__ = ("_data", "grad", "requires_grad", "_grad_fn", "_ctx", "_prev")
+    __slots__ = ("_data", "grad", "requires_grad", "_grad_fn")
 
     def __init__(self, data, requires_grad=False, dtype=None):
-        if isinstance(data, _RawTensor):
-            self._data = data
-        elif isinstance(data, np.ndarray):
-            arr = np.ascontiguousarray(data)
-            if dtype is not None:
-                arr = arr.astype(np.float64 if dtype == DType.float64 else np.float32, copy=False)
-            elif arr.dtype not in (np.float32, np.float64):
-                arr = arr.astype(np.float32)
-            self._data = _RawTensor.from_numpy(arr)
-        elif isinstance(data, (list, tuple, int, float)):
-            np_dt = np.float64 if dtype == DType.float64 else np.float32
-            self._data = _RawTensor.from_numpy(np.array(data, dtype=np_dt))
-        else:
-            raise TypeError(f"Cannot create Tensor from {type(data)}")
+        self._data = _to_raw(data, dtype)
         self.grad: Optional[Tensor] = None
-        self.requires_grad = requires_grad
+        self.requires_grad = bool(requires_grad)
         self._grad_fn = None
-        self._ctx = None
-        self._prev: tuple = ()
 
     @classmethod
-    def _wrap(cls, raw: _RawTensor, requires_grad=False) -> "Tensor":
-        t = object.__new__(cls)
+    def _wrap(cls, raw, requires_grad=False) -> "Tensor":
+        """A handle on an existing native tensor (no copy, no conversion)."""
+        t = cls.__new__(cls)
         t._data = raw
         t.grad = None
         t.requires_grad = requires_grad
         t._grad_fn = None
-        t._ctx = None
-        t._prev = ()
         return t
+
+    def _plus(self, other: "Tensor") -> "Tensor":
+        """Unrecorded sum (gradient accumulation)."""
+        return Tensor._wrap(self._data + other._data)
 
     # ---- factories ----
     @staticmethod
@@ -91,18 +106,15 @@ class Tensor:
 
     @staticmethod
     def from_numpy(arr, requires_grad=False) -> "Tensor":
-        arr = np.ascontiguousarray(arr)
-        if arr.dtype not in (np.float32, np.float64):
-            arr = arr.astype(np.float32)
-        return Tensor._wrap(_RawTensor.from_numpy(arr), requires_grad)
+        return Tensor._wrap(_to_raw(np.asarray(arr), None), requires_grad)
 
     @staticmethod
     def full(shape, value, dtype=DType.float32, requires_grad=False) -> "Tensor":
-        t = Tensor._wrap(_RawTensor(list(shape), dtype), requires_grad)
-        t._data.fill_(float(value))
-        return t
+        raw = _RawTensor(list(shape), dtype)
+        raw.fill_(float(value))
+        return Tensor._wrap(raw, requires_grad)
 
-    # ---- properties ----
+    # ---- queries (forwarded to the native tensor) ----
     def shape(self):
         return self._data.shape()
 
@@ -122,22 +134,22 @@ class Tensor:
         return self._data.numpy()
 
     def item(self):
-        if self._data.numel() != 1:
-            raise ValueError("item() only for single-element tensors")
-        return self._data.numpy().item()
+        values = self._data.numpy().reshape(-1)
+        if values.size != 1:
+            raise ValueError(f"item(): tensor has {values.size} elements, not one")
+        return values[0].item()
 
     def detach(self) -> "Tensor":
-        return Tensor._wrap(self._data, requires_grad=False)
+        return Tensor._wrap(self._data)
 
     def contiguous(self) -> "Tensor":
-        if self._data.is_contiguous():
-            return self
-        return Tensor._wrap(self._data.contiguous(), self.requires_grad)
+        return self if self.is_contiguous() else Tensor._wrap(self._data.contiguous(),
+                                                               self.requires_grad)
 
     def clone(self) -> "Tensor":
         return Tensor._wrap(self._data.clone(), self.requires_grad)
 
-    # ---- in-place (no autograd) ----
+    # ---- in place, unrecorded ----
     def fill_(self, value):
         self._data.fill_(float(value))
         return self
@@ -146,55 +158,61 @@ class Tensor:
         self._data.zero_()
         return self
 
-    # ---- reshape / transpose ----
+    # ---- views ----
     def reshape(self, *shape):
-        if len(shape) == 1 and isinstance(shape[0], (list, tuple)):
-            shape = list(shape[0])
-        return ReshapeOp.apply(self, list(shape))
+        dims = list(shape[0]) if len(shape) == 1 and isinstance(shape[0], (list, tuple)) \
+            else list(shape)
+        return ReshapeOp.apply(self, dims)
 
     def transpose(self, dim0, dim1):
         return TransposeOp.apply(self, dim0, dim1)
 
     def t(self):
-        return self.transpose(0, 1)
+        return TransposeOp.apply(self, 0, 1)
 
-    # ---- arithmetic ----
+    # ---- arithmetic: tensors or Python scalars (promoted to a filled tensor) ----
+    def _operand(self, other) -> "Tensor":
+        if isinstance(other, Tensor):
+            return other
+        if isinstance(other, (int, float, np.floating, np.integer)):
+            return Tensor.full(self.shape(), other, self.dtype())
+        return NotImplemented
+
+    def _binary(self, op: str, other, swap: bool = False):
+        rhs = self._operand(other)
+        if rhs is NotImplemented:
+            return NotImplemented
+        lhs, rhs = (rhs, self) if swap else (self, rhs)
+        return _BINARY[op].apply(lhs, rhs)
+
     def __add__(self, other):
-        if isinstance(other, (int, float)):
-            other = Tensor.full(self.shape(), other, self.dtype())
-        return AddOp.apply(self, other)
+        return self._binary("+", other)
 
     def __radd__(self, other):
-        return self.__add__(other)
+        return self._binary("+", other, swap=True)
 
     def __sub__(self, other):
-        if isinstance(other, (int, float)):
-            other = Tensor.full(self.shape(), other, self.dtype())
-        return SubOp.apply(self, other)
+        return self._binary("-", other)
 
     def __rsub__(self, other):
-        if isinstance(other, (int, float)):
-            other = Tensor.full(self.shape(), other, self.dtype())
-        return SubOp.apply(other, self)
+        return self._binary("-", other, swap=True)
 
     def __mul__(self, other):
-        if isinstance(other, (int, float)):
-            other = Tensor.full(self.shape(), other, self.dtype())
-        return MulOp.apply(self, other)
+        return self._binary("*", other)
 
     def __rmul__(self, other):
-        return self.__mul__(other)
+        return self._binary("*", other, swap=True)
 
     def __neg__(self):
-        return self * -1.0
+        return self._binary("*", -1.0)
 
-    # ---- matmul / reductions / activations ----
     def matmul(self, other):
         return MatMulOp.apply(self, other)
 
     def __matmul__(self, other):
-        return self.matmul(other)
+        return MatMulOp.apply(self, other)
 
+    # ---- reductions / activations ----
     def sum(self):
         return SumOp.apply(self)
 
@@ -204,26 +222,30 @@ class Tensor:
     def gelu(self):
         return GELUOp.apply(self)
 
-    # ---- backward ----
+    # ---- autograd ----
     def backward(self, grad_output=None):
-        _backward(self, grad_output)
+        _run_backward(self, grad_output)
 
     def __repr__(self):
-        n = self.numel()
-        body = repr(self.numpy()) if n <= 10 else f"shape={self.shape()}"
-        s = f"Tensor({body}, dtype={self.dtype()}"
-        if self.requires_grad:
-            s += ", requires_grad=True"
-            if self._grad_fn is not None:
-                s += f", grad_fn={self._grad_fn.__name__}"
-        return s + ")"
+        fields = [f"shape={self.shape()}", f"dtype={self.dtype()}"]
+        if self.numel() <= 10:
+            fields.insert(0, np.array2string(self.numpy(), separator=", "))
+        if self._grad_fn is not None:
+            fields.append(f"grad_fn={self._grad_fn.__name__}")
+        elif self.requires_grad:
+            fields.append("requires_grad=True")
+        return f"Tensor({', '.join(fields)})"
 
     def __len__(self):
-        return self.shape()[0]
+        dims = self.shape()
+        if not dims:
+            raise TypeError("len() of a 0-d tensor")
+        return dims[0]
 
     def __bool__(self):
         if self.numel() != 1:
-            raise RuntimeError("bool() on multi-element tensor is ambiguous")
+            raise RuntimeError(f"the truth value of a tensor with {self.numel()} elements "
+                               "is ambiguous")
         return bool(self.item())
 
 
@@ -240,7 +262,7 @@ def randn_like(t: Tensor) -> Tensor:
 
 
 # ---------------------------------------------------------------------------
-# differentiable operations
+# differentiable operations (backward: one gradient per Tensor argument)
 # ---------------------------------------------------------------------------
 
 class AddOp(Function):
@@ -260,7 +282,10 @@ class SubOp(Function):
 
     @staticmethod
     def backward(ctx, g):
-        return g, Tensor._wrap(g._data * Tensor.full(g.shape(), -1.0, g.dtype())._data)
+        need_a, need_b = ctx.needs_input_grad
+        neg = Tensor._wrap(g._data * Tensor.full(g.shape(), -1.0, g.dtype())._data) \
+            if need_b else None
+        return g, neg
 
 
 class MulOp(Function):
@@ -272,19 +297,23 @@ class MulOp(Function):
     @staticmethod
     def backward(ctx, g):
         a, b = ctx.saved_tensors
-        return Tensor._wrap(g._data * b._data), Tensor._wrap(g._data * a._data)
+        need_a, need_b = ctx.needs_input_grad
+        return (Tensor._wrap(g._data * b._data) if need_a else None,
+                Tensor._wrap(g._data * a._data) if need_b else None)
+
+
+_BINARY = {"+": AddOp, "-": SubOp, "*": MulOp}
 
 
 class ReshapeOp(Function):
     @staticmethod
     def forward(ctx, a, shape):
-        ctx.save_for_backward(list(a.shape()))
+        ctx.in_shape = list(a.shape())
         return Tensor._wrap(a._data.reshape(shape))
 
     @staticmethod
     def backward(ctx, g):
-        (shape,) = ctx.saved_tensors
-        return (Tensor._wrap(g._data.reshape(shape)),)
+        return Tensor._wrap(g._data.reshape(ctx.in_shape))
 
 
 class TransposeOp(Function):
@@ -292,13 +321,12 @@ class TransposeOp(Function):
 
     @staticmethod
     def forward(ctx, a, dim0, dim1):
-        ctx.save_for_backward(dim0, dim1)
+        ctx.dims = (dim0, dim1)
         return Tensor._wrap(a._data.transpose(dim0, dim1))
 
     @staticmethod
     def backward(ctx, g):
-        dim0, dim1 = ctx.saved_tensors
-        return (Tensor._wrap(g._data.transpose(dim0, dim1)),)
+        return Tensor._wrap(g._data.transpose(*ctx.dims))
 
 
 class MatMulOp(Function):
@@ -314,44 +342,48 @@ class MatMulOp(Function):
     @staticmethod
     def backward(ctx, g):
         a, b = ctx.saved_tensors
-        ga = gb = None
-        if a.requires_grad:
-            ga = Tensor._wrap(g._data.matmul(b._data.transpose(0, 1)))    # dY B^T
-        if b.requires_grad:
-            gb = Tensor._wrap(a._data.transpose(0, 1).matmul(g._data))    # A^T dY
+        need_a, need_b = ctx.needs_input_grad
+        ga = Tensor._wrap(g._data.matmul(b._data.transpose(0, 1))) if need_a else None  # dY B^T
+        gb = Tensor._wrap(a._data.transpose(0, 1).matmul(g._data)) if need_b else None  # A^T dY
         return ga, gb
 
 
 class SumOp(Function):
     @staticmethod
     def forward(ctx, a):
-        ctx.save_for_backward(a)
+        ctx.in_shape, ctx.in_dtype = a.shape(), a.dtype()
         return Tensor._wrap(_sum(a._data))
 
     @staticmethod
     def backward(ctx, g):
+        return Tensor.full(ctx.in_shape, g.item(), ctx.in_dtype)
+
+
+class _ActivationOp(Function):
+    """y = act(x) elementwise; backward from the saved input."""
+
+    NAME = ""
+    FORWARD = None
+
+    @classmethod
+    def forward(cls, ctx, a):
+        ctx.save_for_backward(a)
+        return Tensor._wrap(cls.FORWARD(a._data))
+
+    @classmethod
+    def backward(cls, ctx, g):
         (a,) = ctx.saved_tensors
-        return (Tensor.full(a.shape(), g.item(), a.dtype()),)
+        return Tensor._wrap(_activation_backward(g._data, a._data, cls.NAME))
 
 
-def _make_activation_op(name, fwd):
-    class _Op(Function):
-        @staticmethod
-        def forward(ctx, a):
-            ctx.save_for_backward(a)
-            return Tensor._wrap(fwd(a._data))
-
-        @staticmethod
-        def backward(ctx, g):
-            (a,) = ctx.saved_tensors
-            return (Tensor._wrap(_activation_backward(g._data, a._data, name)),)
-
-    _Op.__name__ = f"{name.upper() if name == 'gelu' else name.title()}Op"
-    return _Op
+class ReLUOp(_ActivationOp):
+    NAME = "relu"
+    FORWARD = staticmethod(_relu)
 
 
-ReLUOp = _make_activation_op("relu", _relu)
-GELUOp = _make_activation_op("gelu", _gelu)
+class GELUOp(_ActivationOp):
+    NAME = "gelu"
+    FORWARD = staticmethod(_gelu)
 
 
 class BroadcastAddOp(Function):
@@ -359,14 +391,13 @@ class BroadcastAddOp(Function):
 
     @staticmethod
     def forward(ctx, matrix, row):
-        ctx.save_for_backward(matrix, row)
         return Tensor._wrap(_broadcast_add(matrix._data, row._data))
 
     @staticmethod
     def backward(ctx, g):
-        matrix, row = ctx.saved_tensors
-        g_row = Tensor._wrap(_sum_reduce_rows(g._data)) if row.requires_grad else None
-        return (g if matrix.requires_grad else None), g_row
+        need_m, need_r = ctx.needs_input_grad
+        return (g if need_m else None,
+                Tensor._wrap(_sum_reduce_rows(g._data)) if need_r else None)
 
 
 class LinearOp(Function):
@@ -374,74 +405,71 @@ class LinearOp(Function):
     epilogue).  Backward: dZ = act'(...) dY, dX = dZ W (NN GEMM),
     dW = dZ^T x (TN GEMM), db = column sums of dZ.  For ReLU the mask is
     taken from y (y > 0 exactly where x W^T + b > 0); GELU keeps the
-    pre-activation, so it is fused only when no gradient is recorded."""
+    pre-activation, so its activation is a separate launch when recorded."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, activation):
-        keep_pre = activation == "gelu"
         raw_b = bias._data if bias is not None else None
-        if keep_pre:
-            z = _linear_forward(x._data, weight._data, raw_b, "none")
-            y = _gelu(z)
-            ctx.extra["pre"] = z
+        ctx.activation = activation
+        if activation == "gelu":
+            ctx.pre = _linear_forward(x._data, weight._data, raw_b, "none")
+            y = _gelu(ctx.pre)
         else:
             y = _linear_forward(x._data, weight._data, raw_b, activation)
-            ctx.extra["out"] = y
-        ctx.save_for_backward(x, weight, bias, activation)
+            ctx.out = y
+        ctx.save_for_backward(x, weight)
         return Tensor._wrap(y)
 
     @staticmethod
     def backward(ctx, g):
-        x, weight, bias, activation = ctx.saved_tensors
+        x, weight = ctx.saved_tensors
+        flags = ctx.needs_input_grad
+        need_x, need_w = flags[0], flags[1]
+        need_b = len(flags) > 2 and flags[2]
         dz = g._data
-        if activation == "relu":
-            dz = _activation_backward(dz, ctx.extra["out"], "relu")
-        elif activation == "gelu":
-            dz = _activation_backward(dz, ctx.extra["pre"], "gelu")
-        gx = gw = gb = None
-        if x.requires_grad:
-            gx = Tensor._wrap(_matmul_ex(dz, weight._data, False, False))
-        if weight.requires_grad:
-            gw = Tensor._wrap(_matmul_ex(dz, x._data, True, False))
-        if bias is not None and bias.requires_grad:
-            gb = Tensor._wrap(_sum_reduce_rows(dz))
-        return gx, gw, gb
+        if ctx.activation == "relu":
+            dz = _activation_backward(dz, ctx.out, "relu")
+        elif ctx.activation == "gelu":
+            dz = _activation_backward(dz, ctx.pre, "gelu")
+        return (Tensor._wrap(_matmul_ex(dz, weight._data, False, False)) if need_x else None,
+                Tensor._wrap(_matmul_ex(dz, x._data, True, False)) if need_w else None,
+                Tensor._wrap(_sum_reduce_rows(dz)) if need_b else None)
 
 
 class Conv2dOp(Function):
-    """NCHW conv (reference tensor.py:691-723): im2col + one GEMM forward
-    with the bias in the epilogue; backward data / weight / bias on the GPU."""
+    """NCHW conv (reference tensor.py:691-723): forward with the bias in the
+    GEMM epilogue; backward data / weight / bias on the GPU."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, stride, padding):
         raw_b = bias._data if bias is not None else None
-        out = _conv2d_forward(input._data, weight._data, raw_b, list(stride), list(padding))
-        ctx.save_for_backward(input, weight, bias, tuple(stride), tuple(padding))
-        return Tensor._wrap(out)
+        ctx.geom = (list(stride), list(padding))
+        ctx.save_for_backward(input, weight)
+        return Tensor._wrap(_conv2d_forward(input._data, weight._data, raw_b, list(stride),
+                                            list(padding)))
 
     @staticmethod
     def backward(ctx, g):
-        input, weight, bias, stride, padding = ctx.saved_tensors
-        gi = gw = gb = None
-        if input.requires_grad:
-            gi = Tensor._wrap(_conv2d_backward_data(g._data, weight._data, list(input.shape()),
-                                                    list(stride), list(padding)))
-        if weight.requires_grad:
-            gw = Tensor._wrap(_conv2d_backward_weight(g._data, input._data, list(weight.shape()),
-                                                      list(stride), list(padding)))
-        if bias is not None and bias.requires_grad:
-            gb = Tensor._wrap(_conv2d_backward_bias(g._data))
-        return gi, gw, gb
+        x, w = ctx.saved_tensors
+        stride, padding = ctx.geom
+        flags = ctx.needs_input_grad
+        need_b = len(flags) > 2 and flags[2]
+        gx = Tensor._wrap(_conv2d_backward_data(g._data, w._data, list(x.shape()), stride,
+                                                padding)) if flags[0] else None
+        gw = Tensor._wrap(_conv2d_backward_weight(g._data, x._data, list(w.shape()), stride,
+                                                  padding)) if flags[1] else None
+        gb = Tensor._wrap(_conv2d_backward_bias(g._data)) if need_b else None
+        return gx, gw, gb
 
 
 # ---- functional API (reference tensor.py:727-740) ----
 
 def relu(x):
-    return x.relu()
+    return ReLUOp.apply(x)
 
 
 def gelu(x):
-    return x.gelu()
+    return GELUOp.apply(x)
 
 
 def broadcast_add(matrix, row):
@@ -453,9 +481,9 @@ def linear(x, weight, bias=None, activation="none"):
     return LinearOp.apply(x, weight, bias, activation)
 
 
+def _pair(v):
+    return (v, v) if isinstance(v, int) else tuple(v)
+
+
 def conv2d(input, weight, bias=None, stride=(1, 1), padding=(0, 0)):
-    if isinstance(stride, int):
-        stride = (stride, stride)
-    if isinstance(padding, int):
-        padding = (padding, padding)
-    return Conv2dOp.apply(input, weight, bias, tuple(stride), tuple(padding))
+    return Conv2dOp.apply(input, weight, bias, _pair(stride), _pair(padding))

@@ -407,7 +407,9 @@ def conv2d_backward_data_winograd_workspace_bytes(x_shape, out_channels, padding
 
 
 def conv2d_backward_weight(grad_out, x, w_shape, stride=(1, 1), padding=(0, 0),
-                           precision=L.PREC_FP32, out=None):
+                           precision=L.PREC_FP32, out=None, workspace=None):
+    """`workspace` (at least conv2d_backward_weight_workspace_bytes(...) bytes)
+    makes the call allocation-free."""
     _need(grad_out, "grad_output")
     _need(x, "input")
     Bn, C, H, W, OC, KH, KW, OH, OW = _conv_geom(tuple(x.shape), tuple(w_shape), stride, padding)
@@ -416,10 +418,20 @@ def conv2d_backward_weight(grad_out, x, w_shape, stride=(1, 1), padding=(0, 0),
         raise ValueError("conv2d_backward_weight: bad grad_output / input")
     if out is None:
         out = torch.empty(tuple(w_shape), device=x.device, dtype=torch.float32)
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     L.call("cdx_conv2d_backward_weight_f32", grad_out.data_ptr(), x.data_ptr(), out.data_ptr(),
            Bn, C, OC, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1], precision,
-           None, 0, _stream())
+           ws_ptr, ws_bytes, _stream())
     return out
+
+
+def conv2d_backward_weight_workspace_bytes(x_shape, w_shape, stride=(1, 1),
+                                           padding=(0, 0)) -> int:
+    Bn, C, H, W, OC, KH, KW, _, _ = _conv_geom(tuple(x_shape), tuple(w_shape), stride, padding)
+    return int(L.lib().cdx_conv2d_backward_weight_workspace_size(
+        Bn, C, OC, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1]))
 
 
 def conv2d_backward_bias(grad_out, out=None):

@@ -1,6 +1,6 @@
-// Activation launchers (include/cudeep/kernels/activation.cuh:8-31).  ReLU
-// and GELU (tanh form) run on the GPU in float; the other activation types
-// of the reference are outside this build and throw.
+// Activation launchers (include/cudeep/kernels/activation.cuh:8-31).  Every
+// ActivationType of the reference (ReLU, GELU in its tanh form, SiLU,
+// Sigmoid, Tanh, LeakyReLU) runs on the GPU, in float and double.
 #pragma once
 
 #include "../common.hpp"

@@ -90,10 +90,18 @@ def test_conv_argument_validation():
     # padding above kernel - 1 keeps the col2im route
     assert L.lib().cdx_conv2d_backward_data_workspace_size(1, 3, 4, 5, 5, 3, 3, 1, 1, 3, 0) \
         == 27 * 9 * 3 * 4
-    # backward weight: the larger of the GEMM route (col + reshaped grad_out)
-    # and the implicit route's split partials
-    assert L.lib().cdx_conv2d_backward_weight_workspace_size(32, 64, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
-        == (576 + 64) * 32 * 3136 * 4
+    # backward weight: exactly the route the launch takes.  C5 takes the
+    # implicit kernel: 64 k-slices of [OC, K_col] partials (no column buffer)
+    c5 = (32, 64, 64, 56, 56, 3, 3, 1, 1, 1, 1)
+    need = L.lib().cdx_conv2d_backward_weight_workspace_size(*c5)
+    assert need == 64 * 64 * 576 * 4
+    assert _status("cdx_conv2d_backward_weight_f32", fake, fake, fake, *c5, 0, fake, need - 1,
+                   None) == L.CDX_ERR_WORKSPACE
+    # beyond the implicit kernel's 32-bit range (a 2^15 x 2^15 plane): the GEMM
+    # route's column buffer, then its split-K partials (768 slices of 1 x 1)
+    assert L.lib().cdx_conv2d_backward_weight_workspace_size(1, 1, 1, 2 ** 15, 2 ** 15, 1, 1,
+                                                             1, 1, 0, 0) \
+        == 2 ** 30 * 4 + 768 * 4
     # Winograd backward data: the transposed problem (OC in, IC out, IH x IW tiles)
     assert L.lib().cdx_conv2d_backward_data_winograd_workspace_size(32, 64, 64, 56, 56, 1, 1) \
         == 36 * (64 * 64 + 2 * 64 * 32 * 14 * 14) * 4

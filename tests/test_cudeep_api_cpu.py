@@ -39,3 +39,21 @@ def test_no_cpu_fallback_without_gpu():
     from cudeep_amd import cuDeep
     with pytest.raises(RuntimeError):
         cuDeep.Tensor.zeros([2, 2])
+
+
+def test_one_hip_runtime_whatever_the_import_order():
+    """Importing this package before torch must not map a second HIP runtime
+    (torch's wheel bundles its own libamdhip64.so; two runtimes in one
+    process leave one of them without a device)."""
+    import os
+    import subprocess
+    import sys
+    pytest.importorskip("torch")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import os, cudeep_amd.cuDeep, torch\n"
+            "maps = open(f'/proc/{os.getpid()}/maps').read().splitlines()\n"
+            "print(len({l.split()[-1] for l in maps if 'libamdhip64' in l}))\n")
+    out = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True,
+                         text=True, timeout=300, env=dict(os.environ, PYTHONPATH=root))
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "1"

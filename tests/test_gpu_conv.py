@@ -144,6 +144,36 @@ def test_conv_workspace_and_no_bias():
     assert e <= 2 * e_ref + 2.0 ** -24
 
 
+@pytest.mark.parametrize("g", [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1),    # C5: rows kernel
+                               (2, 5, 13, 11, 7, 3, 2, 2, 1, 1, 0)])       # gather kernel
+def test_backward_weight_workspace_query_is_what_the_launch_takes(g):
+    """cdx_conv2d_backward_weight_workspace_size is the scratch of the route
+    the launch takes: a workspace of exactly that size is accepted, one
+    byte less is refused, and the result equals the self-allocating call's."""
+    import torch
+    import cudeep_amd._lib as L
+    Bn, C, H, W, OC, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    OH, OW = oracle.conv_out_size(H, KH, SH, PH), oracle.conv_out_size(W, KW, SW, PW)
+    dy = normal(rng, (Bn, OC, OH, OW))
+    nbytes = ops().conv2d_backward_weight_workspace_bytes(x.shape, (OC, C, KH, KW), (SH, SW),
+                                                          (PH, PW))
+    say("wgrad workspace", g, nbytes)
+    dx, ddy = dev(x), dev(dy)
+    ref = host(ops().conv2d_backward_weight(ddy, dx, (OC, C, KH, KW), (SH, SW), (PH, PW)))
+    if nbytes > 0:
+        small = torch.empty(nbytes - 1, dtype=torch.uint8, device="cuda")
+        with pytest.raises(L.CdxError) as err:
+            ops().conv2d_backward_weight(ddy, dx, (OC, C, KH, KW), (SH, SW), (PH, PW),
+                                         workspace=small)
+        assert err.value.code == L.CDX_ERR_WORKSPACE
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    got = host(ops().conv2d_backward_weight(ddy, dx, (OC, C, KH, KW), (SH, SW), (PH, PW),
+                                            workspace=ws))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 # ---------------------------------------------------------------------------
 # backward: col2im (bit-exact), data / weight / bias gradients
 # ---------------------------------------------------------------------------

@@ -147,6 +147,24 @@ def test_matmul_float64_and_transposed_views(cd):
     assert oracle.rel_fro(got3, C64) <= 2 * e_ref + 2.0 ** -24
 
 
+def test_native_entry_points_reject_unsupported_dtypes(cd):
+    """matmul_ex takes float32 or float64 operands and linear_forward a
+    float32 bias; anything else is refused on the host before a launch."""
+    from cudeep_amd.cuDeep import _core
+    say("dtype checks")
+    h = _core.Tensor([4, 4], _core.DType.float16)
+    f = _core.Tensor.zeros([4, 4], _core.DType.float32)
+    with pytest.raises(RuntimeError, match="float32 or float64"):
+        _core.matmul_ex(h, h, False, False)
+    with pytest.raises(RuntimeError, match="float32 or float64"):
+        _core.matmul_ex(f, h, False, False)
+    b64 = _core.Tensor.zeros([4], _core.DType.float64)
+    with pytest.raises(RuntimeError, match="linear_forward"):
+        _core.linear_forward(f, f, b64, "none")
+    out = _core.linear_forward(f, f, _core.Tensor.zeros([4], _core.DType.float32), "relu")
+    assert out.numpy().shape == (4, 4)
+
+
 # ---- autograd (reference tests/unit/test_autograd.py) ----------------------
 
 def test_matmul_grad_kat(cd, kats):

@@ -440,6 +440,36 @@ def test_split_k_parity(M, N, K, tA, mode):
         assert oracle.rel_fro(C, want) <= e_ref
 
 
+@pytest.mark.parametrize("epi", ["relu", "gelu", "silu", "sigmoid"])
+@pytest.mark.parametrize("bias_mode", ["col", "row"])
+@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+def test_split_k_epilogue_equals_unsplit(epi, bias_mode, mode):
+    """The split-K reduction applies bias + activation with the same float
+    operations as the GEMM kernels' own epilogue.  P = A B (split, no
+    epilogue) is pushed through an unsplit FP32 GEMM P I_N (exact: products
+    with 1 and 0, sums with 0), whose epilogue must then equal the split
+    GEMM's epilogue bit for bit."""
+    import cudeep_amd as cd
+    M, N, K = 64, 64, 8192
+    rng = np.random.default_rng(17)
+    A = normal(rng, (M, K), 0.05)
+    B = normal(rng, (K, N))
+    bias = normal(rng, (M if bias_mode == "row" else N,))
+    prec = cd.PREC_FP32 if mode == "fp32" else cd.PREC_TF32MODE
+    bm = cd.BIAS_ROW if bias_mode == "row" else cd.BIAS_COL
+    code = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU, "silu": cd.EPI_SILU,
+            "sigmoid": cd.EPI_SIGMOID}[epi]
+    assert ops().gemm_workspace_bytes(M, N, K, precision=prec) > 0     # it does split
+    assert ops().gemm_workspace_bytes(M, N, N) == 0                     # this one does not
+    say("split-K epilogue", epi, bias_mode, mode)
+    dA, dB, db = dev(A), dev(B), dev(bias)
+    fused = host(ops().gemm(dA, dB, precision=prec, bias=db, bias_mode=bm, epilogue=code))
+    P = ops().gemm(dA, dB, precision=prec)
+    eye = dev(np.eye(N, dtype=np.float32))
+    unsplit = host(ops().gemm(P, eye, bias=db, bias_mode=bm, epilogue=code))
+    assert np.array_equal(fused.view(np.uint32), unsplit.view(np.uint32))
+
+
 # ---------------------------------------------------------------------------
 # special values
 # ---------------------------------------------------------------------------
@@ -475,22 +505,88 @@ def test_fp32_special_values_follow_ieee(M, N, K):
     assert oracle.rel_fro(C[fin], C64[fin]) <= 2 * e_ref + (F32_FLOOR if K < 64 else 0.0)
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (4096, 4096, 64)])
-def test_tf32mode_special_values_stay_in_their_rows(M, N, K):
-    """TF32 modes: an infinite operand element makes the outputs it touches
-    non-finite (NaN where the reference's TF32 path gives +-Inf -- the split's
-    cross terms; documented), NaN stays NaN, and every output row without a
-    special operand is finite and inside the TF32-mode gate."""
+# beyond bf16's rounding limit (the split's hi part rounds to Inf) but well
+# inside TF32's finite range under both RZ and RNE
+HUGE = np.float32(3.4e38)
+
+
+def _tf32_special_operands(M, N, K, seed):
+    """Operands with +-Inf, NaN and beyond-bf16 finite elements in A (rows) and
+    B (columns).  The k-rows / k-columns that multiply the huge values hold
+    +-0.25 (products ~8.5e37: finite by a wide margin) and +-2 (products
+    ~6.8e38: overflow by a wide margin), so every output's class (finite,
+    +-Inf, NaN) is the same under any rounding of the operands or order of
+    the sum."""
+    rng = np.random.default_rng(seed)
+    A = normal(rng, (M, K))
+    B = normal(rng, (K, N))
+    kh, kb = 9 % K, 16 % K
+    pat_n = np.array([0.25, -0.25, 2.0, -2.0], np.float32)[np.arange(N) % 4]
+    pat_m = np.array([0.25, 2.0, -0.25, -2.0], np.float32)[np.arange(M) % 4]
+    B[kh, :] = pat_n
+    A[:, kb] = pat_m
+    A[3, 5 % K] = np.inf
+    A[7, 1] = -np.inf
+    A[11, 2] = np.nan
+    A[13, kh] = HUGE
+    A[17, kh] = -HUGE
+    B[4 % K, 6] = np.inf
+    B[8 % K, 10] = -np.inf
+    B[12 % K, 14] = np.nan
+    B[kb, 18] = HUGE
+    B[kb, 22] = -HUGE
+    return A, B
+
+
+def _classes(C):
+    return np.isnan(C), np.isinf(C), np.sign(np.where(np.isinf(C), C, 0))
+
+
+@pytest.mark.parametrize("M,N,K,tA,tB", [
+    (64, 64, 64, False, False),
+    (300, 200, 784, False, False),       # ragged tiles (bounds-checked kernel)
+    (300, 200, 784, True, True),         # both operands transposed
+    (128, 128, 4096, False, False),      # split-K slices repair their own k-range
+    (4096, 4096, 64, False, False),      # two-group 256 x 256 kernel
+    (4096, 4096, 64, True, False),
+])
+def test_tf32mode_special_values_follow_reference(M, N, K, tA, tB):
+    """TF32 modes: +-Inf, NaN and finite operands beyond bf16's range give the
+    reference TF32 kernel's results (matmul_kernel.cu:186-201 feeds raw fp32
+    bits to the MMA): the NaN / Inf pattern and the Inf signs equal those of
+    oracle.gemm_tf32emu (which agrees under RZ and RNE on these operands), and
+    outputs untouched by a special operand stay inside the TF32-mode gate."""
     import cudeep_amd as cd
-    A, B = _special_operands(M, N, K, 909 + M)
-    bad = ~np.isfinite(A).all(axis=1)
-    say("tf32 special values", M, N, K)
+    A, B = _tf32_special_operands(M, N, K, 909 + M + K)
+    rows = [(0, 64)] if M <= 64 else [(0, 64), (M - 64, M)]
+    want = {}
+    for r in rows:
+        with np.errstate(invalid="ignore", over="ignore"):
+            rz = oracle.gemm_tf32emu(A, B, "rz", rows=r)
+            rne = oracle.gemm_tf32emu(A, B, "rne", rows=r)
+        for x, y in zip(_classes(rz), _classes(rne)):
+            assert np.array_equal(x, y)          # the expectation is unambiguous
+        want[r] = rz
+    touched_rows = ~np.isfinite(A).all(axis=1) | (np.abs(A) >= HUGE).any(axis=1)
+    touched_cols = ~np.isfinite(B).all(axis=0) | (np.abs(B) >= HUGE).any(axis=0)
+    clean_cols = ~touched_cols
+    Ad = dev(np.ascontiguousarray(A.T) if tA else A)
+    Bd = dev(np.ascontiguousarray(B.T) if tB else B)
     for prec in (cd.PREC_TF32MODE, cd.PREC_TF32MODE4):
-        C = host(ops().gemm(dev(A), dev(B), precision=prec))
-        assert not np.isfinite(C[bad]).any()
-        assert np.isfinite(C[~bad]).all()
-        Ag = A[~bad]
-        C64 = oracle.dgemm(Ag, B)
-        e = oracle.rel_fro(C[~bad], C64)
-        e_ref = min(oracle.rel_fro(oracle.gemm_tf32emu(Ag, B, m), C64) for m in ("rz", "rne"))
+        say("tf32 special values", M, N, K, tA, tB, prec)
+        C = host(ops().gemm(Ad, Bd, precision=prec, transA=tA, transB=tB))
+        for r, ref in want.items():
+            got = C[r[0]:r[1]]
+            for kind, x, y in zip(("nan", "inf", "sign"), _classes(got), _classes(ref)):
+                assert np.array_equal(x, y), (prec, r, kind, np.argwhere(x != y)[:5])
+        # outputs without a special operand: finite, and inside the gate
+        clean_rows = ~touched_rows
+        assert np.isfinite(C[np.ix_(clean_rows, clean_cols)]).all()
+        r0, r1 = rows[0]
+        sel = clean_rows[r0:r1]
+        Ag = A[r0:r1][sel]
+        C64 = oracle.dgemm(Ag, B)[:, clean_cols]
+        e = oracle.rel_fro(C[r0:r1][sel][:, clean_cols], C64)
+        e_ref = min(oracle.rel_fro(oracle.gemm_tf32emu(Ag, B, m)[:, clean_cols], C64)
+                    for m in ("rz", "rne"))
         assert e <= e_ref, (prec, e, e_ref)
