@@ -63,6 +63,7 @@ SIGNATURES = {
     "cdx_conv2d_backward_data_winograd_f32": (_int, [_vp, _vp, _vp] + [_i64] * 7 + [_int, _vp, _sz, _vp]),
     "cdx_conv2d_backward_weight_workspace_size": (_sz, [_i64] * 11),
     "cdx_conv2d_backward_weight_f32": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),
+    "cdx_conv2d_backward_weight_f32_noalloc": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_int, _vp]),
     "cdx_conv2d_backward_bias_f32": (_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
     "cdx_conv2d_forward_f64": (_int, [_vp, _vp, _vp, _vp] + [_i64] * 11 + [_vp]),
     "cdx_conv2d_backward_data_f64": (_int, [_vp, _vp, _vp] + [_i64] * 11 + [_vp]),

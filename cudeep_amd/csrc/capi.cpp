@@ -5,6 +5,7 @@
 // here falls back to the CPU.
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "cdx_internal.hpp"
@@ -347,6 +348,45 @@ int cdx_col2im_f32(const float* col, float* grad_input, int64_t batch, int64_t i
                                   kernel_w, stride_h, stride_w, pad_h, pad_w, stream);
 }
 
+}  // extern "C"
+
+// ---- scratch of the allocation-free entry point ----------------------------
+// cdx_conv2d_backward_weight_f32_noalloc keeps its split partials here: one
+// copy of the array on every GPU the library runs on, held until the process
+// ends.  On the host the array's name is only a stand-in for the device
+// symbol, never an address: host code uses the device address that
+// hipGetSymbolAddress returns, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[CDX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};   // device address of `scratch`, per device
+
+// The current device's copy of `scratch` (resolved on the first call on that
+// device, with the device current).
+int noalloc_scratch(void** out, const char* fn) {
+    int dev = -1;
+    int st = cdx::hip_error(hipGetDevice(&dev), fn);
+    if (st) return st;
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(CDX_ERR_UNSUPPORTED, std::string(fn) + ": device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        st = cdx::hip_error(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), fn);
+        if (st) return st;
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return CDX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 namespace {
 
 struct ConvSizes {
@@ -651,6 +691,39 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
         st = run_gemm(precision, g, stream);
     }
     return ws.release(st);
+}
+
+int cdx_conv2d_backward_weight_f32_noalloc(const float* grad_output, const float* input,
+                                           float* grad_weight, int64_t batch,
+                                           int64_t in_channels, int64_t out_channels,
+                                           int64_t in_h, int64_t in_w, int64_t kernel_h,
+                                           int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                                           int64_t pad_h, int64_t pad_w, int precision,
+                                           hipStream_t stream) {
+    const char* fn = "cdx_conv2d_backward_weight_f32_noalloc";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
+    if (!valid_precision(precision))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
+    const size_t need = cdx_conv2d_backward_weight_workspace_size(
+        batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
+        pad_h, pad_w);
+    if (need > (size_t)CDX_NOALLOC_SCRATCH_BYTES)
+        return set_error(CDX_ERR_UNSUPPORTED,
+                         std::string(fn) + ": this layer needs " + std::to_string(need) +
+                             " bytes of scratch, more than the " +
+                             std::to_string((size_t)CDX_NOALLOC_SCRATCH_BYTES) +
+                             " the allocation-free entry point holds; call "
+                             "cdx_conv2d_backward_weight_f32 with a workspace instead");
+    void* ws = nullptr;
+    st = noalloc_scratch(&ws, fn);
+    if (st) return st;
+    // with a workspace the general entry point allocates nothing
+    return cdx_conv2d_backward_weight_f32(grad_output, input, grad_weight, batch, in_channels,
+                                          out_channels, in_h, in_w, kernel_h, kernel_w,
+                                          stride_h, stride_w, pad_h, pad_w, precision, ws,
+                                          (size_t)CDX_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int cdx_conv2d_backward_bias_f32(const float* grad_output, float* grad_bias, int64_t batch,

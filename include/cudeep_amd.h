@@ -279,7 +279,8 @@ int cdx_conv2d_backward_data_winograd_f32(const float* grad_output, const float*
  * All precisions take it (exact fp32 products meet the TF32 bounds too);
  * problems beyond its 32-bit index range fall back to im2col + a GEMM that
  * reads col transposed.  The long K = B*S is split across workgroups and
- * reduced in a fixed order.  The workspace size covers both routes.
+ * reduced in a fixed order.  The workspace size query returns exactly what
+ * the route this problem takes uses.
  * Replaces cudeep::kernels::launch_conv2d_backward_weight_kernel<float>
  * (include/cudeep/kernels/conv.cuh:28-36, src/kernels/conv_kernel.cu:486-545).
  * grad_weight is overwritten.  workspace may be NULL. */
@@ -296,6 +297,32 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
                                    int64_t pad_h, int64_t pad_w, int precision,
                                    void* workspace, size_t workspace_bytes,
                                    hipStream_t stream);
+
+/* Bytes of device scratch the allocation-free entry point below owns on each
+ * GPU it runs on (held until the process ends). */
+#define CDX_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* cdx_conv2d_backward_weight_f32 without a workspace argument and without
+ * any allocation: no hipMalloc / hipMallocAsync / hipFree, no allocating
+ * library routine.  Its split partials live in a library-owned device array
+ * of CDX_NOALLOC_SCRATCH_BYTES per GPU.  No counterpart in the reference: it
+ * is for callers that cannot allocate (code under HIP graph capture, tight
+ * training or serving loops, harnesses that forbid allocation).  Same
+ * arguments, routes and results as cdx_conv2d_backward_weight_f32; a layer
+ * whose scratch (cdx_conv2d_backward_weight_workspace_size) exceeds the
+ * limit is refused with CDX_ERR_UNSUPPORTED before anything is launched
+ * (C5's 64x64x3x3 layer at batch 32 needs 9 MiB).  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (different streams
+ * or threads without ordering between them) race and must be serialised by
+ * the caller. */
+int cdx_conv2d_backward_weight_f32_noalloc(const float* grad_output, const float* input,
+                                           float* grad_weight,
+                                           int64_t batch, int64_t in_channels,
+                                           int64_t out_channels, int64_t in_h, int64_t in_w,
+                                           int64_t kernel_h, int64_t kernel_w,
+                                           int64_t stride_h, int64_t stride_w,
+                                           int64_t pad_h, int64_t pad_w, int precision,
+                                           hipStream_t stream);
 
 /* grad_bias[c] = sum over b, s of grad_output[b, c, s] (NCHW, S = OH*OW),
  * deterministic.  Replaces the host-side NumPy reduction of the reference's
