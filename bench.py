@@ -130,7 +130,8 @@ def bench_gemm16(n, dtype, steps, warmup, seed, min_warm_s=0.0):
 
 def bench_mlp(steps, warmup, precision):
     """C4: 784 -> 256 -> 10, batch 8192: fused forward (bias+ReLU epilogue)
-    and backward GEMMs (dX, dW per layer) + bias-grad column sums."""
+    and backward: dW GEMMs that also form the bias gradients (ones column),
+    the ReLU mask in the epilogue of dH = dY2 W2, dX = dZ W1."""
     import torch
     import cudeep_amd.ops as ops
     import cudeep_amd as cd
@@ -143,7 +144,6 @@ def bench_mlp(steps, warmup, precision):
     dY2 = torch.randn((8192, 10), device="cuda", generator=g)
     H = torch.empty((8192, 256), device="cuda")
     Y = torch.empty((8192, 10), device="cuda")
-    dH = torch.empty((8192, 256), device="cuda")
     dZ = torch.empty((8192, 256), device="cuda")
     gW2 = torch.empty((10, 256), device="cuda")
     gW1 = torch.empty((256, 784), device="cuda")
@@ -151,19 +151,46 @@ def bench_mlp(steps, warmup, precision):
     gb1 = torch.empty((256,), device="cuda")
     gb2 = torch.empty((10,), device="cuda")
 
+    # Every launch takes its scratch from a preallocated workspace, so the
+    # step allocates nothing and can be captured as a HIP graph.
+    def wsp(nbytes):
+        return torch.empty(max(nbytes, 4) // 4 + 1, device="cuda")
+    ws_w2 = wsp(ops.gemm_workspace_bytes(10, 256, 8192, precision=precision, transA=True,
+                                         colsum=True))
+    ws_w1 = wsp(ops.gemm_workspace_bytes(256, 784, 8192, precision=precision, transA=True,
+                                         colsum=True))
+    ws_x = wsp(ops.gemm_workspace_bytes(8192, 784, 256, precision=precision))
+    ws_h = wsp(ops.gemm_workspace_bytes(8192, 256, 10, precision=precision))
+    ws_f1 = wsp(ops.gemm_workspace_bytes(8192, 256, 784, precision=precision, transB=True))
+    ws_f2 = wsp(ops.gemm_workspace_bytes(8192, 10, 256, precision=precision, transB=True))
+
     def fwd():
         ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
-                 precision=precision, out=H)
-        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y)
+                 precision=precision, out=H, workspace=ws_f1)
+        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y,
+                 workspace=ws_f2)
+
+    def bwd_layer2():
+        # dW2 = dY2^T H and db2 = column sums of dY2, one launch (+ split-K reduction)
+        ops.gemm(dY2, H, transA=True, precision=precision, out=gW2, colsum=gb2, workspace=ws_w2)
+
+    def bwd_mask():
+        # dZ = (dY2 W2) * (H > 0): the ReLU backward in the GEMM's epilogue
+        ops.gemm(dY2, W2, precision=precision, out=dZ, epilogue=cd.EPI_BWD_RELU, aux=H,
+                 workspace=ws_h)
+
+    def bwd_layer1():
+        # dW1 = dZ^T X and db1 = column sums of dZ, one launch (+ reduction)
+        ops.gemm(dZ, X, transA=True, precision=precision, out=gW1, colsum=gb1, workspace=ws_w1)
+
+    def bwd_dx():
+        ops.gemm(dZ, W1, precision=precision, out=gX, workspace=ws_x)          # dX = dZ W1
 
     def bwd():
-        ops.gemm(dY2, W2, precision=precision, out=dH)                 # dH = dY2 W2
-        ops.gemm(dY2, H, transA=True, precision=precision, out=gW2)   # dW2 = dY2^T H
-        ops.sum_reduce_rows(dY2, out=gb2)
-        ops.activation_backward(dH, H, cd.EPI_RELU, out=dZ)          # ReLU mask (H>0 <=> Z>0)
-        ops.gemm(dZ, W1, precision=precision, out=gX)                 # dX = dZ W1
-        ops.gemm(dZ, X, transA=True, precision=precision, out=gW1)    # dW1 = dZ^T X
-        ops.sum_reduce_rows(dZ, out=gb1)
+        bwd_layer2()
+        bwd_mask()
+        bwd_layer1()
+        bwd_dx()
 
     fwd_ms, _ = time_launches(fwd, steps, warmup)
     bwd_ms, _ = time_launches(bwd, steps, warmup)
@@ -172,31 +199,10 @@ def bench_mlp(steps, warmup, precision):
 
     # The same step as one HIP graph: at this size the eager step is bound by
     # per-launch host work (Python + ctypes), which replaying a captured
-    # graph removes.  Every launch takes its scratch from a preallocated
-    # workspace, so nothing is allocated under capture.
-    def wsp(nbytes):
-        return torch.empty(max(nbytes, 4) // 4 + 1, device="cuda")
-    ws_w2 = wsp(ops.gemm_workspace_bytes(10, 256, 8192, precision=precision, transA=True))
-    ws_w1 = wsp(ops.gemm_workspace_bytes(256, 784, 8192, precision=precision, transA=True))
-    ws_x = wsp(ops.gemm_workspace_bytes(8192, 784, 256, precision=precision))
-    ws_h = wsp(ops.gemm_workspace_bytes(8192, 256, 10, precision=precision))
-    ws_f1 = wsp(ops.gemm_workspace_bytes(8192, 256, 784, precision=precision, transB=True))
-    ws_f2 = wsp(ops.gemm_workspace_bytes(8192, 10, 256, precision=precision, transB=True))
-    ws_b2 = wsp(ops.sum_reduce_rows_workspace_bytes(8192, 10))
-    ws_b1 = wsp(ops.sum_reduce_rows_workspace_bytes(8192, 256))
-
+    # graph removes.
     def step():
-        ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
-                 precision=precision, out=H, workspace=ws_f1)
-        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y,
-                 workspace=ws_f2)
-        ops.gemm(dY2, W2, precision=precision, out=dH, workspace=ws_h)
-        ops.gemm(dY2, H, transA=True, precision=precision, out=gW2, workspace=ws_w2)
-        ops.sum_reduce_rows(dY2, out=gb2, workspace=ws_b2)
-        ops.activation_backward(dH, H, cd.EPI_RELU, out=dZ)
-        ops.gemm(dZ, W1, precision=precision, out=gX, workspace=ws_x)
-        ops.gemm(dZ, X, transA=True, precision=precision, out=gW1, workspace=ws_w1)
-        ops.sum_reduce_rows(dZ, out=gb1, workspace=ws_b1)
+        fwd()
+        bwd()
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -210,28 +216,21 @@ def bench_mlp(steps, warmup, precision):
     graph_ms, _ = time_launches(graph.replay, steps, warmup)
 
     # The same step with the backward's independent branches on two side
-    # streams (dW2 + its bias sum beside dH and the ReLU mask; dW1 + its bias
-    # sum beside dX), each on its own workspaces: the graph runs them
-    # concurrently, overlapping the GEMMs' latency-bound phases and tails.
+    # streams (layer 2's weight + bias gradient beside the masked dH; layer
+    # 1's beside dX), each on its own workspace.
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
 
     def step_forked():
         main = torch.cuda.current_stream()
-        ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
-                 precision=precision, out=H, workspace=ws_f1)
-        ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y,
-                 workspace=ws_f2)
+        fwd()
         s1.wait_stream(main)
         with torch.cuda.stream(s1):
-            ops.gemm(dY2, H, transA=True, precision=precision, out=gW2, workspace=ws_w2)
-            ops.sum_reduce_rows(dY2, out=gb2, workspace=ws_b2)
-        ops.gemm(dY2, W2, precision=precision, out=dH, workspace=ws_h)
-        ops.activation_backward(dH, H, cd.EPI_RELU, out=dZ)
+            bwd_layer2()
+        bwd_mask()
         s2.wait_stream(main)
         with torch.cuda.stream(s2):
-            ops.gemm(dZ, X, transA=True, precision=precision, out=gW1, workspace=ws_w1)
-            ops.sum_reduce_rows(dZ, out=gb1, workspace=ws_b1)
-        ops.gemm(dZ, W1, precision=precision, out=gX, workspace=ws_x)
+            bwd_layer1()
+        bwd_dx()
         main.wait_stream(s1)
         main.wait_stream(s2)
 
@@ -244,10 +243,14 @@ def bench_mlp(steps, warmup, precision):
     with torch.cuda.graph(graph2):
         step_forked()
     graph2_ms, _ = time_launches(graph2.replay, steps, warmup)
-    # per-GEMM timing of the big forward GEMM
+    # the big forward GEMM and the two narrow products on their own
     l1_ms, _ = time_launches(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
                                               epilogue=cd.EPI_RELU, precision=precision, out=H),
                              steps, warmup)
+    l2_ms, _ = time_launches(lambda: ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL,
+                                              precision=precision, out=Y, workspace=ws_f2),
+                             steps, warmup)
+    dh_ms, _ = time_launches(bwd_mask, steps, warmup)
     return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
             "fwd_tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12,
             "bwd_tflops": bwd_flops / (bwd_ms * 1e-3) / 1e12,
@@ -256,7 +259,37 @@ def bench_mlp(steps, warmup, precision):
             "step_graph_forked_ms": graph2_ms,
             "step_graph_forked_tflops": (fwd_flops + bwd_flops) / (graph2_ms * 1e-3) / 1e12,
             "fwd1_fused_ms": l1_ms,
-            "fwd1_fused_tflops": 2.0 * 8192 * 784 * 256 / (l1_ms * 1e-3) / 1e12}
+            "fwd1_fused_tflops": 2.0 * 8192 * 784 * 256 / (l1_ms * 1e-3) / 1e12,
+            "fwd2_ms": l2_ms, "dh_masked_ms": dh_ms}
+
+
+def bench_mlp_api(steps, warmup, precision):
+    """C4 forward + backward through the drop-in Python API: cuDeep.nn
+    Sequential(Linear(784, 256), ReLU, Linear(256, 10)) -> _cudeep_core ->
+    libcudeep.so -> the C-ABI, with the output gradient given (y.backward(dY)),
+    timed eagerly, host work included."""
+    import numpy as np
+    import torch
+    from cudeep_amd import cuDeep
+    prev = cuDeep.get_matmul_precision()
+    cuDeep.set_matmul_precision("fp32" if precision == 0 else "tf32")
+    nn, T = cuDeep.nn, cuDeep.Tensor
+    rng = np.random.default_rng(4)
+    model = nn.Sequential(nn.Linear(784, 256), nn.ReLU(), nn.Linear(256, 10))
+    cuDeep.init.xavier_uniform_(model[0].weight)
+    cuDeep.init.xavier_uniform_(model[2].weight)
+    X = T.from_numpy(rng.standard_normal((8192, 784), dtype=np.float32))
+    dY = T.from_numpy(rng.standard_normal((8192, 10), dtype=np.float32))
+
+    def step():
+        model.zero_grad()
+        y = model(X)
+        y.backward(dY)
+
+    ms, _ = time_launches(step, steps, warmup)
+    cuDeep.set_matmul_precision(prev)
+    flops = 3 * 2.0 * 8192 * (784 * 256 + 256 * 10)
+    return {"step_ms": ms, "step_tflops": flops / (ms * 1e-3) / 1e12}
 
 
 def bench_conv(steps, warmup, precision):
@@ -322,6 +355,37 @@ def bench_conv(steps, warmup, precision):
             "gemm_ms_est": conv_ms - im_ms,
             "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12,
             "winograd_ms": wino_ms, "winograd_tflops_equiv": flops / (wino_ms * 1e-3) / 1e12}
+
+
+def bench_conv_api(steps, warmup, precision):
+    """C5 forward (and forward + backward) through the drop-in Python API:
+    cuDeep.nn.Conv2d(64, 64, 3, padding=1) on [32, 64, 56, 56] ->
+    _cudeep_core -> libcudeep.so -> the C-ABI (the reference's routing: Winograd
+    for this 3x3 stride-1 layer), timed eagerly, host work included."""
+    import numpy as np
+    from cudeep_amd import cuDeep
+    prev = cuDeep.get_matmul_precision()
+    cuDeep.set_matmul_precision("fp32" if precision == 0 else "tf32")
+    T = cuDeep.Tensor
+    rng = np.random.default_rng(5)
+    conv = cuDeep.nn.Conv2d(64, 64, 3, padding=1)
+    cuDeep.init.kaiming_normal_(conv.weight)
+    x = T.from_numpy(rng.standard_normal((32, 64, 56, 56), dtype=np.float32))
+    dy = T.from_numpy(rng.standard_normal((32, 64, 56, 56), dtype=np.float32))
+    with cuDeep.no_grad():
+        fwd_ms, _ = time_launches(lambda: conv(x), steps, warmup)
+    xg = T.from_numpy(rng.standard_normal((32, 64, 56, 56), dtype=np.float32), requires_grad=True)
+
+    def step():
+        conv.zero_grad()
+        xg.grad = None
+        conv(xg).backward(dy)
+
+    step_ms, _ = time_launches(step, steps, warmup)
+    cuDeep.set_matmul_precision(prev)
+    fl = 2.0 * 32 * 64 * 56 * 56 * 64 * 9
+    return {"fwd_ms": fwd_ms, "fwd_tflops": fl / (fwd_ms * 1e-3) / 1e12,
+            "step_ms": step_ms, "step_tflops": 3 * fl / (step_ms * 1e-3) / 1e12}
 
 
 def cpu_baseline(n=4096):
@@ -467,6 +531,10 @@ def main():
             log(f"mlp {name}:", extra[f"mlp_c4_{name}"])
             extra[f"conv_c5_{name}"] = bench_conv(args.steps, args.warmup, prec)
             log(f"conv {name}:", extra[f"conv_c5_{name}"])
+            extra[f"mlp_c4_api_{name}"] = bench_mlp_api(args.steps, args.warmup, prec)
+            log(f"mlp via cuDeep.nn {name}:", extra[f"mlp_c4_api_{name}"])
+            extra[f"conv_c5_api_{name}"] = bench_conv_api(args.steps, args.warmup, prec)
+            log(f"conv via cuDeep.nn {name}:", extra[f"conv_c5_api_{name}"])
         r = bench_gemm(512, cd.PREC_FP32, 200, 50, seed=1)
         extra["fp32_512"] = r
     cpu = None

@@ -9,7 +9,8 @@ HIP_RUNTIME = share_torch_hip_runtime()
 
 from . import _lib  # noqa: E402,F401
 from ._lib import (ACT_LEAKY_RELU, ACT_TANH, CdxError, EPI_GELU, EPI_NONE, EPI_RELU,  # noqa: F401
-                   EPI_SIGMOID, EPI_SILU,
+                   EPI_SIGMOID, EPI_SILU, EPI_BWD_GELU, EPI_BWD_RELU, EPI_BWD_SIGMOID,
+                   EPI_BWD_SILU,
                    BIAS_COL, BIAS_NONE, BIAS_ROW, OP_N, OP_T, PREC_FP32, PREC_TF32MODE,
                    PREC_TF32MODE4)
 

@@ -20,6 +20,8 @@ CDX_ERR_WORKSPACE = 4
 
 OP_N, OP_T = 0, 1
 EPI_NONE, EPI_RELU, EPI_GELU, EPI_SILU, EPI_SIGMOID = 0, 1, 2, 3, 4
+# activation-backward epilogues (cdx_gemm_fused): C = (A B) * act'(aux)
+EPI_BWD_RELU, EPI_BWD_GELU, EPI_BWD_SILU, EPI_BWD_SIGMOID = 8, 9, 10, 11
 ACT_TANH, ACT_LEAKY_RELU = 5, 6   # elementwise activations only
 BIAS_NONE, BIAS_ROW, BIAS_COL = 0, 1, 2
 PREC_FP32, PREC_TF32MODE, PREC_TF32MODE4 = 0, 1, 2
@@ -41,6 +43,9 @@ SIGNATURES = {
     "cdx_gemm_workspace_size": (_sz, [_int, _int, _int, _i64, _i64, _i64]),
     "cdx_gemm_ex_ws": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
                               _vp, _i64, _vp, _int, _int, _vp, _sz, _vp]),
+    "cdx_gemm_fused_workspace_size": (_sz, [_int, _int, _int, _i64, _i64, _i64, _int]),
+    "cdx_gemm_fused": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,
+                              _vp, _i64, _vp, _int, _int, _vp, _i64, _vp, _vp, _sz, _vp]),
     "cdx_matmul_fused_act": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
     "cdx_hgemm_f16": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cdx_gemm16_ex": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64,

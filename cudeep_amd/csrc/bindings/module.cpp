@@ -316,6 +316,27 @@ PYBIND11_MODULE(_cudeep_core, m) {
           },
           py::arg("a"), py::arg("b"), py::arg("trans_a") = false, py::arg("trans_b") = false);
 
+    m.def("linear_weight_grad",
+          [](const Tensor& dz, const Tensor& x, bool with_bias) {
+              Tensor Z = ensure_contiguous(dz), X = ensure_contiguous(x);
+              if (Z.ndim() != 2 || X.ndim() != 2 || Z.shape()[0] != X.shape()[0])
+                  throw std::runtime_error(
+                      "linear_weight_grad: dz [N, out] and x [N, in] required");
+              require_f32(Z, "linear_weight_grad");
+              require_f32(X, "linear_weight_grad");
+              const int64_t batch = Z.shape()[0], out_f = Z.shape()[1], in_f = X.shape()[1];
+              Tensor gw({out_f, in_f}, DType::Float32);
+              Tensor gb({out_f}, DType::Float32);
+              if (out_f > 0)
+                  kernels::launch_linear_weight_grad(
+                      static_cast<const float*>(Z.data()), static_cast<const float*>(X.data()),
+                      static_cast<float*>(gw.data()),
+                      with_bias ? static_cast<float*>(gb.data()) : nullptr, batch, out_f, in_f,
+                      Z.stream());
+              return py::make_tuple(gw, with_bias ? py::cast(gb) : py::none());
+          },
+          py::arg("dz"), py::arg("x"), py::arg("with_bias") = true);
+
     m.def("linear_forward",
           [](const Tensor& x, const Tensor& weight, py::object bias_obj,
              const std::string& activation) {

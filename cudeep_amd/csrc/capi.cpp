@@ -24,6 +24,53 @@ int hip_error(hipError_t e, const char* what) {
     return set_error(CDX_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+namespace {
+
+constexpr int kPoolDevices = 64;
+std::mutex g_pool_mu;
+hipMemPool_t g_pools[kPoolDevices] = {};
+
+int scratch_pool(hipMemPool_t* out, const char* what) {
+    int dev = -1;
+    int st = hip_error(hipGetDevice(&dev), what);
+    if (st) return st;
+    if (dev < 0 || dev >= kPoolDevices)
+        return set_error(CDX_ERR_UNSUPPORTED, std::string(what) + ": device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    if (!g_pools[dev]) {
+        hipMemPoolProps props = {};
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = nullptr;
+        st = hip_error(hipMemPoolCreate(&pool, &props), what);
+        if (st) return st;
+        uint64_t keep = UINT64_MAX;   // never hand freed blocks back on sync
+        st = hip_error(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep), what);
+        if (st) {
+            (void)hipMemPoolDestroy(pool);
+            return st;
+        }
+        g_pools[dev] = pool;
+    }
+    *out = g_pools[dev];
+    return CDX_OK;
+}
+
+}  // namespace
+
+int stream_alloc(void** p, size_t bytes, hipStream_t stream, const char* what) {
+    hipMemPool_t pool = nullptr;
+    int st = scratch_pool(&pool, what);
+    if (st) return st;
+    return hip_error(hipMallocFromPoolAsync(p, bytes, pool, stream), what);
+}
+
+int stream_free(void* p, hipStream_t stream, const char* what) {
+    return hip_error(hipFreeAsync(p, stream), what);
+}
+
 }  // namespace cdx
 
 using cdx::set_error;
@@ -146,6 +193,65 @@ int cdx_gemm_ex_ws(int precision, int opA, int opB, int64_t M, int64_t N, int64_
     return run_gemm(precision, g, stream);
 }
 
+size_t cdx_gemm_fused_workspace_size(int precision, int opA, int opB, int64_t M, int64_t N,
+                                     int64_t K, int with_colsum) {
+    if (!with_colsum) return cdx_gemm_workspace_size(precision, opA, opB, M, N, K);
+    if (!valid_precision(precision) || (opA != CDX_OP_N && opA != CDX_OP_T) ||
+        (opB != CDX_OP_N && opB != CDX_OP_T) || bad_dim(M) || bad_dim(N) || bad_dim(K)) {
+        set_error(CDX_ERR_INVALID_ARG, "cdx_gemm_fused_workspace_size: bad arguments");
+        return 0;
+    }
+    if (M == 0) return 0;
+    cdx::GemmArgs g{opA, opB, M, N, K, nullptr, 1, nullptr, 1, nullptr, N, 0, 0,
+                    nullptr, CDX_BIAS_NONE, CDX_EPI_NONE};
+    return cdx::gemm_f32_workspace(cdx::with_ones_column(g));   // FP32 kernel in every mode
+}
+
+int cdx_gemm_fused(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K,
+                   const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                   int64_t ldc, const float* bias, int bias_mode, int epilogue, const float* aux,
+                   int64_t ldaux, float* colsum, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+    const char* fn = "cdx_gemm_fused";
+    int st = check_gemm(fn, opA, opB, M, N, K, A, lda, B, ldb, C, ldc);
+    if (st) return st;
+    if (!valid_precision(precision))
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad precision");
+    if (bias_mode != CDX_BIAS_NONE && bias_mode != CDX_BIAS_ROW && bias_mode != CDX_BIAS_COL)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad bias_mode");
+    if (bias_mode != CDX_BIAS_NONE && !bias && M > 0 && N > 0)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bias is NULL");
+    const bool bwd = epilogue >= CDX_EPI_BWD_RELU && epilogue <= CDX_EPI_BWD_SIGMOID;
+    if (!valid_epilogue(epilogue) && !bwd)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": bad epilogue");
+    if (bwd) {
+        if (bias_mode != CDX_BIAS_NONE)
+            return set_error(CDX_ERR_INVALID_ARG,
+                             std::string(fn) + ": no bias with an activation-backward epilogue");
+        if (M > 0 && N > 0 && !aux)
+            return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": aux is NULL");
+        if (ldaux < N)
+            return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": ldaux too small");
+    } else if (aux) {
+        return set_error(CDX_ERR_INVALID_ARG,
+                         std::string(fn) + ": aux needs a CDX_EPI_BWD_* epilogue");
+    }
+    if (colsum && (bias_mode != CDX_BIAS_NONE || epilogue != CDX_EPI_NONE))
+        return set_error(CDX_ERR_INVALID_ARG,
+                         std::string(fn) + ": colsum needs bias_mode NONE and epilogue NONE");
+    cdx::GemmArgs g{opA, opB, M, N, K, A, lda, B, ldb, C, ldc, 0, 0, bias, bias_mode, epilogue};
+    g.ws = workspace;
+    g.ws_bytes = workspace ? workspace_bytes : 0;
+    g.aux = aux;
+    g.ldaux = ldaux;
+    if (colsum) {
+        if (M == 0) return CDX_OK;
+        g.colsum = colsum;
+        return cdx::launch_gemm_f32(cdx::with_ones_column(g), stream);
+    }
+    return run_gemm(precision, g, stream);
+}
+
 int cdx_gemm_ex(int precision, int opA, int opB, int64_t M, int64_t N, int64_t K,
                 const float* A, int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
                 const float* bias, int bias_mode, int epilogue, hipStream_t stream) {
@@ -246,8 +352,8 @@ int conv_forward_im2col(const float* input, const float* weight, const float* bi
         if (workspace_bytes < need)
             return set_error(CDX_ERR_WORKSPACE, "cdx_conv2d_forward_f32: workspace too small");
     } else if (need > 0) {
-        st = cdx::hip_error(hipMallocAsync(reinterpret_cast<void**>(&col), need, stream),
-                            "cdx_conv2d_forward_f32: hipMallocAsync");
+        st = cdx::stream_alloc(reinterpret_cast<void**>(&col), need, stream,
+                               "cdx_conv2d_forward_f32: scratch");
         if (st) return st;
         owned = true;
     }
@@ -264,7 +370,7 @@ int conv_forward_im2col(const float* input, const float* weight, const float* bi
         st = run_gemm(precision, g, stream);
     }
     if (owned) {
-        int st2 = cdx::hip_error(hipFreeAsync(col, stream), "cdx_conv2d_forward_f32: hipFreeAsync");
+        int st2 = cdx::stream_free(col, stream, "cdx_conv2d_forward_f32: scratch");
         if (!st) st = st2;
     }
     return st;
@@ -320,8 +426,8 @@ int cdx_conv2d_forward_winograd_f32(const float* input, const float* weight, con
         if (workspace_bytes < need)
             return set_error(CDX_ERR_WORKSPACE, std::string(fn) + ": workspace too small");
     } else {
-        st = cdx::hip_error(hipMallocAsync(reinterpret_cast<void**>(&ws), need, stream),
-                            "cdx_conv2d_forward_winograd_f32: hipMallocAsync");
+        st = cdx::stream_alloc(reinterpret_cast<void**>(&ws), need, stream,
+                               "cdx_conv2d_forward_winograd_f32: scratch");
         if (st) return st;
         owned = true;
     }
@@ -329,7 +435,7 @@ int cdx_conv2d_forward_winograd_f32(const float* input, const float* weight, con
                                          out_channels, in_h, in_w, pad_h, pad_w, precision, ws,
                                          stream);
     if (owned) {
-        int st2 = cdx::hip_error(hipFreeAsync(ws, stream), "cdx_conv2d_forward_winograd_f32: hipFreeAsync");
+        int st2 = cdx::stream_free(ws, stream, "cdx_conv2d_forward_winograd_f32: scratch");
         if (!st) st = st2;
     }
     return st;
@@ -437,13 +543,13 @@ struct Scratch {
             return CDX_OK;
         }
         if (need == 0) return CDX_OK;
-        int st = cdx::hip_error(hipMallocAsync(&ptr, need, s), fn);
+        int st = cdx::stream_alloc(&ptr, need, s, fn);
         owned = st == CDX_OK;
         return st;
     }
     int release(int st) {
         if (owned) {
-            int st2 = cdx::hip_error(hipFreeAsync(ptr, stream), "hipFreeAsync");
+            int st2 = cdx::stream_free(ptr, stream, "scratch free");
             owned = false;
             if (!st) st = st2;
         }

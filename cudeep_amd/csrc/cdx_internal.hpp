@@ -20,6 +20,15 @@ typedef short shortx8 __attribute__((ext_vector_type(8)));
 int set_error(int code, const std::string& msg);
 int hip_error(hipError_t e, const char* what);
 
+// Stream-ordered scratch for calls without a caller workspace: blocks from a
+// library-owned memory pool per device whose release threshold keeps freed
+// memory for reuse.  (The device's default pool hands freed memory back to
+// the driver at every synchronization, so a large workspace -- 231 MB for a
+// C5 backward-data column buffer -- was mapped again on every call, ~150 us
+// of host time per free.)
+int stream_alloc(void** p, size_t bytes, hipStream_t stream, const char* what);
+int stream_free(void* p, hipStream_t stream, const char* what);
+
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // One GEMM problem in the library's internal form.  Element (i, j) of op(A)
@@ -49,7 +58,25 @@ struct GemmArgs {
     // ordered when it is null); gemm_*_workspace() gives the bytes needed.
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // Activation-backward epilogues (CDX_EPI_BWD_*): C = P * act'(aux), aux
+    // [M, N] with leading dimension ldaux (plain output map, no bias).
+    const float* aux = nullptr;
+    int64_t ldaux = 0;
+    // colsum[m] = sum_k op(A)(m, k), computed as an extra output column N of
+    // the product with a virtual column of ones appended to op(B) (FP32
+    // kernel only; plain output map, no bias, no epilogue).
+    float* colsum = nullptr;
+    // Set by with_ones_column(): op(B) has ones_col columns and the product
+    // N = ones_col + 1 (the last one the virtual ones column); -1 = none.
+    int64_t ones_col = -1;
 };
+
+// The GEMM with the ones column appended (for GemmArgs::colsum).
+inline GemmArgs with_ones_column(GemmArgs g) {
+    g.ones_col = g.N;
+    g.N += 1;
+    return g;
+}
 
 // Launchers (no argument validation: the C-ABI validates first).  The
 // *_workspace functions return the split-K partial bytes the same launch
@@ -67,7 +94,8 @@ int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
                  double* C, int64_t ldc, hipStream_t stream);
 
 // Split-K reduction: C = epi(sum_s P[s] + bias) through the output map, the
-// partials summed in slice order (deterministic).  P is [splits][M][N].
+// partials summed in slice order (deterministic).  P is [splits][M][N]; with
+// a ones column its sums go to g.colsum.
 int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStream_t stream);
 
 // Split-K policy shared by the GEMM kernels: split only when the tile grid
@@ -116,17 +144,17 @@ int with_splitk(const GemmArgs& g, int64_t tiles, int bk, hipStream_t stream, La
     if (part) {
         if (g.ws_bytes < bytes) return set_error(CDX_ERR_WORKSPACE, "gemm: workspace too small");
     } else {
-        st = hip_error(hipMallocAsync(reinterpret_cast<void**>(&part), bytes, stream),
-                       "gemm split-K: hipMallocAsync");
+        st = stream_alloc(reinterpret_cast<void**>(&part), bytes, stream, "gemm split-K scratch");
         if (st) return st;
     }
     GemmArgs q = g;
     q.C = part; q.ldc = g.N; q.n_split = 0; q.ldc_split = 0;
     q.bias = nullptr; q.bias_mode = CDX_BIAS_NONE; q.epilogue = CDX_EPI_NONE;
+    q.aux = nullptr; q.colsum = nullptr;   // the reduction applies both
     st = launch(q, splits, k_chunk);
     if (!st) st = launch_splitk_reduce(part, splits, g, stream);
     if (!g.ws) {
-        int st2 = hip_error(hipFreeAsync(part, stream), "gemm split-K: hipFreeAsync");
+        int st2 = stream_free(part, stream, "gemm split-K scratch");
         if (!st) st = st2;
     }
     return st;
@@ -297,12 +325,57 @@ __device__ __forceinline__ float act_fixed(float v) {
     return v;
 }
 
+// Activation-backward epilogues: grad * act'(x) with the same float formulas
+// (and operand order) as the elementwise activation-backward kernels, so the
+// fused and the separate forms agree bit for bit; ReLU is the mask x > 0.
+template <int ACT>
+__device__ __forceinline__ float bwd_fixed(float g, float x) {
+    if constexpr (ACT == CDX_EPI_BWD_RELU) return x > 0.0f ? g : 0.0f;
+    if constexpr (ACT == CDX_EPI_BWD_GELU) return g * gelu_grad_f32(x);
+    if constexpr (ACT == CDX_EPI_BWD_SILU) return g * silu_grad_t(x);
+    if constexpr (ACT == CDX_EPI_BWD_SIGMOID) return g * sigmoid_grad_t(x);
+    return g;
+}
+
+__device__ __forceinline__ bool is_bwd_epilogue(int e) {
+    return e >= CDX_EPI_BWD_RELU && e <= CDX_EPI_BWD_SIGMOID;
+}
+
 // Where a GEMM's output element (m, n) goes, with the bias and activation
-// of the epilogue (see GemmArgs for the output map).
+// of the epilogue (see GemmArgs for the output map).  With colsum set the
+// kernel computes N = n_main + 1 columns and column n_main goes to
+// colsum[m] (plain, no bias or activation).
 struct EpiArgs {
     float* C; int64_t ldc, M, N, n_split, ldc_split;
     const float* bias; int bias_mode, epilogue;
+    const float* aux = nullptr; int64_t ldaux = 0;
+    float* colsum = nullptr; int64_t n_main = 0;
 };
+
+// One output element through the epilogue, the activation chosen at run
+// time: the operations and their order of write_acc_act below.
+__device__ __forceinline__ void store_one(const EpiArgs& e, int64_t m, int64_t n, float v) {
+    if (e.colsum && n == e.n_main) {
+        e.colsum[m] = v;
+        return;
+    }
+    float r;
+    if (is_bwd_epilogue(e.epilogue)) {
+        const float x = e.aux[m * e.ldaux + n];
+        switch (e.epilogue) {
+            case CDX_EPI_BWD_RELU: r = bwd_fixed<CDX_EPI_BWD_RELU>(v, x); break;
+            case CDX_EPI_BWD_GELU: r = bwd_fixed<CDX_EPI_BWD_GELU>(v, x); break;
+            case CDX_EPI_BWD_SILU: r = bwd_fixed<CDX_EPI_BWD_SILU>(v, x); break;
+            default: r = bwd_fixed<CDX_EPI_BWD_SIGMOID>(v, x); break;
+        }
+    } else {
+        const float bcol = e.bias_mode == CDX_BIAS_COL ? e.bias[n] : 0.0f;
+        const float brow = e.bias_mode == CDX_BIAS_ROW ? e.bias[m] : 0.0f;
+        r = apply_act(v + bcol + brow, e.epilogue);
+    }
+    const int64_t col = e.n_split > 0 ? (n / e.n_split) * e.ldc_split + n % e.n_split : n;
+    e.C[m * e.ldc + col] = r;
+}
 
 // Writes one wave's FM x FN grid of 16 x 16 MFMA accumulator tiles (D
 // layout of v_mfma_f32_16x16x*: register r of lane l is row 4 (l / 16) + r,
@@ -333,6 +406,7 @@ __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], cons
         }
         bcol[jn] = (bias_col && (!CHECK || n < e.N)) ? e.bias[n] : 0.0f;
     }
+    constexpr bool BWD = ACT >= CDX_EPI_BWD_RELU;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -343,8 +417,16 @@ __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], cons
             float* crow = e.C + m * e.ldc;
 #pragma unroll
             for (int jn = 0; jn < FN; ++jn) {
-                if (CHECK && n0 + jn * 16 + l16 >= e.N) continue;
-                crow[col_off[jn]] = act_fixed<ACT>(acc[i][jn][r] + bcol[jn] + brow);
+                const int64_t n = n0 + jn * 16 + l16;
+                if (CHECK && n >= e.N) continue;
+                if (CHECK && e.colsum && n == e.n_main) {   // the ones column
+                    e.colsum[m] = acc[i][jn][r];
+                    continue;
+                }
+                if constexpr (BWD)
+                    crow[col_off[jn]] = bwd_fixed<ACT>(acc[i][jn][r], e.aux[m * e.ldaux + n]);
+                else
+                    crow[col_off[jn]] = act_fixed<ACT>(acc[i][jn][r] + bcol[jn] + brow);
             }
         }
     }
@@ -353,6 +435,15 @@ __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], cons
 template <int FM, int FN, bool CHECK, bool SPLITN>
 __device__ __forceinline__ void write_acc(const floatx4 (&acc)[FM][FN], const EpiArgs& e,
                                           int64_t m0, int64_t n0, int lane) {
+    if constexpr (!SPLITN) {   // backward epilogues: plain output map only
+        switch (e.epilogue) {
+            case CDX_EPI_BWD_RELU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_RELU>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_GELU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_GELU>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_SILU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_SILU>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_SIGMOID: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_SIGMOID>(acc, e, m0, n0, lane); return;
+            default: break;
+        }
+    }
     switch (e.epilogue) {
         case CDX_EPI_RELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_RELU>(acc, e, m0, n0, lane); break;
         case CDX_EPI_GELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_GELU>(acc, e, m0, n0, lane); break;

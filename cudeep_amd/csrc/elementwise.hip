@@ -161,15 +161,15 @@ void fill_kernel(T* __restrict__ y, int64_t n, T v) {
         y[i] = v;
 }
 
+// Sum of the split-K partials in slice order, then the GEMM epilogue of
+// each element (store_one: bias, activation or activation backward, output
+// map, ones column) -- the same float operations as the unsplit kernels'.
 __global__ __launch_bounds__(256)
-void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t M, int64_t N,
-                          float* __restrict__ C, int64_t ldc, int64_t n_split,
-                          int64_t ldc_split, const float* __restrict__ bias, int bias_mode,
-                          int act) {
-    const int64_t MN = M * N;
+void splitk_reduce_kernel(const float* __restrict__ P, int splits, EpiArgs e) {
+    const int64_t MN = e.M * e.N;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t m = i / N, n = i - m * N;
+        const int64_t m = i / e.N, n = i - m * e.N;
         float v = P[i];
         // slices in order; 8 loads in flight per group instead of one at a time
         int s = 1;
@@ -181,11 +181,7 @@ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int64_t M, in
             for (int u = 0; u < 8; ++u) v += t[u];
         }
         for (; s < splits; ++s) v += P[(int64_t)s * MN + i];
-        if (bias_mode == CDX_BIAS_COL) v += bias[n];
-        else if (bias_mode == CDX_BIAS_ROW) v += bias[m];
-        v = cdx::apply_act(v, act);   // the GEMM kernels' float epilogue (same rounding)
-        const int64_t col = n_split > 0 ? (n / n_split) * ldc_split + n % n_split : n;
-        C[m * ldc + col] = v;
+        store_one(e, m, n, v);
     }
 }
 
@@ -199,9 +195,10 @@ unsigned grid_for(int64_t n) {
 }  // namespace
 
 int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStream_t stream) {
+    const EpiArgs e{g.C, g.ldc, g.M, g.N, g.n_split, g.ldc_split, g.bias, g.bias_mode,
+                    g.epilogue, g.aux, g.ldaux, g.colsum, g.ones_col};
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(g.M * g.N)), dim3(256), 0, stream,
-                       P, splits, g.M, g.N, g.C, g.ldc, g.n_split, g.ldc_split, g.bias,
-                       g.bias_mode, g.epilogue);
+                       P, splits, e);
     return hip_error(hipGetLastError(), "splitk_reduce_kernel launch");
 }
 

@@ -50,6 +50,8 @@ struct KParams {
     int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
     int64_t sa, sb, sc; // batch strides (elements) for blockIdx.z
     int64_t batch;      // gridDim.z
+    const float* aux;   // activation-backward epilogues: aux [M, N], leading dim ldaux
+    int64_t ldaux;
 };
 
 __device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
@@ -354,16 +356,6 @@ __device__ __forceinline__ void nan_bits(const floatx4 (&acc)[FM][FN], NanBits<F
                 const int bit = (i * FN + j) * 4 + e;
                 if (acc[i][j][e] != acc[i][j][e]) nb.w[bit >> 5] |= 1u << (bit & 31);
             }
-}
-
-// One output element through the epilogue: the same operations, in the same
-// order, as write_acc_act (acc + column bias + row bias, activation, output
-// map).
-__device__ __forceinline__ void store_one(const EpiArgs& e, int64_t m, int64_t n, float v) {
-    const float bcol = e.bias_mode == CDX_BIAS_COL ? e.bias[n] : 0.0f;
-    const float brow = e.bias_mode == CDX_BIAS_ROW ? e.bias[m] : 0.0f;
-    const int64_t col = e.n_split > 0 ? (n / e.n_split) * e.ldc_split + n % e.n_split : n;
-    e.C[m * e.ldc + col] = apply_act(v + bcol + brow, e.epilogue);
 }
 
 template <int FM, int FN, int OPA, int OPB>
@@ -673,7 +665,7 @@ void gemm_bf16x3_kernel(KParams p, int vec) {
     // accumulators; then IEEE values for the outputs an infinite or out-of-
     // range operand touched (split operands only)
     const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
-                      p.bias, p.bias_mode, p.epilogue};
+                      p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux};
     NanBits<FM, FN> nb;
     const bool repair = !H16 && any_nan(acc);
     if (repair) nan_bits(acc, nb);
@@ -893,7 +885,7 @@ void gemm_pingpong_kernel(KParams p) {
     if (grp == 0) slot();
 
     const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
-                      p.bias, p.bias_mode, p.epilogue};
+                      p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux};
     NanBits<8, 4> nb;
     const bool repair = !H16 && any_nan(acc);
     if (repair) nan_bits(acc, nb);
@@ -923,7 +915,7 @@ template <class CF, int OPA, int OPB, int TERMS, int IN>
 int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
-               g.stride_a, g.stride_b, g.stride_c, g.batch};
+               g.stride_a, g.stride_b, g.stride_c, g.batch, g.aux, g.ldaux};
     // vector loads of four elements need 4-element-aligned bases and strides
     constexpr unsigned VB = IN == kInF32 ? 16 : 8;
     bool vec = ((uintptr_t)g.A % VB == 0) && ((uintptr_t)g.B % VB == 0) &&
@@ -947,7 +939,7 @@ template <int OPA, int OPB, int IN>
 int launch_pingpong(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
     KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
-               g.stride_a, g.stride_b, g.stride_c, g.batch};
+               g.stride_a, g.stride_b, g.stride_c, g.batch, g.aux, g.ldaux};
     const int64_t tiles = (g.M / 256) * (g.N / 256);
     if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
     if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");

@@ -46,6 +46,13 @@ struct KParams {
     int64_t sa, sb, sc; // batch strides (elements) for blockIdx.z
     int64_t batch;      // gridDim.z
     int vec_a, vec_b;   // kLoadChecked: operand base, ld and batch stride allow 16-byte loads
+    const float* aux;   // activation-backward epilogues: aux [M, N], leading dim ldaux
+    int64_t ldaux;
+    // op(B)'s own column count and the virtual ones column: with ones >= 0
+    // (= nb) op(B)(k, nb) reads as 1 (checked loads only) and the kernel's N
+    // is nb + 1; colsum receives that column's results.
+    int64_t nb, ones;
+    float* colsum;
 };
 
 // Loads a ROWS x COLS tile (COLS contiguous in memory) starting at (r0, c0)
@@ -59,9 +66,12 @@ struct TileLoader {
     static constexpr bool PARTIAL = TOTAL % NT != 0;  // last pass: some threads idle
     float4 v[NV];
 
+    // ones_row / ones_col >= 0: that row / column (one past the matrix)
+    // reads as 1 within the other dimension's bounds (checked mode only)
     __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld,
                                          int64_t r0, int64_t c0, int64_t rmax,
-                                         int64_t cmax, bool vec, int tid) {
+                                         int64_t cmax, bool vec, int tid,
+                                         int64_t ones_row = -1, int64_t ones_col = -1) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             int idx = tid + i * NT;
@@ -79,6 +89,18 @@ struct TileLoader {
                 v[i].y = (rok && gc + 1 < cmax) ? p[1] : 0.0f;
                 v[i].z = (rok && gc + 2 < cmax) ? p[2] : 0.0f;
                 v[i].w = (rok && gc + 3 < cmax) ? p[3] : 0.0f;
+                if (ones_col >= 0 && rok) {
+                    if (gc + 0 == ones_col) v[i].x = 1.0f;
+                    if (gc + 1 == ones_col) v[i].y = 1.0f;
+                    if (gc + 2 == ones_col) v[i].z = 1.0f;
+                    if (gc + 3 == ones_col) v[i].w = 1.0f;
+                }
+                if (ones_row >= 0 && gr == ones_row) {
+                    v[i].x = gc + 0 < cmax ? 1.0f : 0.0f;
+                    v[i].y = gc + 1 < cmax ? 1.0f : 0.0f;
+                    v[i].z = gc + 2 < cmax ? 1.0f : 0.0f;
+                    v[i].w = gc + 3 < cmax ? 1.0f : 0.0f;
+                }
             }
         }
     }
@@ -177,8 +199,9 @@ void gemm_f32_mfma_kernel(KParams p) {
     auto load_into = [&](LA& a, LB& b, int64_t k0) {
         if (OPA == CDX_OP_N) a.load(p.A, p.lda, bm, k0, p.M, p.K, p.vec_a, tid);
         else                 a.load(p.A, p.lda, k0, bm, p.K, p.M, p.vec_a, tid);
-        if (OPB == CDX_OP_N) b.load(p.B, p.ldb, k0, bn, p.K, p.N, p.vec_b, tid);
-        else                 b.load(p.B, p.ldb, bn, k0, p.N, p.K, p.vec_b, tid);
+        // op(B)'s own columns, plus the ones column when p.ones >= 0
+        if (OPB == CDX_OP_N) b.load(p.B, p.ldb, k0, bn, p.K, p.nb, p.vec_b, tid, -1, p.ones);
+        else                 b.load(p.B, p.ldb, bn, k0, p.nb, p.K, p.vec_b, tid, p.ones, -1);
     };
     auto store_from = [&](const LA& a, const LB& b, int buf) {
         float* sA = lds + buf * (A_ELEMS + B_ELEMS);
@@ -309,7 +332,7 @@ void gemm_f32_mfma_kernel(KParams p) {
     // epilogue: bias, activation and the output map, straight from the
     // accumulators
     const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
-                      p.bias, p.bias_mode, p.epilogue};
+                      p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux, p.colsum, p.nb};
     write_acc<FM, FN, MODE != kLoadAlignedVec, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
 }
 
@@ -328,14 +351,16 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
     KParams kp{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
                g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
-               g.stride_a, g.stride_b, g.stride_c, g.batch, 0, 0};
+               g.stride_a, g.stride_b, g.stride_c, g.batch, 0, 0, g.aux, g.ldaux,
+               g.ones_col >= 0 ? g.ones_col : g.N, g.ones_col, g.colsum};
     // 16-byte loads need 16-byte aligned bases, leading dimensions and batch
     // strides, decided per operand (a 10-column operand no longer sends the
     // other one down the scalar path: C4's dW2 = dY2^T H, 10 x 256 x 8192,
     // 14 us with both operands scalar)
     kp.vec_a = ((uintptr_t)g.A % 16 == 0) && g.lda % 4 == 0 && g.stride_a % 4 == 0;
     kp.vec_b = ((uintptr_t)g.B % 16 == 0) && g.ldb % 4 == 0 && g.stride_b % 4 == 0;
-    bool aligned = kp.vec_a && kp.vec_b && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
+    bool aligned = g.ones_col < 0 && kp.vec_a && kp.vec_b && g.K > 0 && g.M % CF::BM == 0 &&
+                   g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
     if (aligned) {
@@ -379,13 +404,16 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
 //    64x64x16, 4 waves of 32x32, XCD groups of one tile row (~85 TFLOP/s on
 //    64 x 100352 x 576, against 49 with 64x256 tiles).
-//  * NarrowN: N <= 16 (the MLP's 10-class layer): 64x16 tiles instead of
-//    mostly-empty 64x64 ones (8192 x 10 x 256: 9.8 us against 13.4).  A
-//    16-row tile for M <= 16 measured no faster than Medium.
+//  * NarrowN: N <= 16 (the MLP's 10-class layer): 32x16 tiles, 2 waves, and
+//    a deep k-tile (64): such products read A once and are bound by the
+//    latency of their k-loop, so each workgroup takes few, large k-steps and
+//    twice as many workgroups share the GPU (64x16x16 tiles: 8192 x 10 x
+//    256 in 9.5 us, against 13.4 for mostly-empty 64x64 ones).  A 16-row
+//    tile for M <= 16 measured no faster than Medium.
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
 using CfgMedium = Cfg<64, 64, 16, 32, 32, 8, 2>;
 using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1, 2>;
-using CfgNarrowN = Cfg<64, 16, 16, 16, 16, 8, 2>;
+using CfgNarrowN = Cfg<32, 16, 64, 16, 16, 8, 2>;
 
 // Configuration choice, shared by the launcher and the workspace query.
 enum class F32Cfg { NarrowN, SkinnyM, Large, Medium };

@@ -79,6 +79,16 @@ void launch_matmul_ex(const float* A, const float* B, float* C, int64_t M, int64
                                  stream));
 }
 
+void launch_linear_weight_grad(const float* dz, const float* x, float* grad_w, float* grad_b,
+                               int64_t batch, int64_t out_features, int64_t in_features,
+                               hipStream_t stream, int precision) {
+    const int prec = precision >= 0 ? precision : g_precision.load();
+    const int64_t ldz = out_features > 1 ? out_features : 1, ldx = in_features > 1 ? in_features : 1;
+    CUDEEP_CHECK_CDX(cdx_gemm_fused(prec, CDX_OP_T, CDX_OP_N, out_features, in_features, batch,
+                                    dz, ldz, x, ldx, grad_w, in_features, nullptr, CDX_BIAS_NONE,
+                                    CDX_EPI_NONE, nullptr, 0, grad_b, nullptr, 0, stream));
+}
+
 void launch_matmul_dgemm_ex(const double* A, const double* B, double* C, int64_t M, int64_t N,
                             int64_t K, bool transA, bool transB, int64_t lda, int64_t ldb,
                             int64_t ldc, hipStream_t stream) {

@@ -36,6 +36,7 @@ from ._core import (
     conv2d_forward as _conv2d_forward,
     gelu as _gelu,
     linear_forward as _linear_forward,
+    linear_weight_grad as _linear_weight_grad,
     matmul_ex as _matmul_ex,
     relu as _relu,
     sum as _sum,
@@ -402,10 +403,11 @@ class BroadcastAddOp(Function):
 
 class LinearOp(Function):
     """y = act(x W^T + b) as one fused GEMM (bias and ReLU / GELU in the
-    epilogue).  Backward: dZ = act'(...) dY, dX = dZ W (NN GEMM),
-    dW = dZ^T x (TN GEMM), db = column sums of dZ.  For ReLU the mask is
-    taken from y (y > 0 exactly where x W^T + b > 0); GELU keeps the
-    pre-activation, so its activation is a separate launch when recorded."""
+    epilogue).  Backward: dZ = act'(...) dY, dX = dZ W (NN GEMM), and
+    dW = dZ^T x with db = column sums of dZ from the same launch (a column of
+    ones appended to x).  For ReLU the mask is taken from y (y > 0 exactly
+    where x W^T + b > 0); GELU keeps the pre-activation, so its activation is
+    a separate launch when recorded."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, activation):
@@ -431,9 +433,15 @@ class LinearOp(Function):
             dz = _activation_backward(dz, ctx.out, "relu")
         elif ctx.activation == "gelu":
             dz = _activation_backward(dz, ctx.pre, "gelu")
-        return (Tensor._wrap(_matmul_ex(dz, weight._data, False, False)) if need_x else None,
-                Tensor._wrap(_matmul_ex(dz, x._data, True, False)) if need_w else None,
-                Tensor._wrap(_sum_reduce_rows(dz)) if need_b else None)
+        gx = Tensor._wrap(_matmul_ex(dz, weight._data, False, False)) if need_x else None
+        gw = gb = None
+        if need_w:
+            raw_w, raw_b = _linear_weight_grad(dz, x._data, bool(need_b))
+            gw = Tensor._wrap(raw_w)
+            gb = Tensor._wrap(raw_b) if need_b else None
+        elif need_b:
+            gb = Tensor._wrap(_sum_reduce_rows(dz))
+        return gx, gw, gb
 
 
 class Conv2dOp(Function):

@@ -43,11 +43,15 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, precision: int = L.PREC_FP32,
          transA: bool = False, transB: bool = False, bias: torch.Tensor | None = None,
          bias_mode: int = L.BIAS_NONE, epilogue: int = L.EPI_NONE,
          out: torch.Tensor | None = None,
-         workspace: torch.Tensor | None = None) -> torch.Tensor:
+         workspace: torch.Tensor | None = None, aux: torch.Tensor | None = None,
+         colsum: torch.Tensor | None = None) -> torch.Tensor:
     """C = epi(op(A) @ op(B) + bias).  A, B are row-major storage; transA /
     transB select the transpose, so x @ W.T is gemm(x, W, transB=True).
     `workspace` (at least gemm_workspace_bytes(...) bytes) makes the call
-    allocation-free (cdx_gemm_ex_ws)."""
+    allocation-free (cdx_gemm_ex_ws).  Fusions (cdx_gemm_fused): with an
+    EPI_BWD_* epilogue, C = (op(A) @ op(B)) * act'(aux) (aux [M, N]); with
+    `colsum` (a float32 [M] tensor), colsum[m] = sum_k op(A)[m, k] in the
+    same launch (size the workspace with colsum=True)."""
     _need(A, "A")
     _need(B, "B")
     M, K = (A.shape[1], A.shape[0]) if transA else (A.shape[0], A.shape[1])
@@ -72,16 +76,39 @@ def gemm(A: torch.Tensor, B: torch.Tensor, *, precision: int = L.PREC_FP32,
     if workspace is not None:
         _need(workspace, "workspace")
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-    L.call("cdx_gemm_ex_ws", precision, int(transA), int(transB), M, N, K,
+    if aux is None and colsum is None:
+        L.call("cdx_gemm_ex_ws", precision, int(transA), int(transB), M, N, K,
+               A.data_ptr(), _ld(A, "A"), B.data_ptr(), _ld(B, "B"),
+               out.data_ptr(), _ld(out, "out"), bptr, bias_mode, epilogue, ws_ptr, ws_bytes,
+               _stream())
+        return out
+    aux_ptr, ldaux = None, 0
+    if aux is not None:
+        _need(aux, "aux")
+        if tuple(aux.shape) != (M, N):
+            raise ValueError("aux must be [M, N]")
+        aux_ptr, ldaux = aux.data_ptr(), _ld(aux, "aux")
+    cs_ptr = None
+    if colsum is not None:
+        _need(colsum, "colsum")
+        if colsum.numel() != M or not colsum.is_contiguous():
+            raise ValueError("colsum must be a contiguous [M] tensor")
+        cs_ptr = colsum.data_ptr()
+    L.call("cdx_gemm_fused", precision, int(transA), int(transB), M, N, K,
            A.data_ptr(), _ld(A, "A"), B.data_ptr(), _ld(B, "B"),
-           out.data_ptr(), _ld(out, "out"), bptr, bias_mode, epilogue, ws_ptr, ws_bytes,
-           _stream())
+           out.data_ptr(), _ld(out, "out"), bptr, bias_mode, epilogue, aux_ptr, ldaux, cs_ptr,
+           ws_ptr, ws_bytes, _stream())
     return out
 
 
 def gemm_workspace_bytes(M: int, N: int, K: int, *, precision: int = L.PREC_FP32,
-                         transA: bool = False, transB: bool = False) -> int:
-    """Scratch bytes gemm(..., workspace=) needs for op(A) [M, K] @ op(B) [K, N]."""
+                         transA: bool = False, transB: bool = False,
+                         colsum: bool = False) -> int:
+    """Scratch bytes gemm(..., workspace=) needs for op(A) [M, K] @ op(B) [K, N]
+    (with colsum=True: for a call that also forms the row sums of op(A))."""
+    if colsum:
+        return int(L.lib().cdx_gemm_fused_workspace_size(precision, int(transA), int(transB),
+                                                         M, N, K, 1))
     return int(L.lib().cdx_gemm_workspace_size(precision, int(transA), int(transB), M, N, K))
 
 

@@ -61,6 +61,15 @@ void launch_matmul_ex(const float* A, const float* B, float* C, int64_t M, int64
                       int64_t ldc, const float* bias, bool bias_per_col,
                       GemmEpilogue epilogue, hipStream_t stream = nullptr, int precision = -1);
 
+// Weight and bias gradient of a Linear layer in one launch:
+// grad_w[out, in] = dz^T x  and  grad_b[out] = column sums of dz, for
+// dz [batch, out] and x [batch, in] row-major (grad_b may be null: then
+// just the product).  Replaces MatMulOp.backward's dW GEMM plus
+// sum_reduce_rows (python/cuDeep/tensor.py:430-443, :617-631).
+void launch_linear_weight_grad(const float* dz, const float* x, float* grad_w, float* grad_b,
+                               int64_t batch, int64_t out_features, int64_t in_features,
+                               hipStream_t stream = nullptr, int precision = -1);
+
 void launch_matmul_dgemm_ex(const double* A, const double* B, double* C, int64_t M,
                             int64_t N, int64_t K, bool transA, bool transB, int64_t lda,
                             int64_t ldb, int64_t ldc, hipStream_t stream = nullptr);

@@ -21,7 +21,9 @@
  *  - The library keeps no global device state: concurrent calls on different
  *    streams are safe.  Routines that need scratch take a `workspace`
  *    pointer; passing NULL makes the library allocate and free it
- *    stream-ordered (hipMallocAsync / hipFreeAsync), as the reference does.
+ *    stream-ordered, as the reference does -- from a library-owned memory
+ *    pool per device that keeps freed blocks for reuse
+ *    (hipMallocFromPoolAsync / hipFreeAsync).
  */
 #ifndef CUDEEP_AMD_H
 #define CUDEEP_AMD_H
@@ -57,6 +59,14 @@ extern "C" {
 /* elementwise activations only (cdx_activation_*), not GEMM epilogues */
 #define CDX_ACT_TANH       5
 #define CDX_ACT_LEAKY_RELU 6
+/* Activation-backward epilogues (cdx_gemm_fused only): C = P * act'(aux) with
+ * P = op(A) * op(B) and aux the forward pre-activation (for ReLU its output
+ * works too), elementwise with the reference's activation_backward formulas
+ * (src/kernels/activation_kernel.cu:256-319): ReLU aux > 0 ? P : 0. */
+#define CDX_EPI_BWD_RELU    8
+#define CDX_EPI_BWD_GELU    9
+#define CDX_EPI_BWD_SILU    10
+#define CDX_EPI_BWD_SIGMOID 11
 
 #define CDX_BIAS_NONE 0
 #define CDX_BIAS_ROW  1            /* C[m][n] += bias[m]  (conv: per channel) */
@@ -129,6 +139,34 @@ int cdx_gemm_ex_ws(int precision, int opA, int opB,
                    const float* B, int64_t ldb,
                    float* C, int64_t ldc,
                    const float* bias, int bias_mode, int epilogue,
+                   void* workspace, size_t workspace_bytes,
+                   hipStream_t stream);
+
+/* cdx_gemm_ex_ws with the two fusions a Linear layer's backward wants, both
+ * computed by the same launch (the reference runs each as a kernel of its
+ * own: activation_backward, module.cpp:837-872 / activation_kernel.cu:256-319,
+ * and sum_reduce_rows, unary_kernel.cu:204-238, after the GEMMs of
+ * MatMulOp.backward, python/cuDeep/tensor.py:430-443, :617-631):
+ *  - epilogue CDX_EPI_BWD_*: C = act'(aux) (.) (op(A) * op(B)), aux [M, N]
+ *    with leading dimension ldaux (no bias with these epilogues);
+ *  - colsum (may be NULL): colsum[m] = sum over k of op(A)(m, k), the
+ *    product's row sums of op(A) -- with op(A) = dZ^T (opA = T) the bias
+ *    gradient of the layer whose weight gradient dZ^T X the call computes.
+ *    Formed as an extra output column of the product against a column of
+ *    ones (exact products, the GEMM's own accumulation), so it costs no
+ *    extra pass over dZ; requires bias_mode NONE and epilogue NONE and runs
+ *    the FP32 MFMA kernel in every precision mode (its products are exact).
+ * Workspace: cdx_gemm_fused_workspace_size (split-K partials, which then
+ * hold the extra column too); NULL allocates stream-ordered. */
+size_t cdx_gemm_fused_workspace_size(int precision, int opA, int opB,
+                                     int64_t M, int64_t N, int64_t K, int with_colsum);
+int cdx_gemm_fused(int precision, int opA, int opB,
+                   int64_t M, int64_t N, int64_t K,
+                   const float* A, int64_t lda,
+                   const float* B, int64_t ldb,
+                   float* C, int64_t ldc,
+                   const float* bias, int bias_mode, int epilogue,
+                   const float* aux, int64_t ldaux, float* colsum,
                    void* workspace, size_t workspace_bytes,
                    hipStream_t stream);
 

@@ -137,3 +137,24 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(ImportError):
         L.lib()
+
+
+def test_fused_gemm_argument_validation():
+    fake = ctypes.c_void_p(0x1000)
+    args = (0, 0, 0, 4, 4, 4, fake, 4, fake, 4, fake, 4)
+
+    def st(bias, bias_mode, epi, aux, ldaux, colsum):
+        return _status("cdx_gemm_fused", *args, bias, bias_mode, epi, aux, ldaux, colsum,
+                       None, 0, None)
+    assert st(fake, L.BIAS_COL, L.EPI_BWD_RELU, fake, 4, None) == L.CDX_ERR_INVALID_ARG
+    assert b"bias" in L.lib().cdx_last_error()
+    assert st(None, 0, L.EPI_BWD_GELU, None, 4, None) == L.CDX_ERR_INVALID_ARG      # no aux
+    assert st(None, 0, L.EPI_BWD_RELU, fake, 3, None) == L.CDX_ERR_INVALID_ARG      # ldaux < N
+    assert st(None, 0, L.EPI_RELU, fake, 4, None) == L.CDX_ERR_INVALID_ARG          # aux w/o BWD
+    assert st(None, 0, 12, None, 0, None) == L.CDX_ERR_INVALID_ARG                  # bad epilogue
+    assert st(None, 0, L.EPI_RELU, None, 0, fake) == L.CDX_ERR_INVALID_ARG          # colsum + act
+    assert st(fake, L.BIAS_ROW, 0, None, 0, fake) == L.CDX_ERR_INVALID_ARG          # colsum + bias
+    # workspace: C4's dW1 with its bias gradient -- 15 k-slices of [256, 785]
+    assert L.lib().cdx_gemm_fused_workspace_size(0, 1, 0, 256, 784, 8192, 1) == 15 * 256 * 785 * 4
+    assert L.lib().cdx_gemm_fused_workspace_size(1, 1, 0, 256, 784, 8192, 1) == 15 * 256 * 785 * 4
+    assert L.lib().cdx_gemm_fused_workspace_size(0, 1, 0, 256, 784, 8192, 0) == 15 * 256 * 784 * 4

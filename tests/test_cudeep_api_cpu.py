@@ -9,7 +9,8 @@ def test_import_surface():
     for name in ("Tensor", "DType", "Layout", "Stream", "Event", "MemoryPool", "relu", "gelu",
                  "activation_backward", "broadcast_add", "sum_reduce_rows", "sum",
                  "conv2d_forward", "conv2d_backward_data", "conv2d_backward_weight",
-                 "device_info", "linear_forward", "matmul_ex", "conv2d_backward_bias"):
+                 "device_info", "linear_forward", "matmul_ex", "conv2d_backward_bias",
+                 "linear_weight_grad"):
         assert hasattr(_cudeep_core, name), name
     for name in ("Tensor", "nn", "init", "autograd", "no_grad", "conv2d", "linear",
                  "broadcast_add", "relu", "gelu"):

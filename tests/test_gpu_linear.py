@@ -181,3 +181,94 @@ def test_broadcast_add_row():
     say("broadcast add")
     got = host(ops().broadcast_add_row(dev(m), dev(r)))
     assert np.array_equal(got, (m + r[None, :]).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------
+# fused backward: activation-backward epilogue and bias-gradient column
+# ---------------------------------------------------------------------------
+
+BWD_ACTS = ["relu", "gelu", "silu", "sigmoid"]
+
+
+@pytest.mark.parametrize("act", BWD_ACTS)
+@pytest.mark.parametrize("shape", [(8192, 256, 10), (300, 200, 96), (64, 64, 4096)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_bwd_epilogue_equals_gemm_then_activation_backward(act, shape, prec):
+    """dZ = (dY W) * act'(Z) in the GEMM's epilogue is bit for bit the GEMM
+    followed by the reference's activation_backward kernel (the same float
+    formula on the same product), unsplit, ragged and split-K; and against
+    fp64 the fused result is inside the reference route's bar (relu_grad x
+    dgemm: seq-FMA GEMM then the mask)."""
+    import cudeep_amd as cd
+    M, N, K = shape
+    rng = np.random.default_rng(M + N + K + prec)
+    dY = normal(rng, (M, K))
+    W = normal(rng, (K, N), 1.0 / np.sqrt(K))
+    Z = normal(rng, (M, N))
+    code = {"relu": cd.EPI_BWD_RELU, "gelu": cd.EPI_BWD_GELU, "silu": cd.EPI_BWD_SILU,
+            "sigmoid": cd.EPI_BWD_SIGMOID}[act]
+    fwd_code = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU, "silu": cd.EPI_SILU,
+                "sigmoid": cd.EPI_SIGMOID}[act]
+    say("bwd epilogue", act, shape, prec)
+    gY, gW, gZ = dev(dY), dev(W), dev(Z)
+    fused = host(ops().gemm(gY, gW, precision=prec, epilogue=code, aux=gZ))
+    P = ops().gemm(gY, gW, precision=prec)
+    sep = host(ops().activation_backward(P, gZ, fwd_code))
+    assert np.array_equal(fused.view(np.uint32), sep.view(np.uint32))
+    if act == "relu":
+        want = oracle.dgemm(dY, W) * oracle.relu_grad(Z)
+        e = oracle.rel_fro(fused, want)
+        if prec == 0:
+            e_ref = oracle.rel_fro(oracle.sgemm_seqfma(dY, W) * (Z > 0), want)
+            assert e <= 2 * e_ref, (e, e_ref)
+        else:
+            e_ref = min(oracle.rel_fro(oracle.gemm_tf32emu(dY, W, m) * (Z > 0), want)
+                        for m in ("rz", "rne"))
+            assert e <= e_ref, (e, e_ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 784, 8192), (10, 256, 8192), (33, 17, 3001),
+                                   (300, 200, 96), (64, 63, 128)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_weight_grad_with_fused_bias_grad(M, N, K, prec):
+    """dW = dZ^T X with db = column sums of dZ from the same launch (a virtual
+    column of ones appended to X): dW inside the FP32 bar against fp64 (the
+    fused call runs exact FP32 products in every mode), db inside 2x the
+    serial fp32 column sum's error, and the workspace query covers it."""
+    import torch
+    rng = np.random.default_rng(7 * M + N + K)
+    dZ = normal(rng, (K, M))
+    X = normal(rng, (K, N))
+    say("fused bias grad", M, N, K, prec)
+    cs = torch.full((M,), float("nan"), device="cuda")
+    nbytes = ops().gemm_workspace_bytes(M, N, K, precision=prec, transA=True, colsum=True)
+    ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device="cuda")
+    dW = host(ops().gemm(dev(dZ), dev(X), transA=True, precision=prec, colsum=cs,
+                         workspace=ws))
+    db = host(cs)
+    want = oracle.dgemm(dZ, X, transA=True)
+    e_ref = oracle.rel_fro(oracle.sgemm_seqfma(dZ, X, transA=True), want)
+    assert oracle.rel_fro(dW, want) <= 2 * e_ref + 2.0 ** -24
+    db64 = dZ.astype(np.float64).sum(0)
+    eb = oracle.rel_fro(db, db64)
+    eb_ref = oracle.rel_fro(oracle.colsum(dZ), db64)
+    assert eb <= 2 * eb_ref + 2.0 ** -24, (eb, eb_ref)
+    # the same FP32 product without the column has the same tiles and k-slices
+    # when the extra column needs no extra 64-wide tile: then dW is identical
+    if prec == 0 and N > 16 and (N + 63) // 64 == (N + 64) // 64:
+        plain = host(ops().gemm(dev(dZ), dev(X), transA=True))
+        assert np.array_equal(plain.view(np.uint32), dW.view(np.uint32))
+
+
+def test_fused_bias_grad_k_zero_and_empty_columns():
+    """K = 0: dW = 0 and db = 0; N = 0: only db."""
+    import torch
+    say("fused bias grad edge cases")
+    cs = torch.full((5,), float("nan"), device="cuda")
+    out = host(ops().gemm(torch.empty((0, 5), device="cuda"), torch.empty((0, 3), device="cuda"),
+                          transA=True, colsum=cs))
+    assert not out.any() and not host(cs).any()
+    dZ = np.random.default_rng(3).standard_normal((40, 5)).astype(np.float32)
+    cs2 = torch.full((5,), float("nan"), device="cuda")
+    ops().gemm(dev(dZ), torch.empty((40, 0), device="cuda"), transA=True, colsum=cs2)
+    np.testing.assert_allclose(host(cs2), dZ.astype(np.float64).sum(0), rtol=1e-5, atol=1e-5)
