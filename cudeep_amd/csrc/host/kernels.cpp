@@ -14,6 +14,7 @@
 #include "../../../include/cudeep/kernels/matmul.hpp"
 #include "../../../include/cudeep/kernels/reduce.hpp"
 #include "../../../include/cudeep/kernels/unary.hpp"
+#include "../../../include/cudeep/memory.hpp"
 
 namespace cudeep {
 namespace kernels {
@@ -49,6 +50,29 @@ int act_code(ActivationType a) {
     throw std::runtime_error("unknown activation");
 }
 
+// Scratch for one launch.  On the null stream it comes from the runtime's
+// exact-size MemoryPool cache -- after the first call of a size a map lookup,
+// where the stream-ordered pool costs tens of microseconds of host time for
+// a large block -- and is handed back when the launch is enqueued: the next
+// user of the block is ordered after it by the null stream.  On any other
+// stream the C-ABI allocates stream-ordered itself (a cached block could
+// otherwise reach a concurrent stream while still in use).
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    Workspace(size_t n, hipStream_t s) {
+        if (n > 0 && s == nullptr) {
+            ptr = device_malloc(n);
+            bytes = n;
+        }
+    }
+    ~Workspace() {
+        if (ptr) device_free(ptr);
+    }
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+};
+
 }  // namespace
 
 void set_conv_algorithm(ConvAlgorithm a) { g_conv_algo = (int)a; }
@@ -74,9 +98,10 @@ void launch_matmul_ex(const float* A, const float* B, float* C, int64_t M, int64
                       hipStream_t stream, int precision) {
     const int prec = precision >= 0 ? precision : g_precision.load();
     const int bm = bias ? (bias_per_col ? CDX_BIAS_COL : CDX_BIAS_ROW) : CDX_BIAS_NONE;
-    CUDEEP_CHECK_CDX(cdx_gemm_ex(prec, transA ? CDX_OP_T : CDX_OP_N, transB ? CDX_OP_T : CDX_OP_N,
-                                 M, N, K, A, lda, B, ldb, C, ldc, bias, bm, epi_code(epilogue),
-                                 stream));
+    const int oa = transA ? CDX_OP_T : CDX_OP_N, ob = transB ? CDX_OP_T : CDX_OP_N;
+    Workspace ws(cdx_gemm_workspace_size(prec, oa, ob, M, N, K), stream);
+    CUDEEP_CHECK_CDX(cdx_gemm_ex_ws(prec, oa, ob, M, N, K, A, lda, B, ldb, C, ldc, bias, bm,
+                                    epi_code(epilogue), ws.ptr, ws.bytes, stream));
 }
 
 void launch_linear_weight_grad(const float* dz, const float* x, float* grad_w, float* grad_b,
@@ -84,9 +109,12 @@ void launch_linear_weight_grad(const float* dz, const float* x, float* grad_w, f
                                hipStream_t stream, int precision) {
     const int prec = precision >= 0 ? precision : g_precision.load();
     const int64_t ldz = out_features > 1 ? out_features : 1, ldx = in_features > 1 ? in_features : 1;
+    Workspace ws(cdx_gemm_fused_workspace_size(prec, CDX_OP_T, CDX_OP_N, out_features,
+                                               in_features, batch, grad_b != nullptr),
+                 stream);
     CUDEEP_CHECK_CDX(cdx_gemm_fused(prec, CDX_OP_T, CDX_OP_N, out_features, in_features, batch,
                                     dz, ldz, x, ldx, grad_w, in_features, nullptr, CDX_BIAS_NONE,
-                                    CDX_EPI_NONE, nullptr, 0, grad_b, nullptr, 0, stream));
+                                    CDX_EPI_NONE, nullptr, 0, grad_b, ws.ptr, ws.bytes, stream));
 }
 
 void launch_matmul_dgemm_ex(const double* A, const double* B, double* C, int64_t M, int64_t N,
@@ -159,13 +187,16 @@ void launch_conv2d_forward_kernel<float>(const float* input, const float* weight
     const bool wino = algo == ConvAlgorithm::Winograd ||
                       (algo == ConvAlgorithm::Auto && wino_ok && OH * OW >= 16);
     if (wino) {
+        Workspace ws(cdx_conv2d_winograd_workspace_size(batch, IC, OC, IH, IW, PH, PW), stream);
         CUDEEP_CHECK_CDX(cdx_conv2d_forward_winograd_f32(input, weight, bias, output, batch, IC,
                                                          OC, IH, IW, PH, PW, g_precision.load(),
-                                                         nullptr, 0, stream));
+                                                         ws.ptr, ws.bytes, stream));
     } else {
+        Workspace ws(cdx_conv2d_forward_workspace_size(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW),
+                     stream);
         CUDEEP_CHECK_CDX(cdx_conv2d_forward_f32(input, weight, bias, output, batch, IC, OC, IH, IW,
                                                 KH, KW, SH, SW, PH, PW, g_precision.load(),
-                                                nullptr, 0, stream));
+                                                ws.ptr, ws.bytes, stream));
     }
 }
 
@@ -199,13 +230,19 @@ void launch_conv2d_backward_data_kernel<float>(const float* grad_output, const f
                       (algo == ConvAlgorithm::Auto && wino_ok && (int64_t)IH * IW >= 16 &&
                        prec != CDX_PREC_FP32);
     if (wino) {
+        Workspace ws(cdx_conv2d_backward_data_winograd_workspace_size(batch, IC, OC, IH, IW, PH,
+                                                                      PW),
+                     stream);
         CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_winograd_f32(grad_output, weight, grad_input,
                                                                batch, IC, OC, IH, IW, PH, PW,
-                                                               prec, nullptr, 0, stream));
+                                                               prec, ws.ptr, ws.bytes, stream));
     } else {
+        Workspace ws(cdx_conv2d_backward_data_workspace_size(batch, IC, OC, IH, IW, KH, KW, SH, SW,
+                                                             PH, PW),
+                     stream);
         CUDEEP_CHECK_CDX(cdx_conv2d_backward_data_f32(grad_output, weight, grad_input, batch, IC,
                                                       OC, IH, IW, KH, KW, SH, SW, PH, PW, prec,
-                                                      nullptr, 0, stream));
+                                                      ws.ptr, ws.bytes, stream));
     }
 }
 
@@ -223,9 +260,12 @@ void launch_conv2d_backward_weight_kernel<float>(const float* grad_output, const
                                                  float* grad_weight, int batch, int IC, int OC,
                                                  int IH, int IW, int KH, int KW, int SH, int SW,
                                                  int PH, int PW, hipStream_t stream) {
+    Workspace ws(cdx_conv2d_backward_weight_workspace_size(batch, IC, OC, IH, IW, KH, KW, SH, SW,
+                                                           PH, PW),
+                 stream);
     CUDEEP_CHECK_CDX(cdx_conv2d_backward_weight_f32(grad_output, input, grad_weight, batch, IC,
                                                     OC, IH, IW, KH, KW, SH, SW, PH, PW,
-                                                    g_precision.load(), nullptr, 0, stream));
+                                                    g_precision.load(), ws.ptr, ws.bytes, stream));
 }
 
 template <>
@@ -283,18 +323,21 @@ void launch_broadcast_add_row_kernel<double>(const double* m, const double* row,
 template <>
 void launch_sum_reduce_rows_kernel<float>(const float* in, float* out, int64_t rows, int64_t cols,
                                           hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_sum_reduce_rows_f32(in, out, rows, cols, nullptr, 0, s));
+    Workspace ws(cdx_sum_reduce_rows_workspace_size(rows, cols), s);
+    CUDEEP_CHECK_CDX(cdx_sum_reduce_rows_f32(in, out, rows, cols, ws.ptr, ws.bytes, s));
 }
 
 template <>
 void launch_sum_reduce_rows_kernel<double>(const double* in, double* out, int64_t rows,
                                            int64_t cols, hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_sum_reduce_rows_f64(in, out, rows, cols, nullptr, 0, s));
+    Workspace ws(cdx_sum_reduce_rows_workspace_size(rows, cols), s);
+    CUDEEP_CHECK_CDX(cdx_sum_reduce_rows_f64(in, out, rows, cols, ws.ptr, ws.bytes, s));
 }
 
 template <typename T>
 void launch_sum_kernel(const T* input, T* output, int64_t n, hipStream_t s) {
-    CUDEEP_CHECK_CDX(cdx_sum(input, output, n, dtype_code<T>(), nullptr, 0, s));
+    Workspace ws(cdx_sum_workspace_size(dtype_code<T>()), s);
+    CUDEEP_CHECK_CDX(cdx_sum(input, output, n, dtype_code<T>(), ws.ptr, ws.bytes, s));
 }
 
 template <>
