@@ -1,0 +1,1069 @@
+// Kernels of the split-precision ("TF32 mode") and 16-bit-operand GEMMs
+// and their templated launchers.  The explicit instantiations live in
+// gemm_split_*.hip (compiled in parallel); gemm_bf16x3.hip holds the
+// configuration choice and the library entry points.
+//
+// "TF32-mode" GEMM: explicit bf16x3 split-precision MFMA on gfx950
+// (v_mfma_f32_16x16x32_bf16).
+//
+// Replaces the reference's TF32 tensor-core kernels (sgemm_tc_kernel,
+// sgemm_tc_general_kernel, sgemm_persistent_kernel, ...;
+// src/kernels/matmul_kernel.cu:78-452, :942-1143), which feed raw fp32 bits
+// to mma.sync...tf32.  CDNA4 has no TF32 datapath, so each fp32 operand x is
+// split once, while it is staged into LDS, into
+//     hi = bf16_rne(x),   lo = bf16_rne(x - hi)        (x - hi is exact)
+// and every product is formed as  hi*hi + hi*lo + lo*hi  with fp32
+// accumulation.  |x - hi| <= 2^-8 |x| and |x - hi - lo| <= 2^-17 |x|; the
+// dropped lo*lo term is <= 2^-16 |ab|, so each product carries a relative
+// error of at most 2^-15 ~= 3.1e-5 -- against up to ~2e-3 for TF32 operand
+// truncation.  The four-term variant (TERMS = 4) adds lo*lo: then only the
+// split residual remains (<= 2^-16 per product), and operands with at most
+// 16 significant bits -- TF32-rounded inputs among them -- multiply exactly,
+// leaving fp32 accumulation as the only error.
+//
+// Structure: BM x BN output tile per workgroup; fp32 global loads into VGPRs
+// (double-buffered against the MFMAs of the current k-tile), split in
+// registers, written to LDS as k-contiguous bf16 hi / lo planes ([mn][BK+8]),
+// so every MFMA operand is one 16-byte LDS read (8 consecutive k).
+// m/n-contiguous operands are transposed in registers on the way in (each
+// thread loads a 4x4 block and writes four k-runs).  Epilogue as in the
+// FP32 kernel (bias per row/column, activation, plain or NCHW output map).
+//
+// The same kernel, instantiated for 16-bit inputs (IN = f16 or bf16), is the
+// FP16 / BF16 GEMM (the reference's hgemm_tc_kernel, matmul_kernel.cu:745-930):
+// the operands are copied into a single k-contiguous plane and multiplied
+// with one v_mfma_f32_16x16x32_{f16,bf16} per fragment pair, accumulating
+// and writing fp32.
+#pragma once
+
+#include <type_traits>
+
+#include "cdx_internal.hpp"
+
+namespace cdx {
+namespace split {
+
+
+// Operand element types of the kernel (IN template parameter).
+constexpr int kInF32 = 0;   // fp32, split into bf16 hi / lo on the way into LDS
+constexpr int kInF16 = 1;   // fp16, used as is
+constexpr int kInBF16 = 2;  // bf16, used as is
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+struct KParams {
+    const void* A; const void* B; float* C; const float* bias;
+    int64_t M, N, K, lda, ldb, ldc, n_split, ldc_split;
+    int bias_mode, epilogue;
+    int64_t k_chunk;    // split-K: k-range per blockIdx.y slice (gridDim.y > 1)
+    int64_t sa, sb, sc; // batch strides (elements) for blockIdx.z
+    int64_t batch;      // gridDim.z
+    const float* aux;   // activation-backward epilogues: aux [M, N], leading dim ldaux
+    int64_t ldaux;
+};
+
+__device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
+    __bf16 h = (__bf16)x;
+    float r = x - (float)h;
+    __bf16 l = (__bf16)r;
+    hi = __builtin_bit_cast(unsigned short, h);
+    lo = __builtin_bit_cast(unsigned short, l);
+}
+
+__device__ __forceinline__ float ld_guard(const float* p, bool ok) { return ok ? *p : 0.0f; }
+
+// A wave-uniform address made explicit (scalar registers): loads of the form
+// uniform(p) + 32-bit offset can then use the scalar-base global load and
+// keep one VGPR of address per load instead of a 64-bit VGPR pair.
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
+// A load through a global-address-space pointer.  A pointer rebuilt from
+// integers (uniform_ptr) is generic to the compiler, whose flat loads also
+// count against the LDS counter: every wait on an LDS read would then wait
+// for the outstanding global loads too.
+template <class T>
+__device__ __forceinline__ T load_global(const char* p) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    static_assert(sizeof(T) == 16 || sizeof(T) == 8, "16- or 8-byte loads");
+    if constexpr (sizeof(T) == 16)
+        return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) u32x4*)(p));
+    else
+        return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) u32x2*)(p));
+}
+
+// Loads an operand tile for the k-range [k0, k0+BK) and mn-range
+// [mn0, mn0+BMN) into registers, as 4x4 blocks (4 mn x 4 k).  KCONTIG says
+// whether k is the contiguous dimension in memory.
+template <int BMN, int BK, int NT, bool KCONTIG, bool CHECK>
+struct SplitLoader {
+    static constexpr int NB = (BMN / 4) * (BK / 4);   // 4x4 blocks in the tile
+    static constexpr int NV = (NB + NT - 1) / NT;
+    static_assert(NB % NT == 0 || NB < NT, "tile not divisible by thread count");
+    float4 v[NV][4];  // v[blk][q]: KCONTIG -> mn row q, 4 k;  else k row q, 4 mn
+
+    // 4x4 block -> (bc, br).  k-contiguous: consecutive threads walk k
+    // (bc), so a wavefront reads 128 contiguous bytes per row and its
+    // 8-byte LDS stores land on consecutive banks.  m/n-contiguous: the
+    // 8 k-blocks of a column group go to 8 consecutive threads (br fastest),
+    // so each global row is still read as 128 contiguous bytes (8 threads x
+    // 16 B) while the transposed LDS stores of 8 consecutive threads fill 16
+    // consecutive banks instead of striding 4 rows apart (an 8-way conflict).
+    __device__ __forceinline__ static void block_coords(int blk, int& bc, int& br) {
+        if (KCONTIG) { bc = blk % (BK / 4); br = blk / (BK / 4); }
+        else         { br = blk % (BK / 4); bc = blk / (BK / 4); }
+    }
+
+    __device__ __forceinline__ void load(const void* __restrict__ Xv, int64_t ld,
+                                         int64_t mn0, int64_t k0, int64_t mnmax,
+                                         int64_t kmax, bool vec, int tid) {
+        const float* __restrict__ X = static_cast<const float*>(Xv);
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;   // block index along the contiguous / strided dimension
+            block_coords(blk, bc, br);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int64_t gr, gc, rmax, cmax;
+                if (KCONTIG) { gr = mn0 + br * 4 + q; gc = k0 + bc * 4; rmax = mnmax; cmax = kmax; }
+                else         { gr = k0 + br * 4 + q;  gc = mn0 + bc * 4; rmax = kmax; cmax = mnmax; }
+                const float* p = X + gr * ld + gc;
+                if (!CHECK) {
+                    v[b][q] = *reinterpret_cast<const float4*>(p);
+                } else if (vec && gr < rmax && gc + 3 < cmax) {
+                    v[b][q] = *reinterpret_cast<const float4*>(p);
+                } else {
+                    bool rok = gr < rmax;
+                    v[b][q].x = ld_guard(p + 0, rok && gc + 0 < cmax);
+                    v[b][q].y = ld_guard(p + 1, rok && gc + 1 < cmax);
+                    v[b][q].z = ld_guard(p + 2, rok && gc + 2 < cmax);
+                    v[b][q].w = ld_guard(p + 3, rok && gc + 3 < cmax);
+                }
+            }
+        }
+    }
+
+    // Unchecked load, address = wave-uniform base + one 32-bit per-thread
+    // byte offset (`off`, from tile_offset()).  A thread's later blocks sit a
+    // uniform distance from its first (NT blocks further on: NT / (BK/4)
+    // block rows), so only one VGPR of address is live per operand.  The
+    // caller guarantees the tile is in bounds and the offsets fit 32 bits.
+    static constexpr int ES = 4;
+    __device__ __forceinline__ static uint32_t tile_offset(uint32_t ld_bytes, int tid) {
+        int bc, br;
+        block_coords(tid, bc, br);
+        return (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 4 * ES);
+    }
+    __device__ __forceinline__ static uint64_t block_step(int b, uint32_t ld_bytes) {
+        constexpr int ROWS = NT / (BK / 4) * 4;   // block rows between a thread's blocks
+        return KCONTIG ? (uint64_t)b * ROWS * ld_bytes : (uint64_t)b * ROWS * ES;
+    }
+    // k-contiguous operands: the four rows' bases in scalar registers (with
+    // both operands k-contiguous the 64-bit per-row addresses otherwise spill)
+    __device__ __forceinline__ static const char* row_base(const char* p) {
+        return KCONTIG ? uniform_ptr(p) : p;
+    }
+    __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
+                                            uint32_t off) {
+        static_assert(NB % NT == 0, "whole blocks per thread");
+#pragma unroll
+        for (int b = 0; b < NV; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[b][q] = load_global<float4>(
+                    row_base(base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes)) + off);
+    }
+
+    // Writes hi / lo planes, layout [mn][STRIDE] (k contiguous), ushort units.
+    template <int STRIDE>
+    __device__ __forceinline__ void store(unsigned short* __restrict__ hi,
+                                          unsigned short* __restrict__ lo, int tid) const {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;
+            block_coords(blk, bc, br);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {       // r indexes mn within the block
+                float x[4];                     // 4 consecutive k at this mn
+                if (KCONTIG) {
+                    x[0] = v[b][r].x; x[1] = v[b][r].y; x[2] = v[b][r].z; x[3] = v[b][r].w;
+                } else {
+                    // v[b][q] holds k row q; pick component r
+                    for (int q = 0; q < 4; ++q) {
+                        const float4& t = v[b][q];
+                        x[q] = r == 0 ? t.x : r == 1 ? t.y : r == 2 ? t.z : t.w;
+                    }
+                }
+                unsigned short h[4], l[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) split_bf16(x[q], h[q], l[q]);
+                int mn = (KCONTIG ? br : bc) * 4 + r;
+                int kk = (KCONTIG ? bc : br) * 4;
+                uint2 hv, lv;
+                hv.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+                hv.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+                lv.x = (uint32_t)l[0] | ((uint32_t)l[1] << 16);
+                lv.y = (uint32_t)l[2] | ((uint32_t)l[3] << 16);
+                *reinterpret_cast<uint2*>(hi + mn * STRIDE + kk) = hv;
+                *reinterpret_cast<uint2*>(lo + mn * STRIDE + kk) = lv;
+            }
+        }
+    }
+};
+
+// 16-bit operands: the same 4x4-block walk as SplitLoader (same global
+// coalescing and LDS bank pattern), 8-byte loads of four 16-bit values,
+// copied unchanged into one k-contiguous plane.
+template <int BMN, int BK, int NT, bool KCONTIG, bool CHECK>
+struct HalfLoader {
+    static constexpr int NB = (BMN / 4) * (BK / 4);
+    static constexpr int NV = (NB + NT - 1) / NT;
+    static_assert(NB % NT == 0 || NB < NT, "tile not divisible by thread count");
+    uint2 v[NV][4];   // four 16-bit values each: KCONTIG -> mn row q, 4 k; else k row q, 4 mn
+
+    __device__ __forceinline__ static void block_coords(int blk, int& bc, int& br) {
+        SplitLoader<BMN, BK, NT, KCONTIG, CHECK>::block_coords(blk, bc, br);
+    }
+
+    __device__ __forceinline__ void load(const void* __restrict__ Xv, int64_t ld,
+                                         int64_t mn0, int64_t k0, int64_t mnmax,
+                                         int64_t kmax, bool vec, int tid) {
+        const unsigned short* __restrict__ X = static_cast<const unsigned short*>(Xv);
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;
+            block_coords(blk, bc, br);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                int64_t gr, gc, rmax, cmax;
+                if (KCONTIG) { gr = mn0 + br * 4 + q; gc = k0 + bc * 4; rmax = mnmax; cmax = kmax; }
+                else         { gr = k0 + br * 4 + q;  gc = mn0 + bc * 4; rmax = kmax; cmax = mnmax; }
+                const unsigned short* p = X + gr * ld + gc;
+                if (!CHECK || (vec && gr < rmax && gc + 3 < cmax)) {
+                    v[b][q] = *reinterpret_cast<const uint2*>(p);
+                } else {
+                    const bool rok = gr < rmax;
+                    uint32_t e[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) e[t] = (rok && gc + t < cmax) ? p[t] : 0u;
+                    v[b][q].x = e[0] | (e[1] << 16);
+                    v[b][q].y = e[2] | (e[3] << 16);
+                }
+            }
+        }
+    }
+
+    // As SplitLoader::tile_offset / load_at (four 16-bit elements per load).
+    static constexpr int ES = 2;
+    __device__ __forceinline__ static uint32_t tile_offset(uint32_t ld_bytes, int tid) {
+        int bc, br;
+        block_coords(tid, bc, br);
+        return (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 4 * ES);
+    }
+    __device__ __forceinline__ static uint64_t block_step(int b, uint32_t ld_bytes) {
+        constexpr int ROWS = NT / (BK / 4) * 4;
+        return KCONTIG ? (uint64_t)b * ROWS * ld_bytes : (uint64_t)b * ROWS * ES;
+    }
+    // k-contiguous operands: the four rows' bases in scalar registers (with
+    // both operands k-contiguous the 64-bit per-row addresses otherwise spill)
+    __device__ __forceinline__ static const char* row_base(const char* p) {
+        return KCONTIG ? uniform_ptr(p) : p;
+    }
+    __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
+                                            uint32_t off) {
+        static_assert(NB % NT == 0, "whole blocks per thread");
+#pragma unroll
+        for (int b = 0; b < NV; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[b][q] = load_global<uint2>(
+                    row_base(base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes)) + off);
+    }
+
+    // Writes the plane, layout [mn][STRIDE] (k contiguous), ushort units.
+    template <int STRIDE>
+    __device__ __forceinline__ void store(unsigned short* __restrict__ plane, int tid) const {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int blk = tid + b * NT;
+            if (NB < NT && blk >= NB) break;
+            int bc, br;
+            block_coords(blk, bc, br);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {       // r indexes mn within the block
+                uint2 hv;
+                if (KCONTIG) {
+                    hv = v[b][r];
+                } else {
+                    // v[b][q] holds k row q; take its 16-bit element r
+                    uint32_t x[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t w = r < 2 ? v[b][q].x : v[b][q].y;
+                        x[q] = (r & 1) ? (w >> 16) : (w & 0xFFFFu);
+                    }
+                    hv.x = x[0] | (x[1] << 16);
+                    hv.y = x[2] | (x[3] << 16);
+                }
+                const int mn = (KCONTIG ? br : bc) * 4 + r;
+                const int kk = (KCONTIG ? bc : br) * 4;
+                *reinterpret_cast<uint2*>(plane + mn * STRIDE + kk) = hv;
+            }
+        }
+    }
+};
+
+// Special operand values in the split kernels.  The reference's TF32 MMA
+// takes raw fp32 bits (matmul_kernel.cu:186-201), so an infinite operand
+// gives IEEE results: +-Inf, or NaN for Inf * 0 and Inf - Inf.  The split
+// cannot: for x = +-Inf, lo = bf16(x - hi) = bf16(Inf - Inf) = NaN; for a
+// finite x at or beyond bf16's rounding limit (|x| >= 0x7F7F8000), hi
+// rounds to +-Inf and lo = x - hi = -+Inf, so lo*hi(b) and hi*hi(b) are
+// infinities of opposite sign (or lo*0 = NaN).  Either way EVERY output the
+// element touches -- its whole row of C (A) or column (B) -- comes out NaN,
+// and no output untouched by such an element does (a NaN operand gives NaN
+// in both arithmetics; finite sums that overflow stay +-Inf).  So the
+// outputs to repair are exactly the NaN accumulators: after the main loop,
+// each wave tests its 16 x 16 accumulator blocks (one compare per value and
+// one ballot per block, no cost in the k-loop) and recomputes the blocks
+// holding a NaN with FP32 MFMAs straight from global memory (IEEE products,
+// as the reference's), replacing only the NaN values.  Runs in the same
+// k-range as the accumulators (a split-K slice recomputes its own slice).
+// In code: nan_bits() (before the epilogue) records which accumulator values
+// are NaN, one bit per value; the epilogue writes as usual; then, only when
+// some bit is set, repair_nan_outputs() walks the wave's 16 x 16 blocks (a
+// loop, not unrolled: nothing of it is live during the main loop), recomputes
+// each block holding a NaN with FP32 MFMAs straight from global memory and
+// rewrites just the NaN positions through the same epilogue.  The operands
+// are addressed relative to the workgroup tile: A0 = &op(A)(bm, 0),
+// B0 = &op(B)(0, bn).
+template <int FM, int FN>
+struct NanBits {
+    static constexpr int NW = (FM * FN + 7) / 8;   // 4 bits (values) per block
+    uint32_t w[NW];
+};
+
+template <int FM, int FN>
+__device__ __forceinline__ bool any_nan(const floatx4 (&acc)[FM][FN]) {
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nan |= acc[i][j][e] != acc[i][j][e];
+    return __builtin_amdgcn_ballot_w64(nan) != 0;     // wave-uniform
+}
+
+template <int FM, int FN>
+__device__ __forceinline__ void nan_bits(const floatx4 (&acc)[FM][FN], NanBits<FM, FN>& nb) {
+#pragma unroll
+    for (int w = 0; w < NanBits<FM, FN>::NW; ++w) nb.w[w] = 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int bit = (i * FN + j) * 4 + e;
+                if (acc[i][j][e] != acc[i][j][e]) nb.w[bit >> 5] |= 1u << (bit & 31);
+            }
+}
+
+template <int FM, int FN, int OPA, int OPB>
+__device__ __forceinline__ void repair_nan_outputs(const NanBits<FM, FN>& nb, const EpiArgs& e,
+                                                   const float* A0, int64_t lda,
+                                                   const float* B0, int64_t ldb, int64_t K,
+                                                   int64_t bm, int64_t bn, int wm0, int wn0,
+                                                   int lane) {
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int64_t rows = e.M - bm, cols = e.N - bn;   // valid extent of this tile
+#pragma unroll 1
+    for (int blk = 0; blk < FM * FN; ++blk) {
+        uint32_t word = nb.w[0];
+#pragma unroll
+        for (int w = 1; w < NanBits<FM, FN>::NW; ++w)
+            if ((blk >> 3) == w) word = nb.w[w];
+        const uint32_t nib = (word >> ((blk & 7) * 4)) & 0xFu;
+        if (__builtin_amdgcn_ballot_w64(nib != 0) == 0) continue;   // wave-uniform
+        const int i = blk / FN, j = blk % FN;
+        // v_mfma_f32_16x16x4_f32: this lane feeds A(m, k0 + lq) and
+        // B(k0 + lq, n); rows, columns and k outside the problem read as 0
+        const int64_t m = wm0 + i * 16 + l16, n = wn0 + j * 16 + l16;
+        const bool mok = m < rows, nok = n < cols;
+        floatx4 r = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int64_t k0 = 0; k0 < K; k0 += 4) {
+            const int64_t k = k0 + lq;
+            const float a = (mok && k < K) ? (OPA == CDX_OP_N ? A0[m * lda + k] : A0[k * lda + m]) : 0.0f;
+            const float b = (nok && k < K) ? (OPB == CDX_OP_N ? B0[k * ldb + n] : B0[n * ldb + k]) : 0.0f;
+            r = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, r, 0, 0, 0);
+        }
+        const int64_t ncol = wn0 + j * 16 + l16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int64_t mrow = wm0 + i * 16 + 4 * lq + q;
+            if (((nib >> q) & 1u) && mrow < rows && ncol < cols)
+                store_one(e, bm + mrow, bn + ncol, r[q]);
+        }
+    }
+}
+
+// ALIGNED_ONLY: the configuration is only instantiated without bounds
+// checks (its checked variant would not fit the register file); the
+// dispatcher sends it aligned problems only.
+// PIPE: 1 = one register staging set, last k-tile peeled; 2 = two staging
+// sets (load k+2 while splitting k+1) with MFMA / VALU interleave hints.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int GROUP_M_, bool ALIGNED_ONLY_ = false,
+          int PIPE_ = 1>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr int GROUP_M = GROUP_M_;
+    static constexpr bool ALIGNED_ONLY = ALIGNED_ONLY_;
+    static constexpr int PIPE = PIPE_;
+    static constexpr int WAVES_M = BM / WM, WAVES_N = BN / WN;
+    static constexpr int NT = WAVES_M * WAVES_N * 64;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+};
+
+__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int group_m,
+                                              int& tm, int& tn) {
+    int nb = gridDim.x;
+    int bid = blockIdx.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    int per_group = group_m * tiles_n;
+    int g = bid / per_group;
+    int first_m = g * group_m;
+    int gsize = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
+    int in_g = bid - g * per_group;
+    tm = first_m + in_g % gsize;
+    tn = in_g / gsize;
+}
+
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN>
+__global__ __launch_bounds__(CF::NT)
+void gemm_bf16x3_kernel(KParams p, int vec) {
+    constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
+    constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
+    static_assert(BK % 32 == 0, "BK must be a multiple of 32");
+    constexpr bool H16 = IN != kInF32;             // 16-bit operands: one plane
+    constexpr int NPL = H16 ? 1 : 2;               // planes per operand
+    constexpr int ES = H16 ? 2 : 4;                // operand element bytes
+    constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
+    constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
+    constexpr int B_OFF = NPL * A_PLANE;           // stage layout: A hi [, A lo], B hi [, B lo]
+    constexpr int STAGE = NPL * (A_PLANE + B_PLANE);
+    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave / CF::WAVES_N) * CF::WM;
+    const int wn0 = (wave % CF::WAVES_N) * CF::WN;
+    const int l16 = lane & 15;
+    const int lq = lane >> 4;
+
+    int tiles_m = (int)ceil_div(p.M, BM), tiles_n = (int)ceil_div(p.N, BN);
+    int tm, tn;
+    tile_of_block(tiles_m, tiles_n, CF::GROUP_M, tm, tn);
+    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+
+    // Split-K slice: blockIdx.y owns k in [y*k_chunk, min(K, (y+1)*k_chunk))
+    // and writes a plain [M, N] partial (the reduction applies the epilogue).
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? k0 : k0 * p.lda);
+        p.B = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? k0 * p.ldb : k0);
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
+    if (gridDim.z > 1) {
+        p.A = static_cast<const char*>(p.A) + ES * (int64_t)blockIdx.z * p.sa;
+        p.B = static_cast<const char*>(p.B) + ES * (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
+    }
+    const bool v = vec != 0;
+
+    using LoaderA = std::conditional_t<H16, HalfLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>,
+                                       SplitLoader<BM, BK, NT, OPA == CDX_OP_N, CHECK>>;
+    using LoaderB = std::conditional_t<H16, HalfLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK>,
+                                       SplitLoader<BN, BK, NT, OPB == CDX_OP_T, CHECK>>;
+    LoaderA la;
+    LoaderB lb;
+
+    auto load_into = [&](LoaderA& a, LoaderB& b, int64_t k0) {
+        a.load(p.A, p.lda, bm, k0, p.M, p.K, v, tid);
+        b.load(p.B, p.ldb, bn, k0, p.N, p.K, v, tid);
+    };
+    auto store_from = [&](const LoaderA& a, const LoaderB& b, int buf) {
+        unsigned short* s = lds + buf * STAGE;
+        if constexpr (H16) {
+            a.template store<STRIDE>(s, tid);
+            b.template store<STRIDE>(s + B_OFF, tid);
+        } else {
+            a.template store<STRIDE>(s, s + A_PLANE, tid);
+            b.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, tid);
+        }
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // MFMAs over the k-tile held in LDS stage `buf`
+    auto compute = [&](int buf) {
+        const unsigned short* s = lds + buf * STAGE;
+        const unsigned short* sAh = s;
+        const unsigned short* sAl = s + A_PLANE;       // fp32 operands only
+        const unsigned short* sBh = s + B_OFF;
+        const unsigned short* sBl = sBh + B_PLANE;     // fp32 operands only
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            if constexpr (H16) {
+                // 16-bit operands: one MFMA per fragment pair
+                shortx8 a16[FM], b16[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    a16[i] = *reinterpret_cast<const shortx8*>(
+                        sAh + (wm0 + i * 16 + l16) * STRIDE + kk + 8 * lq);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    b16[j] = *reinterpret_cast<const shortx8*>(
+                        sBh + (wn0 + j * 16 + l16) * STRIDE + kk + 8 * lq);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        if constexpr (IN == kInF16)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                __builtin_bit_cast(halfx8, a16[i]), __builtin_bit_cast(halfx8, b16[j]),
+                                acc[i][j], 0, 0, 0);
+                        else
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(bf16x8, a16[i]), __builtin_bit_cast(bf16x8, b16[j]),
+                                acc[i][j], 0, 0, 0);
+                    }
+                continue;
+            }
+            bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int off = (wm0 + i * 16 + l16) * STRIDE + kk + 8 * lq;
+                ah[i] = *reinterpret_cast<const bf16x8*>(sAh + off);
+                al[i] = *reinterpret_cast<const bf16x8*>(sAl + off);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int off = (wn0 + j * 16 + l16) * STRIDE + kk + 8 * lq;
+                bh[j] = *reinterpret_cast<const bf16x8*>(sBh + off);
+                bl[j] = *reinterpret_cast<const bf16x8*>(sBl + off);
+            }
+            if (TERMS == 4) {
+                // Two-level accumulation: the four products of this 32-k
+                // step (small terms first) are summed from zero, so the
+                // MFMA's internal roundings act on a 32-term partial sum
+                // and only the one add below rounds at the size of C.  One
+                // row of tiles at a time keeps the partials to FN registers.
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    floatx4 t[FN];
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            al[i], bl[j], floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], t[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], t[j], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], t[j], 0, 0, 0);
+                        acc[i][j] += t[j];
+                    }
+                }
+                continue;
+            }
+            // small cross terms first, then the dominant hi*hi term
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int64_t nk = ceil_div(p.K, BK);
+    // the two-set pipeline only where it fits the register file unchecked
+    constexpr int PIPE = (CF::PIPE == 2 && !CHECK && (TERMS == 3 || H16)) ? 2 : 1;
+    if (PIPE == 2 && nk >= 2) {
+        // Two register staging sets: tile k+2 is loaded while tile k+1 is
+        // split and stored from the set loaded one iteration earlier, so
+        // the split never waits on global memory; the scheduling hints
+        // interleave that VALU / LDS-write work with the MFMAs.
+        LoaderA la1;
+        LoaderB lb1;
+        auto hints = [&]() {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // VALU
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
+            }
+        };
+        load_into(la, lb, 0);
+        load_into(la1, lb1, BK);
+        store_from(la, lb, 0);
+        __syncthreads();
+        int64_t kt = 0;
+        // loop invariant (kt even): stage 0 holds tile kt, set 1 tile kt+1
+        for (; kt + 3 < nk; kt += 2) {
+            load_into(la, lb, (kt + 2) * BK);
+            compute(0);
+            store_from(la1, lb1, 1);
+            hints();
+            __syncthreads();
+            load_into(la1, lb1, (kt + 3) * BK);
+            compute(1);
+            store_from(la, lb, 0);
+            hints();
+            __syncthreads();
+        }
+        if (kt + 2 < nk) {            // three tiles left
+            load_into(la, lb, (kt + 2) * BK);
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            compute(1);
+            store_from(la, lb, 0);
+            __syncthreads();
+            compute(0);
+        } else {                      // two tiles left
+            compute(0);
+            store_from(la1, lb1, 1);
+            __syncthreads();
+            compute(1);
+        }
+    } else if (nk > 0) {
+        // One staging set, one barrier per k-tile; the last tile is peeled
+        // so the loop body has no branch around the load / store.
+        load_into(la, lb, 0);
+        store_from(la, lb, 0);
+        __syncthreads();
+        int64_t kt = 0;
+        for (; kt + 1 < nk; ++kt) {
+            const int buf = (int)(kt & 1);
+            load_into(la, lb, (kt + 1) * BK);
+            compute(buf);
+            store_from(la, lb, buf ^ 1);
+            __syncthreads();
+        }
+        compute((int)(kt & 1));
+    }
+
+    // epilogue: bias, activation and the output map, straight from the
+    // accumulators; then IEEE values for the outputs an infinite or out-of-
+    // range operand touched (split operands only)
+    const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
+                      p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux};
+    NanBits<FM, FN> nb;
+    const bool repair = !H16 && any_nan(acc);
+    if (repair) nan_bits(acc, nb);
+    write_acc<FM, FN, CHECK, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
+    if constexpr (!H16) {
+        if (repair) {
+            const float* A0 = static_cast<const float*>(p.A) + (OPA == CDX_OP_N ? bm * p.lda : bm);
+            const float* B0 = static_cast<const float*>(p.B) + (OPB == CDX_OP_N ? bn : bn * p.ldb);
+            repair_nan_outputs<FM, FN, OPA, OPB>(nb, epi, A0, p.lda, B0, p.ldb, p.K, bm, bn,
+                                                 wm0, wn0, lane);
+        }
+    }
+}
+
+// 256 x 256 tiles on a two-group ("ping-pong") schedule.  The eight waves
+// form two groups of four, one wave of each group per SIMD; group 0 owns
+// tile rows 0-127, group 1 rows 128-255, each wave a 128 x 64 sub-tile.
+// Every k-tile is worked in four slots separated by workgroup barriers:
+//     MEM_a  read the B fragments and A fragment rows 0-3 of this k-tile;
+//            split + store this thread's A block of the next k-tile (from
+//            registers) into the other LDS stage; load its A block of the
+//            k-tile after that from global memory
+//     MATH_a the MFMAs of A rows 0-3 (registers only)
+//     MEM_b  A fragment rows 4-7; the same store / load for the B block
+//     MATH_b the MFMAs of A rows 4-7
+// Group 1 runs one slot behind group 0 (one extra barrier at the start,
+// group 0 one at the end, so both execute 2 + 4 * nk barriers), so on each
+// SIMD one wave issues MFMAs while the other does its loads, splits and
+// LDS traffic.  Slot order keeps the two LDS stages safe: k-tile t+1 is
+// written in slots 4t..4t+3 (stage (t+1)&1, last read by k-tile t-1 in slot
+// 4t-1) and first read in slot 4t+4.  Global loads are consumed four slots
+// after they are issued.  Aligned problems only (M, N % 256, K % BK, 16-byte
+// operands).  IN = fp32: three terms in gemm_bf16x3_kernel's per-element
+// order (so the same results), BK = 32, LDS 2 x 80 KiB; 16-bit operands: one
+// plane, BK = 64, one MFMA per fragment pair and 32-k step.  Measured at
+// 4096^3 against gemm_bf16x3_kernel's 256 x 256 configurations (the two
+// waves of a SIMD in step): 0.310 against 0.361 ms (bf16x3), 0.172 against
+// 0.234 ms (bf16).
+template <int OPA, int OPB, bool SPLITN, int IN = kInF32>
+__global__ __launch_bounds__(512)
+void gemm_pingpong_kernel(KParams p) {
+    constexpr int BM = 256, BN = 256, NT = 512, GROUP_M = 8;
+    constexpr bool H16 = IN != kInF32;
+    constexpr int BK = H16 ? 64 : 32;
+    constexpr int NK32 = BK / 32;                  // 32-k MFMA steps per k-tile
+    constexpr int NPL = H16 ? 1 : 2;               // planes per operand
+    constexpr int ES = H16 ? 2 : 4;                // operand element bytes
+    constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
+    constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
+    constexpr int B_OFF = NPL * A_PLANE;           // stage: A planes, then B planes
+    constexpr int STAGE = NPL * (A_PLANE + B_PLANE);
+    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int grp = wave >> 2;
+    const int wm0 = grp * 128;
+    const int wn0 = (wave & 3) * 64;
+    const int l16 = lane & 15;
+    const int lq = lane >> 4;
+
+    int tm, tn;
+    tile_of_block((int)(p.M / BM), (int)(p.N / BN), GROUP_M, tm, tn);
+    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? k0 : k0 * p.lda);
+        p.B = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? k0 * p.ldb : k0);
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
+    if (gridDim.z > 1) {
+        p.A = static_cast<const char*>(p.A) + ES * (int64_t)blockIdx.z * p.sa;
+        p.B = static_cast<const char*>(p.B) + ES * (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
+    }
+
+    using LoaderA = std::conditional_t<H16, HalfLoader<BM, BK, NT, OPA == CDX_OP_N, false>,
+                                       SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>>;
+    using LoaderB = std::conditional_t<H16, HalfLoader<BN, BK, NT, OPB == CDX_OP_T, false>,
+                                       SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>>;
+    static_assert(LoaderA::NB % NT == 0 && LoaderB::NB % NT == 0, "whole blocks per thread");
+    LoaderA la;
+    LoaderB lb;
+    auto store_a = [&](unsigned short* s) {
+        if constexpr (H16) la.template store<STRIDE>(s, tid);
+        else la.template store<STRIDE>(s, s + A_PLANE, tid);
+    };
+    auto store_b = [&](unsigned short* s) {
+        if constexpr (H16) lb.template store<STRIDE>(s + B_OFF, tid);
+        else lb.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, tid);
+    };
+
+    floatx4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // fa: fragments of four A rows (one half of the wave's rows), fb: of the
+    // wave's four B columns; [32-k step][plane], plane 0 = hi (or the 16-bit
+    // operand), 1 = lo
+    shortx8 fa[4][NK32][NPL], fb[4][NK32][NPL];
+    auto read_a = [&](const unsigned short* s, int half) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int kk = 0; kk < NK32; ++kk)
+#pragma unroll
+                for (int pl = 0; pl < NPL; ++pl)
+                    fa[i][kk][pl] = *reinterpret_cast<const shortx8*>(
+                        s + pl * A_PLANE + (wm0 + (half * 4 + i) * 16 + l16) * STRIDE + kk * 32 + 8 * lq);
+    };
+    auto read_b = [&](const unsigned short* s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int kk = 0; kk < NK32; ++kk)
+#pragma unroll
+                for (int pl = 0; pl < NPL; ++pl)
+                    fb[j][kk][pl] = *reinterpret_cast<const shortx8*>(
+                        s + B_OFF + pl * B_PLANE + (wn0 + j * 16 + l16) * STRIDE + kk * 32 + 8 * lq);
+    };
+    auto mfma = [](const shortx8& a, const shortx8& b, const floatx4& c) {
+        if constexpr (IN == kInF16)
+            return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, a),
+                                                          __builtin_bit_cast(halfx8, b), c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                           __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    };
+    // MFMAs of fragment rows half*4 .. half*4+3; fp32 operands: lo*hi and
+    // hi*lo first, then hi*hi
+    auto math = [&](int half) {
+        __builtin_amdgcn_s_setprio(1);
+        if constexpr (H16) {
+#pragma unroll
+            for (int kk = 0; kk < NK32; ++kk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[half * 4 + i][j] = mfma(fa[i][kk][0], fb[j][kk][0], acc[half * 4 + i][j]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[half * 4 + i][j] = mfma(fa[i][0][1], fb[j][0][0], acc[half * 4 + i][j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[half * 4 + i][j] = mfma(fa[i][0][0], fb[j][0][1], acc[half * 4 + i][j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[half * 4 + i][j] = mfma(fa[i][0][0], fb[j][0][0], acc[half * 4 + i][j]);
+        }
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // slot boundary: nothing moves across it
+    auto slot = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Global addressing: a wave-uniform base per k-tile plus 32-bit per-
+    // thread offsets (the launcher checks 256 rows of either operand span
+    // less than 4 GiB).  k-contiguous operands step ES*BK bytes per k-tile,
+    // m/n-contiguous ones BK rows.
+    const uint32_t lda_b = (uint32_t)(p.lda * ES), ldb_b = (uint32_t)(p.ldb * ES);
+    const uint32_t offa = LoaderA::tile_offset(lda_b, tid);
+    const uint32_t offb = LoaderB::tile_offset(ldb_b, tid);
+    const char* baseA = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? bm * p.lda : bm);
+    const char* baseB = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? bn : bn * p.ldb);
+    const int64_t stepA = OPA == CDX_OP_N ? (int64_t)ES * BK : (int64_t)BK * p.lda * ES;
+    const int64_t stepB = OPB == CDX_OP_N ? (int64_t)BK * p.ldb * ES : (int64_t)ES * BK;
+
+    const int64_t nk = p.K / BK;
+    la.load_at(baseA, lda_b, offa);
+    lb.load_at(baseB, ldb_b, offb);
+    store_a(lds);
+    store_b(lds);
+    if (nk > 1) {
+        la.load_at(baseA + stepA, lda_b, offa);
+        lb.load_at(baseB + stepB, ldb_b, offb);
+    }
+    __syncthreads();
+    if (grp == 1) slot();
+    // At the top of iteration t: stage t&1 holds k-tile t; la / lb hold (or
+    // are loading) k-tile t+1.
+    for (int64_t t = 0; t < nk; ++t) {
+        const unsigned short* s = lds + (t & 1) * STAGE;
+        unsigned short* sn = lds + ((t + 1) & 1) * STAGE;
+        read_b(s);
+        read_a(s, 0);
+        if (t + 1 < nk) {
+            store_a(sn);
+            if (t + 2 < nk) la.load_at(baseA + (t + 2) * stepA, lda_b, offa);
+        }
+        slot();
+        math(0);
+        slot();
+        read_a(s, 1);
+        if (t + 1 < nk) {
+            store_b(sn);
+            if (t + 2 < nk) lb.load_at(baseB + (t + 2) * stepB, ldb_b, offb);
+        }
+        slot();
+        math(1);
+        slot();
+    }
+    if (grp == 0) slot();
+
+    const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
+                      p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux};
+    NanBits<8, 4> nb;
+    const bool repair = !H16 && any_nan(acc);
+    if (repair) nan_bits(acc, nb);
+    write_acc<8, 4, false, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
+    if constexpr (!H16) {
+        // operands through the loop's own live values: the tile bases and
+        // the byte strides (no other kernel argument is kept across the loop)
+        if (repair)
+            repair_nan_outputs<8, 4, OPA, OPB>(nb, epi, reinterpret_cast<const float*>(baseA),
+                                               (int64_t)(lda_b / 4),
+                                               reinterpret_cast<const float*>(baseB),
+                                               (int64_t)(ldb_b / 4), nk * BK, bm, bn, wm0, wn0, lane);
+    }
+}
+
+template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN = kInF32>
+int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
+    int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
+    if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
+    hipLaunchKernelGGL((gemm_bf16x3_kernel<CF, OPA, OPB, CHECK, SPLITN, TERMS, IN>),
+                       dim3((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch), dim3(CF::NT), 0, stream, kp, vec);
+    return hip_error(hipGetLastError(), "gemm_bf16x3_kernel launch");
+}
+
+template <class CF, int OPA, int OPB, int TERMS, int IN>
+int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
+               g.stride_a, g.stride_b, g.stride_c, g.batch, g.aux, g.ldaux};
+    // vector loads of four elements need 4-element-aligned bases and strides
+    constexpr unsigned VB = IN == kInF32 ? 16 : 8;
+    bool vec = ((uintptr_t)g.A % VB == 0) && ((uintptr_t)g.B % VB == 0) &&
+               g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+               g.stride_a % 4 == 0 && g.stride_b % 4 == 0;
+    bool aligned = vec && g.K > 0 && g.M % CF::BM == 0 && g.N % CF::BN == 0 &&
+                   g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
+    bool split = g.n_split > 0;
+    if (aligned)
+        return split ? launch_cfg<CF, OPA, OPB, false, true, TERMS, IN>(kp, 1, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, false, false, TERMS, IN>(kp, 1, splits, stream);
+    if constexpr (CF::ALIGNED_ONLY) {
+        return set_error(CDX_ERR_UNSUPPORTED, "gemm_bf16x3: unaligned problem sent to an aligned-only tile");
+    } else {
+        return split ? launch_cfg<CF, OPA, OPB, true, true, TERMS, IN>(kp, vec, splits, stream)
+                     : launch_cfg<CF, OPA, OPB, true, false, TERMS, IN>(kp, vec, splits, stream);
+    }
+}
+
+template <int OPA, int OPB, int IN>
+int launch_pingpong(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
+               g.stride_a, g.stride_b, g.stride_c, g.batch, g.aux, g.ldaux};
+    const int64_t tiles = (g.M / 256) * (g.N / 256);
+    if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
+    const dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch);
+    if (g.n_split > 0)
+        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, true, IN>), grid, dim3(512), 0, stream, kp);
+    else
+        hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, false, IN>), grid, dim3(512), 0, stream, kp);
+    return hip_error(hipGetLastError(), "gemm_pingpong_kernel launch");
+}
+
+// The ping-pong kernel for fp32 operands (three terms) or 16-bit ones; the
+// dispatcher sends it problems for which pingpong_fits() holds.
+template <int IN>
+int launch_pingpong_ops(const GemmArgs& g0, hipStream_t stream) {
+    constexpr int BK = IN == kInF32 ? 32 : 64;
+    const int64_t tiles = (g0.M / 256) * (g0.N / 256);
+    return with_splitk(g0, tiles, BK, stream,
+                       [&](const GemmArgs& g, int splits, int64_t k_chunk) {
+        if (k_chunk % BK != 0)
+            return set_error(CDX_ERR_UNSUPPORTED, "gemm: k slice not a multiple of the k-tile");
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_N, CDX_OP_N, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_pingpong<CDX_OP_N, CDX_OP_T, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_pingpong<CDX_OP_T, CDX_OP_N, IN>(g, splits, k_chunk, stream);
+        return launch_pingpong<CDX_OP_T, CDX_OP_T, IN>(g, splits, k_chunk, stream);
+    });
+}
+
+// Split-K slices of these kernels hold at least this much k (see
+// choose_splitk).
+constexpr int64_t kSplitMinK = 1024;
+
+template <class CF, int TERMS = 3, int IN = kInF32>
+int launch_ops(const GemmArgs& g0, hipStream_t stream) {
+    const int64_t tiles = ceil_div(g0.M, CF::BM) * ceil_div(g0.N, CF::BN);
+    return with_splitk(g0, tiles, CF::BK, stream,
+                       [&](const GemmArgs& g, int splits, int64_t k_chunk) {
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_N, CDX_OP_N, TERMS, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_mode<CF, CDX_OP_N, CDX_OP_T, TERMS, IN>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_mode<CF, CDX_OP_T, CDX_OP_N, TERMS, IN>(g, splits, k_chunk, stream);
+        return launch_mode<CF, CDX_OP_T, CDX_OP_T, TERMS, IN>(g, splits, k_chunk, stream);
+    }, kSplitMinK);
+}
+
+// Tile configurations (measured on MI355X, NN):
+//  * Huge: 256x256x32, 8 waves of 128x64; 160 KiB of LDS (one workgroup
+//    per CU); one staging set (two do not fit 256 registers); ~410-430
+//    logical TFLOP/s at 4096^3 in a back-to-back loop.
+//  * Large: 128x128x64, 8 waves of 32x64, two staging sets; ~260 at 2048^3
+//    (one set: ~237).
+//  * Small: 64x64x64, 4 waves of 32x32, for small / narrow problems.  The
+//    deeper k-tile halves the k-iterations of short-K problems, which are
+//    bound by per-iteration latency (8192 x 256 x 784: 30 us against 75
+//    with BK = 32); 16-wide tiles for N or M <= 16 measured no faster.
+//  * SkinnyM: M <= 64 with a long N (conv GEMM): 64x128x32, 4 waves of
+//    32x64, two staging sets (64 x 100352 x 576 in a back-to-back loop:
+//    49.5 us = 149 logical TFLOP/s, against 55.5 with 64x64x64 tiles, 65.5
+//    with 64x128x64 and 57-58 with 64x256x32).
+using CfgHuge = Cfg<256, 256, 32, 128, 64, 8, true>;
+using CfgLarge = Cfg<128, 128, 64, 32, 64, 8, false, 2>;
+using CfgSkinnyM = Cfg<64, 128, 32, 32, 64, 1, false, 2>;
+using CfgSmall = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
+
+// True when launch_mode would run CF without bounds checks (no split-K).
+template <class CF>
+bool aligned_for(const GemmArgs& g) {
+    return ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
+           g.ldb % 4 == 0 && g.stride_a % 4 == 0 && g.stride_b % 4 == 0 && g.K > 0 &&
+           g.M % CF::BM == 0 && g.N % CF::BN == 0 && g.K % CF::BK == 0;
+}
+
+// The ping-pong kernel addresses a 256-row (or 32-k-row) operand panel with
+// 32-bit byte offsets.
+inline bool pingpong_fits(const GemmArgs& g) {
+    return g.lda < (int64_t(1) << 22) && g.ldb < (int64_t(1) << 22);
+}
+
+// 16-bit operands: one plane and one MFMA per fragment pair, so a k-tile of
+// 64 costs the LDS of the split kernel's 32.
+using Cfg16Huge = Cfg<256, 256, 64, 128, 64, 8, true, 1>;
+using Cfg16Large = Cfg<128, 128, 64, 32, 64, 8, false, 2>;
+using Cfg16Small = Cfg<64, 64, 64, 32, 32, 8, false, 2>;
+
+
+// Explicit instantiations (one gemm_split_*.hip file each group).
+extern template int launch_ops<CfgSkinnyM, 3, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<CfgHuge, 3, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<CfgLarge, 3, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<CfgSmall, 3, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<CfgSkinnyM, 4, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<CfgLarge, 4, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<CfgSmall, 4, kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<Cfg16Huge, 1, kInF16>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<Cfg16Large, 1, kInF16>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<Cfg16Small, 1, kInF16>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<Cfg16Huge, 1, kInBF16>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<Cfg16Large, 1, kInBF16>(const GemmArgs&, hipStream_t);
+extern template int launch_ops<Cfg16Small, 1, kInBF16>(const GemmArgs&, hipStream_t);
+extern template int launch_pingpong_ops<kInF32>(const GemmArgs&, hipStream_t);
+extern template int launch_pingpong_ops<kInF16>(const GemmArgs&, hipStream_t);
+extern template int launch_pingpong_ops<kInBF16>(const GemmArgs&, hipStream_t);
+
+}  // namespace split
+}  // namespace cdx
