@@ -54,6 +54,7 @@ SIGNATURES = {
     "cdx_im2col_f32": (_int, [_vp, _vp] + [_i64] * 10 + [_vp]),
     "cdx_conv2d_forward_workspace_size": (_sz, [_i64] * 10),
     "cdx_conv2d_forward_f32": (_int, [_vp, _vp, _vp, _vp] + [_i64] * 11 + [_int, _vp, _sz, _vp]),
+    "cdx_conv2d_forward_implicit_f32": (_int, [_vp, _vp, _vp, _vp] + [_i64] * 11 + [_vp]),
     "cdx_sum_reduce_rows_workspace_size": (_sz, [_i64, _i64]),
     "cdx_sum_reduce_rows_f32": (_int, [_vp, _vp, _i64, _i64, _vp, _sz, _vp]),
     "cdx_broadcast_add_row_f32": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),

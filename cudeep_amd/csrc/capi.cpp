@@ -132,6 +132,26 @@ int check_conv(const char* fn, int64_t batch, int64_t IC, int64_t OC, int64_t IH
     return CDX_OK;
 }
 
+// Bytes of the im2col column buffer [IC*KH*KW, B*OH*OW].
+size_t col_bytes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                 int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    const int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    return (size_t)(IC * KH * KW) * (size_t)(batch * OH * OW) * sizeof(float);
+}
+
+// The reference's forward dispatch (conv_kernel.cu:242-275) below its
+// Winograd route: a layer whose column buffer would exceed 4 MiB runs the
+// implicit GEMM (no buffer) unless it is a 3x3 stride-1 layer with >= 16
+// output pixels per image (the Winograd shape, which keeps the im2col route
+// here when it is not sent to Winograd).
+bool forward_takes_implicit(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH,
+                            int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    const int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    if (KH == 3 && KW == 3 && SH == 1 && SW == 1 && OH * OW >= 16) return false;
+    return col_bytes(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW) > ((size_t)4 << 20) &&
+           cdx::conv_fwd_implicit_ok(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW);
+}
+
 }  // namespace
 
 extern "C" {
@@ -317,9 +337,34 @@ size_t cdx_conv2d_forward_workspace_size(int64_t batch, int64_t in_channels, int
     if (check_conv("cdx_conv2d_forward_workspace_size", batch, in_channels, 1, in_h, in_w,
                    kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w))
         return 0;
+    if (forward_takes_implicit(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                               stride_w, pad_h, pad_w))
+        return 0;
+    return col_bytes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
+                     pad_h, pad_w);
+}
+
+int cdx_conv2d_forward_implicit_f32(const float* input, const float* weight, const float* bias,
+                                    float* output, int64_t batch, int64_t in_channels,
+                                    int64_t out_channels, int64_t in_h, int64_t in_w,
+                                    int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                    int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                    hipStream_t stream) {
+    const char* fn = "cdx_conv2d_forward_implicit_f32";
+    int st = check_conv(fn, batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w);
+    if (st) return st;
     const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
     const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
-    return (size_t)(in_channels * kernel_h * kernel_w) * (size_t)(batch * OH * OW) * sizeof(float);
+    if (batch == 0 || out_channels == 0 || OH * OW == 0) return CDX_OK;
+    if (!output || !weight || !input)
+        return set_error(CDX_ERR_INVALID_ARG, std::string(fn) + ": NULL pointer");
+    if (!cdx::conv_fwd_implicit_ok(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                                   stride_w, pad_h, pad_w))
+        return set_error(CDX_ERR_UNSUPPORTED, std::string(fn) + ": geometry beyond 32-bit indices");
+    return cdx::launch_conv_fwd_implicit_f32(input, weight, bias, output, batch, in_channels,
+                                             out_channels, in_h, in_w, kernel_h, kernel_w,
+                                             stride_h, stride_w, pad_h, pad_w, stream);
 }
 
 }  // extern "C"
@@ -386,6 +431,16 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight, const float*
                            int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
                            int64_t pad_w, int precision, void* workspace,
                            size_t workspace_bytes, hipStream_t stream) {
+    if (!check_conv("cdx_conv2d_forward_f32", batch, in_channels, out_channels, in_h, in_w,
+                    kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w) &&
+        forward_takes_implicit(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                               stride_w, pad_h, pad_w)) {
+        if (!valid_precision(precision))
+            return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: bad precision");
+        return cdx_conv2d_forward_implicit_f32(input, weight, bias, output, batch, in_channels,
+                                               out_channels, in_h, in_w, kernel_h, kernel_w,
+                                               stride_h, stride_w, pad_h, pad_w, stream);
+    }
     return conv_forward_im2col(input, weight, bias, output, batch, in_channels, out_channels,
                                in_h, in_w, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w,
                                precision, workspace, workspace_bytes, stream, false);

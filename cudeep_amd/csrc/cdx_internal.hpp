@@ -31,6 +31,24 @@ int stream_free(void* p, hipStream_t stream, const char* what);
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Division by a run-time constant d (1 <= d < 2^31) of n < 2^31 by a
+// multiply-high: q = (mulhi(n, m) + n) >> l (Granlund & Montgomery 1994).
+struct DivMagic {
+    uint32_t m;
+    int l;
+};
+
+inline DivMagic div_magic(int64_t d) {
+    int l = 0;
+    while (((int64_t)1 << l) < d) ++l;
+    const uint64_t m = ((((uint64_t)1 << 32) * (((uint64_t)1 << l) - (uint64_t)d)) / (uint64_t)d) + 1;
+    return {(uint32_t)m, l};
+}
+
+__device__ __forceinline__ uint32_t div_u31(uint32_t n, DivMagic g) {
+    return (__umulhi(n, g.m) + n) >> g.l;
+}
+
 // One GEMM problem in the library's internal form.  Element (i, j) of op(A)
 // is A[i*lda + j] (opA = N) or A[j*lda + i] (opA = T); likewise for B.
 // C is written through the output map:
@@ -192,6 +210,17 @@ size_t conv_wgrad_implicit_floats(int64_t batch, int64_t IC, int64_t OC, int64_t
 int launch_conv_wgrad_f32(const float* dy, const float* x, float* dw, float* ws, int64_t batch,
                           int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
                           int64_t SH, int64_t SW, int64_t PH, int64_t PW, hipStream_t stream);
+
+// Conv forward as an implicit GEMM (FP32 MFMA, operands gathered from the
+// NCHW input while staging k-tiles; no column buffer), with bias; output
+// NCHW.  conv_fwd_implicit_ok() gives the geometries it takes (32-bit
+// in-image and pixel indices).
+bool conv_fwd_implicit_ok(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH,
+                          int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW);
+int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bias, float* y,
+                                 int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                                 int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                                 int64_t PW, hipStream_t stream);
 
 int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,

@@ -10,10 +10,10 @@
 //  * plane kernel (input plane <= 64 KiB): one workgroup per (b, ic) input
 //    plane.  The plane is read from HBM once, coalesced, into LDS; the
 //    workgroup then writes the KH*KW column rows that plane feeds.  Each
-//    thread owns 4 consecutive s, computes (oh, ow) once, and for every
-//    (kh, kw) gathers from LDS and issues one 16-byte store, so every
-//    wavefront writes 1 KiB contiguous runs.  HBM traffic is the
-//    compulsory minimum: the input once plus the column buffer once.
+//    thread computes (oh, ow) of its output pixels once and for every
+//    (kh, kw) gathers from LDS and stores, consecutive lanes on consecutive
+//    pixels.  HBM traffic is the compulsory minimum: the input once plus
+//    the column buffer once.
 //  * generic kernel (larger planes): one thread per 4 consecutive s of one
 //    (k, b) row, gathering straight from global memory.
 // Index math is 32-bit where the value is bounded by one plane or one row
@@ -71,7 +71,14 @@ void im2col_kernel(const float* __restrict__ in, float* __restrict__ col, Im2col
 
 constexpr int kPlaneMaxFloats = 16384;   // 64 KiB of LDS per input plane
 
-template <int VS>
+// One workgroup per (b, ic) input plane, staged in LDS.  Lanes walk
+// consecutive output pixels s (a thread owns s, s + 256, ... U at a time),
+// so each LDS gather of a wavefront reads consecutive words -- conflict-free
+// except where a row of the output wraps -- and each store instruction of a
+// wavefront writes 256 contiguous bytes of a column row.  (Four consecutive
+// s per thread with 16-byte stores made every gather a 4-way bank conflict:
+// lanes 16 apart read words 64 apart.)
+template <int U>
 __global__ __launch_bounds__(256)
 void im2col_plane_kernel(const float* __restrict__ in, float* __restrict__ col, Im2colGeom g) {
     extern __shared__ float plane[];
@@ -84,35 +91,28 @@ void im2col_plane_kernel(const float* __restrict__ in, float* __restrict__ col, 
 
     const int spatial = (int)g.spatial, OW = (int)g.OW;
     const int KH = (int)g.KH, KW = (int)g.KW;
-    const int runs_per_row = (spatial + VS - 1) / VS;
     // row (k, b) starts at ((ic*KH*KW + kk) * batch + b) * spatial
     float* row0 = col + ((int64_t)ic * KH * KW * g.batch + b) * g.spatial;
     const int64_t row_step = g.batch * g.spatial;   // next kk
-    for (int t = threadIdx.x; t < runs_per_row; t += blockDim.x) {
-        const int s0 = t * VS;
-        int ih0[VS], iw0[VS];
+    for (int s0 = threadIdx.x; s0 < spatial; s0 += 256 * U) {
+        int ih0[U], iw0[U];
+        bool live[U];
 #pragma unroll
-        for (int e = 0; e < VS; ++e) {
-            const int s = s0 + e < spatial ? s0 + e : spatial - 1;
-            const int oh = s / OW, ow = s - (s / OW) * OW;
-            ih0[e] = oh * (int)g.SH - (int)g.PH;
-            iw0[e] = ow * (int)g.SW - (int)g.PW;
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + 256 * u;
+            live[u] = s < spatial;
+            const int oh = s / OW, ow = s - oh * OW;
+            ih0[u] = oh * (int)g.SH - (int)g.PH;
+            iw0[u] = ow * (int)g.SW - (int)g.PW;
         }
         float* dst = row0 + s0;
         for (int kh = 0; kh < KH; ++kh) {
             for (int kw = 0; kw < KW; ++kw) {
-                float v[VS];
 #pragma unroll
-                for (int e = 0; e < VS; ++e) {
-                    const int ih = ih0[e] + kh, iw = iw0[e] + kw;
-                    v[e] = (ih >= 0 && ih < IH && iw >= 0 && iw < IW) ? plane[ih * IW + iw] : 0.0f;
-                }
-                if (VS == 4) {
-                    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < VS; ++e)
-                        if (s0 + e < spatial) dst[e] = v[e];
+                for (int u = 0; u < U; ++u) {
+                    const int ih = ih0[u] + kh, iw = iw0[u] + kw;
+                    const float v = (ih >= 0 && ih < IH && iw >= 0 && iw < IW) ? plane[ih * IW + iw] : 0.0f;
+                    if (live[u]) dst[256 * u] = v;
                 }
                 dst += row_step;
             }
@@ -378,12 +378,8 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
     if (IH * IW <= kPlaneMaxFloats && batch * IC <= INT32_MAX && g.spatial <= INT32_MAX &&
         KH * KW <= 4096) {
         const size_t lds = (size_t)(IH * IW) * sizeof(float);
-        if (vec)
-            hipLaunchKernelGGL(im2col_plane_kernel<4>, dim3((unsigned)(batch * IC)), dim3(256),
-                               lds, stream, in, col, g);
-        else
-            hipLaunchKernelGGL(im2col_plane_kernel<1>, dim3((unsigned)(batch * IC)), dim3(256),
-                               lds, stream, in, col, g);
+        hipLaunchKernelGGL(im2col_plane_kernel<4>, dim3((unsigned)(batch * IC)), dim3(256),
+                           lds, stream, in, col, g);
         return hip_error(hipGetLastError(), "im2col_plane_kernel launch");
     }
     const int64_t threads = g.runs * ((g.spatial + VS - 1) / VS);

@@ -62,23 +62,6 @@ constexpr int WG_STRIDE = WG_BK + 4;                      // LDS row stride (flo
 static_assert(WG_BN % 32 == 0 && WG_BK % 16 == 0 && WG_BN % WG_RPP == 0 && WG_RPP >= WG_BM,
               "tile shape");
 
-// n / d for n < 2^31, d < 2^31: q = (mulhi(n, m) + n) >> l
-struct DivMagic {
-    uint32_t m;
-    int l;
-};
-
-DivMagic div_magic(int64_t d) {
-    int l = 0;
-    while (((int64_t)1 << l) < d) ++l;
-    const uint64_t m = ((((uint64_t)1 << 32) * (((uint64_t)1 << l) - (uint64_t)d)) / (uint64_t)d) + 1;
-    return {(uint32_t)m, l};
-}
-
-__device__ __forceinline__ uint32_t div_u31(uint32_t n, DivMagic g) {
-    return (__umulhi(n, g.m) + n) >> g.l;
-}
-
 struct WgGeom {
     int64_t B, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, OH, OW;
     int64_t S() const { return OH * OW; }

@@ -261,6 +261,33 @@ def conv2d_forward(x, w, bias=None, stride=(1, 1), padding=(0, 0),
     return out
 
 
+def conv2d_implicit(x, w, bias=None, stride=(1, 1), padding=(0, 0), out=None):
+    """NCHW convolution as an implicit GEMM, no column buffer
+    (cdx_conv2d_forward_implicit_f32; FP32 products)."""
+    _need(x, "input")
+    _need(w, "weight")
+    if x.dim() != 4 or w.dim() != 4 or not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("conv2d_implicit: input / weight must be contiguous NCHW / OIHW")
+    Bn, C, H, W = x.shape
+    OC, C2, KH, KW = w.shape
+    if C != C2:
+        raise ValueError("conv2d_implicit: channel mismatch")
+    OH = conv_out_size(H, KH, stride[0], padding[0])
+    OW = conv_out_size(W, KW, stride[1], padding[1])
+    if OH <= 0 or OW <= 0:
+        raise ValueError("conv2d_implicit: kernel larger than padded input")
+    if bias is not None:
+        _need(bias, "bias")
+        if bias.numel() != OC or not bias.is_contiguous():
+            raise ValueError("conv2d_implicit: bias must have out_channels elements")
+    if out is None:
+        out = torch.empty((Bn, OC, OH, OW), device=x.device, dtype=torch.float32)
+    L.call("cdx_conv2d_forward_implicit_f32", x.data_ptr(), w.data_ptr(),
+           None if bias is None else bias.data_ptr(), out.data_ptr(), Bn, C, OC, H, W, KH, KW,
+           stride[0], stride[1], padding[0], padding[1], _stream())
+    return out
+
+
 def conv2d_winograd(x, w, bias=None, padding=(0, 0), precision=L.PREC_FP32, workspace=None,
                     out=None):
     """3x3 stride-1 NCHW convolution by Winograd F(4x4, 3x3)

@@ -213,7 +213,8 @@ int cdx_im2col_f32(const float* input, float* col,
                    int64_t stride_h, int64_t stride_w,
                    int64_t pad_h, int64_t pad_w, hipStream_t stream);
 
-/* Bytes of workspace cdx_conv2d_forward_f32 needs (the im2col buffer). */
+/* Bytes of workspace cdx_conv2d_forward_f32 needs: the im2col buffer, or 0
+ * for layers it sends to the implicit GEMM (see below). */
 size_t cdx_conv2d_forward_workspace_size(
     int64_t batch, int64_t in_channels, int64_t in_h, int64_t in_w,
     int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
@@ -221,6 +222,10 @@ size_t cdx_conv2d_forward_workspace_size(
 
 /* NCHW conv forward: im2col -> one GEMM weight[OC,K_col] * col -> NCHW
  * output with the bias added in the GEMM epilogue (no transpose pass).
+ * Layers whose column buffer would exceed 4 MiB, other than 3x3 stride-1
+ * layers with >= 16 output pixels per image, run the implicit GEMM of
+ * cdx_conv2d_forward_implicit_f32 instead (no workspace), as the reference
+ * dispatches them to its implicit kernel (conv_kernel.cu:263-275).
  * Replaces cudeep::kernels::launch_conv2d_forward_kernel<float>
  * (include/cudeep/kernels/conv.cuh:8-16, src/kernels/conv_kernel.cu:225-335).
  * bias may be NULL.  precision is CDX_PREC_*.  workspace may be NULL. */
@@ -233,6 +238,20 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight,
                            int64_t pad_h, int64_t pad_w, int precision,
                            void* workspace, size_t workspace_bytes,
                            hipStream_t stream);
+
+/* NCHW conv forward as an implicit GEMM: the filter and the input window
+ * are gathered into LDS per k-tile (FP32 products, fp32 accumulation), bias
+ * added, no column buffer and no workspace.  Replaces
+ * implicit_gemm_conv2d_kernel (src/kernels/conv_kernel.cu:172-215).
+ * Geometries needing 64-bit pixel or in-image indices return
+ * CDX_ERR_UNSUPPORTED.  bias may be NULL. */
+int cdx_conv2d_forward_implicit_f32(const float* input, const float* weight,
+                                    const float* bias, float* output,
+                                    int64_t batch, int64_t in_channels,
+                                    int64_t out_channels, int64_t in_h, int64_t in_w,
+                                    int64_t kernel_h, int64_t kernel_w,
+                                    int64_t stride_h, int64_t stride_w,
+                                    int64_t pad_h, int64_t pad_w, hipStream_t stream);
 
 /* Bytes of workspace cdx_conv2d_forward_winograd_f32 needs:
  * 36 * (OC*IC + IC*T + OC*T) floats, T = batch * ceil(OH/4) * ceil(OW/4). */

@@ -74,6 +74,7 @@ def lib():
         L.orc_im2col.argtypes = [_vp, _vp] + [_i64] * 10
         L.orc_transpose_bias.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64]
         L.orc_conv2d_direct64.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 11
+        L.orc_conv2d_implicit.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 11
         L.orc_colsum.argtypes = [_vp, _vp, _i64, _i64]
         L.orc_col2im.argtypes = [_vp, _vp] + [_i64] * 10
         L.orc_col2im64.argtypes = [_vp, _vp] + [_i64] * 10
@@ -208,6 +209,28 @@ def conv2d_direct64(x, w, bias=None, stride=(1, 1), padding=(0, 0)):
     out = np.empty((Bn, OC, OH, OW), np.float64)
     b = None if bias is None else _c32(bias)
     lib().orc_conv2d_direct64(_p(x), _p(w), None if b is None else _p(b), _p(out),
+                              Bn, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW)
+    return out
+
+
+def conv2d_ref_implicit(x, w, bias=None, stride=(1, 1), padding=(0, 0), batches=None):
+    """The reference's implicit-GEMM route restated on the CPU
+    (implicit_gemm_conv2d_kernel, conv_kernel.cu:172-215): per output one fp32
+    FMA chain starting from the bias, taps ic -> kh -> kw, padding taps
+    skipped.  Its error vs fp64 is the yardstick for layers the reference
+    sends to that kernel.  `batches` restricts it to those images."""
+    x, w = _c32(x), _c32(w)
+    if batches is not None:
+        x = np.ascontiguousarray(x[list(batches)])
+    Bn, IC, IH, IW = x.shape
+    OC, IC2, KH, KW = w.shape
+    assert IC == IC2
+    SH, SW = stride
+    PH, PW = padding
+    OH, OW = conv_out_size(IH, KH, SH, PH), conv_out_size(IW, KW, SW, PW)
+    out = np.empty((Bn, OC, OH, OW), np.float32)
+    b = None if bias is None else _c32(bias)
+    lib().orc_conv2d_implicit(_p(x), _p(w), None if b is None else _p(b), _p(out),
                               Bn, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW)
     return out
 

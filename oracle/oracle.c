@@ -19,6 +19,8 @@
  *   orc_transpose_bias  src/kernels/conv_kernel.cu:74-93.
  *   orc_conv2d_direct64 src/kernels/conv_kernel.cu:113-159 (naive kernel:
  *                       cross-correlation, zero padding), output size :235-236.
+ *   orc_conv2d_implicit src/kernels/conv_kernel.cu:172-215 (implicit_gemm_conv2d_kernel:
+ *                       acc = bias, then one fmaf per in-range tap, ic -> kh -> kw).
  *   orc_col2im          src/kernels/conv_kernel.cu:344-380 (fp32, kh then kw).
  *   orc_col2im64        the same gather in double (yardstick).
  *   orc_colsum          src/kernels/unary_kernel.cu:204-238 (serial fp32 sum
@@ -299,6 +301,37 @@ void orc_conv2d_direct64(const float* input, const float* weight, const float* b
                                 if (iw < 0 || iw >= IW) continue;
                                 acc += (double)input[((b * IC + ic) * IH + ih) * IW + iw] *
                                        (double)weight[((oc * IC + ic) * KH + kh) * KW + kw];
+                            }
+                        }
+                    out[((b * OC + oc) * OH + oh) * OW + ow] = acc;
+                }
+}
+
+/* fp32 restatement of implicit_gemm_conv2d_kernel (conv_kernel.cu:172-215),
+ * the reference's forward route for layers whose column buffer would exceed
+ * 4 MiB outside 3x3 stride 1 (:263-275): per output, acc = bias[oc] (or 0),
+ * then acc += in * w over ic, kh, kw ascending, skipping taps outside the
+ * image (the `continue`s), nvcc-contracted to one fmaf per tap. */
+void orc_conv2d_implicit(const float* input, const float* weight, const float* bias,
+                         float* out, int64_t batch, int64_t IC, int64_t OC,
+                         int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                         int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t oc = 0; oc < OC; ++oc)
+            for (int64_t oh = 0; oh < OH; ++oh)
+                for (int64_t ow = 0; ow < OW; ++ow) {
+                    float acc = bias ? bias[oc] : 0.0f;
+                    for (int64_t ic = 0; ic < IC; ++ic)
+                        for (int64_t kh = 0; kh < KH; ++kh) {
+                            int64_t ih = oh * SH - PH + kh;
+                            if (ih < 0 || ih >= IH) continue;
+                            for (int64_t kw = 0; kw < KW; ++kw) {
+                                int64_t iw = ow * SW - PW + kw;
+                                if (iw < 0 || iw >= IW) continue;
+                                acc = fmaf(input[((b * IC + ic) * IH + ih) * IW + iw],
+                                           weight[((oc * IC + ic) * KH + kh) * KW + kw], acc);
                             }
                         }
                     out[((b * OC + oc) * OH + oh) * OW + ow] = acc;

@@ -6,6 +6,9 @@
     reference route restated on the CPU (im2col -> seq-FMA SGEMM ->
     transpose + bias); TF32 mode against the emulated TF32 route.
   * the reference's conv known answers (identity, 3x3 ones, bias, padding).
+  * implicit-GEMM forward (the reference's route for large non-3x3 layers):
+    relFro <= 2 x that of its bias-first FMA chain restated on the CPU,
+    including a C5-size 7x7 layer routed there by cdx_conv2d_forward_f32.
 """
 import numpy as np
 import pytest
@@ -126,6 +129,77 @@ def test_conv_c5_full_batch_sampled(prec):
                 errs.append(oracle.rel_fro(yr, d64))
             print(f"C5 item {i}: tf32mode gpu={e:.3e} tf32 route rz/rne={errs}")
             assert e <= min(errs)
+
+
+IMPLICIT_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
+    (2, 3, 20, 21, 32, 7, 7, 1, 1, 3, 3),      # 7x7 stem-like, Kc = 147 (% 4 != 0)
+    (2, 5, 11, 13, 70, 5, 5, 2, 2, 2, 2),      # OC > one 64-channel tile
+    (1, 16, 9, 9, 8, 1, 1, 1, 1, 0, 0),        # 1x1
+    (3, 4, 10, 7, 9, 3, 5, 2, 1, 2, 0),        # rectangular kernel, mixed strides
+    (1, 2, 3, 3, 5, 3, 3, 1, 1, 0, 0),         # single output pixel
+    (2, 8, 6, 130, 16, 3, 3, 1, 2, 1, 1),      # pixels not a multiple of the 128 tile
+    (1, 37, 12, 12, 65, 2, 2, 2, 2, 0, 0),     # Kc = 148: k-tail, OC = 65
+    (2, 16, 14, 14, 64, 3, 3, 1, 1, 1, 1),     # 3x3 stride 1 through the implicit kernel
+]
+
+
+def _implicit_gate(x, w, b, stride, padding, y, batches=None):
+    xs = x if batches is None else x[list(batches)]
+    d64 = oracle.conv2d_direct64(xs, w, b, stride, padding)
+    ref = oracle.conv2d_ref_implicit(xs, w, b, stride, padding)
+    return oracle.rel_fro(y, d64), oracle.rel_fro(ref, d64)
+
+
+@pytest.mark.parametrize("g", IMPLICIT_GEOMS)
+def test_conv_implicit_parity(g):
+    """Implicit-GEMM forward (cdx_conv2d_forward_implicit_f32): relFro vs
+    fp64 <= 2 x that of the reference's implicit kernel restated on the CPU
+    (bias-first FMA chain, conv_kernel.cu:172-215)."""
+    Bn, C, H, W, OC, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(700 + sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    w = normal(rng, (OC, C, KH, KW), std=np.sqrt(2.0 / (C * KH * KW)))
+    b = normal(rng, (OC,), 0.1)
+    say("conv implicit", g)
+    y = host(ops().conv2d_implicit(dev(x), dev(w), dev(b), (SH, SW), (PH, PW)))
+    e, e_ref = _implicit_gate(x, w, b, (SH, SW), (PH, PW), y)
+    assert e <= 2 * e_ref + 2.0 ** -24, (e, e_ref)
+    y0 = host(ops().conv2d_implicit(dev(x), dev(w), None, (SH, SW), (PH, PW)))
+    e0, e0_ref = _implicit_gate(x, w, None, (SH, SW), (PH, PW), y0)
+    assert e0 <= 2 * e0_ref + 2.0 ** -24, (e0, e0_ref)
+
+
+@pytest.mark.parametrize("name", ["conv_identity_1x1", "conv_3x3_ones", "conv_3x3_bias",
+                                  "conv_3x3_pad1"])
+def test_conv_implicit_kats(kats, name):
+    k = kats[name]
+    x = np.array(k["x"], np.float32).reshape(k["x_shape"])
+    w = np.array(k["w"], np.float32).reshape(k["w_shape"])
+    b = None if k["bias"] is None else dev(np.array(k["bias"], np.float32))
+    say("conv implicit kat", name)
+    y = host(ops().conv2d_implicit(dev(x), dev(w), b, k["stride"], k["padding"]))
+    assert np.array_equal(y.ravel(), np.array(k["y"], np.float32))
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_forward_large_7x7_takes_implicit_route(prec):
+    """A 7x7 layer at C5's size (32 x 64 x 56^2 -> 64, pad 3) would need a
+    1.26 GB column buffer: cdx_conv2d_forward_f32 routes it to the implicit
+    GEMM like the reference (conv_kernel.cu:263-275): workspace query 0, and
+    images 0 and 31 pass the implicit route's parity gate."""
+    rng = np.random.default_rng(7077)
+    x = normal(rng, (32, 64, 56, 56))
+    w = normal(rng, (64, 64, 7, 7), std=np.sqrt(2.0 / (64 * 49)))
+    b = normal(rng, (64,), 0.1)
+    assert ops().conv2d_workspace_bytes(x.shape, w.shape, (1, 1), (3, 3)) == 0
+    # a 3x3 stride-1 layer of the same size keeps the im2col route
+    assert ops().conv2d_workspace_bytes(x.shape, (64, 64, 3, 3), (1, 1), (1, 1)) == 576 * 100352 * 4
+    say("conv 7x7 C5-size prec", prec)
+    y = host(ops().conv2d_forward(dev(x), dev(w), dev(b), (1, 1), (3, 3), precision=prec))
+    assert y.shape == (32, 64, 56, 56) and np.isfinite(y).all()
+    e, e_ref = _implicit_gate(x, w, b, (1, 1), (3, 3), y[[0, 31]], batches=(0, 31))
+    print(f"7x7 C5-size items 0, 31: gpu={e:.3e} reference implicit route={e_ref:.3e}")
+    assert e <= 2 * e_ref
 
 
 def test_conv_workspace_and_no_bias():

@@ -201,6 +201,55 @@ def test_conv_kats(kats, name):
     assert np.array_equal(r.ravel(), y.astype(np.float32))
 
 
+@pytest.mark.parametrize("name", ["conv_identity_1x1", "conv_3x3_ones",
+                                  "conv_3x3_bias", "conv_3x3_pad1"])
+def test_conv_implicit_kats(kats, name):
+    k = kats[name]
+    x, w, b = _conv_kat(k)
+    r = oracle.conv2d_ref_implicit(x, w, b, k["stride"], k["padding"])
+    assert np.array_equal(r.ravel(), np.array(k["y"], np.float32))
+
+
+@pytest.mark.parametrize("geom", [(2, 3, 6, 7, 2, 3, 3, 1, 1, 1, 1),
+                                  (1, 2, 7, 5, 3, 5, 3, 2, 1, 2, 0),
+                                  (2, 2, 5, 6, 2, 1, 1, 1, 1, 0, 0)])
+def test_conv_implicit_is_bias_first_fma_chain(geom):
+    """conv2d_ref_implicit against an exact-rational restatement of the
+    reference's implicit kernel (conv_kernel.cu:172-215): acc = bias, then one
+    correctly rounded fma per in-range tap, ic -> kh -> kw.  Fails if the bias
+    is added last, a tap order changes, or padding taps are not skipped."""
+    Bn, IC, H, W, OC, KH, KW, SH, SW, PH, PW = geom
+    rng = np.random.default_rng(31 + sum(geom))
+    x = rng.standard_normal((Bn, IC, H, W)).astype(np.float32)
+    w = rng.standard_normal((OC, IC, KH, KW)).astype(np.float32)
+    b = (rng.standard_normal(OC) * 100).astype(np.float32)   # large: bias order matters
+    got = oracle.conv2d_ref_implicit(x, w, b, (SH, SW), (PH, PW))
+    OH, OW = oracle.conv_out_size(H, KH, SH, PH), oracle.conv_out_size(W, KW, SW, PW)
+    want = np.empty((Bn, OC, OH, OW), np.float32)
+    for bi in range(Bn):
+        for oc in range(OC):
+            for oh in range(OH):
+                for ow in range(OW):
+                    acc = b[oc]
+                    for ic in range(IC):
+                        for kh in range(KH):
+                            ih = oh * SH - PH + kh
+                            if not 0 <= ih < H:
+                                continue
+                            for kw in range(KW):
+                                iw = ow * SW - PW + kw
+                                if 0 <= iw < W:
+                                    acc = fma_f32(x[bi, ic, ih, iw], w[oc, ic, kh, kw], acc)
+                    want[bi, oc, oh, ow] = acc
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # integer-valued operands: every partial sum exact, so = fp64 closed form
+    xi = rng.integers(-4, 5, x.shape).astype(np.float32)
+    wi = rng.integers(-4, 5, w.shape).astype(np.float32)
+    bi_ = rng.integers(-9, 10, OC).astype(np.float32)
+    assert np.array_equal(oracle.conv2d_ref_implicit(xi, wi, bi_, (SH, SW), (PH, PW)),
+                          oracle.conv2d_direct64(xi, wi, bi_, (SH, SW), (PH, PW)).astype(np.float32))
+
+
 def test_im2col_1x1_is_relayout():
     rng = np.random.default_rng(2)
     x = rng.standard_normal((3, 5, 4, 6)).astype(np.float32)
