@@ -384,12 +384,14 @@ PYBIND11_MODULE(_cudeep_core, m) {
         if (a == "auto") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Auto);
         else if (a == "im2col") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Im2col);
         else if (a == "winograd") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Winograd);
-        else throw std::runtime_error("set_conv_algorithm: 'auto', 'im2col' or 'winograd'");
+        else if (a == "implicit") kernels::set_conv_algorithm(kernels::ConvAlgorithm::Implicit);
+        else throw std::runtime_error("set_conv_algorithm: 'auto', 'im2col', 'winograd' or 'implicit'");
     }, py::arg("algorithm"));
     m.def("get_conv_algorithm", []() {
         const auto a = kernels::get_conv_algorithm();
         return a == kernels::ConvAlgorithm::Im2col     ? "im2col"
                : a == kernels::ConvAlgorithm::Winograd ? "winograd"
+               : a == kernels::ConvAlgorithm::Implicit ? "implicit"
                                                        : "auto";
     });
 

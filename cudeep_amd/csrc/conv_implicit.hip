@@ -19,13 +19,17 @@
 // row and gathers 8 consecutive k of one output pixel:
 //  * the pixel's (b, oh, ow) is decoded once per kernel (multiply-high
 //    divisions), giving its image base and window origin (ih0, iw0);
-//  * the 8 taps' (ic, kh, kw) are decoded once per k-tile from a k that is
-//    uniform across the wave, then stepped (kw, then kh, then ic), so the
-//    per-element work is two bounds tests and one load; consecutive lanes
-//    hold consecutive pixels, so each load instruction reads along an input
-//    row.
+//  * the 8 taps (ic, kh, kw) of a k-tile are the same for every lane of a
+//    wave: eight lanes decode one each and the wave reads them back with
+//    readlane, so the per-element work is two bounds tests, one add and one
+//    load; consecutive lanes hold consecutive pixels, so each load
+//    instruction reads along an input row.
 // Both operands sit k-contiguous in LDS ([row][16 + 4]), double buffered; the
-// next k-tile's loads are issued before the current k-tile's MFMAs.
+// next k-tile's loads are issued before the current k-tile's MFMAs and
+// stored after them.  (Measured on MI355X: 32-deep k-tiles, or k ordered by
+// 32-channel chunks of one tap, were slower -- fewer resident waves, and in
+// the channel order every filter element of a k-tile sits on its own cache
+// line.)
 // FP32 products in every precision mode, as the reference's kernel.
 #include "cdx_internal.hpp"
 
@@ -41,7 +45,7 @@ struct CfArgs {
     const float* bias;   // [OC] or null
     float* y;            // [B][OC][S]
     int OC, Kc, N, S;    // N = B*S
-    int OW, IH, IW, plane, KH, KW, SH, SW, PH, PW;
+    int OW, IH, IW, plane, KH, KW, KHW, SH, SW, PH, PW;
     int64_t img_x, img_y;                // IC*IH*IW, OC*S
     DivMagic div_s, div_ow, div_khw, div_kw;
     int vec_w;                           // Kc % 4 == 0 and w 16-byte aligned
@@ -50,8 +54,21 @@ struct CfArgs {
 struct CfStage {
     float4 a;       // filter row ra, k columns ca .. ca+3
     float g[8];     // gathered column: pixel gn, 8 consecutive k
+    uint32_t ok;    // bit e: g[e] in range; bits 8-11: a's components
 };
 
+// Keeps a loaded value opaque to the compiler, so the select that zeroes an
+// out-of-range slot (applied when the stage is stored, after the MFMAs)
+// cannot be folded back into a conditional load at the load site, which
+// would split the loop into branches and wait for each load at once.
+__device__ __forceinline__ float opaque(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// VECW: Kc % 4 == 0 and a 16-byte-aligned filter, so each filter run of 4
+// k is wholly inside or outside its row (one 16-byte load).
+template <bool VECW>
 __global__ __launch_bounds__(CF_NT)
 void conv_fwd_implicit_kernel(CfArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[2][(CF_BM + CF_BN) * CF_STRIDE];
@@ -61,10 +78,10 @@ void conv_fwd_implicit_kernel(CfArgs p) {
     const int wm0 = (wave >> 1) * 32, wn0 = (wave & 1) * 64;
     const int n0 = blockIdx.x * CF_BN, oc0 = blockIdx.y * CF_BM;
 
-    // filter staging slot
+    // filter staging slot (this launch's channels)
     const int ra = tid >> 2, ca = (tid & 3) * 4;
     const bool a_ok = oc0 + ra < p.OC;
-    const float* wrow = p.w + (int64_t)(a_ok ? oc0 + ra : 0) * p.Kc;   // (this launch's channels)
+    const float* wrow = p.w + (int64_t)(a_ok ? oc0 + ra : 0) * p.Kc;
 
     // gather slot: pixel gn of the tile, k offsets 8*kg .. 8*kg + 7
     const int gn = tid & (CF_BN - 1);
@@ -77,47 +94,68 @@ void conv_fwd_implicit_kernel(CfArgs p) {
     const uint32_t oh = div_u31(s, p.div_ow);
     const uint32_t ow = s - oh * (uint32_t)p.OW;
     const int ih0 = (int)oh * p.SH - p.PH, iw0 = (int)ow * p.SW - p.PW;
+    const int pix0 = ih0 * p.IW + iw0;   // in-plane offset of tap (0, 0)
     const float* ximg = p.x + (int64_t)b * p.img_x;
 
+    // Per k-tile, lane e < 8 of each wave decodes tap k + e of the wave's
+    // 8 k (ic, kh, kw -> in-image offset ic*IH*IW + kh*IW + kw, and kh, kw;
+    // -1 past Kc), and the wave reads the 8 taps back as scalars with
+    // readlane: the tap walk costs a few vector instructions per k-tile
+    // instead of a chain of scalar ones per element.  Every load is issued
+    // from an in-bounds address (out-of-range slots read element 0 of their
+    // row or image) and store() zeroes those slots.
     auto load = [&](CfStage& st, int k0) {
         const int ka = k0 + ca;
-        if (p.vec_w && a_ok && ka + 3 < p.Kc) {
-            st.a = *reinterpret_cast<const float4*>(wrow + ka);
+        uint32_t ok = 0;
+        if constexpr (VECW) {
+            const bool in = a_ok & (ka < p.Kc);
+            st.a = *reinterpret_cast<const float4*>(wrow + (in ? ka : 0));
+            ok |= in ? 0xF00u : 0u;
         } else {
-            st.a.x = a_ok && ka + 0 < p.Kc ? wrow[ka + 0] : 0.0f;
-            st.a.y = a_ok && ka + 1 < p.Kc ? wrow[ka + 1] : 0.0f;
-            st.a.z = a_ok && ka + 2 < p.Kc ? wrow[ka + 2] : 0.0f;
-            st.a.w = a_ok && ka + 3 < p.Kc ? wrow[ka + 3] : 0.0f;
+            float e[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const bool in = a_ok & (ka + c < p.Kc);
+                e[c] = wrow[in ? ka + c : 0];
+                ok |= in ? 1u << (8 + c) : 0u;
+            }
+            st.a = make_float4(e[0], e[1], e[2], e[3]);
         }
-        // taps k .. k+7, k uniform across the wave
-        const int k = k0 + 8 * kg;
-        const uint32_t ku = k < p.Kc ? (uint32_t)k : 0u;
-        int ic = (int)div_u31(ku, p.div_khw);
-        const int r = (int)ku - ic * p.KH * p.KW;
-        int kh = (int)div_u31((uint32_t)r, p.div_kw);
-        int kw = r - kh * p.KW;
+        const int kt = k0 + 8 * kg + (lane & 7);
+        const bool t_ok = kt < p.Kc;
+        const uint32_t ku = t_ok ? (uint32_t)kt : 0u;
+        const uint32_t ic = div_u31(ku, p.div_khw);
+        const uint32_t r = ku - ic * (uint32_t)p.KHW;
+        const uint32_t kh = div_u31(r, p.div_kw);
+        const uint32_t kw = r - kh * (uint32_t)p.KW;
+        const int t_off = (int)(ic * (uint32_t)p.plane + kh * (uint32_t)p.IW + kw);
+        const int t_hw = t_ok ? (int)((kh << 16) | kw) : -1;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int ih = ih0 + kh, iw = iw0 + kw;
-            const bool ok = n_ok && k + e < p.Kc && (unsigned)ih < (unsigned)p.IH &&
-                            (unsigned)iw < (unsigned)p.IW;
-            st.g[e] = ok ? ximg[ic * p.plane + ih * p.IW + iw] : 0.0f;
-            if (++kw == p.KW) {
-                kw = 0;
-                if (++kh == p.KH) {
-                    kh = 0;
-                    ++ic;
-                }
-            }
+            const int off = __builtin_amdgcn_readlane(t_off, e);
+            const int hw = __builtin_amdgcn_readlane(t_hw, e);
+            const int ih = ih0 + (hw >> 16), iw = iw0 + (hw & 0xFFFF);
+            const bool in = n_ok & (hw >= 0) & ((unsigned)ih < (unsigned)p.IH) &
+                            ((unsigned)iw < (unsigned)p.IW);
+            st.g[e] = ximg[in ? pix0 + off : 0];
+            ok |= in ? 1u << e : 0u;
         }
+        st.ok = ok;
     };
     auto store = [&](const CfStage& st, int buf) {
         float* sA = lds[buf];
         float* sB = sA + CF_BM * CF_STRIDE;
-        *reinterpret_cast<float4*>(sA + ra * CF_STRIDE + ca) = st.a;
+        auto z = [&](float v, int bit) {
+            const float o = opaque(v);
+            return (st.ok >> bit) & 1u ? o : 0.0f;
+        };
+        *reinterpret_cast<float4*>(sA + ra * CF_STRIDE + ca) =
+            make_float4(z(st.a.x, 8), z(st.a.y, 9), z(st.a.z, 10), z(st.a.w, 11));
         float* dst = sB + gn * CF_STRIDE + 8 * kg;
-        *reinterpret_cast<float4*>(dst) = make_float4(st.g[0], st.g[1], st.g[2], st.g[3]);
-        *reinterpret_cast<float4*>(dst + 4) = make_float4(st.g[4], st.g[5], st.g[6], st.g[7]);
+        *reinterpret_cast<float4*>(dst) =
+            make_float4(z(st.g[0], 0), z(st.g[1], 1), z(st.g[2], 2), z(st.g[3], 3));
+        *reinterpret_cast<float4*>(dst + 4) =
+            make_float4(z(st.g[4], 4), z(st.g[5], 5), z(st.g[6], 6), z(st.g[7], 7));
     };
 
     floatx4 acc[2][4];
@@ -148,18 +186,23 @@ void conv_fwd_implicit_kernel(CfArgs p) {
                 }
     };
 
+    // one barrier per k-tile; the next k-tile's loads are in flight during
+    // this one's MFMAs (a scheduling barrier keeps the LDS stores, which wait
+    // for them, after the MFMAs); the last k-tile is peeled
     const int nk = (int)ceil_div(p.Kc, CF_BK);
     CfStage st;
     load(st, 0);
     store(st, 0);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const bool more = kt + 1 < nk;
-        if (more) load(st, (kt + 1) * CF_BK);
+    int kt = 0;
+    for (; kt + 1 < nk; ++kt) {
+        load(st, (kt + 1) * CF_BK);
         compute(kt & 1);
-        if (more) store(st, (kt + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        store(st, (kt + 1) & 1);
         __syncthreads();
     }
+    compute(kt & 1);
 
     // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
     // column l % 16; output (oc, n) -> y[b][oc][s] + bias[oc]
@@ -189,7 +232,7 @@ bool conv_fwd_implicit_ok(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int
     // 32-bit pixel, in-image and tap indices; window origins within int range
     return OH >= 1 && OW >= 1 && batch * OH * OW < lim && IC * IH * IW < lim &&
            IC * KH * KW < lim && OH * SH + KH + IH < lim && OW * SW + KW + IW < lim &&
-           PH < lim && PW < lim;
+           PH < lim && PW < lim && KH < 32768 && KW < 32768;   // (kh, kw) packed in 16 bits
 }
 
 int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bias, float* y,
@@ -203,7 +246,7 @@ int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bi
     p.x = x;
     p.Kc = (int)(IC * KH * KW); p.S = (int)(OH * OW); p.N = (int)(batch * OH * OW);
     p.OW = (int)OW; p.IH = (int)IH; p.IW = (int)IW; p.plane = (int)(IH * IW);
-    p.KH = (int)KH; p.KW = (int)KW; p.SH = (int)SH; p.SW = (int)SW; p.PH = (int)PH; p.PW = (int)PW;
+    p.KH = (int)KH; p.KW = (int)KW; p.KHW = (int)(KH * KW); p.SH = (int)SH; p.SW = (int)SW; p.PH = (int)PH; p.PW = (int)PW;
     p.img_x = IC * IH * IW; p.img_y = OC * OH * OW;
     p.div_s = div_magic(p.S); p.div_ow = div_magic(OW);
     p.div_khw = div_magic(KH * KW); p.div_kw = div_magic(KW);
@@ -217,7 +260,10 @@ int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bi
         p.bias = bias ? bias + oc0 : nullptr;
         p.y = y + oc0 * p.S;
         const dim3 grid((unsigned)ceil_div(p.N, CF_BN), (unsigned)ceil_div(oc_n, CF_BM));
-        hipLaunchKernelGGL(conv_fwd_implicit_kernel, grid, dim3(CF_NT), 0, stream, p);
+        if (p.vec_w)
+            hipLaunchKernelGGL(conv_fwd_implicit_kernel<true>, grid, dim3(CF_NT), 0, stream, p);
+        else
+            hipLaunchKernelGGL(conv_fwd_implicit_kernel<false>, grid, dim3(CF_NT), 0, stream, p);
         const int st = hip_error(hipGetLastError(), "conv_fwd_implicit_kernel launch");
         if (st) return st;
     }

@@ -186,7 +186,11 @@ void launch_conv2d_forward_kernel<float>(const float* input, const float* weight
         throw std::runtime_error("conv2d: Winograd needs a 3x3 kernel with stride 1");
     const bool wino = algo == ConvAlgorithm::Winograd ||
                       (algo == ConvAlgorithm::Auto && wino_ok && OH * OW >= 16);
-    if (wino) {
+    if (algo == ConvAlgorithm::Implicit) {
+        CUDEEP_CHECK_CDX(cdx_conv2d_forward_implicit_f32(input, weight, bias, output, batch, IC,
+                                                         OC, IH, IW, KH, KW, SH, SW, PH, PW,
+                                                         stream));
+    } else if (wino) {
         Workspace ws(cdx_conv2d_winograd_workspace_size(batch, IC, OC, IH, IW, PH, PW), stream);
         CUDEEP_CHECK_CDX(cdx_conv2d_forward_winograd_f32(input, weight, bias, output, batch, IC,
                                                          OC, IH, IW, PH, PW, g_precision.load(),

@@ -12,14 +12,18 @@ namespace kernels {
 
 // Algorithm of launch_conv2d_forward_kernel<float> and
 // launch_conv2d_backward_data_kernel<float>.  Auto follows the reference's
-// forward routing (src/kernels/conv_kernel.cu:242-248): Winograd F(4x4,
+// forward routing (src/kernels/conv_kernel.cu:242-275): Winograd F(4x4,
 // 3x3) for 3x3 stride-1 layers with at least 16 output pixels per image,
-// im2col + GEMM otherwise; backward data applies the same rule to the
-// transposed convolution it runs (3x3, stride 1, padding <= 2, at least 16
-// input pixels per image) in the TF32 modes, and keeps the GEMM route in
-// FP32 (whose error bound is twice the reference's GEMM + col2im route).
-// Winograd on another geometry throws.
-enum class ConvAlgorithm { Auto, Im2col, Winograd };
+// the implicit GEMM for other layers whose column buffer would exceed
+// 4 MiB, im2col + GEMM otherwise; backward data applies the Winograd rule
+// to the transposed convolution it runs (3x3, stride 1, padding <= 2, at
+// least 16 input pixels per image) in the TF32 modes, and keeps the GEMM
+// route in FP32 (whose error bound is twice the reference's GEMM + col2im
+// route).  Im2col never takes Winograd (large non-3x3 layers still take
+// the implicit GEMM, which needs no column buffer); Implicit forces the
+// implicit GEMM forward (backward data as Im2col).  Winograd on another
+// geometry throws.
+enum class ConvAlgorithm { Auto, Im2col, Winograd, Implicit };
 void set_conv_algorithm(ConvAlgorithm a);
 ConvAlgorithm get_conv_algorithm();
 

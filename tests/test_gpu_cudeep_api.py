@@ -340,9 +340,10 @@ def test_conv2d_layer_float64(cd):
 
 def test_conv_algorithm_routing(cd):
     """launch_conv2d_forward_kernel routes like the reference
-    (conv_kernel.cu:242-248): 3x3 stride-1 layers with >= 16 output pixels
-    go to Winograd F(4x4, 3x3), the rest to im2col + GEMM; both can be
-    forced.  Backward data follows the same rule on its transposed conv."""
+    (conv_kernel.cu:242-275): 3x3 stride-1 layers with >= 16 output pixels
+    go to Winograd F(4x4, 3x3), the rest to im2col + GEMM (or the implicit
+    GEMM beyond a 4 MiB column buffer); each can be forced.  Backward data
+    follows the Winograd rule on its transposed conv."""
     from cudeep_amd.cuDeep import _core
     prev = cd.get_conv_algorithm()
     rng = np.random.default_rng(12)
@@ -371,6 +372,11 @@ def test_conv_algorithm_routing(cd):
         # fewer than 16 output pixels per image: im2col
         small = _core.Tensor.from_numpy(x[:, :, :5, :5].copy())
         assert np.array_equal(run("auto", pad=(0, 0), xt=small), run("im2col", pad=(0, 0), xt=small))
+        # forced implicit GEMM (the reference's route for large non-3x3 layers)
+        y_imp = run("implicit")
+        assert cd.get_conv_algorithm() == "implicit"
+        e_imp = oracle.rel_fro(oracle.conv2d_ref_implicit(x, w, b, (1, 1), (1, 1)), y64)
+        assert oracle.rel_fro(y_imp, y64) <= 2 * e_imp
 
         # backward data: the same rule on the transposed convolution in the
         # TF32 modes; FP32 keeps the GEMM route under auto
