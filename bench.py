@@ -243,14 +243,25 @@ def bench_mlp(steps, warmup, precision):
     with torch.cuda.graph(graph2):
         step_forked()
     graph2_ms, _ = time_launches(graph2.replay, steps, warmup)
-    # the big forward GEMM and the two narrow products on their own
-    l1_ms, _ = time_launches(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
-                                              epilogue=cd.EPI_RELU, precision=precision, out=H),
-                             steps, warmup)
-    l2_ms, _ = time_launches(lambda: ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL,
-                                              precision=precision, out=Y, workspace=ws_f2),
-                             steps, warmup)
-    dh_ms, _ = time_launches(bwd_mask, steps, warmup)
+    # the big forward GEMM and the two narrow products on their own, each as
+    # a HIP graph of 20 back-to-back launches (kernel time, not the ~20 us
+    # per-launch host cost of an eager ctypes call)
+    def per_launch_ms(fn, reps=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        ms, _ = time_launches(g.replay, steps, warmup)
+        return ms / reps
+    l1_ms = per_launch_ms(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
+                                           epilogue=cd.EPI_RELU, precision=precision, out=H,
+                                           workspace=ws_f1))
+    l2_ms = per_launch_ms(lambda: ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL,
+                                           precision=precision, out=Y, workspace=ws_f2))
+    dh_ms = per_launch_ms(bwd_mask)
     return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
             "fwd_tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12,
             "bwd_tflops": bwd_flops / (bwd_ms * 1e-3) / 1e12,

@@ -107,6 +107,10 @@ size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms);
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream);
 // 16-bit operands (in_dtype CDX_DTYPE_F16 or CDX_DTYPE_BF16), fp32 accumulation and C.
 int launch_gemm_16(const GemmArgs& g, int in_dtype, hipStream_t stream);
+// GEMMs with K <= 16 (narrow_kind 1) or N <= 16 (2), plain output map, no
+// batch / ones column (0: use the tiled kernels); no workspace.
+int narrow_kind(const GemmArgs& g);
+int launch_gemm_narrow(const GemmArgs& g, hipStream_t stream);
 int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
                  const double* A, int64_t lda, const double* B, int64_t ldb,
                  double* C, int64_t ldc, hipStream_t stream);

@@ -69,7 +69,7 @@ int dispatch16(const GemmArgs& g, hipStream_t stream) {
 }  // namespace
 
 size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms) {
-    if (tn_split_to_f32(g, terms)) return gemm_f32_workspace(g);
+    if (narrow_kind(g) || tn_split_to_f32(g, terms)) return gemm_f32_workspace(g);
     switch (choose_bf(g, terms)) {
         case BfCfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case BfCfg::Huge: return ws_of<CfgHuge>(g);
@@ -78,8 +78,11 @@ size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms) {
     }
 }
 
+// Products with K <= 16 or N <= 16 (narrow_kind) take the FP32 narrow
+// kernels in the TF32 modes too: they are bound by memory, not by the MFMA
+// rate, and their exact fp32 products are inside the TF32-mode error bar.
 int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream) {
-    if (tn_split_to_f32(g, terms)) return launch_gemm_f32(g, stream);
+    if (narrow_kind(g) || tn_split_to_f32(g, terms)) return launch_gemm_f32(g, stream);
     return terms == 4 ? dispatch<4>(g, stream) : dispatch<3>(g, stream);
 }
 

@@ -449,6 +449,7 @@ size_t ws_of(const GemmArgs& g) {
 }  // namespace
 
 size_t gemm_f32_workspace(const GemmArgs& g) {
+    if (narrow_kind(g)) return 0;
     bool blocked;
     const F32Cfg c = choose_f32(g, blocked);
     if (blocked) return 0;
@@ -461,6 +462,7 @@ size_t gemm_f32_workspace(const GemmArgs& g) {
 }
 
 int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
+    if (narrow_kind(g)) return launch_gemm_narrow(g, stream);
     bool blocked;
     const F32Cfg c = choose_f32(g, blocked);
     if (blocked) {

@@ -1,0 +1,261 @@
+// GEMMs with a tiny inner or output dimension, which the tiled MFMA kernels
+// run at a few percent of their rate because a k-loop of a handful of steps
+// is all latency (the MLP's 10-wide layer: C4's 8192 x 10 x 256 forward and
+// 8192 x 256 x 10 hidden-layer gradient).  Both are bound by the bytes they
+// move, so each is organised around one pass over memory:
+//
+//  * tiny K (K <= 16): each thread forms 4 consecutive outputs of a few rows
+//    as fp32 FMA chains over k ascending -- the reference SGEMM's own
+//    arithmetic (sgemm_general_kernel, src/kernels/matmul_kernel.cu:632-647)
+//    -- reading op(A)'s rows and op(B)'s 4 columns (cached; tiny) and
+//    writing C through the epilogue.  Traffic: C written once (plus aux read
+//    once for the activation-backward epilogues).
+//  * narrow N (N <= 16): a workgroup owns 16 rows; its four waves split K in
+//    four contiguous quarters, each running v_mfma_f32_16x16x4_f32 on
+//    operands read straight from global memory (no LDS staging: op(A)'s rows
+//    are read once, op(B) is a few KB and stays in cache), with the library's
+//    k-permutation (lane group g feeds MFMA q with k = 4g + q, so a
+//    k-contiguous operand is one 16-byte load per 16 k).  The four partial
+//    16 x 16 tiles are summed in LDS in wave order (deterministic) and
+//    written through the epilogue.  Traffic: op(A) read once, C written once.
+//
+// Both compute fp32 products in every precision mode (exact products: inside
+// the TF32-mode error bar, as for the other FP32-routed shapes).  Plain
+// row-major output map only, no batch, no ones column; everything else goes
+// to the tiled kernels.
+#include <type_traits>
+
+#include "cdx_internal.hpp"
+
+namespace cdx {
+namespace {
+
+struct NarrowArgs {
+    const float* A; const float* B; float* C; const float* bias;
+    int64_t M, N, K, lda, ldb, ldc;
+    int bias_mode, epilogue;
+    const float* aux; int64_t ldaux;
+    int opA, opB;
+    int vec_a, vec_b;   // 16-byte loads allowed (aligned base and leading dim)
+};
+
+// (narrow-N kernel: transposition chosen at run time)
+__device__ __forceinline__ float opa(const NarrowArgs& p, int64_t m, int64_t k) {
+    return p.opA == CDX_OP_N ? p.A[m * p.lda + k] : p.A[k * p.lda + m];
+}
+__device__ __forceinline__ float opb(const NarrowArgs& p, int64_t k, int64_t n) {
+    return p.opB == CDX_OP_N ? p.B[k * p.ldb + n] : p.B[n * p.ldb + k];
+}
+
+// One thread: row m, columns n0 .. n0+3.  OPA / OPB / ACT fixed at compile
+// time (straight-line code); VEC: 16-byte accesses to op(B) (OPB = N), aux
+// and C where a thread's 4 columns are whole.
+// rows per thread: op(B)'s 4 columns stay in registers across them (C4's
+// 8192 x 256 x 10 hidden gradient: 1, 2, 4 and 8 rows measured 6.7, 7.3,
+// 6.4 and 9.8 us -- op(B) re-reads through L1 against fewer threads in
+// flight; a plain copy of the same 8.4 MB takes 3.4 us)
+constexpr int TK_ROWS = 4;
+
+template <int OPA, int OPB, int ACT, bool VEC>
+__global__ __launch_bounds__(256)
+void gemm_tinyk_kernel(NarrowArgs p) {
+    const int64_t ngroups = ceil_div(p.N, 4);
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ceil_div(p.M, TK_ROWS) * ngroups) return;
+    const int64_t m0 = (t / ngroups) * TK_ROWS, n0 = (t % ngroups) * 4;
+    constexpr bool BWD = ACT >= CDX_EPI_BWD_RELU;
+    // WH: this thread's 4 columns are whole (16-byte accesses); one branch
+    // here, straight-line code below
+    auto run = [&](auto wh_c) {
+        constexpr bool WH = decltype(wh_c)::value;
+        // op(B)'s 4 columns for all 16 k, loaded once for TK_ROWS rows (k >= K
+        // clamped to k = 0, always in range, so the loads issue together;
+        // the chains stop at K)
+        float bv[16][4];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int64_t kk = k < p.K ? k : 0;
+            if constexpr (OPB == CDX_OP_N && WH) {
+                const float4 v = *reinterpret_cast<const float4*>(p.B + kk * p.ldb + n0);
+                bv[k][0] = v.x; bv[k][1] = v.y; bv[k][2] = v.z; bv[k][3] = v.w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int64_t n = n0 + c < p.N ? n0 + c : n0;
+                    bv[k][c] = OPB == CDX_OP_N ? p.B[kk * p.ldb + n] : p.B[n * p.ldb + kk];
+                }
+            }
+        }
+        float bcol[4] = {0.f, 0.f, 0.f, 0.f};
+        if (!BWD && p.bias_mode == CDX_BIAS_COL) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) bcol[c] = p.bias[n0 + c < p.N ? n0 + c : n0];
+        }
+#pragma unroll
+        for (int i = 0; i < TK_ROWS; ++i) {
+            const int64_t m = m0 + i;
+            if (m >= p.M) break;
+            // the activation input first: its load overlaps the operand loads
+            float x[4] = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (BWD) {
+                const float* ax = p.aux + m * p.ldaux + n0;
+                if constexpr (WH) {
+                    const float4 v = *reinterpret_cast<const float4*>(ax);
+                    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) x[c] = ax[n0 + c < p.N ? c : 0];
+                }
+            }
+            float av[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int64_t kk = k < p.K ? k : 0;
+                av[k] = OPA == CDX_OP_N ? p.A[m * p.lda + kk] : p.A[kk * p.lda + m];
+            }
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                if (k >= p.K) break;   // K is uniform: a scalar branch
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[c] = fmaf(av[k], bv[k][c], acc[c]);
+            }
+            float r[4];
+            if constexpr (BWD) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) r[c] = bwd_fixed<ACT>(acc[c], x[c]);
+            } else {
+                const float brow = p.bias_mode == CDX_BIAS_ROW ? p.bias[m] : 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) r[c] = act_fixed<ACT>(acc[c] + bcol[c] + brow);
+            }
+            float* cr = p.C + m * p.ldc + n0;
+            if constexpr (WH) {
+                *reinterpret_cast<float4*>(cr) = make_float4(r[0], r[1], r[2], r[3]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (n0 + c < p.N) cr[c] = r[c];
+            }
+        }
+    };
+    if (VEC && n0 + 3 < p.N) run(std::true_type{});
+    else run(std::false_type{});
+}
+
+template <int OPA, int OPB, int ACT>
+int launch_tinyk3(const NarrowArgs& p, bool vec, dim3 grid, hipStream_t stream) {
+    if (vec)
+        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, true>), grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, false>), grid, dim3(256), 0, stream, p);
+    return hip_error(hipGetLastError(), "gemm_tinyk_kernel launch");
+}
+
+template <int OPA, int OPB>
+int launch_tinyk2(const NarrowArgs& p, bool vec, dim3 grid, hipStream_t stream) {
+    switch (p.epilogue) {
+        case CDX_EPI_RELU: return launch_tinyk3<OPA, OPB, CDX_EPI_RELU>(p, vec, grid, stream);
+        case CDX_EPI_GELU: return launch_tinyk3<OPA, OPB, CDX_EPI_GELU>(p, vec, grid, stream);
+        case CDX_EPI_SILU: return launch_tinyk3<OPA, OPB, CDX_EPI_SILU>(p, vec, grid, stream);
+        case CDX_EPI_SIGMOID: return launch_tinyk3<OPA, OPB, CDX_EPI_SIGMOID>(p, vec, grid, stream);
+        case CDX_EPI_BWD_RELU: return launch_tinyk3<OPA, OPB, CDX_EPI_BWD_RELU>(p, vec, grid, stream);
+        case CDX_EPI_BWD_GELU: return launch_tinyk3<OPA, OPB, CDX_EPI_BWD_GELU>(p, vec, grid, stream);
+        case CDX_EPI_BWD_SILU: return launch_tinyk3<OPA, OPB, CDX_EPI_BWD_SILU>(p, vec, grid, stream);
+        case CDX_EPI_BWD_SIGMOID: return launch_tinyk3<OPA, OPB, CDX_EPI_BWD_SIGMOID>(p, vec, grid, stream);
+        default: return launch_tinyk3<OPA, OPB, CDX_EPI_NONE>(p, vec, grid, stream);
+    }
+}
+
+// Four waves per workgroup, one 16-row tile, K in four quarters.
+__global__ __launch_bounds__(256)
+void gemm_narrow_n_kernel(NarrowArgs p, int64_t kq) {
+    __shared__ float red[4][16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int64_t m0 = (int64_t)blockIdx.x * 16;
+    const int64_t m = m0 + l16;
+    const bool m_ok = m < p.M, n_ok = l16 < p.N;
+    const int64_t kb = wave * kq, ke = kb + kq < p.K ? kb + kq : p.K;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    // A row m (this lane's MFMA row) and B column n = l16
+    const bool va = p.vec_a && p.opA == CDX_OP_N && m_ok;
+    const bool vb = p.vec_b && p.opB == CDX_OP_T && n_ok;
+    for (int64_t k0 = kb; k0 < ke; k0 += 16) {
+        const int64_t k = k0 + 4 * lq;   // this lane's 4 k
+        float a[4], b[4];
+        if (va && k + 3 < ke) {
+            const float4 v = *reinterpret_cast<const float4*>(p.A + m * p.lda + k);
+            a[0] = v.x; a[1] = v.y; a[2] = v.z; a[3] = v.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) a[q] = (m_ok && k + q < ke) ? opa(p, m, k + q) : 0.0f;
+        }
+        if (vb && k + 3 < ke) {
+            const float4 v = *reinterpret_cast<const float4*>(p.B + (int64_t)l16 * p.ldb + k);
+            b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) b[q] = (n_ok && k + q < ke) ? opb(p, k + q, l16) : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[q], b[q], acc, 0, 0, 0);
+    }
+    // D layout: register r of lane l is row 4*(l/16) + r, column l % 16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][l16] = acc[r];
+    __syncthreads();
+    const int row = tid >> 4, col = tid & 15;
+    if (m0 + row < p.M && col < p.N) {
+        const float v = ((red[0][row][col] + red[1][row][col]) + red[2][row][col]) + red[3][row][col];
+        const EpiArgs e{p.C, p.ldc, p.M, p.N, 0, 0, p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux};
+        store_one(e, m0 + row, col, v);
+    }
+}
+
+NarrowArgs args_of(const GemmArgs& g) {
+    NarrowArgs p{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
+                 g.M, g.N, g.K, g.lda, g.ldb, g.ldc, g.bias_mode, g.epilogue, g.aux, g.ldaux,
+                 g.opA, g.opB, 0, 0};
+    p.vec_a = (uintptr_t)g.A % 16 == 0 && g.lda % 4 == 0;
+    p.vec_b = (uintptr_t)g.B % 16 == 0 && g.ldb % 4 == 0;
+    return p;
+}
+
+}  // namespace
+
+int narrow_kind(const GemmArgs& g) {
+    if (g.batch != 1 || g.n_split > 0 || g.colsum || g.ones_col >= 0 || g.M <= 0 || g.N <= 0)
+        return 0;
+    if (g.K >= 1 && g.K <= 16) return 1;                    // tiny K
+    if (g.N <= 16 && g.K >= 64 && g.M >= 64) return 2;      // narrow N
+    return 0;
+}
+
+int launch_gemm_narrow(const GemmArgs& g, hipStream_t stream) {
+    const NarrowArgs p = args_of(g);
+    if (narrow_kind(g) == 1) {
+        const int64_t threads = ceil_div(g.M, TK_ROWS) * ceil_div(g.N, 4);
+        const int64_t blocks = ceil_div(threads, 256);
+        if (blocks > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many rows");
+        // 16-byte accesses: C (and aux, and op(B) when not transposed)
+        // 16-byte aligned with 4-element leading dimensions
+        const bool bwd = g.epilogue >= CDX_EPI_BWD_RELU && g.epilogue <= CDX_EPI_BWD_SIGMOID;
+        const bool vec = (uintptr_t)g.C % 16 == 0 && g.ldc % 4 == 0 &&
+                         (g.opB == CDX_OP_T || (p.vec_b != 0)) &&
+                         (!bwd || ((uintptr_t)g.aux % 16 == 0 && g.ldaux % 4 == 0));
+        const dim3 grid((unsigned)blocks);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_tinyk2<CDX_OP_N, CDX_OP_N>(p, vec, grid, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_tinyk2<CDX_OP_N, CDX_OP_T>(p, vec, grid, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_tinyk2<CDX_OP_T, CDX_OP_N>(p, vec, grid, stream);
+        return launch_tinyk2<CDX_OP_T, CDX_OP_T>(p, vec, grid, stream);
+    }
+    const int64_t blocks = ceil_div(g.M, 16);
+    if (blocks > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many rows");
+    const int64_t kq = ceil_div(ceil_div(g.K, 4), 16) * 16;   // whole 16-k steps per wave
+    hipLaunchKernelGGL(gemm_narrow_n_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, kq);
+    return hip_error(hipGetLastError(), "gemm_narrow_n_kernel launch");
+}
+
+}  // namespace cdx

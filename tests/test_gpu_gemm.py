@@ -117,6 +117,40 @@ def test_fp32_gemm_parity_shapes(M, N, K, tA, tB):
     assert e <= 2 * e_ref + floor, (e, e_ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 256, 10), (37, 129, 1), (300, 17, 16), (5, 3, 7)])
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("mode", ["fp32", "tf32"])
+def test_tiny_k_bit_exact_with_reference_chain(M, N, K, tA, tB, mode):
+    """K <= 16 runs an fp32 FMA chain per output over k ascending -- the
+    reference SGEMM's arithmetic (matmul_kernel.cu:632-647) -- in every
+    precision mode: bit-exact with the oracle's seq-FMA restatement."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(M + 7 * N + 31 * K)
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (N, K) if tB else (K, N))
+    prec = cd.PREC_FP32 if mode == "fp32" else cd.PREC_TF32MODE
+    say("tiny-K bit-exact", M, N, K, tA, tB, mode)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, precision=prec))
+    want = oracle.sgemm_seqfma(A, B, tA, tB)
+    assert np.array_equal(C.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(8192, 256), (100, 64), (4097, 1000)])
+@pytest.mark.parametrize("N", [1, 10, 16])
+@pytest.mark.parametrize("tA,tB", [(False, True), (True, False)])
+def test_narrow_n_parity(M, N, K, tA, tB):
+    """N <= 16 (the MLP's 10-class layer): MFMA on operands read straight
+    from global memory, K in four quarters summed in a fixed order."""
+    rng = np.random.default_rng(M + N + K)
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (N, K) if tB else (K, N))
+    say("narrow-N", M, N, K, tA, tB)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB))
+    C64, e_ref = _ref_errors(A, B, tA, tB)
+    e = oracle.rel_fro(C, C64)
+    assert e <= 2 * e_ref + F32_FLOOR, (e, e_ref)
+
+
 def test_fp32_c1_512_uniform():
     """C1: 512^3, A, B ~ U[-1, 1]."""
     rng = np.random.default_rng(101)
