@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 FP32_PEAK_TFLOPS = 157.3      # MI355X dense FP32 MFMA
 BF16_PEAK_TFLOPS = 2516.6     # MI355X dense BF16 MFMA; bf16x3 logical ceiling = /3
+HEAD_SETTLE_S = 0.3           # untimed clock-settling launches before the headline
 HBM_PEAK_GBS = 8000.0
 
 
@@ -88,6 +89,22 @@ def time_launches(fn, steps, warmup, min_warm_s=0.0):
     torch.cuda.synchronize()
     per = [e0.elapsed_time(e1) for e0, e1 in evs]
     return outer0.elapsed_time(outer1) / steps, per
+
+
+def per_launch_ms(steps, warmup, fn, reps=20):
+    """Kernel time of fn's launches: a HIP graph of `reps` back-to-back calls,
+    replayed `steps` times after `warmup` replays (no per-launch host cost;
+    fn must take its scratch from preallocated buffers)."""
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    ms, _ = time_launches(g.replay, steps, warmup)
+    return ms / reps
 
 
 def bench_gemm(n, precision, steps, warmup, seed, min_warm_s=0.0):
@@ -246,22 +263,12 @@ def bench_mlp(steps, warmup, precision):
     # the big forward GEMM and the two narrow products on their own, each as
     # a HIP graph of 20 back-to-back launches (kernel time, not the ~20 us
     # per-launch host cost of an eager ctypes call)
-    def per_launch_ms(fn, reps=20):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
-                fn()
-        ms, _ = time_launches(g.replay, steps, warmup)
-        return ms / reps
-    l1_ms = per_launch_ms(lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
+    l1_ms = per_launch_ms(steps, warmup, lambda: ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL,
                                            epilogue=cd.EPI_RELU, precision=precision, out=H,
                                            workspace=ws_f1))
-    l2_ms = per_launch_ms(lambda: ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL,
+    l2_ms = per_launch_ms(steps, warmup, lambda: ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL,
                                            precision=precision, out=Y, workspace=ws_f2))
-    dh_ms = per_launch_ms(bwd_mask)
+    dh_ms = per_launch_ms(steps, warmup, bwd_mask)
     return {"fwd_ms": fwd_ms, "bwd_ms": bwd_ms,
             "fwd_tflops": fwd_flops / (fwd_ms * 1e-3) / 1e12,
             "bwd_tflops": bwd_flops / (bwd_ms * 1e-3) / 1e12,
@@ -289,11 +296,14 @@ def bench_mlp_api(steps, warmup, precision):
     model = nn.Sequential(nn.Linear(784, 256), nn.ReLU(), nn.Linear(256, 10))
     cuDeep.init.xavier_uniform_(model[0].weight)
     cuDeep.init.xavier_uniform_(model[2].weight)
-    X = T.from_numpy(rng.standard_normal((8192, 784), dtype=np.float32))
+    # the input requires its gradient: C4's backward includes dX of the first
+    # layer (dX = dY W)
+    X = T.from_numpy(rng.standard_normal((8192, 784), dtype=np.float32), requires_grad=True)
     dY = T.from_numpy(rng.standard_normal((8192, 10), dtype=np.float32))
 
     def step():
         model.zero_grad()
+        X.grad = None
         y = model(X)
         y.backward(dY)
 
@@ -305,7 +315,8 @@ def bench_mlp_api(steps, warmup, precision):
 
 def bench_conv(steps, warmup, precision):
     """C5: N=32, C=64, 56x56 -> 64, 3x3, s1, p1: im2col + GEMM (bias in the
-    epilogue, output written NCHW), Winograd, and the backward routes."""
+    epilogue, output written NCHW), Winograd, the implicit GEMM, the backward
+    routes; and a 7x7 layer of the same size (implicit route)."""
     import torch
     import cudeep_amd as cd
     import cudeep_amd.ops as ops
@@ -319,7 +330,7 @@ def bench_conv(steps, warmup, precision):
     col = ws.view(576, 100352)
     conv_ms, _ = time_launches(lambda: ops.conv2d_forward(x, w, b, (1, 1), (1, 1), precision,
                                                           workspace=ws, out=y), steps, warmup)
-    im_ms, _ = time_launches(lambda: ops.im2col(x, 3, 3, (1, 1), (1, 1), out=col), steps, warmup)
+    im_ms = per_launch_ms(steps, warmup, lambda: ops.im2col(x, 3, 3, (1, 1), (1, 1), out=col))
     flops = 2.0 * 32 * 64 * 56 * 56 * 64 * 9
     im2col_bytes = 576 * 100352 * 4 + 32 * 64 * 56 * 56 * 4
     # Winograd F(4x4, 3x3) route (the reference's route for this layer); TFLOP/s
@@ -358,13 +369,29 @@ def bench_conv(steps, warmup, precision):
     bd_ms, _ = time_launches(bwd_data, steps, warmup)
     bdw_ms, _ = time_launches(bwd_data_wino, steps, warmup)
     bw_ms, _ = time_launches(bwd_weight, steps, warmup)
+    # the im2col route's GEMM on its own (weight [64, 576] x col [576, 100352],
+    # plain row-major output instead of the NCHW map; same kernel family)
+    gflat = torch.empty((64, 100352), device="cuda")
+    gemm_ms = per_launch_ms(steps, warmup, lambda: ops.gemm(w.view(64, 576), col,
+                                                           precision=precision, out=gflat))
+    # implicit GEMM (no column buffer): this layer forced through it, and a
+    # 7x7 layer of the same size, which the forward routes there (its column
+    # buffer would be 1.26 GB)
+    imp_ms, _ = time_launches(lambda: ops.conv2d_implicit(x, w, b, (1, 1), (1, 1), out=y),
+                              steps, warmup)
+    w7 = torch.randn((64, 64, 7, 7), device="cuda", generator=g) * (2.0 / 3136) ** 0.5
+    c7_ms, _ = time_launches(lambda: ops.conv2d_forward(x, w7, b, (1, 1), (3, 3), precision,
+                                                        out=y), max(3, steps // 5), 3)
+    flops7 = 2.0 * 32 * 64 * 56 * 56 * 64 * 49
     return {"conv_ms": conv_ms, "conv_tflops": flops / (conv_ms * 1e-3) / 1e12,
+            "gemm_ms": gemm_ms, "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12,
+            "implicit_3x3_ms": imp_ms, "implicit_3x3_tflops": flops / (imp_ms * 1e-3) / 1e12,
+            "conv7x7_implicit_ms": c7_ms,
+            "conv7x7_implicit_tflops": flops7 / (c7_ms * 1e-3) / 1e12,
             "bwd_ms": bwd_ms, "bwd_tflops": 2 * flops / (bwd_ms * 1e-3) / 1e12,
             "bwd_data_im2col_ms": bd_ms, "bwd_data_winograd_ms": bdw_ms,
             "bwd_weight_ms": bw_ms,
             "im2col_ms": im_ms, "im2col_gbs": im2col_bytes / (im_ms * 1e-3) / 1e9,
-            "gemm_ms_est": conv_ms - im_ms,
-            "gemm_tflops_est": flops / max(conv_ms - im_ms, 1e-6) / 1e-3 / 1e12,
             "winograd_ms": wino_ms, "winograd_tflops_equiv": flops / (wino_ms * 1e-3) / 1e12}
 
 
@@ -513,9 +540,6 @@ def main():
                        min_warm_s=0.1)
         log("tf32mode 4096^3:", r)
         return
-    log("headline: fp32 4096^3")
-    head = bench_gemm(4096, cd.PREC_FP32, args.steps, args.warmup, seed=2)
-    log("fp32 4096^3:", head)
     extra = {}
     # The reduced-precision GEMMs run ~12 % slower for their first ~20 ms of
     # back-to-back launches (the clock settles under the new load; measured
@@ -537,6 +561,18 @@ def main():
             r = bench_gemm16(4096, dt, args.steps, w_extra, seed=6, min_warm_s=warm_s)
             extra[f"{dt}_gemm_4096"] = r
             log(f"{dt} GEMM 4096^3:", r)
+    # The headline is timed while the clock is settled under sustained MFMA
+    # work: measured on one MI355X, 4096^3 FP32 launches run at 125-126
+    # TFLOP/s from idle (or after 0.5 s idle) and at 135 TFLOP/s after 0.3 s
+    # of back-to-back MFMA launches.  So it runs straight after the
+    # reduced-precision GEMM lines, and after its W warmup launches keeps
+    # launching untimed until HEAD_SETTLE_S has passed; the timed region is
+    # still exactly K launches.
+    log("headline: fp32 4096^3")
+    head = bench_gemm(4096, cd.PREC_FP32, args.steps, args.warmup, seed=2,
+                      min_warm_s=HEAD_SETTLE_S)
+    log("fp32 4096^3:", head)
+    if not args.headline_only:
         for prec, name in ((cd.PREC_FP32, "fp32"), (cd.PREC_TF32MODE, "tf32mode")):
             extra[f"mlp_c4_{name}"] = bench_mlp(args.steps, args.warmup, prec)
             log(f"mlp {name}:", extra[f"mlp_c4_{name}"])
@@ -570,6 +606,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_settle_s": HEAD_SETTLE_S,
         "ms_per_step": round(head["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
