@@ -181,11 +181,17 @@ def bench_mlp(steps, warmup, precision):
     ws_f1 = wsp(ops.gemm_workspace_bytes(8192, 256, 784, precision=precision, transB=True))
     ws_f2 = wsp(ops.gemm_workspace_bytes(8192, 10, 256, precision=precision, transB=True))
 
-    def fwd():
+    def fwd1():
         ops.gemm(X, W1, transB=True, bias=b1, bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU,
                  precision=precision, out=H, workspace=ws_f1)
+
+    def fwd2():
         ops.gemm(H, W2, transB=True, bias=b2, bias_mode=cd.BIAS_COL, precision=precision, out=Y,
                  workspace=ws_f2)
+
+    def fwd():
+        fwd1()
+        fwd2()
 
     def bwd_layer2():
         # dW2 = dY2^T H and db2 = column sums of dY2, one launch (+ split-K reduction)
@@ -232,16 +238,18 @@ def bench_mlp(steps, warmup, precision):
         step()
     graph_ms, _ = time_launches(graph.replay, steps, warmup)
 
-    # The same step with the backward's independent branches on two side
-    # streams (layer 2's weight + bias gradient beside the masked dH; layer
-    # 1's beside dX), each on its own workspace.
+    # The same step with its independent branches on two side streams, each
+    # launch on its own workspace: with the output gradient dY2 given, layer
+    # 2's forward and its weight + bias gradient need only H, so they run
+    # beside the masked dH; layer 1's weight + bias gradient beside dX.
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
 
     def step_forked():
         main = torch.cuda.current_stream()
-        fwd()
+        fwd1()
         s1.wait_stream(main)
         with torch.cuda.stream(s1):
+            fwd2()
             bwd_layer2()
         bwd_mask()
         s2.wait_stream(main)

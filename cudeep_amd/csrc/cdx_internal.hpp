@@ -410,12 +410,24 @@ __device__ __forceinline__ void store_one(const EpiArgs& e, int64_t m, int64_t n
     e.C[m * e.ldc + col] = r;
 }
 
+// Row (or column) of element `idx` (0..15) of 16 x 16 accumulator block
+// `blk` in a wave tile whose blocks are interleaved V at a time: block blk
+// covers rows 16 V (blk / V) + V idx + blk % V.  V = 1 is the plain layout
+// (rows 16 blk + idx); V = 2 / 4 is the layout an m/n-contiguous operand
+// gets when each lane reads V consecutive rows with one LDS read and feeds
+// them to V different MFMAs.
+template <int V>
+__device__ __forceinline__ int blk_pos(int blk, int idx) {
+    return 16 * V * (blk / V) + V * idx + blk % V;
+}
+
 // Writes one wave's FM x FN grid of 16 x 16 MFMA accumulator tiles (D
 // layout of v_mfma_f32_16x16x*: register r of lane l is row 4 (l / 16) + r,
-// column l % 16), whose top-left element is (m0, n0).  The activation is a
+// column l % 16 of its block), whose top-left element is (m0, n0); VM / VN
+// are the row / column block interleaves (blk_pos).  The activation is a
 // template parameter so the per-element code is straight-line; CHECK adds
 // the M / N bounds tests that ragged tiles need.
-template <int FM, int FN, bool CHECK, bool SPLITN, int ACT>
+template <int FM, int FN, bool CHECK, bool SPLITN, int ACT, int VM = 1, int VN = 1>
 __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], const EpiArgs& e,
                                               int64_t m0, int64_t n0, int lane) {
     const int l16 = lane & 15, lq = lane >> 4;
@@ -424,7 +436,7 @@ __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], cons
     float bcol[FN];
 #pragma unroll
     for (int jn = 0; jn < FN; ++jn) {
-        const int64_t n = n0 + jn * 16 + l16;
+        const int64_t n = n0 + blk_pos<VN>(jn, l16);
         col_off[jn] = n;
         if (SPLITN) {
             // NCHW map; 32-bit quotient when it fits (a 64-bit divide is a
@@ -444,13 +456,13 @@ __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], cons
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int64_t m = m0 + i * 16 + 4 * lq + r;
+            const int64_t m = m0 + blk_pos<VM>(i, 4 * lq + r);
             if (CHECK && m >= e.M) continue;
             const float brow = bias_row ? e.bias[m] : 0.0f;
             float* crow = e.C + m * e.ldc;
 #pragma unroll
             for (int jn = 0; jn < FN; ++jn) {
-                const int64_t n = n0 + jn * 16 + l16;
+                const int64_t n = n0 + blk_pos<VN>(jn, l16);
                 if (CHECK && n >= e.N) continue;
                 if (CHECK && e.colsum && n == e.n_main) {   // the ones column
                     e.colsum[m] = acc[i][jn][r];
@@ -465,24 +477,24 @@ __device__ __forceinline__ void write_acc_act(const floatx4 (&acc)[FM][FN], cons
     }
 }
 
-template <int FM, int FN, bool CHECK, bool SPLITN>
+template <int FM, int FN, bool CHECK, bool SPLITN, int VM = 1, int VN = 1>
 __device__ __forceinline__ void write_acc(const floatx4 (&acc)[FM][FN], const EpiArgs& e,
                                           int64_t m0, int64_t n0, int lane) {
     if constexpr (!SPLITN) {   // backward epilogues: plain output map only
         switch (e.epilogue) {
-            case CDX_EPI_BWD_RELU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_RELU>(acc, e, m0, n0, lane); return;
-            case CDX_EPI_BWD_GELU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_GELU>(acc, e, m0, n0, lane); return;
-            case CDX_EPI_BWD_SILU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_SILU>(acc, e, m0, n0, lane); return;
-            case CDX_EPI_BWD_SIGMOID: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_SIGMOID>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_RELU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_RELU, VM, VN>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_GELU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_GELU, VM, VN>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_SILU: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_SILU, VM, VN>(acc, e, m0, n0, lane); return;
+            case CDX_EPI_BWD_SIGMOID: write_acc_act<FM, FN, CHECK, false, CDX_EPI_BWD_SIGMOID, VM, VN>(acc, e, m0, n0, lane); return;
             default: break;
         }
     }
     switch (e.epilogue) {
-        case CDX_EPI_RELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_RELU>(acc, e, m0, n0, lane); break;
-        case CDX_EPI_GELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_GELU>(acc, e, m0, n0, lane); break;
-        case CDX_EPI_SILU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_SILU>(acc, e, m0, n0, lane); break;
-        case CDX_EPI_SIGMOID: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_SIGMOID>(acc, e, m0, n0, lane); break;
-        default: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_NONE>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_RELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_RELU, VM, VN>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_GELU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_GELU, VM, VN>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_SILU: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_SILU, VM, VN>(acc, e, m0, n0, lane); break;
+        case CDX_EPI_SIGMOID: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_SIGMOID, VM, VN>(acc, e, m0, n0, lane); break;
+        default: write_acc_act<FM, FN, CHECK, SPLITN, CDX_EPI_NONE, VM, VN>(acc, e, m0, n0, lane); break;
     }
 }
 

@@ -53,6 +53,7 @@ struct KParams {
     // is nb + 1; colsum receives that column's results.
     int64_t nb, ones;
     float* colsum;
+    int interior;   // kLoadChecked: whole tiles may take the unchecked path
 };
 
 // Loads a ROWS x COLS tile (COLS contiguous in memory) starting at (r0, c0)
@@ -145,23 +146,56 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int grou
     tn = in_g / gsize;
 }
 
+// Reads V consecutive floats of one LDS row (V = 1, 2 or 4: one 4-, 8- or
+// 16-byte read) into fragment slots f[blk0 .. blk0 + V - 1][j].
+template <int V, int F>
+__device__ __forceinline__ void read_rows(const float* p, float (&f)[F][4], int blk0, int j) {
+    if constexpr (V == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(p);
+        f[blk0][j] = t.x; f[blk0 + 1][j] = t.y; f[blk0 + 2][j] = t.z; f[blk0 + 3][j] = t.w;
+    } else if constexpr (V == 2) {
+        const float2 t = *reinterpret_cast<const float2*>(p);
+        f[blk0][j] = t.x; f[blk0 + 1][j] = t.y;
+    } else {
+        f[blk0][j] = *p;
+    }
+}
+
+// LDS geometry and fragment-read widths of one configuration.
+//  * m/n-contiguous operands are read V consecutive rows (columns) per lane
+//    with one LDS read, feeding V MFMAs whose blocks are interleaved
+//    (blk_pos); k-contiguous operands keep the plain layout.  (Measured on
+//    MI355X: 16-byte reads gain 1-4 %; 8-byte reads gain only on A when B is
+//    read 16 bytes at a time too -- 2048^3 TN 141 -> 132 us -- and lose
+//    elsewhere: 2048^3 TT 132 -> 138 us, 8192 x 784 x 256 NN on 64 x 64
+//    tiles 44 -> 45 us.)
+//  * k-contiguous operands are [mn][BK+4], m/n-contiguous ones [BK][mn+4]:
+//    with 4-byte reads, lane groups lq = 0..3 read rows 4 apart, 16 banks
+//    apart with the pad; wider reads take one contiguous row segment per
+//    16 lanes.
+template <class CF, int OPA, int OPB>
+struct Geo {
+    static constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
+    static constexpr int VB = OPB == CDX_OP_T ? 1 : (CF::FN % 4 == 0 ? 4 : 1);
+    static constexpr int VA = OPA == CDX_OP_N ? 1 : (CF::FM % 4 == 0 ? 4 : CF::FM % 2 == 0 && VB == 4 ? 2 : 1);
+    static constexpr int A_STRIDE = OPA == CDX_OP_N ? BK + 4 : BM + 4;
+    static constexpr int A_ELEMS = OPA == CDX_OP_N ? BM * A_STRIDE : BK * A_STRIDE;
+    static constexpr int B_STRIDE = OPB == CDX_OP_N ? BN + 4 : BK + 4;
+    static constexpr int B_ELEMS = OPB == CDX_OP_N ? BK * B_STRIDE : BN * B_STRIDE;
+    static constexpr int LDS_FLOATS = 2 * (A_ELEMS + B_ELEMS);
+};
+
+// One workgroup's output tile (top-left (bm, bn)) over the k-range of p.
 // BLK: two-level k sum -- each pair of k-tiles (32 k) is summed from zero in
 // `part`, then added to `acc` (a rounding chain of ~32 + K/32 additions).
 template <class CF, int OPA, int OPB, int MODE, bool SPLITN, bool BLK>
-__global__ __launch_bounds__(CF::NT)
-void gemm_f32_mfma_kernel(KParams p) {
-    constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
+__device__ __forceinline__ void gemm_tile(const KParams& p, int64_t bm, int64_t bn, float* lds) {
+    using G = Geo<CF, OPA, OPB>;
+    constexpr int BK = CF::BK;
     constexpr int NT = CF::NT, FM = CF::FM, FN = CF::FN;
-    static_assert(BK % 16 == 0, "BK must be a multiple of 16");
-
-    // LDS geometry: k-contiguous operands are [mn][BK+4], mn-contiguous
-    // operands are [BK][mn+4].
-    constexpr int A_STRIDE = OPA == CDX_OP_N ? BK + 4 : BM + 4;
-    constexpr int A_ELEMS = OPA == CDX_OP_N ? BM * A_STRIDE : BK * A_STRIDE;
-    constexpr int B_STRIDE = OPB == CDX_OP_N ? BN + 4 : BK + 4;
-    constexpr int B_ELEMS = OPB == CDX_OP_N ? BK * B_STRIDE : BN * B_STRIDE;
-    __shared__ __attribute__((aligned(16))) float lds[2 * (A_ELEMS + B_ELEMS)];
-
+    constexpr int VA = G::VA, VB = G::VB;
+    constexpr int A_STRIDE = G::A_STRIDE, A_ELEMS = G::A_ELEMS;
+    constexpr int B_STRIDE = G::B_STRIDE, B_ELEMS = G::B_ELEMS;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -170,27 +204,8 @@ void gemm_f32_mfma_kernel(KParams p) {
     const int l16 = lane & 15;
     const int lq = lane >> 4;   // 0..3
 
-    int tiles_m = (int)ceil_div(p.M, BM), tiles_n = (int)ceil_div(p.N, BN);
-    int tm, tn;
-    tile_of_block(tiles_m, tiles_n, CF::GROUP_M, tm, tn);
-    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
-
-    // Split-K slice: blockIdx.y owns k in [y*k_chunk, min(K, (y+1)*k_chunk))
-    // and writes a plain [M, N] partial (the reduction applies the epilogue).
-    if (gridDim.y > 1) {
-        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
-        p.A += OPA == CDX_OP_N ? k0 : k0 * p.lda;
-        p.B += OPB == CDX_OP_N ? k0 * p.ldb : k0;
-        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
-        p.C += (int64_t)blockIdx.y * p.M * p.N;
-    }
-    if (gridDim.z > 1) {
-        p.A += (int64_t)blockIdx.z * p.sa;
-        p.B += (int64_t)blockIdx.z * p.sb;
-        p.C += (int64_t)blockIdx.z * p.sc;
-    }
-
-    // Global tile loaders in memory orientation.
+    constexpr int BM = CF::BM, BN = CF::BN;
+// Global tile loaders in memory orientation.
     using LA = TileLoader<OPA == CDX_OP_N ? BM : BK, OPA == CDX_OP_N ? BK : BM, NT, MODE>;
     using LB = TileLoader<OPB == CDX_OP_N ? BK : BN, OPB == CDX_OP_N ? BN : BK, NT, MODE>;
     LA la;
@@ -238,27 +253,35 @@ void gemm_f32_mfma_kernel(KParams p) {
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 16) {
             float a[FM][4], b[FN][4];
+            if constexpr (OPA == CDX_OP_N) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int m = wm0 + i * 16 + l16;
-                if (OPA == CDX_OP_N) {
+                for (int i = 0; i < FM; ++i) {
+                    const int m = wm0 + i * 16 + l16;
                     float4 t = *reinterpret_cast<const float4*>(sA + m * A_STRIDE + kk + 4 * lq);
                     a[i][0] = t.x; a[i][1] = t.y; a[i][2] = t.z; a[i][3] = t.w;
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) a[i][j] = sA[(kk + 4 * lq + j) * A_STRIDE + m];
                 }
+            } else {
+#pragma unroll
+                for (int g = 0; g < FM / VA; ++g)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        read_rows<VA>(sA + (kk + 4 * lq + j) * A_STRIDE + wm0 + 16 * VA * g + VA * l16,
+                                      a, g * VA, j);
             }
+            if constexpr (OPB == CDX_OP_T) {
 #pragma unroll
-            for (int jn = 0; jn < FN; ++jn) {
-                const int n = wn0 + jn * 16 + l16;
-                if (OPB == CDX_OP_N) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[jn][j] = sB[(kk + 4 * lq + j) * B_STRIDE + n];
-                } else {
+                for (int jn = 0; jn < FN; ++jn) {
+                    const int n = wn0 + jn * 16 + l16;
                     float4 t = *reinterpret_cast<const float4*>(sB + n * B_STRIDE + kk + 4 * lq);
                     b[jn][0] = t.x; b[jn][1] = t.y; b[jn][2] = t.z; b[jn][3] = t.w;
                 }
+            } else {
+#pragma unroll
+                for (int g = 0; g < FN / VB; ++g)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        read_rows<VB>(sB + (kk + 4 * lq + j) * B_STRIDE + wn0 + 16 * VB * g + VB * l16,
+                                      b, g * VB, j);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -333,7 +356,49 @@ void gemm_f32_mfma_kernel(KParams p) {
     // accumulators
     const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
                       p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux, p.colsum, p.nb};
-    write_acc<FM, FN, MODE != kLoadAlignedVec, SPLITN>(acc, epi, bm + wm0, bn + wn0, lane);
+    write_acc<FM, FN, MODE != kLoadAlignedVec, SPLITN, VA, VB>(acc, epi, bm + wm0, bn + wn0, lane);
+}
+
+// MODE kLoadChecked launches (ragged M / N, unaligned operands, the ones
+// column) run their interior tiles -- clear of the edges and of the ones
+// column -- through the unchecked 16-byte loads and epilogue when
+// p.interior allows (both operands 16-byte loadable, K and the split-K
+// chunk whole k-tiles): 8192 x 784 x 256 NN has 12 of every 13 tile
+// columns interior (44 -> 40 us).
+template <class CF, int OPA, int OPB, int MODE, bool SPLITN, bool BLK>
+__global__ __launch_bounds__(CF::NT)
+void gemm_f32_mfma_kernel(KParams p) {
+    constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK;
+    static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+    __shared__ __attribute__((aligned(16))) float lds[Geo<CF, OPA, OPB>::LDS_FLOATS];
+
+    int tiles_m = (int)ceil_div(p.M, BM), tiles_n = (int)ceil_div(p.N, BN);
+    int tm, tn;
+    tile_of_block(tiles_m, tiles_n, CF::GROUP_M, tm, tn);
+    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+
+    // Split-K slice: blockIdx.y owns k in [y*k_chunk, min(K, (y+1)*k_chunk))
+    // and writes a plain [M, N] partial (the reduction applies the epilogue).
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A += OPA == CDX_OP_N ? k0 : k0 * p.lda;
+        p.B += OPB == CDX_OP_N ? k0 * p.ldb : k0;
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
+    if (gridDim.z > 1) {
+        p.A += (int64_t)blockIdx.z * p.sa;
+        p.B += (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
+    }
+    if constexpr (MODE == kLoadChecked) {
+        // p.nb: op(B)'s own columns, so the ones column stays on the checked path
+        if (p.interior && bm + BM <= p.M && bn + BN <= p.nb) {
+            gemm_tile<CF, OPA, OPB, kLoadAlignedVec, SPLITN, BLK>(p, bm, bn, lds);
+            return;
+        }
+    }
+    gemm_tile<CF, OPA, OPB, MODE, SPLITN, BLK>(p, bm, bn, lds);
 }
 
 template <class CF, int OPA, int OPB, int MODE, bool SPLITN, bool BLK>
@@ -363,6 +428,7 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
                    g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     bool split = g.n_split > 0;
+    kp.interior = kp.vec_a && kp.vec_b && g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
     if (aligned) {
         return split ? launch_cfg<CF, OPA, OPB, kLoadAlignedVec, true, BLK>(kp, splits, stream)
                      : launch_cfg<CF, OPA, OPB, kLoadAlignedVec, false, BLK>(kp, splits, stream);
@@ -410,13 +476,18 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    twice as many workgroups share the GPU (64x16x16 tiles: 8192 x 10 x
 //    256 in 9.5 us, against 13.4 for mostly-empty 64x64 ones).  A 16-row
 //    tile for M <= 16 measured no faster than Medium.
+//  * W112: N a multiple of 112 but not of 64 (C4's 784-wide backward-data
+//    product): 128x112x16, 8 waves of 16x112, so no tile column is ragged
+//    (8192 x 784 x 256 NN: 35.5 us, against 40.0 on 64x64 tiles with a
+//    16-wide edge column, 57 with 4 waves of 32x112, 52 with 256x112).
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
 using CfgMedium = Cfg<64, 64, 16, 32, 32, 8, 2>;
 using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1, 2>;
 using CfgNarrowN = Cfg<32, 16, 64, 16, 16, 8, 2>;
+using CfgW112 = Cfg<128, 112, 16, 16, 112, 8, 2>;
 
 // Configuration choice, shared by the launcher and the workspace query.
-enum class F32Cfg { NarrowN, SkinnyM, Large, Medium };
+enum class F32Cfg { NarrowN, SkinnyM, Large, Medium, W112 };
 
 // Large tiles are ~8 % faster per tile, but a CU's time is set by its largest
 // share of tiles: Large is taken when its busiest-CU share (rounded up to
@@ -436,6 +507,9 @@ F32Cfg choose_f32(const GemmArgs& g, bool& blocked) {
     blocked = g.blocked_sum && !split && g.opA == CDX_OP_N && g.opB == CDX_OP_N;
     if (g.N <= 16) return F32Cfg::NarrowN;
     if (split && !blocked) return F32Cfg::Medium;
+    if (!blocked && !split && g.N % 112 == 0 && g.N % 64 != 0 &&
+        ceil_div(g.M, 128) * (g.N / 112) >= 256)
+        return F32Cfg::W112;
     if (g.M <= 64 && g.N >= 4096) return F32Cfg::SkinnyM;
     if (large_balanced(g.M, g.N)) return F32Cfg::Large;
     return F32Cfg::Medium;
@@ -457,6 +531,7 @@ size_t gemm_f32_workspace(const GemmArgs& g) {
         case F32Cfg::NarrowN: return ws_of<CfgNarrowN>(g);
         case F32Cfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case F32Cfg::Large: return ws_of<CfgLarge>(g);
+        case F32Cfg::W112: return ws_of<CfgW112>(g);
         default: return ws_of<CfgMedium>(g);
     }
 }
@@ -477,6 +552,7 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
         case F32Cfg::NarrowN: return launch_ops<CfgNarrowN>(g, stream);
         case F32Cfg::SkinnyM: return launch_ops<CfgSkinnyM>(g, stream);
         case F32Cfg::Large: return launch_ops<CfgLarge>(g, stream);
+        case F32Cfg::W112: return launch_ops<CfgW112>(g, stream);
         default: return launch_ops<CfgMedium>(g, stream);
     }
 }

@@ -56,7 +56,12 @@ __device__ __forceinline__ float opb(const NarrowArgs& p, int64_t k, int64_t n) 
 // flight; a plain copy of the same 8.4 MB takes 3.4 us)
 constexpr int TK_ROWS = 4;
 
-template <int OPA, int OPB, int ACT, bool VEC>
+// WAVE_ROWS: ceil(N / 4) is a multiple of 64, so the 64 threads of a wave
+// share their rows m0 .. m0 + 3; the wave then loads those rows' op(A)
+// elements once (lane 16 i + k holds row m0 + i, column k) and every lane
+// takes them with readlane, instead of 16 uniform loads per row per lane
+// (C4's 8192 x 256 x 10 masked dH: 7.7 -> 4.x us).
+template <int OPA, int OPB, int ACT, bool VEC, bool WAVE_ROWS>
 __global__ __launch_bounds__(256)
 void gemm_tinyk_kernel(NarrowArgs p) {
     const int64_t ngroups = ceil_div(p.N, 4);
@@ -64,6 +69,15 @@ void gemm_tinyk_kernel(NarrowArgs p) {
     if (t >= ceil_div(p.M, TK_ROWS) * ngroups) return;
     const int64_t m0 = (t / ngroups) * TK_ROWS, n0 = (t % ngroups) * 4;
     constexpr bool BWD = ACT >= CDX_EPI_BWD_RELU;
+    static_assert(TK_ROWS * 16 == 64, "one op(A) element per lane");
+    int aw = 0;
+    if constexpr (WAVE_ROWS) {
+        const int lane = threadIdx.x & 63;
+        int64_t ma = m0 + (lane >> 4);
+        if (ma >= p.M) ma = m0;
+        const int64_t ka = (lane & 15) < p.K ? (lane & 15) : 0;
+        aw = __float_as_int(OPA == CDX_OP_N ? p.A[ma * p.lda + ka] : p.A[ka * p.lda + ma]);
+    }
     // WH: this thread's 4 columns are whole (16-byte accesses); one branch
     // here, straight-line code below
     auto run = [&](auto wh_c) {
@@ -110,8 +124,12 @@ void gemm_tinyk_kernel(NarrowArgs p) {
             float av[16];
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                const int64_t kk = k < p.K ? k : 0;
-                av[k] = OPA == CDX_OP_N ? p.A[m * p.lda + kk] : p.A[kk * p.lda + m];
+                if constexpr (WAVE_ROWS) {
+                    av[k] = __int_as_float(__builtin_amdgcn_readlane(aw, 16 * i + k));
+                } else {
+                    const int64_t kk = k < p.K ? k : 0;
+                    av[k] = OPA == CDX_OP_N ? p.A[m * p.lda + kk] : p.A[kk * p.lda + m];
+                }
             }
             float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -145,10 +163,13 @@ void gemm_tinyk_kernel(NarrowArgs p) {
 
 template <int OPA, int OPB, int ACT>
 int launch_tinyk3(const NarrowArgs& p, bool vec, dim3 grid, hipStream_t stream) {
-    if (vec)
-        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, true>), grid, dim3(256), 0, stream, p);
+    const bool wave_rows = ceil_div(p.N, 4) % 64 == 0;
+    if (vec && wave_rows)
+        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, true, true>), grid, dim3(256), 0, stream, p);
+    else if (vec)
+        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, true, false>), grid, dim3(256), 0, stream, p);
     else
-        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, false>), grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((gemm_tinyk_kernel<OPA, OPB, ACT, false, false>), grid, dim3(256), 0, stream, p);
     return hip_error(hipGetLastError(), "gemm_tinyk_kernel launch");
 }
 

@@ -211,6 +211,31 @@ def test_fp32_mid_size_tile_choice(M, N, K, tA, tB):
     assert _checksum_identity(A.T if tA else A, B.T if tB else B, C) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 784, 256), (5000, 784, 100), (4100, 1008, 77)])
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+def test_fp32_w112_tiles(M, N, K, tA, tB):
+    """Widths that are multiples of 112 but not of 64 take 128 x 112 tiles
+    (C4's 784-wide backward-data product, ragged M and K too): sampled rows
+    against the seq-FMA restatement, the column-checksum identity, and a
+    fused bias + ReLU epilogue against the unfused product."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(M + 5 * N + 11 * K + 2 * tA + tB)
+    A = normal(rng, (K, M) if tA else (M, K))
+    B = normal(rng, (N, K) if tB else (K, N))
+    say("fp32 w112", M, N, K, tA, tB)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB))
+    for r0 in (0, M // 2 + 3, M - 64):
+        rows = (r0, r0 + 64)
+        C64, e_ref = _ref_errors(A, B, tA, tB, rows=rows)
+        e = oracle.rel_fro(C[r0:r0 + 64], C64)
+        assert e <= 2 * e_ref, (rows, e, e_ref)
+    assert _checksum_identity(A.T if tA else A, B.T if tB else B, C) < 1e-5
+    bias = normal(rng, (N,))
+    Cf = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, bias=dev(bias),
+                         bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU))
+    assert np.array_equal(Cf, np.maximum(C + bias[None, :], 0))
+
+
 @pytest.mark.parametrize("n", [2048, 4096])
 @pytest.mark.parametrize("terms", [3, 4])
 def test_tf32mode_c3(n, terms):
