@@ -468,8 +468,10 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    1024 x 1024 73 against 81, 8192 x 256 x 784 (NT) 32 against 36, 8192 x
 //    784 x 256 41 against 45; 1024^3 NT the one loss (26 against 24).
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
-//    64x64x16, 4 waves of 32x32, XCD groups of one tile row (~85 TFLOP/s on
-//    64 x 100352 x 576, against 49 with 64x256 tiles).
+//    64x64x16, 4 waves of 16x64 (16-byte B fragment reads), XCD groups of
+//    one tile row: 64 x 100352 x 576 in 70-72 us, against 73-74 with 4
+//    waves of 32x32, 81 with 64x128 tiles of 8 waves of 16x64, 123-125 with
+//    64x128 / 64x256 tiles of 32x64 waves, 218 with BK = 32.
 //  * NarrowN: N <= 16 (the MLP's 10-class layer): 32x16 tiles, 2 waves, and
 //    a deep k-tile (64): such products read A once and are bound by the
 //    latency of their k-loop, so each workgroup takes few, large k-steps and
@@ -480,14 +482,18 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    product): 128x112x16, 8 waves of 16x112, so no tile column is ragged
 //    (8192 x 784 x 256 NN: 35.5 us, against 40.0 on 64x64 tiles with a
 //    16-wide edge column, 57 with 4 waves of 32x112, 52 with 256x112).
+//  * SplitTall: split-K slices of products with M >= 128: 128x64x16, 8
+//    waves of 32x32 (C4's weight + bias gradient 256 x 785 x 8192: 48.4 us
+//    against 54.5 on 64x64 slices; 128x128: 51.5; any BK = 32 slice: 58-79).
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
 using CfgMedium = Cfg<64, 64, 16, 32, 32, 8, 2>;
-using CfgSkinnyM = Cfg<64, 64, 16, 32, 32, 1, 2>;
+using CfgSkinnyM = Cfg<64, 64, 16, 16, 64, 1, 2>;
 using CfgNarrowN = Cfg<32, 16, 64, 16, 16, 8, 2>;
 using CfgW112 = Cfg<128, 112, 16, 16, 112, 8, 2>;
+using CfgSplitTall = Cfg<128, 64, 16, 32, 32, 8, 2>;
 
 // Configuration choice, shared by the launcher and the workspace query.
-enum class F32Cfg { NarrowN, SkinnyM, Large, Medium, W112 };
+enum class F32Cfg { NarrowN, SkinnyM, Large, Medium, W112, SplitTall };
 
 // Large tiles are ~8 % faster per tile, but a CU's time is set by its largest
 // share of tiles: Large is taken when its busiest-CU share (rounded up to
@@ -506,7 +512,7 @@ F32Cfg choose_f32(const GemmArgs& g, bool& blocked) {
     const bool split = g.batch == 1 && splitk_applies(ceil_div(g.M, 64) * ceil_div(g.N, 64), g.K);
     blocked = g.blocked_sum && !split && g.opA == CDX_OP_N && g.opB == CDX_OP_N;
     if (g.N <= 16) return F32Cfg::NarrowN;
-    if (split && !blocked) return F32Cfg::Medium;
+    if (split && !blocked) return g.M >= 128 ? F32Cfg::SplitTall : F32Cfg::Medium;
     if (!blocked && !split && g.N % 112 == 0 && g.N % 64 != 0 &&
         ceil_div(g.M, 128) * (g.N / 112) >= 256)
         return F32Cfg::W112;
@@ -532,6 +538,7 @@ size_t gemm_f32_workspace(const GemmArgs& g) {
         case F32Cfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case F32Cfg::Large: return ws_of<CfgLarge>(g);
         case F32Cfg::W112: return ws_of<CfgW112>(g);
+        case F32Cfg::SplitTall: return ws_of<CfgSplitTall>(g);
         default: return ws_of<CfgMedium>(g);
     }
 }
@@ -553,6 +560,7 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
         case F32Cfg::SkinnyM: return launch_ops<CfgSkinnyM>(g, stream);
         case F32Cfg::Large: return launch_ops<CfgLarge>(g, stream);
         case F32Cfg::W112: return launch_ops<CfgW112>(g, stream);
+        case F32Cfg::SplitTall: return launch_ops<CfgSplitTall>(g, stream);
         default: return launch_ops<CfgMedium>(g, stream);
     }
 }

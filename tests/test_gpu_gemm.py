@@ -474,7 +474,7 @@ def test_leading_dimension_views():
 
 @pytest.mark.parametrize("M,N,K,tA", [(64, 64, 8192, False), (100, 50, 5000, False),
                                       (256, 784, 8192, True), (10, 256, 8192, True),
-                                      (33, 17, 3001, True)])
+                                      (33, 17, 3001, True), (200, 300, 4096, False)])
 @pytest.mark.parametrize("mode", ["fp32", "tf32", "tf32x4"])
 def test_split_k_parity(M, N, K, tA, mode):
     import cudeep_amd as cd
