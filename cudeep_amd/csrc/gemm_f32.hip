@@ -459,6 +459,14 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 // Tile configurations (chosen by measurement on MI355X).  All use the two-set
 // register pipeline, which measured 4-12 % faster everywhere (4096^3: 138
 // against 133 TFLOP/s; 2048^3: 130 against 114).
+//  * Huge: 128x128x16, 4 waves of 64x32 (one per SIMD; several workgroups
+//    per CU), for problems with at least two 128x128 tiles per CU: 4096^3
+//    in 977-983 us against 997-1000 with Large (64x32 wave tiles read A
+//    with four 16-byte fragment reads and B with eight 4-byte reads per 16
+//    k for 32 MFMAs).  With one tile per CU (2048^3) one wave per SIMD
+//    hides less latency: 133.5 against 131.4 us, so Large stays there.
+//    (Measured slower: 256x128 tiles of 16 waves of 64x32 at 2048^3, 64x64
+//    wave tiles (spills), 8-byte B reads, one register staging set.)
 //  * Large: 128x128x16, 8 waves of 32x64 -> 2 waves per SIMD, 32 fp32
 //    accumulators per lane.
 //  * Medium: 64x64x16, 4 waves of 32x32, for problems whose 128x128 tiles
@@ -486,6 +494,7 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    waves of 32x32 (C4's weight + bias gradient 256 x 785 x 8192: 48.4 us
 //    against 54.5 on 64x64 slices; 128x128: 51.5; any BK = 32 slice: 58-79).
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
+using CfgHuge = Cfg<128, 128, 16, 64, 32, 8, 2>;
 using CfgMedium = Cfg<64, 64, 16, 32, 32, 8, 2>;
 using CfgSkinnyM = Cfg<64, 64, 16, 16, 64, 1, 2>;
 using CfgNarrowN = Cfg<32, 16, 64, 16, 16, 8, 2>;
@@ -493,7 +502,7 @@ using CfgW112 = Cfg<128, 112, 16, 16, 112, 8, 2>;
 using CfgSplitTall = Cfg<128, 64, 16, 32, 32, 8, 2>;
 
 // Configuration choice, shared by the launcher and the workspace query.
-enum class F32Cfg { NarrowN, SkinnyM, Large, Medium, W112, SplitTall };
+enum class F32Cfg { NarrowN, SkinnyM, Huge, Large, Medium, W112, SplitTall };
 
 // Large tiles are ~8 % faster per tile, but a CU's time is set by its largest
 // share of tiles: Large is taken when its busiest-CU share (rounded up to
@@ -517,7 +526,8 @@ F32Cfg choose_f32(const GemmArgs& g, bool& blocked) {
         ceil_div(g.M, 128) * (g.N / 112) >= 256)
         return F32Cfg::W112;
     if (g.M <= 64 && g.N >= 4096) return F32Cfg::SkinnyM;
-    if (large_balanced(g.M, g.N)) return F32Cfg::Large;
+    if (large_balanced(g.M, g.N))
+        return ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 512 ? F32Cfg::Huge : F32Cfg::Large;
     return F32Cfg::Medium;
 }
 
@@ -537,6 +547,7 @@ size_t gemm_f32_workspace(const GemmArgs& g) {
         case F32Cfg::NarrowN: return ws_of<CfgNarrowN>(g);
         case F32Cfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case F32Cfg::Large: return ws_of<CfgLarge>(g);
+        case F32Cfg::Huge: return ws_of<CfgHuge>(g);
         case F32Cfg::W112: return ws_of<CfgW112>(g);
         case F32Cfg::SplitTall: return ws_of<CfgSplitTall>(g);
         default: return ws_of<CfgMedium>(g);
@@ -552,6 +563,7 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
             case F32Cfg::NarrowN: return launch_blocked<CfgNarrowN>(g, stream);
             case F32Cfg::SkinnyM: return launch_blocked<CfgSkinnyM>(g, stream);
             case F32Cfg::Large: return launch_blocked<CfgLarge>(g, stream);
+            case F32Cfg::Huge: return launch_blocked<CfgHuge>(g, stream);
             default: return launch_blocked<CfgMedium>(g, stream);
         }
     }
@@ -559,6 +571,7 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
         case F32Cfg::NarrowN: return launch_ops<CfgNarrowN>(g, stream);
         case F32Cfg::SkinnyM: return launch_ops<CfgSkinnyM>(g, stream);
         case F32Cfg::Large: return launch_ops<CfgLarge>(g, stream);
+        case F32Cfg::Huge: return launch_ops<CfgHuge>(g, stream);
         case F32Cfg::W112: return launch_ops<CfgW112>(g, stream);
         case F32Cfg::SplitTall: return launch_ops<CfgSplitTall>(g, stream);
         default: return launch_ops<CfgMedium>(g, stream);
