@@ -324,19 +324,31 @@ void conv_wgrad_f32_kernel(WgArgs p) {
 // per CU (about 256 in all; two per CU with twice the slices measured slower).
 // Measured on MI355X at C5 (32 x 64 x 56^2, OC 64): 84.5 us per launch plus
 // the slice reduction, against 100+ us for conv_wgrad_f32_kernel.
-constexpr int RW_BM = 64, RW_ICT = 16, RW_BN = RW_ICT * 9, RW_NT = 768;
+constexpr int RW_BM = 64;
 
-template <int BKP>
+// Input-channel tile ICT and wave layout.  16 channels: 12 waves of 16 x 48
+// (three per SIMD; see above).  64 channels (the whole dW row of a 64-channel
+// layer, so each dY row is fetched by one workgroup instead of four): 16
+// waves of 16 x 144 (four per SIMD), each k-tile 126 MFMAs per wave against
+// 42, so a barrier and the staging stores are spread over three times the
+// work; rows of at most 56 pixels (two LDS stages of 64 x 56 dY and 192 x 56
+// input values: 131 KiB).
+template <int ICT> struct RwTile;
+template <> struct RwTile<16> { static constexpr int NT = 768, WAVES_N = 3, FMW = 1, JB = 3; };
+template <> struct RwTile<64> { static constexpr int NT = 512, WAVES_N = 4, FMW = 2, JB = 9; };
+
+template <int BKP, int ICT>
 struct RwShape {
     static constexpr int KQ = BKP / 4;                       // MFMA steps per k-tile
     static constexpr int A_STRIDE = BKP + 4;                 // dY row pitch (floats)
     static constexpr int XB = KQ + 2 <= 16 ? 16 : 48;        // x block pitch per lane group
     static constexpr int X_LEN = 3 * XB + KQ + 2;            // floats used per x row
     static constexpr int X_RS = ((X_LEN - 3 + 31) / 32) * 32 + 3;   // >= X_LEN, = 3 mod 32
-    static constexpr int X_ROWS = RW_ICT * 3;
+    static constexpr int NT = RwTile<ICT>::NT;
+    static constexpr int X_ROWS = ICT * 3;
     static constexpr int STAGE = RW_BM * A_STRIDE + X_ROWS * X_RS;
-    static constexpr int NA = (RW_BM * KQ + RW_NT - 1) / RW_NT;       // dY float4 per thread
-    static constexpr int NX = (X_ROWS * KQ + RW_NT - 1) / RW_NT;      // x float4 per thread
+    static constexpr int NA = (RW_BM * KQ + NT - 1) / NT;       // dY float4 per thread
+    static constexpr int NX = (X_ROWS * KQ + NT - 1) / NT;      // x float4 per thread
     static_assert(KQ % 2 == 0 && X_RS >= X_LEN && X_RS % 32 == 3, "row-window shape");
     // LDS column(s) of row position P (0 .. BKP+1): its own block, and the
     // previous block too for the first two positions of a block (c2 = c1 when
@@ -358,10 +370,12 @@ struct RwArgs {
     int vec_dy, vec_x;             // 16-byte loads allowed
 };
 
-template <int BKP>
-__global__ __launch_bounds__(RW_NT)
+template <int BKP, int ICT>
+__global__ __launch_bounds__(RwTile<ICT>::NT)
 void conv_wgrad_rows_kernel(RwArgs p) {
-    using SH_ = RwShape<BKP>;
+    using SH_ = RwShape<BKP, ICT>;
+    using TL = RwTile<ICT>;
+    constexpr int RW_NT = TL::NT, FMW = TL::FMW, JB = TL::JB;
     constexpr int KQ = SH_::KQ, A_STRIDE = SH_::A_STRIDE, X_RS = SH_::X_RS;
     constexpr int STAGE = SH_::STAGE, NA = SH_::NA, NX = SH_::NX;
     __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
@@ -369,11 +383,11 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lq = lane >> 4;
-    const int wm0 = (wave / 3) * 16, wn0 = (wave % 3) * 48;
+    const int wm0 = (wave / TL::WAVES_N) * 16 * FMW, wn0 = (wave % TL::WAVES_N) * 16 * JB;
 
-    const int tiles_n = (int)ceil_div(p.IC, RW_ICT);
+    const int tiles_n = (int)ceil_div(p.IC, ICT);
     const int64_t bm = (int64_t)(blockIdx.x / tiles_n) * RW_BM;
-    const int64_t bic = (int64_t)(blockIdx.x % tiles_n) * RW_ICT;
+    const int64_t bic = (int64_t)(blockIdx.x % tiles_n) * ICT;
     const int r_begin = blockIdx.y * p.rows_chunk;
     const int r_end = min(p.rows_total, r_begin + p.rows_chunk);
     const int nk = r_end - r_begin;
@@ -398,7 +412,7 @@ void conv_wgrad_rows_kernel(RwArgs p) {
         a_dst[u] = row * A_STRIDE + 4 * q;
         a_q4[u] = 4 * q;
     }
-    int x_src[NX], x_row[NX], x_c1[NX][4], x_c2[NX][4], x_q4[NX], x_kh[NX];
+    int x_src[NX], x_row[NX], x_q4[NX], x_kh[NX];
     bool x_ok[NX];
 #pragma unroll
     for (int u = 0; u < NX; ++u) {
@@ -408,8 +422,6 @@ void conv_wgrad_rows_kernel(RwArgs p) {
         x_ok[u] = idx < SH_::X_ROWS * KQ && bic + icl < p.IC;
         x_src[u] = x_ok[u] ? icl * p.IH * p.IW + kh * p.IW + 4 * q : 0;
         x_row[u] = row * X_RS;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) SH_::cols_of(p.PW + 4 * q + j, x_c1[u][j], x_c2[u][j]);
         x_q4[u] = 4 * q;
         x_kh[u] = kh;
     }
@@ -512,8 +524,10 @@ void conv_wgrad_rows_kernel(RwArgs p) {
             if (tid + u * RW_NT < SH_::X_ROWS * KQ) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    sX[x_row[u] + x_c1[u][j]] = st.vx[u][j];
-                    sX[x_row[u] + x_c2[u][j]] = st.vx[u][j];
+                    int c1, c2;   // (recomputed: a few integer ops per k-tile)
+                    SH_::cols_of(p.PW + x_q4[u] + j, c1, c2);
+                    sX[x_row[u] + c1] = st.vx[u][j];
+                    sX[x_row[u] + c2] = st.vx[u][j];
                 }
             }
         if (h_thread) {
@@ -523,43 +537,72 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     };
 
     // this lane's B rows: filter row n -> (channel, kh, kw) -> LDS row and shift
-    int b_off[3];
+    int b_off[JB];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int n = wn0 + j * 16 + l16;          // 0 .. 143
+    for (int j = 0; j < JB; ++j) {
+        const int n = wn0 + j * 16 + l16;          // 0 .. 9 ICT - 1
         const int icl = n / 9, tap = n - (n / 9) * 9;
         const int kh = tap / 3, kw = tap - (tap / 3) * 3;
         b_off[j] = RW_BM * A_STRIDE + (icl * 3 + kh) * X_RS + SH_::XB * lq + kw;
     }
     const int a_off = (wm0 + l16) * A_STRIDE + KQ * lq;
 
-    floatx4 acc[3];
+    floatx4 acc[FMW][JB];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < FMW; ++i)
+#pragma unroll
+        for (int j = 0; j < JB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    // (the 64-channel form steps through the k-tile without unrolling: fully
+    // unrolled, the compiler hoists all 140 fragment reads of a k-tile and
+    // spills)
+    constexpr int T_UNROLL = JB > 3 ? 1 : KQ / 2;
     auto compute = [&](int buf) {
         const float* s = lds + buf * STAGE;
-#pragma unroll
+#pragma unroll T_UNROLL
         for (int t0 = 0; t0 < KQ; t0 += 2) {
-            const float2 a = *reinterpret_cast<const float2*>(s + a_off + t0);
-            float b[3][2];
+            float2 a[FMW];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
+            for (int i = 0; i < FMW; ++i)
+                a[i] = *reinterpret_cast<const float2*>(s + a_off + 16 * i * A_STRIDE + t0);
+            float b[JB][2];
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
                 b[j][0] = s[b_off[j] + t0];
                 b[j][1] = s[b_off[j] + t0 + 1];
             }
 #pragma unroll
-            for (int j = 0; j < 3; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b[j][0], acc[j], 0, 0, 0);
+            for (int i = 0; i < FMW; ++i)
 #pragma unroll
-            for (int j = 0; j < 3; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b[j][1], acc[j], 0, 0, 0);
+                for (int j = 0; j < JB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j][0], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < FMW; ++i)
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j][1], acc[i][j], 0, 0, 0);
         }
     };
 
     // Two register staging sets: tile k+2 is loaded while tile k is
     // multiplied and tile k+1 (loaded an iteration earlier) is written to LDS.
-    if (nk > 0) {
+    if (ICT == 64 && nk > 0) {
+        // One staging set: a k-tile's MFMAs (252 per wave, two waves per
+        // SIMD) outlast the next tile's loads, and a second set does not fit
+        // in the registers beside 72 accumulators.
+        Stage st;
+        st.vh = 0.0f;
+        load(st);
+        store(st, 0);
+        __syncthreads();
+        for (int k = 0; k < nk; ++k) {
+            const bool more = k + 1 < nk;
+            if (more) load(st);
+            compute(k & 1);
+            if (more) store(st, (k & 1) ^ 1);
+            __syncthreads();
+        }
+    } else if (nk > 0) {
         Stage s0, s1;
         s0.vh = s1.vh = 0.0f;
         load(s0);
@@ -584,14 +627,16 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     // column l % 16
     float* out = p.out + (int64_t)blockIdx.y * p.OC * p.Kc;
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int64_t nn = bic * 9 + wn0 + j * 16 + l16;
+    for (int i = 0; i < FMW; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t m = bm + wm0 + 4 * lq + r;
-            if (m < p.OC && nn < p.Kc) out[m * p.Kc + nn] = acc[j][r];
+        for (int j = 0; j < JB; ++j) {
+            const int64_t nn = bic * 9 + wn0 + j * 16 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t m = bm + wm0 + 16 * i + 4 * lq + r;
+                if (m < p.OC && nn < p.Kc) out[m * p.Kc + nn] = acc[i][j][r];
+            }
         }
-    }
 }
 
 // Pixels per k-tile: the output width rounded up to 32 / 56 / 64, or 64-pixel
@@ -603,20 +648,21 @@ bool rows_applies(const WgGeom& g) {
     // input planes, and the row segments are counted in int: 32-bit
     const int64_t lim = (int64_t)1 << 31;
     return g.KH == 3 && g.KW == 3 && g.SH == 1 && g.SW == 1 && g.PW >= 0 && g.PW <= 2 &&
-           g.PH >= 0 && RW_BM * g.OH * g.OW < lim && RW_ICT * g.IH * g.IW < lim &&
+           g.PH >= 0 && RW_BM * g.OH * g.OW < lim && 64 * g.IH * g.IW < lim &&
            g.B * g.OH * ceil_div(g.OW, rw_bkp(g.OW)) < lim;
 }
 
 struct RwPlan {
-    int bkp, nseg, rows_total, tiles, splits, chunk;
+    int bkp, ict, nseg, rows_total, tiles, splits, chunk;
 };
 
-RwPlan rw_plan(const WgGeom& g) {
+RwPlan rw_plan_for(const WgGeom& g, int ict) {
     RwPlan r;
     r.bkp = rw_bkp(g.OW);
+    r.ict = ict;
     r.nseg = (int)ceil_div(g.OW, r.bkp);
     r.rows_total = (int)(g.B * g.OH * r.nseg);
-    r.tiles = (int)(ceil_div(g.OC, RW_BM) * ceil_div(g.IC, RW_ICT));
+    r.tiles = (int)(ceil_div(g.OC, RW_BM) * ceil_div(g.IC, r.ict));
     // about CDX_WGRAD_ROWS_WGS workgroups, at least 4 row segments per slice
     int64_t s = CDX_WGRAD_ROWS_WGS / r.tiles;
     if (s > r.rows_total / 4) s = r.rows_total / 4;
@@ -624,6 +670,21 @@ RwPlan rw_plan(const WgGeom& g) {
     r.chunk = (int)ceil_div(r.rows_total, s);
     r.splits = (int)ceil_div(r.rows_total, r.chunk);
     return r;
+}
+
+// The 64-channel tile where it applies (IC a multiple of 64, rows of at
+// most 56 pixels) and each slice is at least 16 row segments long: its
+// partials are four times the 16-channel form's (the whole 64 x 9 IC tile
+// per workgroup), which the slice's work has to outweigh.  Measured on
+// MI355X with the reduction: 64 x 128 x 56^2 552 against 626 us, 32 x 512
+// x 14^2 704 against 862, 32 x 256 x 28^2 357 against 445; C5 (7 row
+// segments per slice) 96 against 93, so C5 keeps the 16-channel tile.
+RwPlan rw_plan(const WgGeom& g) {
+    if (g.IC % 64 == 0 && rw_bkp(g.OW) <= 56) {
+        const RwPlan r = rw_plan_for(g, 64);
+        if (r.chunk >= 16) return r;
+    }
+    return rw_plan_for(g, 16);
 }
 
 }  // namespace
@@ -664,12 +725,20 @@ int launch_conv_wgrad_f32(const float* dy, const float* x, float* dw, float* ws,
         p.vec_dy = g.OW % 4 == 0 && (uintptr_t)dy % 16 == 0;
         p.vec_x = IW % 4 == 0 && (uintptr_t)x % 16 == 0;
         const dim3 grid((unsigned)r.tiles, (unsigned)r.splits);
-        if (r.bkp == 32)
-            hipLaunchKernelGGL(conv_wgrad_rows_kernel<32>, grid, dim3(RW_NT), 0, stream, p);
-        else if (r.bkp == 56)
-            hipLaunchKernelGGL(conv_wgrad_rows_kernel<56>, grid, dim3(RW_NT), 0, stream, p);
-        else
-            hipLaunchKernelGGL(conv_wgrad_rows_kernel<64>, grid, dim3(RW_NT), 0, stream, p);
+        const dim3 b16(RwTile<16>::NT), b64(RwTile<64>::NT);
+        if (r.ict == 64) {
+            if (r.bkp == 32)
+                hipLaunchKernelGGL((conv_wgrad_rows_kernel<32, 64>), grid, b64, 0, stream, p);
+            else
+                hipLaunchKernelGGL((conv_wgrad_rows_kernel<56, 64>), grid, b64, 0, stream, p);
+        } else {
+            if (r.bkp == 32)
+                hipLaunchKernelGGL((conv_wgrad_rows_kernel<32, 16>), grid, b16, 0, stream, p);
+            else if (r.bkp == 56)
+                hipLaunchKernelGGL((conv_wgrad_rows_kernel<56, 16>), grid, b16, 0, stream, p);
+            else
+                hipLaunchKernelGGL((conv_wgrad_rows_kernel<64, 16>), grid, b16, 0, stream, p);
+        }
         int st = hip_error(hipGetLastError(), "conv_wgrad_rows_kernel launch");
         if (st || r.splits == 1) return st;
         GemmArgs red{CDX_OP_N, CDX_OP_N, OC, g.Kc(), 0, nullptr, 1, nullptr, 1, dw, g.Kc(), 0, 0,

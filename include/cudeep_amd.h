@@ -357,7 +357,7 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
 
 /* Bytes of device scratch the allocation-free entry point below owns on each
  * GPU it runs on (held until the process ends). */
-#define CDX_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define CDX_NOALLOC_SCRATCH_BYTES (40u << 20)
 
 /* cdx_conv2d_backward_weight_f32 without a workspace argument and without
  * any allocation: no hipMalloc / hipMallocAsync / hipFree, no allocating
@@ -368,7 +368,8 @@ int cdx_conv2d_backward_weight_f32(const float* grad_output, const float* input,
  * arguments, routes and results as cdx_conv2d_backward_weight_f32; a layer
  * whose scratch (cdx_conv2d_backward_weight_workspace_size) exceeds the
  * limit is refused with CDX_ERR_UNSUPPORTED before anything is launched
- * (C5's 64x64x3x3 layer at batch 32 needs 9 MiB).  Every call on one GPU
+ * (C5's 64x64x3x3 layer at batch 32 needs 9 MiB, larger 3x3 stride-1
+ * layers on the 64-channel row-window kernel 36 MiB).  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (different streams
  * or threads without ordering between them) race and must be serialised by
  * the caller. */

@@ -110,9 +110,9 @@ def test_conv_argument_validation():
                    0, None, 0, None) == L.CDX_ERR_UNSUPPORTED
     assert _status("cdx_conv2d_backward_data_winograd_f32", fake, fake, fake, 1, 2, 2, 8, 8, 1, 1,
                    0, fake, 4, None) == L.CDX_ERR_WORKSPACE
-    # GEMM split-K scratch: C4's dW1 (256 x 784 x 8192, TN) in FP32 runs 15
-    # slices of 560 k on the 64x64 split-K tile; 4096^3 never splits
-    assert L.lib().cdx_gemm_workspace_size(0, 1, 0, 256, 784, 8192) == 15 * 256 * 784 * 4
+    # GEMM split-K scratch: C4's dW1 (256 x 784 x 8192, TN) in FP32 runs 29
+    # slices of 288 k on the 128x64 split-K tile (26 tiles); 4096^3 never splits
+    assert L.lib().cdx_gemm_workspace_size(0, 1, 0, 256, 784, 8192) == 29 * 256 * 784 * 4
     assert L.lib().cdx_gemm_workspace_size(0, 0, 0, 4096, 4096, 4096) == 0
     assert L.lib().cdx_gemm_workspace_size(1, 0, 0, 4096, 4096, 4096) == 0
     assert L.lib().cdx_gemm_workspace_size(0, 0, 0, 0, 4096, 4096) == 0
@@ -154,7 +154,7 @@ def test_fused_gemm_argument_validation():
     assert st(None, 0, 12, None, 0, None) == L.CDX_ERR_INVALID_ARG                  # bad epilogue
     assert st(None, 0, L.EPI_RELU, None, 0, fake) == L.CDX_ERR_INVALID_ARG          # colsum + act
     assert st(fake, L.BIAS_ROW, 0, None, 0, fake) == L.CDX_ERR_INVALID_ARG          # colsum + bias
-    # workspace: C4's dW1 with its bias gradient -- 15 k-slices of [256, 785]
-    assert L.lib().cdx_gemm_fused_workspace_size(0, 1, 0, 256, 784, 8192, 1) == 15 * 256 * 785 * 4
-    assert L.lib().cdx_gemm_fused_workspace_size(1, 1, 0, 256, 784, 8192, 1) == 15 * 256 * 785 * 4
-    assert L.lib().cdx_gemm_fused_workspace_size(0, 1, 0, 256, 784, 8192, 0) == 15 * 256 * 784 * 4
+    # workspace: C4's dW1 with its bias gradient -- 29 k-slices of [256, 785]
+    assert L.lib().cdx_gemm_fused_workspace_size(0, 1, 0, 256, 784, 8192, 1) == 29 * 256 * 785 * 4
+    assert L.lib().cdx_gemm_fused_workspace_size(1, 1, 0, 256, 784, 8192, 1) == 29 * 256 * 785 * 4
+    assert L.lib().cdx_gemm_fused_workspace_size(0, 1, 0, 256, 784, 8192, 0) == 29 * 256 * 784 * 4

@@ -337,6 +337,31 @@ def test_conv_backward_parity(g, prec):
     assert oracle.rel_fro(db, db64) <= 2 * e_ref + 2.0 ** -24
 
 
+@pytest.mark.parametrize("g,ws_expect", [
+    ((128, 64, 32, 32, 64, 3, 3, 1, 1, 1, 1), 256 * 64 * 576 * 4),
+    ((64, 128, 20, 20, 70, 3, 3, 1, 1, 1, 1), 64 * 70 * 1152 * 4)])
+def test_conv_backward_weight_64_channel_tile(g, ws_expect):
+    """3x3 stride-1 layers with a multiple of 64 input channels and long
+    K slices take the row-window kernel's 64-channel tile (the workspace
+    size pins the route: 256 / 64 slices of the whole OC x 9 IC partial):
+    dW against the fp64 oracle at 2x the reference route's error, in both
+    precision modes' gates (ragged OC in the second layer)."""
+    Bn, C, H, W, OC, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    OH, OW = oracle.conv_out_size(H, KH, SH, PH), oracle.conv_out_size(W, KW, SW, PW)
+    dy = normal(rng, (Bn, OC, OH, OW))
+    w_shape = (OC, C, KH, KW)
+    assert ops().conv2d_backward_weight_workspace_bytes(x.shape, w_shape, (SH, SW),
+                                                        (PH, PW)) == ws_expect
+    say("wgrad 64-channel tile", g)
+    dw = host(ops().conv2d_backward_weight(dev(dy), dev(x), w_shape, (SH, SW), (PH, PW)))
+    dw64 = oracle.conv2d_backward_weight64(dy, x, w_shape, (SH, SW), (PH, PW))
+    ew_ref = oracle.rel_fro(oracle.conv2d_backward_weight_ref(dy, x, w_shape, (SH, SW), (PH, PW)),
+                            dw64)
+    assert oracle.rel_fro(dw, dw64) <= 2 * ew_ref
+
+
 def test_conv_backward_c5_full():
     """C5 backward at full size: N=32, C=64, 56x56, OC=64, 3x3, s1, p1.
     dW checked against the fp64 oracle in full (it reduces over the whole

@@ -13,7 +13,7 @@ import pytest
 
 from tests.gpu_util import dev, host, normal, require_gpu, say
 
-NOALLOC_BYTES = 16 << 20
+NOALLOC_BYTES = 40 << 20
 
 
 def _lib():
@@ -33,7 +33,8 @@ def _args(g):
 
 def test_implicit_route_layers_fit_the_scratch():
     """The implicit kernels split K over about 256 workgroups, so their
-    partials stay near 9-10 MiB whatever the layer: all of these fit."""
+    partials stay near 9-10 MiB (36 MiB on the 64-channel row-window
+    kernel) whatever the layer: all of these fit."""
     L = _lib()
     for g in [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1), (32, 512, 14, 14, 512, 3, 3, 1, 1, 1, 1),
               (64, 128, 56, 56, 128, 3, 3, 1, 1, 1, 1), (32, 512, 14, 14, 512, 1, 1, 1, 1, 0, 0),
@@ -58,6 +59,7 @@ def test_refuses_layers_beyond_the_scratch_before_any_launch():
 
 
 CALLS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW), in this order
+    (128, 64, 32, 32, 64, 3, 3, 1, 1, 1, 1),   # 64-channel row-window tile, 256 slices (36 MiB)
     (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1),    # C5: row-window kernel, 64 partial slices
     (4, 32, 28, 28, 16, 3, 3, 1, 1, 1, 1),     # smaller: fewer, smaller slices
     (2, 5, 13, 11, 7, 3, 2, 2, 1, 1, 0),       # gather kernel, ragged
