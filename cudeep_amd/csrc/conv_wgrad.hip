@@ -325,6 +325,9 @@ void conv_wgrad_f32_kernel(WgArgs p) {
 // Measured on MI355X at C5 (32 x 64 x 56^2, OC 64): 84.5 us per launch plus
 // the slice reduction, against 100+ us for conv_wgrad_f32_kernel.
 constexpr int RW_BM = 64;
+#ifndef RW_SEGS16
+#define RW_SEGS16 2
+#endif
 
 // Input-channel tile ICT and wave layout.  16 channels: 12 waves of 16 x 48
 // (three per SIMD; see above).  64 channels (the whole dW row of a 64-channel
@@ -370,7 +373,13 @@ struct RwArgs {
     int vec_dy, vec_x;             // 16-byte loads allowed
 };
 
-template <int BKP, int ICT>
+// SEGS: row segments per k-tile (1, or 2 to double the MFMA work between
+// barriers and the distance the register prefetch runs ahead).  WHOLE: every
+// segment lies inside its dY and input rows with 16-byte loads allowed (the
+// host checks OW % BKP == 0, IW >= OW and alignment), so the loads are one
+// straight-line sequence: the compiler can then wait for exactly the tile
+// being stored instead of for every load in flight.
+template <int BKP, int ICT, int SEGS, bool WHOLE>
 __global__ __launch_bounds__(RwTile<ICT>::NT)
 void conv_wgrad_rows_kernel(RwArgs p) {
     using SH_ = RwShape<BKP, ICT>;
@@ -378,7 +387,9 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     constexpr int RW_NT = TL::NT, FMW = TL::FMW, JB = TL::JB;
     constexpr int KQ = SH_::KQ, A_STRIDE = SH_::A_STRIDE, X_RS = SH_::X_RS;
     constexpr int STAGE = SH_::STAGE, NA = SH_::NA, NX = SH_::NX;
-    __shared__ __attribute__((aligned(16))) float lds[2 * STAGE];
+    // (+ one slot per thread: where threads without a halo column write, so
+    // the halo store is not a divergent branch)
+    __shared__ __attribute__((aligned(16))) float lds[2 * SEGS * STAGE + RW_NT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -445,51 +456,65 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     const float* dy_blk = p.dy + bm * p.OH * p.OW;            // this tile's first channel
     const float* x_blk = p.x + bic * p.IH * p.IW;
 
-    // registers staging one k-tile
+    // registers staging one k-tile.  ok: bit u -- va[u] is real, bit 8 + u
+    // -- vx[u], bit 31 -- vh; the others are zeroed when stored (a select at
+    // the load would make every load wait for its data at once).
+    static_assert(NA <= 8 && NX <= 16, "ok mask layout");
     struct Stage {
         floatx4 va[NA], vx[NX];
         float vh;
+        uint32_t ok;
     };
-    auto load = [&](Stage& st) {
-        const int ow0 = ld_seg * BKP;
+    // valid = false: a k-tile's missing last segment -- the same loads from
+    // the first segment's addresses, every element marked not real (one
+    // instruction sequence either way, so the waits stay exact)
+    auto load = [&](Stage& st, bool valid) {
+        const int l_seg = valid ? ld_seg : 0, l_oh = valid ? ld_oh : 0, l_b = valid ? ld_b : 0;
+        const int ow0 = l_seg * BKP;
         // wave-uniform bases: dY row (b, oc = bm, oh) at ow0; x row (b, ic = bic,
         // ih = oh - PH) at ow0
-        const float* yk = dy_blk + (int64_t)ld_b * p.OC * p.OH * p.OW + (int64_t)ld_oh * p.OW + ow0;
-        const float* xk = x_blk + (int64_t)ld_b * p.IC * p.IH * p.IW +
-                          (int64_t)(ld_oh - p.PH) * p.IW + ow0;
-        if (p.vec_dy && p.vec_x && ow0 + BKP <= p.OW && ow0 + BKP <= p.IW) {
+        const float* yk = dy_blk + (int64_t)l_b * p.OC * p.OH * p.OW + (int64_t)l_oh * p.OW + ow0;
+        const float* xk = x_blk + (int64_t)l_b * p.IC * p.IH * p.IW +
+                          (int64_t)(l_oh - p.PH) * p.IW + ow0;
+        if (WHOLE || (p.vec_dy && p.vec_x && ow0 + BKP <= p.OW && ow0 + BKP <= p.IW)) {
             // whole segment inside both rows: 16-byte loads from addresses that
             // are always valid (a skipped row reads the tile's first dY row or
-            // the input's first element), zeroed by a select -- no branches
+            // the input's first element), zeroed at the store -- no branches
+            uint32_t ok = 0;
 #pragma unroll
             for (int u = 0; u < NA; ++u) {
-                const floatx4 v = *reinterpret_cast<const floatx4*>(yk + a_src[u]);
-                st.va[u] = a_ok[u] ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                st.va[u] = *reinterpret_cast<const floatx4*>(yk + a_src[u]);
+                ok |= (uint32_t)(a_ok[u] && valid) << u;
             }
 #pragma unroll
             for (int u = 0; u < NX; ++u) {
-                const bool rok = x_ok[u] && (unsigned)(ld_oh - p.PH + x_kh[u]) < (unsigned)p.IH;
+                const bool rok = valid && x_ok[u] &&
+                                 (unsigned)(l_oh - p.PH + x_kh[u]) < (unsigned)p.IH;
                 const float* src = rok ? xk + x_src[u] : p.x;
-                const floatx4 v = *reinterpret_cast<const floatx4*>(src);
-                st.vx[u] = rok ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                st.vx[u] = *reinterpret_cast<const floatx4*>(src);
+                ok |= (uint32_t)rok << (8 + u);
             }
+            st.ok = ok;
         } else {
+            st.ok = 0x7fffffffu;   // elementwise-zeroed below
 #pragma unroll
             for (int u = 0; u < NA; ++u) {
                 const float* src = yk + a_src[u];
                 const int ow = ow0 + a_q4[u];
-                if (a_ok[u] && p.vec_dy && ow + 3 < p.OW) {
+                const bool aok = valid && a_ok[u];
+                if (aok && p.vec_dy && ow + 3 < p.OW) {
                     st.va[u] = *reinterpret_cast<const floatx4*>(src);
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) st.va[u][j] = a_ok[u] && ow + j < p.OW ? src[j] : 0.0f;
+                    for (int j = 0; j < 4; ++j) st.va[u][j] = aok && ow + j < p.OW ? src[j] : 0.0f;
                 }
             }
 #pragma unroll
             for (int u = 0; u < NX; ++u) {
                 const float* src = xk + x_src[u];
                 const int iw = ow0 + x_q4[u];
-                const bool rok = x_ok[u] && (unsigned)(ld_oh - p.PH + x_kh[u]) < (unsigned)p.IH;
+                const bool rok = valid && x_ok[u] &&
+                                 (unsigned)(l_oh - p.PH + x_kh[u]) < (unsigned)p.IH;
                 if (rok && p.vec_x && iw + 3 < p.IW) {
                     st.vx[u] = *reinterpret_cast<const floatx4*>(src);
                 } else {
@@ -498,13 +523,17 @@ void conv_wgrad_rows_kernel(RwArgs p) {
                 }
             }
         }
-        if (h_thread) {
+        {
+            // every thread loads (non-halo threads the input's first element),
+            // so no branch splits the load sequence
             const int iw = ow0 + h_col;
-            const bool ok = h_ok && (unsigned)(ld_oh - p.PH + h_kh) < (unsigned)p.IH &&
+            const bool ok = valid && h_thread && h_ok &&
+                            (unsigned)(l_oh - p.PH + h_kh) < (unsigned)p.IH &&
                             (unsigned)iw < (unsigned)p.IW;
-            st.vh = ok ? xk[h_src] : 0.0f;
+            st.vh = *(ok ? xk + h_src : p.x);
+            st.ok = (st.ok & 0x7fffffffu) | ((uint32_t)ok << 31);
         }
-        if (++ld_seg == p.nseg) {
+        if (valid && ++ld_seg == p.nseg) {
             ld_seg = 0;
             if (++ld_oh == p.OH) {
                 ld_oh = 0;
@@ -512,13 +541,21 @@ void conv_wgrad_rows_kernel(RwArgs p) {
             }
         }
     };
+    // (opaque: keeps the zeroing select here, away from the load)
+    auto zsel = [](float v, bool keep) {
+        asm volatile("" : "+v"(v));
+        return keep ? v : 0.0f;
+    };
+    auto zsel4 = [&](floatx4 v, bool keep) {
+        return floatx4{zsel(v[0], keep), zsel(v[1], keep), zsel(v[2], keep), zsel(v[3], keep)};
+    };
     auto store = [&](const Stage& st, int buf) {
         float* sA = lds + buf * STAGE;
         float* sX = sA + RW_BM * A_STRIDE;
 #pragma unroll
         for (int u = 0; u < NA; ++u)
             if (tid + u * RW_NT < RW_BM * KQ)
-                *reinterpret_cast<floatx4*>(sA + a_dst[u]) = st.va[u];
+                *reinterpret_cast<floatx4*>(sA + a_dst[u]) = zsel4(st.va[u], (st.ok >> u) & 1u);
 #pragma unroll
         for (int u = 0; u < NX; ++u)
             if (tid + u * RW_NT < SH_::X_ROWS * KQ) {
@@ -526,13 +563,16 @@ void conv_wgrad_rows_kernel(RwArgs p) {
                 for (int j = 0; j < 4; ++j) {
                     int c1, c2;   // (recomputed: a few integer ops per k-tile)
                     SH_::cols_of(p.PW + x_q4[u] + j, c1, c2);
-                    sX[x_row[u] + c1] = st.vx[u][j];
-                    sX[x_row[u] + c2] = st.vx[u][j];
+                    const float v = zsel(st.vx[u][j], (st.ok >> (8 + u)) & 1u);
+                    sX[x_row[u] + c1] = v;
+                    sX[x_row[u] + c2] = v;
                 }
             }
-        if (h_thread) {
-            sX[h_row + h_c1] = st.vh;
-            sX[h_row + h_c2] = st.vh;
+        {
+            const float v = zsel(st.vh, st.ok >> 31);
+            float* dummy = lds + 2 * SEGS * STAGE + tid;
+            *(h_thread ? sX + h_row + h_c1 : dummy) = v;
+            *(h_thread ? sX + h_row + h_c2 : dummy) = v;
         }
     };
 
@@ -584,43 +624,69 @@ void conv_wgrad_rows_kernel(RwArgs p) {
         }
     };
 
+    // A k-tile is SEGS consecutive row segments, each in its own LDS
+    // sub-stage (buffer buf, segment s at sub-stage buf * SEGS + s); a
+    // missing last segment is staged as zeros (zero dY adds nothing).
+    // (Callers load a segment only while ld_left > 0.)
+    struct Group {
+        Stage s[SEGS];
+    };
+    int ld_left = nk;   // segments not yet loaded
+    auto load_g = [&](Group& gr) {
+#pragma unroll
+        for (int q = 0; q < SEGS; ++q) {
+            load(gr.s[q], ld_left > 0);
+            --ld_left;
+        }
+    };
+    auto store_g = [&](const Group& gr, int buf) {
+#pragma unroll
+        for (int q = 0; q < SEGS; ++q) store(gr.s[q], buf * SEGS + q);
+    };
+    auto compute_g = [&](int buf) {
+#pragma unroll 1
+        for (int q = 0; q < SEGS; ++q) compute(buf * SEGS + q);
+    };
+    const int nkt = (nk + SEGS - 1) / SEGS;   // k-tiles
+
     // Two register staging sets: tile k+2 is loaded while tile k is
     // multiplied and tile k+1 (loaded an iteration earlier) is written to LDS.
-    if (ICT == 64 && nk > 0) {
+    if ((ICT == 64 || SEGS > 1) && nkt > 0) {
         // One staging set: a k-tile's MFMAs (252 per wave, two waves per
-        // SIMD) outlast the next tile's loads, and a second set does not fit
-        // in the registers beside 72 accumulators.
-        Stage st;
-        st.vh = 0.0f;
-        load(st);
-        store(st, 0);
+        // SIMD, for 64 channels; 84 per wave, three per SIMD, for two
+        // segments of 16 channels) outlast the next tile's loads.  With one
+        // set, the wait before a store is for the newest loads only -- with
+        // two, the compiler's waits at the stores also waited for the other
+        // set's loads just issued.
+        Group st;
+        load_g(st);
+        store_g(st, 0);
         __syncthreads();
-        for (int k = 0; k < nk; ++k) {
-            const bool more = k + 1 < nk;
-            if (more) load(st);
-            compute(k & 1);
-            if (more) store(st, (k & 1) ^ 1);
+        for (int k = 0; k < nkt; ++k) {
+            const bool more = k + 1 < nkt;
+            if (more) load_g(st);
+            compute_g(k & 1);
+            if (more) store_g(st, (k & 1) ^ 1);
             __syncthreads();
         }
-    } else if (nk > 0) {
-        Stage s0, s1;
-        s0.vh = s1.vh = 0.0f;
-        load(s0);
-        if (nk > 1) load(s1);
-        store(s0, 0);
+    } else if (nkt > 0) {
+        Group s0, s1;
+        load_g(s0);
+        if (nkt > 1) load_g(s1);
+        store_g(s0, 0);
         __syncthreads();
         int k = 0;
-        for (; k + 1 < nk; k += 2) {        // LDS stage 0: tile k; s1: tile k+1
-            if (k + 2 < nk) load(s0);       // tile k+2
-            compute(0);
-            store(s1, 1);
+        for (; k + 1 < nkt; k += 2) {       // LDS stage 0: tile k; s1: tile k+1
+            if (k + 2 < nkt) load_g(s0);    // tile k+2
+            compute_g(0);
+            store_g(s1, 1);
             __syncthreads();
-            if (k + 3 < nk) load(s1);       // tile k+3
-            compute(1);
-            if (k + 2 < nk) store(s0, 0);
+            if (k + 3 < nkt) load_g(s1);    // tile k+3
+            compute_g(1);
+            if (k + 2 < nkt) store_g(s0, 0);
             __syncthreads();
         }
-        if (k < nk) compute(0);             // odd count: the last tile, in stage 0
+        if (k < nkt) compute_g(0);          // odd count: the last tile, in stage 0
     }
 
     // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
@@ -687,6 +753,24 @@ RwPlan rw_plan(const WgGeom& g) {
     return rw_plan_for(g, 16);
 }
 
+template <bool WHOLE>
+void launch_rows(const RwPlan& r, dim3 grid, dim3 b16, dim3 b64, const RwArgs& p,
+                 hipStream_t stream) {
+    if (r.ict == 64) {
+        if (r.bkp == 32)
+            hipLaunchKernelGGL((conv_wgrad_rows_kernel<32, 64, 1, WHOLE>), grid, b64, 0, stream, p);
+        else
+            hipLaunchKernelGGL((conv_wgrad_rows_kernel<56, 64, 1, WHOLE>), grid, b64, 0, stream, p);
+    } else {
+        if (r.bkp == 32)
+            hipLaunchKernelGGL((conv_wgrad_rows_kernel<32, 16, RW_SEGS16, WHOLE>), grid, b16, 0, stream, p);
+        else if (r.bkp == 56)
+            hipLaunchKernelGGL((conv_wgrad_rows_kernel<56, 16, RW_SEGS16, WHOLE>), grid, b16, 0, stream, p);
+        else
+            hipLaunchKernelGGL((conv_wgrad_rows_kernel<64, 16, 1, WHOLE>), grid, b16, 0, stream, p);
+    }
+}
+
 }  // namespace
 
 bool conv_wgrad_implicit_ok(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
@@ -726,19 +810,9 @@ int launch_conv_wgrad_f32(const float* dy, const float* x, float* dw, float* ws,
         p.vec_x = IW % 4 == 0 && (uintptr_t)x % 16 == 0;
         const dim3 grid((unsigned)r.tiles, (unsigned)r.splits);
         const dim3 b16(RwTile<16>::NT), b64(RwTile<64>::NT);
-        if (r.ict == 64) {
-            if (r.bkp == 32)
-                hipLaunchKernelGGL((conv_wgrad_rows_kernel<32, 64>), grid, b64, 0, stream, p);
-            else
-                hipLaunchKernelGGL((conv_wgrad_rows_kernel<56, 64>), grid, b64, 0, stream, p);
-        } else {
-            if (r.bkp == 32)
-                hipLaunchKernelGGL((conv_wgrad_rows_kernel<32, 16>), grid, b16, 0, stream, p);
-            else if (r.bkp == 56)
-                hipLaunchKernelGGL((conv_wgrad_rows_kernel<56, 16>), grid, b16, 0, stream, p);
-            else
-                hipLaunchKernelGGL((conv_wgrad_rows_kernel<64, 16>), grid, b16, 0, stream, p);
-        }
+        const bool whole = p.vec_dy && p.vec_x && g.OW % r.bkp == 0 && IW >= g.OW;
+        if (whole) launch_rows<true>(r, grid, b16, b64, p, stream);
+        else launch_rows<false>(r, grid, b16, b64, p, stream);
         int st = hip_error(hipGetLastError(), "conv_wgrad_rows_kernel launch");
         if (st || r.splits == 1) return st;
         GemmArgs red{CDX_OP_N, CDX_OP_N, OC, g.Kc(), 0, nullptr, 1, nullptr, 1, dw, g.Kc(), 0, 0,
