@@ -110,6 +110,9 @@ int launch_gemm_16(const GemmArgs& g, int in_dtype, hipStream_t stream);
 // GEMMs with K <= 16 (narrow_kind 1) or N <= 16 (2), plain output map, no
 // batch / ones column (0: use the tiled kernels); no workspace.
 int narrow_kind(const GemmArgs& g);
+// The FP32 GEMM's 128 x 112 tiles apply (widths a multiple of 112 but not
+// of 64, enough rows): faster than the split-precision kernels there.
+bool f32_takes_w112(const GemmArgs& g);
 int launch_gemm_narrow(const GemmArgs& g, hipStream_t stream);
 int launch_dgemm(int opA, int opB, int64_t M, int64_t N, int64_t K,
                  const double* A, int64_t lda, const double* B, int64_t ldb,

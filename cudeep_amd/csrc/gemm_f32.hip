@@ -538,6 +538,11 @@ size_t ws_of(const GemmArgs& g) {
 
 }  // namespace
 
+bool f32_takes_w112(const GemmArgs& g) {
+    bool blocked;
+    return choose_f32(g, blocked) == F32Cfg::W112;
+}
+
 size_t gemm_f32_workspace(const GemmArgs& g) {
     if (narrow_kind(g)) return 0;
     bool blocked;

@@ -234,6 +234,11 @@ def test_fp32_w112_tiles(M, N, K, tA, tB):
     Cf = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, bias=dev(bias),
                          bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU))
     assert np.array_equal(Cf, np.maximum(C + bias[None, :], 0))
+    # the TF32 modes run these shapes on the same FP32 kernel (exact products,
+    # inside their error bar): the same bits
+    for prec in (cd.PREC_TF32MODE, cd.PREC_TF32MODE4):
+        Ct = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB, precision=prec))
+        assert np.array_equal(Ct.view(np.uint32), C.view(np.uint32))
 
 
 @pytest.mark.parametrize("n", [2048, 4096])
