@@ -469,12 +469,14 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    wave tiles (spills), 8-byte B reads, one register staging set.)
 //  * Large: 128x128x16, 8 waves of 32x64 -> 2 waves per SIMD, 32 fp32
 //    accumulators per lane.
-//  * Medium: 64x64x16, 4 waves of 32x32, for problems whose 128x128 tiles
-//    would spread unevenly over the 256 CUs, for the split-K slices (few
-//    tiles, long K: the weight gradients) and for small problems.  Against
-//    8 waves of 16x32 on the same tile: 2048^3 141 against 157 us, 4096 x
-//    1024 x 1024 73 against 81, 8192 x 256 x 784 (NT) 32 against 36, 8192 x
-//    784 x 256 41 against 45; 1024^3 NT the one loss (26 against 24).
+//  * Medium: 64x64x16, 4 waves of 16x64, for problems whose 128x128 tiles
+//    would spread unevenly over the 256 CUs, for the split-K slices of
+//    products with M < 128 and for small problems.  Against 4 waves of 32x32
+//    on the same tile: 3072^3 447 against 458 us, 4100^3 1358 against 1385,
+//    8192 x 256 x 784 (NT) 31.6 against 32.5; 4 waves of 64x16 about the
+//    same, 64x128 / 128x64 tiles of 64x32 / 32x64 waves 1.3-1.8x slower.
+//    (8 waves of 16x32 measured slower than 4 of 32x32 earlier: 2048^3 141
+//    against 157 us.)
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
 //    64x64x16, 4 waves of 16x64 (16-byte B fragment reads), XCD groups of
 //    one tile row: 64 x 100352 x 576 in 70-72 us, against 73-74 with 4
@@ -495,7 +497,7 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    against 54.5 on 64x64 slices; 128x128: 51.5; any BK = 32 slice: 58-79).
 using CfgLarge = Cfg<128, 128, 16, 32, 64, 8, 2>;
 using CfgHuge = Cfg<128, 128, 16, 64, 32, 8, 2>;
-using CfgMedium = Cfg<64, 64, 16, 32, 32, 8, 2>;
+using CfgMedium = Cfg<64, 64, 16, 16, 64, 8, 2>;
 using CfgSkinnyM = Cfg<64, 64, 16, 16, 64, 1, 2>;
 using CfgNarrowN = Cfg<32, 16, 64, 16, 16, 8, 2>;
 using CfgW112 = Cfg<128, 112, 16, 16, 112, 8, 2>;
