@@ -392,9 +392,12 @@ int launch_im2col_f32(const float* in, float* col, int64_t batch, int64_t IC,
     const int64_t chunk_rows = std::max<int64_t>(1, std::min<int64_t>(g.OH, ceil_div(1024, g.OW)));
     const int64_t chunks = ceil_div(g.OH, chunk_rows);
     const int64_t chunk_in_rows = (chunk_rows - 1) * SH + KH;
+    // (the plane kernel's row and column origins oh*SH - PH, ow*SW - PW + kw
+    // are int: strides and paddings beyond that take the 64-bit kernel)
     if (chunk_in_rows * IW <= kPlaneMaxFloats && batch * IC <= INT32_MAX &&
         g.spatial + 1024 <= INT32_MAX && KH * KW <= 4096 && chunks <= 65535 &&
-        g.OH * SH < INT32_MAX) {
+        g.OH * SH < INT32_MAX && g.OW * SW + KW < INT32_MAX && PH < INT32_MAX &&
+        PW < INT32_MAX) {
         const size_t lds = (size_t)(chunk_in_rows * IW) * sizeof(float);
         hipLaunchKernelGGL(im2col_plane_kernel<4>, dim3((unsigned)(batch * IC), (unsigned)chunks),
                            dim3(256), lds, stream, in, col, g, (int)chunk_rows);

@@ -56,6 +56,27 @@ def test_im2col_bit_exact(g):
     assert np.array_equal(col.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("g", [
+    # strides / paddings beyond 32 bits: the window origins ow*SW - PW need
+    # 64-bit arithmetic (only output column 1 lands inside the image; cut
+    # to 32 bits, SW = 2^32 + 1 and PW = 2^32 would read like 1 and 0)
+    (1, 2, 4, 4, 1, 1, 1, 2**32 + 1, 0, 2**32),
+    (1, 2, 4, 4, 1, 3, 1, 2**32 + 1, 1, 2**32),
+    (1, 2, 4, 4, 1, 1, 1, 2**31 + 1, 0, 2**31),
+    (2, 1, 4, 5, 3, 1, 2**32 + 1, 1, 2**32, 0),
+])
+def test_im2col_huge_stride_padding(g):
+    Bn, C, H, W, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(7)
+    x = normal(rng, (Bn, C, H, W))
+    say("im2col huge stride/padding", g)
+    col = host(ops().im2col(dev(x), KH, KW, (SH, SW), (PH, PW)))
+    want = oracle.im2col(x, KH, KW, SH, SW, PH, PW)
+    assert col.shape == want.shape
+    assert np.count_nonzero(want) > 0          # some taps inside the image
+    assert np.array_equal(col.view(np.uint32), want.view(np.uint32))
+
+
 def test_im2col_c5_full_bit_exact():
     """C5 geometry: N=32, C=64, 56x56, 3x3, s1, p1 -> col [576, 100352]."""
     rng = np.random.default_rng(555)
