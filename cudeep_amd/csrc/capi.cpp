@@ -576,6 +576,15 @@ bool bwd_data_as_forward(int64_t OC, int64_t KH, int64_t KW, int64_t SH, int64_t
     return OC > 0 && SH == 1 && SW == 1 && PH <= KH - 1 && PW <= KW - 1;
 }
 
+// Stride-1 backward data as the row-window implicit conv of grad_out with the
+// flipped filter (no column buffer), where that kernel's window fits.
+bool bwd_data_rowwin(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                     int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    if (!bwd_data_as_forward(OC, KH, KW, SH, SW, PH, PW)) return false;
+    const int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
+    return cdx::conv_rowwin_ok(batch, OC, IC, OH, OW, KH, KW, 1, 1, KH - 1 - PH, KW - 1 - PW);
+}
+
 // Workspace of the implicit backward-weight kernel (0 when it does not apply).
 size_t wgrad_implicit_floats(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
                              int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
@@ -648,6 +657,9 @@ size_t cdx_conv2d_backward_data_workspace_size(int64_t batch, int64_t in_channel
         return 0;
     ConvSizes z = conv_sizes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
                              stride_w, pad_h, pad_w);
+    if (bwd_data_rowwin(batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w))   // flipped filter only
+        return (size_t)in_channels * out_channels * (size_t)(kernel_h * kernel_w) * sizeof(float);
     if (bwd_data_as_forward(out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w)) {
         // flipped filter [IC, OC, KH, KW] + im2col of grad_out [OC*KH*KW, B*IH*IW]
         const size_t khw = (size_t)(kernel_h * kernel_w);
@@ -682,6 +694,24 @@ int cdx_conv2d_backward_data_f32(const float* grad_output, const float* weight, 
     Scratch ws;
     st = ws.acquire(workspace, workspace_bytes, need, stream, fn);
     if (st) return st;
+    if (bwd_data_rowwin(batch, in_channels, out_channels, in_h, in_w, kernel_h, kernel_w,
+                        stride_h, stride_w, pad_h, pad_w)) {
+        // stride 1: grad_input = conv(grad_out, flipped filter, padding KH-1-PH, KW-1-PW)
+        // through the row-window implicit kernel (FP32 products in every
+        // precision mode, k summed in two levels: the reference sums OC
+        // products per grad_col entry, then KH*KW entries in col2im, and one
+        // K = OC*KH*KW running sum would be a ~KH*KW times longer rounding
+        // chain)
+        float* wf = static_cast<float*>(ws.ptr);
+        st = cdx::launch_flip_filter_f32(weight, wf, out_channels, in_channels,
+                                         kernel_h * kernel_w, stream);
+        if (!st)
+            st = cdx::launch_conv_rowwin_f32(grad_output, wf, nullptr, grad_input, batch,
+                                             out_channels, in_channels, z.OH, z.OW, kernel_h,
+                                             kernel_w, 1, 1, kernel_h - 1 - pad_h,
+                                             kernel_w - 1 - pad_w, true, stream);
+        return ws.release(st);
+    }
     if (bwd_data_as_forward(out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w)) {
         // stride 1: grad_input = conv(grad_out, flipped filter, padding KH-1-PH, KW-1-PW),
         // one im2col + one long-K GEMM straight into NCHW (no grad_col, no col2im)

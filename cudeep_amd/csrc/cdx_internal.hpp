@@ -228,6 +228,16 @@ int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bi
                                  int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
                                  int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
                                  int64_t PW, hipStream_t stream);
+// The same product in its row-window form (the input window of a 128-pixel
+// tile staged in LDS per 16-channel chunk; any kernel size and stride whose
+// window fits).  two_level: each run of 32 consecutive k summed from zero,
+// then added to the total (the FP32 backward-data route).
+bool conv_rowwin_ok(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                    int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW);
+int launch_conv_rowwin_f32(const float* x, const float* w, const float* bias, float* y,
+                           int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                           int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                           int64_t PW, bool two_level, hipStream_t stream);
 
 int launch_col2im_f32(const float* col, float* grad_in, int64_t batch, int64_t IC,
                       int64_t IH, int64_t IW, int64_t KH, int64_t KW,

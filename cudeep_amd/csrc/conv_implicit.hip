@@ -31,6 +31,8 @@
 // the channel order every filter element of a k-tile sits on its own cache
 // line.)
 // FP32 products in every precision mode, as the reference's kernel.
+#include <algorithm>
+
 #include "cdx_internal.hpp"
 
 namespace cdx {
@@ -223,7 +225,435 @@ void conv_fwd_implicit_kernel(CfArgs p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-window form: every kernel size and stride whose input window fits in LDS.
+//
+// A workgroup owns 64 output channels x 128 consecutive output pixels s of
+// one image.  Those pixels lie in at most R output rows starting at oh_lo,
+// which read the input rows ih = oh_lo*SH - PH + r, r < NR = (R-1)*SH + KH,
+// and the columns iw = c - PW, c < WP = (OW-1)*SW + KW.  Per chunk of ICT
+// input channels the workgroup stages that window of each channel into LDS
+// once, zero outside the image (the padding is materialised), so every
+// column-matrix element of the tile is one LDS read:
+//
+//   col[(ic, kh, kw), s] = win[ic - ic0][(oh(s) - oh_lo)*SH + kh][ow(s)*SW + kw]
+//                        = win_flat[base(s) + off(k)]
+//   base(s) = (oh(s) - oh_lo)*SH*WP + ow(s)*SW            (per lane, fixed)
+//   off(k)  = (ic - ic0)*NR*WP + kh*WP + kw               (table built once)
+//
+// An input element is fetched about NR / R times per 64 output channels
+// (C5: 6 rows staged per ~2.3 output rows) instead of KH*KW times, and the
+// k-loop has no bounds tests: 4 waves of 32 x 64, per 16 k one 16-byte read
+// of four tap offsets, 16 LDS reads of B and 32 v_mfma_f32_16x16x4_f32 (the
+// library's k-permutation: lane group g feeds MFMA q with k = 4g + q).  The
+// filter comes straight from L2 into registers, prefetched two 16-k groups
+// ahead, so those loads are issued before the next chunk's staging loads
+// (vector loads retire in order).  A chunk holds ICT*KH*KW taps padded to a
+// multiple of 16; padded taps read a zero slot (never a staged value, so an
+// Inf input cannot turn a padded 0 * x into NaN).
+//
+// TWO_LEVEL: the FP32 backward-data route's two-level k sum -- each run of
+// 32 consecutive k is summed from zero, then added to the total.
+
+constexpr int RF_BM = 64, RF_BN = 128, RF_NT = 256;
+constexpr int RF_KCP_MAX = 1024;   // taps per chunk (padded): the offset table's size
+constexpr int RF_CPG = 2;          // window channels staged per 16-k group
+constexpr int RF_LDS_MAX = 64 * 1024;
+
+struct RfArgs {
+    const float* x;      // [B][IC][IH][IW]
+    const float* w;      // [OC][Kc]
+    const float* bias;   // [OC] or null
+    float* y;            // [B][OC][S]
+    int IC, OC, IH, IW, OW, S, KW, KHW, SH, SW, PH, PW, Kc, plane;
+    int ICT, NR, WP, CP;      // channels per chunk, staged rows, row pitch, channel pitch
+    int kc_real, KCP;         // ICT*KHW taps per chunk, padded to a multiple of 16
+    int EB;                   // window buffer: ICT + 1 channel planes, the last all zero
+    int nchunks, tiles_img;
+    int64_t img_x, img_y;     // IC*IH*IW, OC*S
+    DivMagic div_ow, div_wp, div_tiles, div_khw, div_kw;
+};
+
+// PP: window positions per thread (CP <= 256 PP).  MASKED: a chunk has
+// padded taps or the last chunk has fewer than ICT channels, so some filter
+// values read are zeroed; otherwise every filter element read is in range
+// and used as loaded.
+template <int PP, bool VECW, bool MASKED, bool TWO_LEVEL>
+__global__ __launch_bounds__(RF_NT)
+void conv_rowwin_kernel(RfArgs p) {
+    // LDS: tap byte offsets [KCP] | window buffer 0 [EB] | window buffer 1 [EB]
+    extern __shared__ __attribute__((aligned(16))) int rf_smem[];
+    int* off = rf_smem;
+    float* lf = reinterpret_cast<float*>(rf_smem + p.KCP);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lq = lane >> 4;
+    const int wm0 = (wave >> 1) * 32, wn0 = (wave & 1) * 64;
+
+    const uint32_t bx = blockIdx.x;
+    const uint32_t b = div_u31(bx, p.div_tiles);
+    const int s0 = (int)(bx - b * (uint32_t)p.tiles_img) * RF_BN;
+    const int oc0 = blockIdx.y * RF_BM;
+    const int oh_lo = (int)div_u31((uint32_t)s0, p.div_ow);
+    const float* ximg = p.x + (int64_t)b * p.img_x;
+
+    // tap byte offsets of one chunk (the same for every chunk); padded taps
+    // read the zero plane (channel ICT); and the zero planes themselves
+    const int zplane = p.ICT * p.CP;
+    for (int k = tid; k < p.KCP; k += RF_NT) {
+        int o = zplane;
+        if (k < p.kc_real) {
+            const uint32_t icl = div_u31((uint32_t)k, p.div_khw);
+            const uint32_t t = (uint32_t)k - icl * (uint32_t)p.KHW;
+            const uint32_t kh = div_u31(t, p.div_kw);
+            const uint32_t kw = t - kh * (uint32_t)p.KW;
+            o = (int)(icl * (uint32_t)p.CP + kh * (uint32_t)p.WP + kw);
+        }
+        off[k] = 4 * o;
+    }
+    for (int i = tid; i < p.CP; i += RF_NT) {
+        lf[zplane + i] = 0.0f;
+        lf[p.EB + zplane + i] = 0.0f;
+    }
+
+    // this lane's pixel offsets in the window (pixels past the image read
+    // the tile's first pixel; their results are not stored)
+    int base[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int s = s0 + wn0 + 16 * j + l16;
+        const uint32_t sc = (uint32_t)(s < p.S ? s : s0);
+        const uint32_t oh = div_u31(sc, p.div_ow);
+        const int ow = (int)(sc - oh * (uint32_t)p.OW);
+        base[j] = ((int)oh - oh_lo) * p.SH * p.WP + ow * p.SW;
+    }
+
+    // Staging.  This thread's window positions q = tid + 256 m (m < PP) of
+    // every channel: in-plane input offset (0 outside the image) and
+    // validity, decoded once per workgroup.  The next chunk's window goes
+    // through registers RF_CPG channels at a time, one slice per 16-k group:
+    // loaded before the group's filter loads and stored into the other
+    // window buffer after its MFMAs, so few registers stay live and the
+    // filter loads stay in flight.  Loads are issued from in-range addresses;
+    // out-of-image positions and channels past IC are zeroed when stored.
+    int pos[PP];
+    uint32_t pos_ok = 0;
+    {
+        const int ih_lo = oh_lo * p.SH - p.PH;
+#pragma unroll
+        for (int m = 0; m < PP; ++m) {
+            const int q = tid + RF_NT * m;
+            const uint32_t qc = (uint32_t)(q < p.CP ? q : 0);
+            const uint32_t r = div_u31(qc, p.div_wp);
+            const int ih = ih_lo + (int)r, iw = (int)(qc - r * (uint32_t)p.WP) - p.PW;
+            const bool ok = q < p.CP && (unsigned)ih < (unsigned)p.IH && (unsigned)iw < (unsigned)p.IW;
+            pos[m] = ok ? ih * p.IW + iw : 0;
+            pos_ok |= ok ? 1u << m : 0u;
+        }
+    }
+    // (groups past the chunk's channels restage its last channel: the same
+    // values again, so every group issues the same loads and stores)
+    float sv[RF_CPG][PP];
+    auto slice_load = [&](int c, int g) {
+#pragma unroll
+        for (int h = 0; h < RF_CPG; ++h) {
+            const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
+            const int icc = ic < p.IC ? ic : 0;   // wave-uniform
+            const float* src = ximg + icc * p.plane;
+#pragma unroll
+            for (int m = 0; m < PP; ++m) sv[h][m] = src[pos[m]];
+        }
+    };
+    auto slice_store = [&](int c, int dst, int g) {
+#pragma unroll
+        for (int h = 0; h < RF_CPG; ++h) {
+            const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
+            const uint32_t ok = ic < p.IC ? pos_ok : 0u;
+            float* d = lf + dst + icl * p.CP + tid;
+#pragma unroll
+            for (int m = 0; m < PP; ++m) {
+                const float v = opaque(sv[h][m]);
+                if (tid + RF_NT * m < p.CP) d[RF_NT * m] = (ok >> m) & 1 ? v : 0.0f;
+            }
+        }
+    };
+
+    // filter fragments for one 16-k group: rows oc0 + wm0 + 16 i + l16
+    // (rows past OC read row 0; their results are not stored), k = 4 lq + q
+    // of the group
+    const int nkg = p.KCP / 16;
+    int ld_c = 0, ld_g = 0;   // the next group to load
+    const float* wrow[2];
+    bool row_ok[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int oc = oc0 + wm0 + 16 * i + l16;
+        row_ok[i] = oc < p.OC;
+        wrow[i] = p.w + (int64_t)(row_ok[i] ? oc : 0) * p.Kc;
+    }
+    struct AFrag { float v[2][4]; uint32_t ok; };
+    auto a_load = [&](AFrag& a) {
+        // prefetches past the last group re-read the last group (unused)
+        const int lc = ld_c < p.nchunks ? ld_c : p.nchunks - 1;
+        const int kl = 16 * ld_g + 4 * lq;
+        const int kg = lc * p.kc_real + kl;
+        uint32_t ok = 0xFFu;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if constexpr (VECW) {
+                bool in = true;
+                if constexpr (MASKED) in = (kl < p.kc_real) & (kg < p.Kc);
+                const float4 t = *reinterpret_cast<const float4*>(wrow[i] + (in ? kg : 0));
+                a.v[i][0] = t.x; a.v[i][1] = t.y; a.v[i][2] = t.z; a.v[i][3] = t.w;
+                if constexpr (MASKED) ok &= in ? 0xFFu : ~(0xFu << (4 * i));
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bool in = true;
+                    if constexpr (MASKED) in = (kl + q < p.kc_real) & (kg + q < p.Kc);
+                    a.v[i][q] = wrow[i][in ? kg + q : 0];
+                    if constexpr (MASKED) ok &= in ? 0xFFu : ~(1u << (4 * i + q));
+                }
+            }
+        }
+        a.ok = ok;
+        if (++ld_g == nkg) { ld_g = 0; ++ld_c; }
+    };
+
+    floatx4 acc[2][4], part[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // per chunk: byte address of each pixel block's (0, 0) tap in the
+    // chunk's window buffer
+    const char* lfb = reinterpret_cast<const char*>(lf);
+    int pb[4];
+    auto set_buffer = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pb[j] = 4 * (buf + base[j]);
+    };
+    auto compute = [&](const AFrag& a, int g) {
+        const int4 o = *reinterpret_cast<const int4*>(off + 16 * g + 4 * lq);
+        const int oq[4] = {o.x, o.y, o.z, o.w};
+        float av[2][4], bv[4][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (MASKED) {
+                    const float v = opaque(a.v[i][q]);
+                    av[i][q] = (a.ok >> (4 * i + q)) & 1 ? v : 0.0f;
+                } else {
+                    av[i][q] = a.v[i][q];
+                }
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                bv[j][q] = *reinterpret_cast<const float*>(lfb + pb[j] + oq[q]);
+        floatx4 (&tgt)[2][4] = TWO_LEVEL ? part : acc;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    tgt[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][q], bv[j][q], tgt[i][j], 0, 0, 0);
+    };
+    auto fold = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] += part[i][j];
+                part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+    };
+
+    // Every group issues the same loads (past the last chunk they read
+    // valid, unused addresses and store into the idle buffer), so the loop
+    // is straight-line and each wait covers only the loads it needs.  Two
+    // filter fragment sets alternate: a group computes with its set, then
+    // refills it with the group two ahead (no register copies, so a refill
+    // is waited for only when its group starts).
+    const int groups = p.nchunks * nkg;
+    AFrag a0, a1;
+    a_load(a0);
+    a_load(a1);
+    for (int g = 0; g * RF_CPG < p.ICT; ++g) {
+        slice_load(0, g);
+        slice_store(0, 0, g);
+    }
+    __syncthreads();
+    int gi = 0, c = 0, g = 0;
+    int cb = 0, nb = p.EB;   // window buffer of chunk c, and of chunk c + 1
+    set_buffer(cb);
+    auto step = [&](AFrag& a) {
+        // (scheduling barriers keep the slice loads ahead of the MFMAs and
+        // the slice stores, which wait for them, behind)
+        slice_load(c + 1, g);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(a, g);
+        a_load(a);
+        if (TWO_LEVEL && (gi & 1)) fold();
+        __builtin_amdgcn_sched_barrier(0);
+        slice_store(c + 1, nb, g);
+        ++gi;
+        if (++g == nkg) {
+            // the rest of chunk c + 1's window (chunks with fewer groups
+            // than channel pairs: 1x1 taps); then every wave's reads of
+            // buffer cb and writes of buffer nb are complete
+            for (int h = nkg; h * RF_CPG < p.ICT; ++h) {
+                slice_load(c + 1, h);
+                slice_store(c + 1, nb, h);
+            }
+            __syncthreads();
+            ++c;
+            g = 0;
+            const int t = cb; cb = nb; nb = t;
+            set_buffer(cb);
+        }
+    };
+    for (int t = 0; t + 1 < groups; t += 2) {
+        step(a0);
+        step(a1);
+    }
+    if (groups & 1) step(a0);
+    if (TWO_LEVEL && (groups & 1)) fold();
+
+    // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
+    // column l % 16; output (oc, s) -> y[b][oc][s] + bias[oc]
+    float* yimg = p.y + (int64_t)b * p.img_y;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int s = s0 + wn0 + 16 * j + l16;
+        if (s >= p.S) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oc = oc0 + wm0 + 16 * i + 4 * lq + r;
+                if (oc < p.OC)
+                    yimg[(int64_t)oc * p.S + s] = acc[i][j][r] + (p.bias ? p.bias[oc] : 0.0f);
+            }
+    }
+}
+
+// Launch plan of the row-window form, or ok = false where its window does
+// not fit (then the gather form above runs).
+struct RfPlan {
+    bool ok = false;
+    int ict = 0, nr = 0, wp = 0, kcp = 0, eb = 0, pp = 0;
+    size_t lds = 0;
+};
+
+RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                   int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    RfPlan pl;
+    const int64_t OH = (IH + 2 * PH - KH) / SH + 1, OW = (IW + 2 * PW - KW) / SW + 1;
+    const int64_t lim = INT32_MAX / 2;
+    const int64_t S = OH * OW;
+    // 32-bit in-image, pixel, tap and filter indices
+    if (OH < 1 || OW < 1 || S >= lim || IC * IH * IW >= lim || OC * S >= lim ||
+        IC * KH * KW >= lim || OC * IC * KH * KW >= lim || batch * ceil_div(S, RF_BN) >= lim ||
+        PH >= lim || PW >= lim || OH * SH + KH >= lim || OW * SW + KW >= lim)
+        return pl;
+    const int64_t rows = std::min<int64_t>(OH, (OW - 1 + RF_BN - 1) / OW + 1);
+    const int64_t nr = (rows - 1) * SH + KH, wp = (OW - 1) * SW + KW;
+    const int64_t cp = nr * wp, khw = KH * KW;
+    if (cp > 4 * RF_NT) return pl;   // at most 4 window positions per thread
+    // channels per chunk: up to 16 (no more than IC needs), halved until
+    // both window buffers (ICT + 1 planes each) and the tap table fit
+    auto kcp_of = [&](int64_t ict) { return ceil_div(ict * khw, 16) * 16; };
+    auto lds_of = [&](int64_t ict) { return (kcp_of(ict) + 2 * (ict + 1) * cp) * 4; };
+    int64_t ict = 16;
+    while (ict > 1 && ict / 2 >= IC) ict /= 2;
+    while (ict > 1 && (lds_of(ict) > RF_LDS_MAX || kcp_of(ict) > RF_KCP_MAX)) ict /= 2;
+    if (lds_of(ict) > RF_LDS_MAX || kcp_of(ict) > RF_KCP_MAX) return pl;
+    pl.ok = true;
+    pl.ict = (int)ict; pl.nr = (int)nr; pl.wp = (int)wp;
+    pl.kcp = (int)kcp_of(ict); pl.eb = (int)((ict + 1) * cp);
+    pl.pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
+    pl.lds = (size_t)lds_of(ict);
+    return pl;
+}
+
+template <int PP, bool VECW, bool MASKED>
+void rowwin_go(const RfArgs& p, bool two_level, dim3 grid, size_t lds, hipStream_t stream) {
+    if (two_level)
+        hipLaunchKernelGGL((conv_rowwin_kernel<PP, VECW, MASKED, true>), grid, dim3(RF_NT), lds, stream, p);
+    else
+        hipLaunchKernelGGL((conv_rowwin_kernel<PP, VECW, MASKED, false>), grid, dim3(RF_NT), lds, stream, p);
+}
+
+template <int PP>
+void rowwin_go_pp(const RfArgs& p, bool vecw, bool masked, bool two_level, dim3 grid, size_t lds,
+                  hipStream_t stream) {
+    if (vecw) {
+        if (masked) rowwin_go<PP, true, true>(p, two_level, grid, lds, stream);
+        else rowwin_go<PP, true, false>(p, two_level, grid, lds, stream);
+    } else {
+        if (masked) rowwin_go<PP, false, true>(p, two_level, grid, lds, stream);
+        else rowwin_go<PP, false, false>(p, two_level, grid, lds, stream);
+    }
+}
+
+int launch_rowwin(const float* x, const float* w, const float* bias, float* y, int64_t batch,
+                  int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH, int64_t KW,
+                  int64_t SH, int64_t SW, int64_t PH, int64_t PW, const RfPlan& pl,
+                  bool two_level, hipStream_t stream) {
+    const int64_t OH = (IH + 2 * PH - KH) / SH + 1, OW = (IW + 2 * PW - KW) / SW + 1;
+    RfArgs p;
+    p.x = x;
+    p.IC = (int)IC; p.IH = (int)IH; p.IW = (int)IW; p.OW = (int)OW; p.S = (int)(OH * OW);
+    p.KW = (int)KW; p.KHW = (int)(KH * KW); p.SH = (int)SH; p.SW = (int)SW;
+    p.PH = (int)PH; p.PW = (int)PW; p.Kc = (int)(IC * KH * KW); p.plane = (int)(IH * IW);
+    p.ICT = pl.ict; p.NR = pl.nr; p.WP = pl.wp; p.CP = pl.nr * pl.wp;
+    p.kc_real = pl.ict * p.KHW; p.KCP = pl.kcp; p.EB = pl.eb;
+    p.nchunks = (int)ceil_div(IC, pl.ict);
+    p.tiles_img = (int)ceil_div(p.S, RF_BN);
+    p.img_x = IC * IH * IW; p.img_y = OC * OH * OW;
+    p.div_ow = div_magic(OW); p.div_wp = div_magic(p.WP);
+    p.div_tiles = div_magic(p.tiles_img); p.div_khw = div_magic(p.KHW); p.div_kw = div_magic(KW);
+    const bool vecw = p.Kc % 4 == 0 && p.kc_real % 4 == 0 && (uintptr_t)w % 16 == 0;
+    const bool masked = IC % pl.ict != 0 || p.kc_real != p.KCP;
+    const int64_t chunk = (int64_t)65535 * RF_BM;   // output channels per launch (grid y)
+    for (int64_t oc0 = 0; oc0 < OC; oc0 += chunk) {
+        const int64_t oc_n = OC - oc0 < chunk ? OC - oc0 : chunk;
+        p.OC = (int)oc_n;
+        p.w = w + oc0 * p.Kc;
+        p.bias = bias ? bias + oc0 : nullptr;
+        p.y = y + oc0 * p.S;
+        const dim3 grid((unsigned)(batch * p.tiles_img), (unsigned)ceil_div(oc_n, RF_BM));
+        if (pl.pp == 1) rowwin_go_pp<1>(p, vecw, masked, two_level, grid, pl.lds, stream);
+        else if (pl.pp == 2) rowwin_go_pp<2>(p, vecw, masked, two_level, grid, pl.lds, stream);
+        else rowwin_go_pp<4>(p, vecw, masked, two_level, grid, pl.lds, stream);
+        const int st = hip_error(hipGetLastError(), "conv_rowwin_kernel launch");
+        if (st) return st;
+    }
+    return CDX_OK;
+}
+
 }  // namespace
+
+bool conv_rowwin_ok(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
+                    int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    return rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW).ok;
+}
+
+int launch_conv_rowwin_f32(const float* x, const float* w, const float* bias, float* y,
+                           int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
+                           int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
+                           int64_t PW, bool two_level, hipStream_t stream) {
+    const RfPlan pl = rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    if (!pl.ok)
+        return set_error(CDX_ERR_UNSUPPORTED, "conv row-window kernel: window does not fit in LDS");
+    return launch_rowwin(x, w, bias, y, batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, pl,
+                         two_level, stream);
+}
 
 bool conv_fwd_implicit_ok(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH,
                           int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
@@ -241,6 +671,11 @@ int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bi
                                  int64_t PW, hipStream_t stream) {
     if (!conv_fwd_implicit_ok(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW))
         return set_error(CDX_ERR_UNSUPPORTED, "conv implicit forward: geometry beyond 32-bit indices");
+    // the row-window form wherever its input window fits in LDS
+    const RfPlan pl = rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    if (pl.ok)
+        return launch_rowwin(x, w, bias, y, batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, pl,
+                             false, stream);
     const int64_t OH = (IH + 2 * PH - KH) / SH + 1, OW = (IW + 2 * PW - KW) / SW + 1;
     CfArgs p;
     p.x = x;

@@ -81,9 +81,9 @@ def test_conv_argument_validation():
     # workspace size query = K_col * B * OH * OW * 4
     assert L.lib().cdx_conv2d_forward_workspace_size(32, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
         == 576 * 32 * 56 * 56 * 4
-    # backward data, stride 1: flipped filter + im2col of grad_out [OC*9, B*IH*IW]
+    # backward data, stride 1 (row-window implicit kernel): the flipped filter only
     assert L.lib().cdx_conv2d_backward_data_workspace_size(32, 64, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
-        == (64 * 64 * 9 + 64 * 9 * 32 * 56 * 56) * 4
+        == 64 * 64 * 9 * 4
     # stride 2: grad_col [K_col, B*S] + grad_out in [OC, B*S]
     assert L.lib().cdx_conv2d_backward_data_workspace_size(2, 3, 4, 9, 9, 3, 3, 2, 2, 1, 1) \
         == (27 * 2 * 25 + 4 * 2 * 25) * 4

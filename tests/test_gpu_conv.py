@@ -161,6 +161,9 @@ IMPLICIT_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
     (2, 8, 6, 130, 16, 3, 3, 1, 2, 1, 1),      # pixels not a multiple of the 128 tile
     (1, 37, 12, 12, 65, 2, 2, 2, 2, 0, 0),     # Kc = 148: k-tail, OC = 65
     (2, 16, 14, 14, 64, 3, 3, 1, 1, 1, 1),     # 3x3 stride 1 through the implicit kernel
+    # row-window form: 5 chunks of 8 channels, a 7 x 104 window (3 of 4
+    # positions per thread used), 200 taps per chunk padded to 208
+    (2, 40, 12, 100, 24, 5, 5, 1, 1, 2, 2),
 ]
 
 
