@@ -255,7 +255,7 @@ void conv_fwd_implicit_kernel(CfArgs p) {
 // TWO_LEVEL: the FP32 backward-data route's two-level k sum -- each run of
 // 32 consecutive k is summed from zero, then added to the total.
 
-constexpr int RF_BM = 64, RF_BN = 128, RF_NT = 256;
+constexpr int RF_BM = 64, RF_NT = 256;
 constexpr int RF_KCP_MAX = 1024;   // taps per chunk (padded): the offset table's size
 constexpr int RF_CPG = 2;          // window channels staged per 16-k group
 constexpr int RF_LDS_MAX = 64 * 1024;
@@ -278,9 +278,10 @@ struct RfArgs {
 // padded taps or the last chunk has fewer than ICT channels, so some filter
 // values read are zeroed; otherwise every filter element read is in range
 // and used as loaded.
-template <int PP, bool VECW, bool MASKED, bool TWO_LEVEL>
+template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL>
 __global__ __launch_bounds__(RF_NT)
 void conv_rowwin_kernel(RfArgs p) {
+    constexpr int TN = 16 * FN;   // output pixels per tile
     // LDS: tap byte offsets [KCP] | window buffer 0 [EB] | window buffer 1 [EB]
     extern __shared__ __attribute__((aligned(16))) int rf_smem[];
     int* off = rf_smem;
@@ -288,11 +289,11 @@ void conv_rowwin_kernel(RfArgs p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lq = lane >> 4;
-    const int wm0 = (wave >> 1) * 32, wn0 = (wave & 1) * 64;
+    const int wm0 = wave * 16;   // each wave: 16 output channels x the tile's TN pixels
 
     const uint32_t bx = blockIdx.x;
     const uint32_t b = div_u31(bx, p.div_tiles);
-    const int s0 = (int)(bx - b * (uint32_t)p.tiles_img) * RF_BN;
+    const int s0 = (int)(bx - b * (uint32_t)p.tiles_img) * TN;
     const int oc0 = blockIdx.y * RF_BM;
     const int oh_lo = (int)div_u31((uint32_t)s0, p.div_ow);
     const float* ximg = p.x + (int64_t)b * p.img_x;
@@ -318,10 +319,10 @@ void conv_rowwin_kernel(RfArgs p) {
 
     // this lane's pixel offsets in the window (pixels past the image read
     // the tile's first pixel; their results are not stored)
-    int base[4];
+    int base[FN];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int s = s0 + wn0 + 16 * j + l16;
+    for (int j = 0; j < FN; ++j) {
+        const int s = s0 + 16 * j + l16;
         const uint32_t sc = (uint32_t)(s < p.S ? s : s0);
         const uint32_t oh = div_u31(sc, p.div_ow);
         const int ow = (int)(sc - oh * (uint32_t)p.OW);
@@ -378,41 +379,38 @@ void conv_rowwin_kernel(RfArgs p) {
         }
     };
 
-    // filter fragments for one 16-k group: rows oc0 + wm0 + 16 i + l16
-    // (rows past OC read row 0; their results are not stored), k = 4 lq + q
-    // of the group
+    // filter fragments for one 16-k group: row oc0 + wm0 + l16 (rows past
+    // OC read row 0; their results are not stored), k = 4 lq + q of the
+    // group
     const int nkg = p.KCP / 16;
     int ld_c = 0, ld_g = 0;   // the next group to load
-    const float* wrow[2];
-    bool row_ok[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int oc = oc0 + wm0 + 16 * i + l16;
-        row_ok[i] = oc < p.OC;
-        wrow[i] = p.w + (int64_t)(row_ok[i] ? oc : 0) * p.Kc;
+    const float* wrow[1];
+    {
+        const int oc = oc0 + wm0 + l16;
+        wrow[0] = p.w + (int64_t)(oc < p.OC ? oc : 0) * p.Kc;
     }
-    struct AFrag { float v[2][4]; uint32_t ok; };
+    struct AFrag { float v[1][4]; uint32_t ok; };
     auto a_load = [&](AFrag& a) {
         // prefetches past the last group re-read the last group (unused)
         const int lc = ld_c < p.nchunks ? ld_c : p.nchunks - 1;
         const int kl = 16 * ld_g + 4 * lq;
         const int kg = lc * p.kc_real + kl;
-        uint32_t ok = 0xFFu;
+        uint32_t ok = 0xFu;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 1; ++i) {
             if constexpr (VECW) {
                 bool in = true;
                 if constexpr (MASKED) in = (kl < p.kc_real) & (kg < p.Kc);
                 const float4 t = *reinterpret_cast<const float4*>(wrow[i] + (in ? kg : 0));
                 a.v[i][0] = t.x; a.v[i][1] = t.y; a.v[i][2] = t.z; a.v[i][3] = t.w;
-                if constexpr (MASKED) ok &= in ? 0xFFu : ~(0xFu << (4 * i));
+                if constexpr (MASKED) ok &= in ? 0xFu : 0u;
             } else {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     bool in = true;
                     if constexpr (MASKED) in = (kl + q < p.kc_real) & (kg + q < p.Kc);
                     a.v[i][q] = wrow[i][in ? kg + q : 0];
-                    if constexpr (MASKED) ok &= in ? 0xFFu : ~(1u << (4 * i + q));
+                    if constexpr (MASKED) ok &= in ? 0xFu : ~(1u << q);
                 }
             }
         }
@@ -420,57 +418,49 @@ void conv_rowwin_kernel(RfArgs p) {
         if (++ld_g == nkg) { ld_g = 0; ++ld_c; }
     };
 
-    floatx4 acc[2][4], part[2][4];
+    floatx4 acc[FN], part[FN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[j] = part[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // per chunk: byte address of each pixel block's (0, 0) tap in the
     // chunk's window buffer
     const char* lfb = reinterpret_cast<const char*>(lf);
-    int pb[4];
+    int pb[FN];
     auto set_buffer = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) pb[j] = 4 * (buf + base[j]);
+        for (int j = 0; j < FN; ++j) pb[j] = 4 * (buf + base[j]);
     };
     auto compute = [&](const AFrag& a, int g) {
         const int4 o = *reinterpret_cast<const int4*>(off + 16 * g + 4 * lq);
         const int oq[4] = {o.x, o.y, o.z, o.w};
-        float av[2][4], bv[4][4];
+        float av[4], bv[FN][4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if constexpr (MASKED) {
-                    const float v = opaque(a.v[i][q]);
-                    av[i][q] = (a.ok >> (4 * i + q)) & 1 ? v : 0.0f;
-                } else {
-                    av[i][q] = a.v[i][q];
-                }
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (MASKED) {
+                const float v = opaque(a.v[0][q]);
+                av[q] = (a.ok >> q) & 1 ? v : 0.0f;
+            } else {
+                av[q] = a.v[0][q];
             }
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < FN; ++j)
                 bv[j][q] = *reinterpret_cast<const float*>(lfb + pb[j] + oq[q]);
-        floatx4 (&tgt)[2][4] = TWO_LEVEL ? part : acc;
+        floatx4 (&tgt)[FN] = TWO_LEVEL ? part : acc;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    tgt[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][q], bv[j][q], tgt[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j)
+                tgt[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[q], bv[j][q], tgt[j], 0, 0, 0);
     };
     auto fold = [&]() {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] += part[i][j];
-                part[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-            }
+        for (int j = 0; j < FN; ++j) {
+            acc[j] += part[j];
+            part[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
     };
 
     // Every group issues the same loads (past the last chunk they read
@@ -528,77 +518,104 @@ void conv_rowwin_kernel(RfArgs p) {
     // column l % 16; output (oc, s) -> y[b][oc][s] + bias[oc]
     float* yimg = p.y + (int64_t)b * p.img_y;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int s = s0 + wn0 + 16 * j + l16;
+    for (int j = 0; j < FN; ++j) {
+        const int s = s0 + 16 * j + l16;
         if (s >= p.S) continue;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int oc = oc0 + wm0 + 16 * i + 4 * lq + r;
-                if (oc < p.OC)
-                    yimg[(int64_t)oc * p.S + s] = acc[i][j][r] + (p.bias ? p.bias[oc] : 0.0f);
-            }
+        for (int r = 0; r < 4; ++r) {
+            const int oc = oc0 + wm0 + 4 * lq + r;
+            if (oc < p.OC)
+                yimg[(int64_t)oc * p.S + s] = acc[j][r] + (p.bias ? p.bias[oc] : 0.0f);
+        }
     }
 }
 
-// Launch plan of the row-window form, or ok = false where its window does
-// not fit (then the gather form above runs).
+// Launch plan of the row-window form, or ok = false where no window fits
+// (then the gather form above runs).
 struct RfPlan {
     bool ok = false;
-    int ict = 0, nr = 0, wp = 0, kcp = 0, eb = 0, pp = 0;
+    int fn = 0, ict = 0, nr = 0, wp = 0, kcp = 0, eb = 0, pp = 0;
     size_t lds = 0;
 };
 
+// Tile width and channel chunk: the choice that gives the busiest CU the
+// least work -- ceil(workgroups / 256 CUs) tiles of TN pixels, times the
+// padded-tap waste, plus 15 % where those tiles are more than its LDS lets
+// one CU hold at once (a partial second round runs a CU at low occupancy);
+// near-ties (within 3 %) go to more channels per chunk, then wider tiles.
+// (C5, 32 x 64 x 56^2, 3x3: 112-pixel tiles of 16 channels, 896 workgroups
+// at 4 per CU; 128-pixel tiles leave 800 workgroups at 3 per CU, 32 of
+// them in a second round.)
 RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
-                   int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
-    RfPlan pl;
+                   int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW, bool two_level) {
+    RfPlan best;
+    // workgroups one CU holds by registers (4 waves each): 4, or 3 with the
+    // two-level sum's second accumulator set
+    const int64_t by_regs = two_level ? 3 : 4;
     const int64_t OH = (IH + 2 * PH - KH) / SH + 1, OW = (IW + 2 * PW - KW) / SW + 1;
     const int64_t lim = INT32_MAX / 2;
-    const int64_t S = OH * OW;
+    const int64_t S = OH * OW, khw = KH * KW;
     // 32-bit in-image, pixel, tap and filter indices
     if (OH < 1 || OW < 1 || S >= lim || IC * IH * IW >= lim || OC * S >= lim ||
-        IC * KH * KW >= lim || OC * IC * KH * KW >= lim || batch * ceil_div(S, RF_BN) >= lim ||
+        IC * khw >= lim || OC * IC * khw >= lim || batch * S >= lim ||
         PH >= lim || PW >= lim || OH * SH + KH >= lim || OW * SW + KW >= lim)
-        return pl;
-    const int64_t rows = std::min<int64_t>(OH, (OW - 1 + RF_BN - 1) / OW + 1);
-    const int64_t nr = (rows - 1) * SH + KH, wp = (OW - 1) * SW + KW;
-    const int64_t cp = nr * wp, khw = KH * KW;
-    if (cp > 4 * RF_NT) return pl;   // at most 4 window positions per thread
-    // channels per chunk: up to 16 (no more than IC needs), halved until
-    // both window buffers (ICT + 1 planes each) and the tap table fit
-    auto kcp_of = [&](int64_t ict) { return ceil_div(ict * khw, 16) * 16; };
-    auto lds_of = [&](int64_t ict) { return (kcp_of(ict) + 2 * (ict + 1) * cp) * 4; };
-    int64_t ict = 16;
-    while (ict > 1 && ict / 2 >= IC) ict /= 2;
-    while (ict > 1 && (lds_of(ict) > RF_LDS_MAX || kcp_of(ict) > RF_KCP_MAX)) ict /= 2;
-    if (lds_of(ict) > RF_LDS_MAX || kcp_of(ict) > RF_KCP_MAX) return pl;
-    pl.ok = true;
-    pl.ict = (int)ict; pl.nr = (int)nr; pl.wp = (int)wp;
-    pl.kcp = (int)kcp_of(ict); pl.eb = (int)((ict + 1) * cp);
-    pl.pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
-    pl.lds = (size_t)lds_of(ict);
-    return pl;
+        return best;
+    double best_cost = 0.0;
+    for (const int fn : {8, 7, 5}) {
+        const int64_t tn = 16 * fn;
+        const int64_t rows = std::min<int64_t>(OH, (OW - 1 + tn - 1) / OW + 1);
+        const int64_t nr = (rows - 1) * SH + KH, wp = (OW - 1) * SW + KW, cp = nr * wp;
+        if (cp > 4 * RF_NT) continue;   // at most 4 window positions per thread
+        const int64_t wgs = batch * ceil_div(S, tn) * ceil_div(OC, RF_BM);
+        const int64_t per_cu = ceil_div(wgs, 256);
+        int64_t ict = 16;
+        while (ict > 1 && ict / 2 >= IC) ict /= 2;
+        for (; ict >= 1; ict /= 2) {
+            const int64_t kcp = ceil_div(ict * khw, 16) * 16;
+            const int64_t lds = (kcp + 2 * (ict + 1) * cp) * 4;
+            if (lds > RF_LDS_MAX || kcp > RF_KCP_MAX) continue;
+            const int64_t resident = std::min<int64_t>(by_regs, (160 * 1024) / lds);
+            const double cost = (double)per_cu * tn * ((double)kcp / (double)(ict * khw)) *
+                                (per_cu > resident ? 1.15 : 1.0);
+            if (!best.ok || cost < best_cost * 0.97) {
+                best.ok = true;
+                best_cost = cost;
+                best.fn = fn; best.ict = (int)ict; best.nr = (int)nr; best.wp = (int)wp;
+                best.kcp = (int)kcp; best.eb = (int)((ict + 1) * cp);
+                best.pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
+                best.lds = (size_t)lds;
+            }
+        }
+    }
+    return best;
 }
 
-template <int PP, bool VECW, bool MASKED>
+template <int FN, int PP, bool VECW, bool MASKED>
 void rowwin_go(const RfArgs& p, bool two_level, dim3 grid, size_t lds, hipStream_t stream) {
     if (two_level)
-        hipLaunchKernelGGL((conv_rowwin_kernel<PP, VECW, MASKED, true>), grid, dim3(RF_NT), lds, stream, p);
+        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, true>), grid, dim3(RF_NT), lds, stream, p);
     else
-        hipLaunchKernelGGL((conv_rowwin_kernel<PP, VECW, MASKED, false>), grid, dim3(RF_NT), lds, stream, p);
+        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, false>), grid, dim3(RF_NT), lds, stream, p);
 }
 
-template <int PP>
+template <int FN, int PP>
 void rowwin_go_pp(const RfArgs& p, bool vecw, bool masked, bool two_level, dim3 grid, size_t lds,
                   hipStream_t stream) {
     if (vecw) {
-        if (masked) rowwin_go<PP, true, true>(p, two_level, grid, lds, stream);
-        else rowwin_go<PP, true, false>(p, two_level, grid, lds, stream);
+        if (masked) rowwin_go<FN, PP, true, true>(p, two_level, grid, lds, stream);
+        else rowwin_go<FN, PP, true, false>(p, two_level, grid, lds, stream);
     } else {
-        if (masked) rowwin_go<PP, false, true>(p, two_level, grid, lds, stream);
-        else rowwin_go<PP, false, false>(p, two_level, grid, lds, stream);
+        if (masked) rowwin_go<FN, PP, false, true>(p, two_level, grid, lds, stream);
+        else rowwin_go<FN, PP, false, false>(p, two_level, grid, lds, stream);
     }
+}
+
+template <int FN>
+void rowwin_go_fn(const RfArgs& p, int pp, bool vecw, bool masked, bool two_level, dim3 grid,
+                  size_t lds, hipStream_t stream) {
+    if (pp == 1) rowwin_go_pp<FN, 1>(p, vecw, masked, two_level, grid, lds, stream);
+    else if (pp == 2) rowwin_go_pp<FN, 2>(p, vecw, masked, two_level, grid, lds, stream);
+    else rowwin_go_pp<FN, 4>(p, vecw, masked, two_level, grid, lds, stream);
 }
 
 int launch_rowwin(const float* x, const float* w, const float* bias, float* y, int64_t batch,
@@ -614,7 +631,7 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
     p.ICT = pl.ict; p.NR = pl.nr; p.WP = pl.wp; p.CP = pl.nr * pl.wp;
     p.kc_real = pl.ict * p.KHW; p.KCP = pl.kcp; p.EB = pl.eb;
     p.nchunks = (int)ceil_div(IC, pl.ict);
-    p.tiles_img = (int)ceil_div(p.S, RF_BN);
+    p.tiles_img = (int)ceil_div(p.S, 16 * pl.fn);
     p.img_x = IC * IH * IW; p.img_y = OC * OH * OW;
     p.div_ow = div_magic(OW); p.div_wp = div_magic(p.WP);
     p.div_tiles = div_magic(p.tiles_img); p.div_khw = div_magic(p.KHW); p.div_kw = div_magic(KW);
@@ -628,9 +645,9 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
         p.bias = bias ? bias + oc0 : nullptr;
         p.y = y + oc0 * p.S;
         const dim3 grid((unsigned)(batch * p.tiles_img), (unsigned)ceil_div(oc_n, RF_BM));
-        if (pl.pp == 1) rowwin_go_pp<1>(p, vecw, masked, two_level, grid, pl.lds, stream);
-        else if (pl.pp == 2) rowwin_go_pp<2>(p, vecw, masked, two_level, grid, pl.lds, stream);
-        else rowwin_go_pp<4>(p, vecw, masked, two_level, grid, pl.lds, stream);
+        if (pl.fn == 8) rowwin_go_fn<8>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
+        else if (pl.fn == 7) rowwin_go_fn<7>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
+        else rowwin_go_fn<5>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
         const int st = hip_error(hipGetLastError(), "conv_rowwin_kernel launch");
         if (st) return st;
     }
@@ -641,14 +658,14 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
 
 bool conv_rowwin_ok(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
                     int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
-    return rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW).ok;
+    return rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, true).ok;
 }
 
 int launch_conv_rowwin_f32(const float* x, const float* w, const float* bias, float* y,
                            int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW,
                            int64_t KH, int64_t KW, int64_t SH, int64_t SW, int64_t PH,
                            int64_t PW, bool two_level, hipStream_t stream) {
-    const RfPlan pl = rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    const RfPlan pl = rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, two_level);
     if (!pl.ok)
         return set_error(CDX_ERR_UNSUPPORTED, "conv row-window kernel: window does not fit in LDS");
     return launch_rowwin(x, w, bias, y, batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, pl,
@@ -672,7 +689,7 @@ int launch_conv_fwd_implicit_f32(const float* x, const float* w, const float* bi
     if (!conv_fwd_implicit_ok(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW))
         return set_error(CDX_ERR_UNSUPPORTED, "conv implicit forward: geometry beyond 32-bit indices");
     // the row-window form wherever its input window fits in LDS
-    const RfPlan pl = rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW);
+    const RfPlan pl = rowwin_plan(batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, false);
     if (pl.ok)
         return launch_rowwin(x, w, bias, y, batch, IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, pl,
                              false, stream);
