@@ -347,8 +347,9 @@ def bench_conv(steps, warmup, precision):
                       device="cuda")
     wino_ms, _ = time_launches(lambda: ops.conv2d_winograd(x, w, b, (1, 1), precision,
                                                            workspace=wws, out=y), steps, warmup)
-    # backward: data (stride 1: im2col of dY + GEMM with the flipped filter;
-    # or Winograd on the transposed conv), weight (im2col + GEMM dY col^T), bias
+    # backward: data (stride 1: the row-window implicit conv of dY with the
+    # flipped filter; or Winograd on the transposed conv), weight (the
+    # row-window implicit weight-gradient kernel), bias
     dy = torch.randn((32, 64, 56, 56), device="cuda", generator=g)
     dx = torch.empty_like(x)
     dw = torch.empty_like(w)
@@ -366,7 +367,7 @@ def bench_conv(steps, warmup, precision):
         ops.conv2d_backward_weight(dy, x, w.shape, (1, 1), (1, 1), precision, out=dw)
 
     # the routes launch_conv2d_backward_data_kernel takes (Auto): Winograd in
-    # the TF32 modes, the flipped-filter GEMM route in FP32
+    # the TF32 modes, the flipped-filter implicit conv in FP32
     bwd_data_auto = bwd_data if precision == cd.PREC_FP32 else bwd_data_wino
 
     def bwd():
@@ -387,6 +388,8 @@ def bench_conv(steps, warmup, precision):
     # buffer would be 1.26 GB)
     imp_ms, _ = time_launches(lambda: ops.conv2d_implicit(x, w, b, (1, 1), (1, 1), out=y),
                               steps, warmup)
+    imp_kernel_ms = per_launch_ms(steps, warmup,
+                                  lambda: ops.conv2d_implicit(x, w, b, (1, 1), (1, 1), out=y))
     w7 = torch.randn((64, 64, 7, 7), device="cuda", generator=g) * (2.0 / 3136) ** 0.5
     c7_ms, _ = time_launches(lambda: ops.conv2d_forward(x, w7, b, (1, 1), (3, 3), precision,
                                                         out=y), max(3, steps // 5), 3)
@@ -394,10 +397,12 @@ def bench_conv(steps, warmup, precision):
     return {"conv_ms": conv_ms, "conv_tflops": flops / (conv_ms * 1e-3) / 1e12,
             "gemm_ms": gemm_ms, "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12,
             "implicit_3x3_ms": imp_ms, "implicit_3x3_tflops": flops / (imp_ms * 1e-3) / 1e12,
+            "implicit_3x3_kernel_ms": imp_kernel_ms,
+            "implicit_3x3_kernel_tflops": flops / (imp_kernel_ms * 1e-3) / 1e12,
             "conv7x7_implicit_ms": c7_ms,
             "conv7x7_implicit_tflops": flops7 / (c7_ms * 1e-3) / 1e12,
             "bwd_ms": bwd_ms, "bwd_tflops": 2 * flops / (bwd_ms * 1e-3) / 1e12,
-            "bwd_data_im2col_ms": bd_ms, "bwd_data_winograd_ms": bdw_ms,
+            "bwd_data_implicit_ms": bd_ms, "bwd_data_winograd_ms": bdw_ms,
             "bwd_weight_ms": bw_ms,
             "im2col_ms": im_ms, "im2col_gbs": im2col_bytes / (im_ms * 1e-3) / 1e9,
             "winograd_ms": wino_ms, "winograd_tflops_equiv": flops / (wino_ms * 1e-3) / 1e12}

@@ -12,6 +12,10 @@
 // nothing of the Kc x B*S column matrix (1.26 GB for a 7x7 layer at
 // 32 x 64 x 56^2) is ever materialised.
 //
+// Two forms: the row-window form further down (the input window of a tile
+// staged in LDS per channel chunk; every layer whose window fits, and the
+// stride-1 backward-data route) and, for the rest, the gather form:
+//
 // Tile: 64 (OC) x 128 (output pixels n = b*S + s) x 16 (k); 4 waves of
 // 32 x 64, v_mfma_f32_16x16x4_f32 with the library's k-permutation (lane
 // group g feeds MFMA q with k = 4g + q, so each operand fragment is one

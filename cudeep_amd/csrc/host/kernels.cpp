@@ -223,7 +223,7 @@ void launch_conv2d_backward_data_kernel<float>(const float* grad_output, const f
     // in the TF32 modes only: the reference's backward data is GEMM +
     // col2im, and in FP32 the Winograd transforms' rounding (~10x that
     // route's error) would not stay within twice its error, so Auto keeps
-    // the GEMM route there.
+    // cdx_conv2d_backward_data_f32's flipped-filter implicit route there.
     const int prec = g_precision.load();
     const bool wino_ok = KH == 3 && KW == 3 && SH == 1 && SW == 1 && PH <= 2 && PW <= 2;
     const ConvAlgorithm algo = get_conv_algorithm();

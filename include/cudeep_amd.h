@@ -285,10 +285,13 @@ int cdx_col2im_f32(const float* col, float* grad_input,
 
 /* Conv backward data.  Stride 1 (with pad_h <= kernel_h - 1, pad_w <=
  * kernel_w - 1): the forward convolution of grad_out with the filter
- * channel-swapped and spatially reversed, padded kernel - 1 - pad (im2col of
- * grad_out + one long-K GEMM written straight to NCHW; in FP32 the GEMM
- * sums k in two levels, keeping the rounding chain no longer than the
- * reference's OC-term dot products + KH*KW-term col2im sums).  Other strides:
+ * channel-swapped and spatially reversed, padded kernel - 1 - pad: an
+ * implicit GEMM from per-tile input windows staged in LDS (no column buffer;
+ * workspace = the flipped filter; FP32 products in every precision mode), or
+ * where that window does not fit, im2col of grad_out + one long-K GEMM
+ * written straight to NCHW.  Both sum k in two levels, keeping the rounding
+ * chain no longer than the reference's OC-term dot products + KH*KW-term
+ * col2im sums.  Other strides:
  * grad_col = weight^T * grad_out[OC, B*S] (one GEMM with a transposed
  * operand, no weight transpose pass), then col2im.  Both compute the
  * reference's sums (src/kernels/conv_kernel.cu:417-478) in another order.

@@ -1,5 +1,5 @@
 """Seeded random sweep of conv backward weight and data (cdx_conv2d_backward_*
-through cudeep_amd.ops) and the im2col forward: mostly 3x3 stride-1 layers
+through cudeep_amd.ops), the im2col forward and the implicit forward: mostly 3x3 stride-1 layers
 with random widths (1 .. 130: one or two row segments of the row-window
 weight-gradient kernel), pads 0 .. 2, channel counts off the 16-channel and
 64-channel tile sizes, plus other kernel sizes and strides.  FP32 mode gates:
@@ -62,3 +62,9 @@ def test_conv_random_sweep(seed):
         y64 = oracle.conv2d_direct64(x, w, None, st, pd)
         ey_ref = oracle.rel_fro(oracle.conv2d_ref_im2col(x, w, None, st, pd), y64)
         assert oracle.rel_fro(y, y64) <= 2 * ey_ref + 2.0 ** -24, (g, "forward")
+        # implicit forward (the row-window kernel wherever its window fits)
+        b = normal(rng, (OC,), 0.1)
+        yi = host(o.conv2d_implicit(dev(x), dev(w), dev(b), st, pd))
+        yi64 = oracle.conv2d_direct64(x, w, b, st, pd)
+        ei_ref = oracle.rel_fro(oracle.conv2d_ref_implicit(x, w, b, st, pd), yi64)
+        assert oracle.rel_fro(yi, yi64) <= 2 * ei_ref + 2.0 ** -24, (g, "implicit forward")
