@@ -232,13 +232,13 @@ void conv_fwd_implicit_kernel(CfArgs p) {
 // ---------------------------------------------------------------------------
 // Row-window form: every kernel size and stride whose input window fits in LDS.
 //
-// A workgroup owns 64 output channels x 128 consecutive output pixels s of
-// one image.  Those pixels lie in at most R output rows starting at oh_lo,
-// which read the input rows ih = oh_lo*SH - PH + r, r < NR = (R-1)*SH + KH,
-// and the columns iw = c - PW, c < WP = (OW-1)*SW + KW.  Per chunk of ICT
-// input channels the workgroup stages that window of each channel into LDS
-// once, zero outside the image (the padding is materialised), so every
-// column-matrix element of the tile is one LDS read:
+// A workgroup owns 64 output channels x TN (80, 112 or 128) consecutive
+// output pixels s of one image.  Those pixels lie in at most R output rows
+// starting at oh_lo, which read the input rows ih = oh_lo*SH - PH + r,
+// r < NR = (R-1)*SH + KH, and the columns iw = c - PW, c < WP = (OW-1)*SW +
+// KW.  Per chunk of ICT input channels the workgroup stages that window of
+// each channel into LDS once, zero outside the image (the padding is
+// materialised), so every column-matrix element of the tile is one LDS read:
 //
 //   col[(ic, kh, kw), s] = win[ic - ic0][(oh(s) - oh_lo)*SH + kh][ow(s)*SW + kw]
 //                        = win_flat[base(s) + off(k)]
@@ -246,15 +246,17 @@ void conv_fwd_implicit_kernel(CfArgs p) {
 //   off(k)  = (ic - ic0)*NR*WP + kh*WP + kw               (table built once)
 //
 // An input element is fetched about NR / R times per 64 output channels
-// (C5: 6 rows staged per ~2.3 output rows) instead of KH*KW times, and the
-// k-loop has no bounds tests: 4 waves of 32 x 64, per 16 k one 16-byte read
-// of four tap offsets, 16 LDS reads of B and 32 v_mfma_f32_16x16x4_f32 (the
+// (C5 with 112-pixel tiles: 5 rows staged per 2 output rows) instead of
+// KH*KW times, and the k-loop has no bounds tests.  Each of the 4 waves
+// computes 16 output channels x the whole tile: per 16 k one 16-byte read of
+// four tap offsets, 4*FN LDS reads of B and 4*FN v_mfma_f32_16x16x4_f32 (the
 // library's k-permutation: lane group g feeds MFMA q with k = 4g + q).  The
-// filter comes straight from L2 into registers, prefetched two 16-k groups
-// ahead, so those loads are issued before the next chunk's staging loads
-// (vector loads retire in order).  A chunk holds ICT*KH*KW taps padded to a
-// multiple of 16; padded taps read a zero slot (never a staged value, so an
-// Inf input cannot turn a padded 0 * x into NaN).
+// filter comes straight from L2 into registers two 16-k groups ahead; the
+// next chunk's window is staged through registers a slice per group (both
+// described at the loop below).  A chunk holds ICT*KH*KW taps padded to a
+// multiple of 16; padded taps read a zero channel plane kept at the end of
+// each window buffer (never a staged value, so an Inf input cannot turn a
+// padded 0 * x into NaN).  rowwin_plan() picks TN and ICT.
 //
 // TWO_LEVEL: the FP32 backward-data route's two-level k sum -- each run of
 // 32 consecutive k is summed from zero, then added to the total.
