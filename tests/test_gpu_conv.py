@@ -164,6 +164,10 @@ IMPLICIT_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
     # row-window form: 5 chunks of 8 channels, a 7 x 104 window (3 of 4
     # positions per thread used), 200 taps per chunk padded to 208
     (2, 40, 12, 100, 24, 5, 5, 1, 1, 2, 2),
+    # enough workgroups that the plan takes 128- and 112-pixel tiles (the
+    # small layers above take 80)
+    (48, 8, 20, 32, 16, 3, 3, 1, 1, 1, 1),
+    (42, 8, 20, 32, 16, 3, 3, 1, 1, 1, 1),
 ]
 
 
@@ -322,6 +326,9 @@ BWD_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
     (1, 4, 5, 70, 8, 3, 3, 1, 1, 1, 1),
     (2, 16, 9, 61, 16, 3, 3, 1, 1, 1, 1),
     (1, 20, 6, 33, 70, 3, 3, 1, 1, 2, 2),
+    # backward data through 128- and 112-pixel row-window tiles
+    (48, 8, 20, 32, 16, 3, 3, 1, 1, 1, 1),
+    (42, 8, 20, 32, 16, 3, 3, 1, 1, 1, 1),
 ]
 
 
