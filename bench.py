@@ -529,8 +529,8 @@ def cpu_configs():
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not run)"}))
+        print(json.dumps({"error": "this build runs the hot path on one GPU; --gpus must be 1 "
+                                   "(no multi-GPU path is built or run)"}))
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
