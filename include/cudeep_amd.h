@@ -239,9 +239,10 @@ int cdx_conv2d_forward_f32(const float* input, const float* weight,
                            void* workspace, size_t workspace_bytes,
                            hipStream_t stream);
 
-/* NCHW conv forward as an implicit GEMM: the filter and the input window
- * are gathered into LDS per k-tile (FP32 products, fp32 accumulation), bias
- * added, no column buffer and no workspace.  Replaces
+/* NCHW conv forward as an implicit GEMM: each tile's input window is staged
+ * in LDS once per chunk of input channels (the taps become LDS offsets), or,
+ * where that window does not fit, gathered per k-tile; FP32 products, fp32
+ * accumulation, bias added, no column buffer and no workspace.  Replaces
  * implicit_gemm_conv2d_kernel (src/kernels/conv_kernel.cu:172-215).
  * Geometries needing 64-bit pixel or in-image indices return
  * CDX_ERR_UNSUPPORTED.  bias may be NULL. */
