@@ -480,8 +480,9 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //  * SkinnyM: M <= 64 with a long N (the conv GEMM, M = out channels):
 //    64x64x16, 4 waves of 16x64 (16-byte B fragment reads), XCD groups of
 //    one tile row: 64 x 100352 x 576 in 70-72 us, against 73-74 with 4
-//    waves of 32x32, 81 with 64x128 tiles of 8 waves of 16x64, 123-125 with
-//    64x128 / 64x256 tiles of 32x64 waves, 218 with BK = 32.
+//    waves of 32x32, 81 with 8 waves of 16x32 or 32x16, 81 with 64x128
+//    tiles of 8 waves of 16x64, 79-84 with 64x32 / 32x64 tiles, 123-125
+//    with 64x128 / 64x256 tiles of 32x64 waves, 218 with BK = 32.
 //  * NarrowN: N <= 16 (the MLP's 10-class layer): 32x16 tiles, 2 waves, and
 //    a deep k-tile (64): such products read A once and are bound by the
 //    latency of their k-loop, so each workgroup takes few, large k-steps and
