@@ -417,7 +417,9 @@ def _conv_geom(x_shape, w_shape, stride, padding):
 
 
 def conv2d_backward_data(grad_out, w, x_shape, stride=(1, 1), padding=(0, 0),
-                         precision=L.PREC_FP32, out=None):
+                         precision=L.PREC_FP32, out=None, workspace=None):
+    """`workspace` (at least conv2d_backward_data_workspace_bytes(...) bytes)
+    makes the call allocation-free."""
     _need(grad_out, "grad_output")
     _need(w, "weight")
     Bn, C, H, W, OC, KH, KW, OH, OW = _conv_geom(tuple(x_shape), tuple(w.shape), stride, padding)
@@ -426,10 +428,20 @@ def conv2d_backward_data(grad_out, w, x_shape, stride=(1, 1), padding=(0, 0),
         raise ValueError("conv2d_backward_data: bad grad_output / weight")
     if out is None:
         out = torch.empty((Bn, C, H, W), device=w.device, dtype=torch.float32)
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     L.call("cdx_conv2d_backward_data_f32", grad_out.data_ptr(), w.data_ptr(), out.data_ptr(),
            Bn, C, OC, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1], precision,
-           None, 0, _stream())
+           ws_ptr, ws_bytes, _stream())
     return out
+
+
+def conv2d_backward_data_workspace_bytes(x_shape, w_shape, stride=(1, 1),
+                                         padding=(0, 0)) -> int:
+    Bn, C, H, W, OC, KH, KW, _, _ = _conv_geom(tuple(x_shape), tuple(w_shape), stride, padding)
+    return int(L.lib().cdx_conv2d_backward_data_workspace_size(
+        Bn, C, OC, H, W, KH, KW, stride[0], stride[1], padding[0], padding[1]))
 
 
 def conv2d_backward_data_winograd(grad_out, w, x_shape, padding=(0, 0), precision=L.PREC_FP32,

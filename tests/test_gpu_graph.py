@@ -163,3 +163,68 @@ def test_captured_step_replays_match_eager(prec, forked):
         gW1 = (dZd.T @ Xd).float()
         assert (eager["gW1"] - gW1).norm() <= 1e-4 * gW1.norm()
     assert np.isfinite(eager["gX"].cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_step_graph_capture_replays(prec):
+    """A conv layer's forward (implicit route, no workspace) and backward
+    (data: the flipped-filter row-window kernel, FP32 products in both
+    precision modes; weight: implicit kernel with its split partials; bias) on caller
+    workspaces, captured once and replayed with new inputs written eagerly
+    between replays: every replay equals the eager step bit for bit, and the
+    eager gradients pass fp64 checks."""
+    import torch
+    import torch.nn.functional as F
+    ops = _ops()
+    g = torch.Generator(device="cuda").manual_seed(11)
+    B, C, H, W, OC = 4, 24, 20, 22, 32
+    x = torch.randn((B, C, H, W), device="cuda", generator=g)
+    w = torch.randn((OC, C, 3, 3), device="cuda", generator=g) * 0.1
+    b = torch.randn((OC,), device="cuda", generator=g) * 0.1
+    dy = torch.randn((B, OC, H, W), device="cuda", generator=g)
+    st, pd = (1, 1), (1, 1)
+    ws_d = torch.empty(ops.conv2d_backward_data_workspace_bytes(x.shape, w.shape, st, pd) // 4 + 1,
+                       device="cuda")
+    ws_w = torch.empty(ops.conv2d_backward_weight_workspace_bytes(x.shape, w.shape, st, pd) // 4 + 1,
+                       device="cuda")
+    outs = {"y": torch.empty((B, OC, H, W), device="cuda"), "dx": torch.empty_like(x),
+            "dw": torch.empty_like(w), "db": torch.empty_like(b)}
+
+    def step(o):
+        ops.conv2d_implicit(x, w, b, st, pd, out=o["y"])
+        ops.conv2d_backward_data(dy, w, x.shape, st, pd, prec, out=o["dx"], workspace=ws_d)
+        ops.conv2d_backward_weight(dy, x, w.shape, st, pd, prec, out=o["dw"], workspace=ws_w)
+        ops.conv2d_backward_bias(dy, out=o["db"])
+
+    say("conv graph capture", "prec", prec)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(outs)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(outs)
+    torch.cuda.synchronize()
+    eager = {k: torch.empty_like(v) for k, v in outs.items()}
+    for r in range(3):
+        x.normal_(generator=g)
+        dy.normal_(generator=g)
+        for v in outs.values():
+            v.fill_(float("nan"))
+        torch.cuda.synchronize()
+        say("conv graph replay", r)
+        graph.replay()
+        torch.cuda.synchronize()
+        step(eager)
+        torch.cuda.synchronize()
+        for k in outs:
+            assert torch.equal(outs[k], eager[k]), (r, k)
+        xd, wd, dyd = x.double().cpu(), w.double().cpu(), dy.double().cpu()
+        y64 = F.conv2d(xd, wd, b.double().cpu(), padding=1)
+        dx64 = F.conv_transpose2d(dyd, wd, padding=1)
+        dw64 = F.conv2d(xd.transpose(0, 1), dyd.transpose(0, 1), padding=1).transpose(0, 1)
+        tol = 1e-5 if prec == 0 else 1e-3
+        for got, want in ((eager["y"], y64), (eager["dx"], dx64), (eager["dw"], dw64)):
+            got = got.double().cpu()
+            assert (got - want).norm() <= tol * want.norm()
