@@ -127,7 +127,9 @@ int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStrea
 // cannot fill the GPU (fewer than 128 tiles) and K is long; aim at ~768
 // workgroups with at least min_k k per slice.  FP32 (BK 16) uses min_k 256
 // (measured on the MLP / conv weight gradients: 10x256x8192 best at 32
-// slices, 256x784x8192 at ~16, 64x576x100352 at ~64-128); the bf16x3 kernels
+// slices; 256x784x8192 at ~16 on 64x64 slices and at the 29 this gives on
+// the 128x64 slices it takes now -- 15 / 20 slices: 52.5-55.9 against 48
+// us; 64x576x100352 at ~64-128); the bf16x3 kernels
 // (BK 32-64, a longer pipeline fill per slice) 1024 (256x784x8192: 8 slices
 // 47.6 us NN / 35.2 NT against 55.9 / 42.3 at 15).  Returns the slice count
 // and sets *k_chunk (a multiple of bk).
