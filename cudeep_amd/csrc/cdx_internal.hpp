@@ -108,8 +108,11 @@ int launch_gemm_bf16x3(const GemmArgs& g, int terms, hipStream_t stream);
 // 16-bit operands (in_dtype CDX_DTYPE_F16 or CDX_DTYPE_BF16), fp32 accumulation and C.
 int launch_gemm_16(const GemmArgs& g, int in_dtype, hipStream_t stream);
 // GEMMs with K <= 16 (narrow_kind 1) or N <= 16 (2), plain output map, no
-// batch / ones column (0: use the tiled kernels); no workspace.
+// batch / ones column, no workspace; or M <= 16 with op(B) = B and K >= 1024
+// (3, ones column allowed: split-K partials of skinny_m_workspace bytes).
+// 0: use the tiled kernels.
 int narrow_kind(const GemmArgs& g);
+size_t skinny_m_workspace(const GemmArgs& g);
 // The FP32 GEMM's 128 x 112 tiles apply (widths a multiple of 112 but not
 // of 64, enough rows): faster than the split-precision kernels there.
 bool f32_takes_w112(const GemmArgs& g);

@@ -547,7 +547,7 @@ bool f32_takes_w112(const GemmArgs& g) {
 }
 
 size_t gemm_f32_workspace(const GemmArgs& g) {
-    if (narrow_kind(g)) return 0;
+    if (const int nk = narrow_kind(g)) return nk == 3 ? skinny_m_workspace(g) : 0;
     bool blocked;
     const F32Cfg c = choose_f32(g, blocked);
     if (blocked) return 0;

@@ -18,11 +18,21 @@
 //    k-contiguous operand is one 16-byte load per 16 k).  The four partial
 //    16 x 16 tiles are summed in LDS in wave order (deterministic) and
 //    written through the epilogue.  Traffic: op(A) read once, C written once.
+//  * skinny M (M <= 16, op(B) = B, long K: the MLP's 10-wide weight
+//    gradient dW2 = dY2^T H, 10 x 256 x 8192, its bias gradient as the ones
+//    column): K in slices of >= 128 rows; a workgroup owns 64 columns of one
+//    slice, each thread 4 columns (one 16-byte op(B) load per row) of 8 rows
+//    per step, with 16 x 4 fp32 FMA chains over its rows; the 4 lane groups
+//    of a wave are summed by shuffles and the 4 waves in LDS, in a fixed
+//    order, into a [slices][M][N] partial.  A second kernel sums the slices
+//    (4 waves per output row and 64 columns, slices dealt round-robin, the
+//    waves combined in order) through the epilogue.  Traffic: op(B) read
+//    once, the partials (<= 16 MB) written and read once.
 //
-// Both compute fp32 products in every precision mode (exact products: inside
+// All compute fp32 products in every precision mode (exact products: inside
 // the TF32-mode error bar, as for the other FP32-routed shapes).  Plain
-// row-major output map only, no batch, no ones column; everything else goes
-// to the tiled kernels.
+// row-major output map only, no batch, no ones column (skinny M: with the
+// ones column); everything else goes to the tiled kernels.
 #include <type_traits>
 
 #include "cdx_internal.hpp"
@@ -235,6 +245,147 @@ void gemm_narrow_n_kernel(NarrowArgs p, int64_t kq) {
     }
 }
 
+// ---- skinny M ----
+constexpr int SM_COLS = 64;          // columns per workgroup
+constexpr int SM_KC_MIN = 128;       // k rows per slice, at least (16 row groups x 8)
+constexpr int64_t SM_SLICES_MAX = 256;
+constexpr int64_t SM_PART_MAX = int64_t(4) << 20;   // partial floats, at most (16 MB)
+
+struct SkinnyPlan { int64_t kc; int slices; };
+
+// g.N counts the ones column when there is one.
+SkinnyPlan skinny_plan(const GemmArgs& g) {
+    int64_t smax = SM_PART_MAX / (g.M * g.N);
+    if (smax > SM_SLICES_MAX) smax = SM_SLICES_MAX;
+    if (smax < 1) smax = 1;
+    const int64_t kc = ceil_div(ceil_div(g.K, smax), SM_KC_MIN) * SM_KC_MIN;
+    return {kc, (int)ceil_div(g.K, kc)};
+}
+
+// Grid (column blocks, slices).  Thread: column quad c4 = tid % 16, row
+// group rg = tid / 16 (a 16-lane DPP row); it takes rows kb + rg + 16 u +
+// 128 j of its slice (k ascending) and op(B)'s columns n0 .. n0+3 (nb real
+// columns; column ones_col, if any, is all ones).  op(A) costs one load per
+// row: lane c4 of the row group holds element (min(c4, M-1), k) and each
+// element reaches the whole row group by a DPP row broadcast (16 uniform
+// loads per row per lane before: 12.7 us for C4's dW2 partials).  Rows past
+// the slice contribute exact zeros (both factors zeroed, so no Inf * 0).
+constexpr int SM_U = 8;   // rows per thread in flight
+
+// acc[m][c] += op(A)(m, k) * b[c] for m = M .. 15, op(A)(m, k) taken from
+// lane m of this lane's 16-lane row (DPP row_newbcast:m, control 0x150 + m).
+template <int M>
+__device__ __forceinline__ void skinny_fma_rows(float (&acc)[16][4], int a_bits, const float (&b)[4]) {
+    if constexpr (M < 16) {
+        const float am = __int_as_float(__builtin_amdgcn_update_dpp(0, a_bits, 0x150 + M, 0xf, 0xf, false));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[M][c] = fmaf(am, b[c], acc[M][c]);
+        skinny_fma_rows<M + 1>(acc, a_bits, b);
+    }
+}
+template <int OPA>
+__global__ __launch_bounds__(256)
+void gemm_skinny_m_partial_kernel(NarrowArgs p, int64_t nb, int64_t ones_col, int64_t kc,
+                                  float* __restrict__ P) {
+    __shared__ float red[4][16][SM_COLS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c4 = tid & 15, rg = tid >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * SM_COLS + 4 * c4;
+    const int64_t kb = (int64_t)blockIdx.y * kc;
+    const int64_t ke = kb + kc < p.K ? kb + kc : p.K;
+    const int64_t ma = c4 < p.M ? c4 : p.M - 1;
+    const bool whole = p.vec_b && n0 + 3 < nb;
+    float acc[16][4];
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
+    for (int64_t k0 = kb + rg; k0 < ke; k0 += 16 * SM_U) {
+        float a[SM_U], b[SM_U][4];
+#pragma unroll
+        for (int u = 0; u < SM_U; ++u) {
+            const int64_t k = k0 + 16 * u;
+            const bool ok = k < ke;
+            const int64_t kk = ok ? k : kb;
+            if (whole) {
+                const float4 v = *reinterpret_cast<const float4*>(p.B + kk * p.ldb + n0);
+                b[u][0] = v.x; b[u][1] = v.y; b[u][2] = v.z; b[u][3] = v.w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int64_t n = n0 + c;
+                    b[u][c] = n < nb ? p.B[kk * p.ldb + n] : (n == ones_col ? 1.0f : 0.0f);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) b[u][c] = ok ? b[u][c] : 0.0f;
+            const float av = OPA == CDX_OP_N ? p.A[ma * p.lda + kk] : p.A[kk * p.lda + ma];
+            a[u] = ok ? av : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < SM_U; ++u) skinny_fma_rows<0>(acc, __float_as_int(a[u]), b[u]);
+    }
+    // the wave's 4 row groups (lanes 16 apart hold the same columns)
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float v = acc[m][c];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[m][c] = v;
+        }
+    if (lane < 16) {
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+            if (m < p.M) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) red[wave][m][4 * lane + c] = acc[m][c];
+            }
+    }
+    __syncthreads();
+    float* ps = P + (int64_t)blockIdx.y * p.M * p.N;
+    for (int i = tid; i < p.M * SM_COLS; i += 256) {
+        const int m = i / SM_COLS, col = i % SM_COLS;
+        const int64_t n = (int64_t)blockIdx.x * SM_COLS + col;
+        if (n < p.N)
+            ps[m * p.N + n] = ((red[0][m][col] + red[1][m][col]) + red[2][m][col]) + red[3][m][col];
+    }
+}
+
+// Grid (column blocks, M): wave w sums slices w, w + 4, ... of 64 columns of
+// one row (16 loads in flight), the 4 waves are combined in order and the
+// result goes through the epilogue.
+__global__ __launch_bounds__(256)
+void gemm_skinny_m_reduce_kernel(const float* __restrict__ P, int slices, EpiArgs e) {
+    __shared__ float red[4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t m = blockIdx.y, n = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t MN = e.M * e.N;
+    const float* q = P + m * e.N + (n < e.N ? n : 0);
+    float v = 0.0f;
+    int s = wave;
+    for (; s + 60 < slices; s += 64) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) t[u] = q[(int64_t)(s + 4 * u) * MN];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v += t[u];
+    }
+    for (; s + 12 < slices; s += 16) {
+        float t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = q[(int64_t)(s + 4 * u) * MN];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v += t[u];
+    }
+    for (; s < slices; s += 4) v += q[(int64_t)s * MN];
+    red[wave][lane] = v;
+    __syncthreads();
+    if (wave == 0 && n < e.N)
+        store_one(e, m, n, ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]);
+}
+
 NarrowArgs args_of(const GemmArgs& g) {
     NarrowArgs p{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
                  g.M, g.N, g.K, g.lda, g.ldb, g.ldc, g.bias_mode, g.epilogue, g.aux, g.ldaux,
@@ -247,15 +398,56 @@ NarrowArgs args_of(const GemmArgs& g) {
 }  // namespace
 
 int narrow_kind(const GemmArgs& g) {
-    if (g.batch != 1 || g.n_split > 0 || g.colsum || g.ones_col >= 0 || g.M <= 0 || g.N <= 0)
-        return 0;
+    if (g.batch != 1 || g.n_split > 0 || g.M <= 0 || g.N <= 0) return 0;
+    if (g.M <= 16 && g.opB == CDX_OP_N && g.K >= 1024 && g.N <= 4097) return 3;   // skinny M
+    if (g.colsum || g.ones_col >= 0) return 0;
     if (g.K >= 1 && g.K <= 16) return 1;                    // tiny K
     if (g.N <= 16 && g.K >= 64 && g.M >= 64) return 2;      // narrow N
     return 0;
 }
 
+size_t skinny_m_workspace(const GemmArgs& g) {
+    return (size_t)skinny_plan(g).slices * (size_t)g.M * (size_t)g.N * sizeof(float);
+}
+
+static int launch_skinny_m(const GemmArgs& g, const NarrowArgs& p, hipStream_t stream) {
+    const SkinnyPlan sp = skinny_plan(g);
+    const int64_t nb = g.ones_col >= 0 ? g.ones_col : g.N;
+    const dim3 grid1((unsigned)ceil_div(g.N, SM_COLS), (unsigned)sp.slices);
+    const dim3 grid2((unsigned)ceil_div(g.N, 64), (unsigned)g.M);
+    const size_t bytes = skinny_m_workspace(g);
+    float* part = static_cast<float*>(g.ws);
+    int st = CDX_OK;
+    if (part) {
+        if (g.ws_bytes < bytes) return set_error(CDX_ERR_WORKSPACE, "gemm: workspace too small");
+    } else {
+        st = stream_alloc(reinterpret_cast<void**>(&part), bytes, stream, "gemm skinny-M scratch");
+        if (st) return st;
+    }
+    if (g.opA == CDX_OP_N)
+        hipLaunchKernelGGL(gemm_skinny_m_partial_kernel<CDX_OP_N>, grid1, dim3(256), 0, stream, p,
+                           nb, g.ones_col, sp.kc, part);
+    else
+        hipLaunchKernelGGL(gemm_skinny_m_partial_kernel<CDX_OP_T>, grid1, dim3(256), 0, stream, p,
+                           nb, g.ones_col, sp.kc, part);
+    st = hip_error(hipGetLastError(), "gemm_skinny_m_partial_kernel launch");
+    if (!st) {
+        const EpiArgs e{g.C, g.ldc, g.M, g.N, g.n_split, g.ldc_split, g.bias, g.bias_mode,
+                        g.epilogue, g.aux, g.ldaux, g.colsum, g.ones_col};
+        hipLaunchKernelGGL(gemm_skinny_m_reduce_kernel, grid2, dim3(256), 0, stream, part,
+                           sp.slices, e);
+        st = hip_error(hipGetLastError(), "gemm_skinny_m_reduce_kernel launch");
+    }
+    if (!g.ws) {
+        const int st2 = stream_free(part, stream, "gemm skinny-M scratch");
+        if (!st) st = st2;
+    }
+    return st;
+}
+
 int launch_gemm_narrow(const GemmArgs& g, hipStream_t stream) {
     const NarrowArgs p = args_of(g);
+    if (narrow_kind(g) == 3) return launch_skinny_m(g, p, stream);
     if (narrow_kind(g) == 1) {
         const int64_t threads = ceil_div(g.M, TK_ROWS) * ceil_div(g.N, 4);
         const int64_t blocks = ceil_div(threads, 256);

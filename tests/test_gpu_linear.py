@@ -260,6 +260,42 @@ def test_weight_grad_with_fused_bias_grad(M, N, K, prec):
         assert np.array_equal(plain.view(np.uint32), dW.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K,transA", [(1, 100, 5000, True), (16, 4096, 1024, False),
+                                          (7, 33, 2049, True), (12, 520, 70000, True),
+                                          (16, 64, 1024, False), (10, 257, 8191, True)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_skinny_m_long_k(M, N, K, transA, prec):
+    """M <= 16 with K >= 1024 (the 10-wide layer's weight-gradient shape): the
+    split-K FMA kernel and its slice reduction -- ragged and unaligned
+    widths, op(A) either way, the slice cap (K = 70000), with the ones
+    column (bias gradient) on a caller workspace, and with a bias + ReLU
+    epilogue applied by the reduction."""
+    import torch
+    import cudeep_amd as cd
+    rng = np.random.default_rng(131 * M + N + K)
+    A = normal(rng, (K, M) if transA else (M, K))
+    B = normal(rng, (K, N))
+    bias = normal(rng, (N,))
+    say("skinny M", M, N, K, transA, prec)
+    want = oracle.dgemm(A, B, transA=transA)
+    e_ref = oracle.rel_fro(oracle.sgemm_seqfma(A, B, transA=transA), want)
+    nbytes = ops().gemm_workspace_bytes(M, N, K, precision=prec, transA=transA, colsum=True)
+    assert nbytes > 0
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
+    cs = torch.full((M,), float("nan"), device="cuda")
+    C = host(ops().gemm(dev(A), dev(B), transA=transA, precision=prec, colsum=cs, workspace=ws))
+    assert oracle.rel_fro(C, want) <= 2 * e_ref + 2.0 ** -24
+    opA = A.T if transA else A                       # [M, K]
+    db64 = opA.astype(np.float64).sum(1)
+    eb_ref = oracle.rel_fro(oracle.colsum(np.ascontiguousarray(opA.T)), db64)
+    assert oracle.rel_fro(host(cs), db64) <= 2 * eb_ref + 2.0 ** -24
+    Y = host(ops().gemm(dev(A), dev(B), transA=transA, precision=prec, bias=dev(bias),
+                        bias_mode=cd.BIAS_COL, epilogue=cd.EPI_RELU))
+    ref = np.maximum(want + bias, 0.0)
+    # ReLU is 1-Lipschitz: the error stays within the product's (+ the bias add's rounding)
+    assert np.linalg.norm(Y - ref) <= (2 * e_ref + 2.0 ** -23) * np.linalg.norm(want + bias)
+
+
 def test_fused_bias_grad_k_zero_and_empty_columns():
     """K = 0: dW = 0 and db = 0; N = 0: only db."""
     import torch
