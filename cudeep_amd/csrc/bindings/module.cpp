@@ -4,9 +4,11 @@
 // sum_reduce_rows, sum, relu / gelu / sigmoid / silu / activation_backward, Stream / Event /
 // MemoryPool, device_info), with the same names, argument names and
 // defaults, plus the entry points this build adds: linear_forward (one
-// fused GEMM for x W^T + b with an activation), matmul_ex (transposed
-// operands), conv2d_backward_bias (GPU bias gradient) and the matmul
-// precision switch.  Errors surface as RuntimeError (std::runtime_error).
+// fused GEMM for x W^T + b with an activation), linear_weight_grad /
+// linear_input_grad (a Linear layer's backward GEMMs with the bias gradient
+// and the producer's activation derivative in their epilogues), matmul_ex
+// (transposed operands), conv2d_backward_bias (GPU bias gradient) and the
+// matmul precision switch.  Errors surface as RuntimeError (std::runtime_error).
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -336,6 +338,38 @@ PYBIND11_MODULE(_cudeep_core, m) {
               return py::make_tuple(gw, with_bias ? py::cast(gb) : py::none());
           },
           py::arg("dz"), py::arg("x"), py::arg("with_bias") = true);
+
+    m.def("linear_input_grad",
+          [](const Tensor& dz, const Tensor& weight, py::object aux_obj,
+             const std::string& activation) {
+              Tensor Z = ensure_contiguous(dz), W = ensure_contiguous(weight);
+              if (Z.ndim() != 2 || W.ndim() != 2 || Z.shape()[1] != W.shape()[0])
+                  throw std::runtime_error(
+                      "linear_input_grad: dz [N, out] and weight [out, in] required");
+              require_f32(Z, "linear_input_grad");
+              require_f32(W, "linear_input_grad");
+              const kernels::GemmEpilogue act = parse_epi(activation);
+              const int64_t batch = Z.shape()[0], out_f = Z.shape()[1], in_f = W.shape()[1];
+              Tensor A;
+              const float* aptr = nullptr;
+              if (act != kernels::GemmEpilogue::None) {
+                  if (aux_obj.is_none())
+                      throw std::runtime_error("linear_input_grad: an activation needs aux");
+                  A = ensure_contiguous(aux_obj.cast<Tensor>());
+                  require_f32(A, "linear_input_grad");
+                  if (A.ndim() != 2 || A.shape()[0] != batch || A.shape()[1] != in_f)
+                      throw std::runtime_error("linear_input_grad: aux must be [N, in]");
+                  aptr = static_cast<const float*>(A.data());
+              }
+              Tensor gx({batch, in_f}, DType::Float32);
+              if (batch * in_f == 0) return gx;
+              kernels::launch_linear_input_grad(
+                  static_cast<const float*>(Z.data()), static_cast<const float*>(W.data()), aptr,
+                  static_cast<float*>(gx.data()), batch, out_f, in_f, act, Z.stream());
+              return gx;
+          },
+          py::arg("dz"), py::arg("weight"), py::arg("aux") = py::none(),
+          py::arg("activation") = "none");
 
     m.def("linear_forward",
           [](const Tensor& x, const Tensor& weight, py::object bias_obj,

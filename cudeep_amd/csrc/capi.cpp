@@ -143,11 +143,15 @@ size_t col_bytes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH, 
 // Winograd route: a layer whose column buffer would exceed 4 MiB runs the
 // implicit GEMM (no buffer) unless it is a 3x3 stride-1 layer with >= 16
 // output pixels per image (the Winograd shape, which keeps the im2col route
-// here when it is not sent to Winograd).
+// here when it is not sent to Winograd).  The reference's naive-kernel
+// shapes (K_col < 9 or fewer than 4 output pixels per image, checked before
+// the implicit route at conv_kernel.cu:250) take the im2col route, which
+// computes the same sums.
 bool forward_takes_implicit(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH,
                             int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
     const int64_t OH = conv_out(IH, KH, SH, PH), OW = conv_out(IW, KW, SW, PW);
     if (KH == 3 && KW == 3 && SH == 1 && SW == 1 && OH * OW >= 16) return false;
+    if (IC * KH * KW < 9 || OH * OW < 4) return false;
     return col_bytes(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW) > ((size_t)4 << 20) &&
            cdx::conv_fwd_implicit_ok(batch, IC, IH, IW, KH, KW, SH, SW, PH, PW);
 }

@@ -53,21 +53,29 @@ int act_code(ActivationType a) {
 // Scratch for one launch.  On the null stream it comes from the runtime's
 // exact-size MemoryPool cache -- after the first call of a size a map lookup,
 // where the stream-ordered pool costs tens of microseconds of host time for
-// a large block -- and is handed back when the launch is enqueued: the next
-// user of the block is ordered after it by the null stream.  On any other
-// stream the C-ABI allocates stream-ordered itself (a cached block could
-// otherwise reach a concurrent stream while still in use).
+// a large block -- and is handed back when the launch is enqueued, behind an
+// event recorded after the launch: the pool gives the block out again only
+// once that event has completed, so no later user, on whatever stream,
+// overwrites it while the kernel still runs.  On any other stream the C-ABI
+// allocates stream-ordered itself.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
-    Workspace(size_t n, hipStream_t s) {
+    hipStream_t stream = nullptr;
+    Workspace(size_t n, hipStream_t s) : stream(s) {
         if (n > 0 && s == nullptr) {
             ptr = device_malloc(n);
             bytes = n;
         }
     }
     ~Workspace() {
-        if (ptr) device_free(ptr);
+        if (!ptr) return;
+        try {
+            MemoryPool::instance().deallocate_after(ptr, stream);
+        } catch (...) {
+            // no event could be recorded: the block stays allocated (never
+            // handed out again) rather than throwing from a destructor
+        }
     }
     Workspace(const Workspace&) = delete;
     Workspace& operator=(const Workspace&) = delete;
@@ -115,6 +123,29 @@ void launch_linear_weight_grad(const float* dz, const float* x, float* grad_w, f
     CUDEEP_CHECK_CDX(cdx_gemm_fused(prec, CDX_OP_T, CDX_OP_N, out_features, in_features, batch,
                                     dz, ldz, x, ldx, grad_w, in_features, nullptr, CDX_BIAS_NONE,
                                     CDX_EPI_NONE, nullptr, 0, grad_b, ws.ptr, ws.bytes, stream));
+}
+
+void launch_linear_input_grad(const float* dz, const float* weight, const float* aux,
+                              float* grad_x, int64_t batch, int64_t out_features,
+                              int64_t in_features, GemmEpilogue act, hipStream_t stream,
+                              int precision) {
+    const int prec = precision >= 0 ? precision : g_precision.load();
+    const int64_t ldz = out_features > 1 ? out_features : 1, ldw = in_features > 1 ? in_features : 1;
+    int epi = CDX_EPI_NONE;
+    switch (act) {
+        case GemmEpilogue::None: break;
+        case GemmEpilogue::ReLU: epi = CDX_EPI_BWD_RELU; break;
+        case GemmEpilogue::GELU: epi = CDX_EPI_BWD_GELU; break;
+        case GemmEpilogue::SiLU: epi = CDX_EPI_BWD_SILU; break;
+        case GemmEpilogue::Sigmoid: epi = CDX_EPI_BWD_SIGMOID; break;
+    }
+    Workspace ws(cdx_gemm_fused_workspace_size(prec, CDX_OP_N, CDX_OP_N, batch, in_features,
+                                               out_features, 0),
+                 stream);
+    CUDEEP_CHECK_CDX(cdx_gemm_fused(prec, CDX_OP_N, CDX_OP_N, batch, in_features, out_features,
+                                    dz, ldz, weight, ldw, grad_x, in_features, nullptr,
+                                    CDX_BIAS_NONE, epi, epi == CDX_EPI_NONE ? nullptr : aux,
+                                    in_features, nullptr, ws.ptr, ws.bytes, stream));
 }
 
 void launch_matmul_dgemm_ex(const double* A, const double* B, double* C, int64_t M, int64_t N,

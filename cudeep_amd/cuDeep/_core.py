@@ -12,7 +12,7 @@ try:
         MemoryPool,
         relu, gelu, sigmoid, silu, tanh_act, leaky_relu, activation_backward,
         broadcast_add, sum_reduce_rows, sum,
-        matmul_ex, linear_forward, linear_weight_grad,
+        matmul_ex, linear_forward, linear_weight_grad, linear_input_grad,
         conv2d_forward, conv2d_backward_data, conv2d_backward_weight, conv2d_backward_bias,
         set_matmul_precision, get_matmul_precision, set_conv_algorithm, get_conv_algorithm,
         device_info,

@@ -17,6 +17,17 @@ consumers have contributed, from a gradient buffer private to this pass.
 Leaf tensors (no node) that require gradients accumulate into ``.grad``
 across passes; a recorded result's ``.grad`` is set to the total gradient
 it received in the latest pass.
+
+Activation-backward fusion.  During a pass, ``sole_consumer(node)`` tells a
+backward whether it is the only recorded consumer feeding gradient into
+``node``.  A Linear whose input came out of a ReLU / GELU with no other
+consumer then forms its input gradient with that activation's derivative
+already applied (in its GEMM epilogue) and the activation's backward passes
+it through: one elementwise launch less per activation, the same bits for
+every parameter and leaf gradient.  The activation's output then records,
+as its ``.grad``, that gradient with the derivative applied (the gradient of
+the activation's input).  ``set_fuse_activation_backward(False)`` turns the
+fusion off, for callers that read activations' ``.grad``.
 """
 from __future__ import annotations
 
@@ -44,6 +55,27 @@ class no_grad:
 
 def is_grad_enabled() -> bool:
     return _GradMode.enabled
+
+
+_fuse_activation_backward = True
+_pass_counts = []     # consumer counts of the backward passes running (innermost last)
+
+
+def set_fuse_activation_backward(enabled: bool) -> None:
+    """Whether a Linear applies its input's activation derivative in its
+    input-gradient GEMM (process-wide, default on)."""
+    global _fuse_activation_backward
+    _fuse_activation_backward = bool(enabled)
+
+
+def fuse_activation_backward_enabled() -> bool:
+    return _fuse_activation_backward
+
+
+def sole_consumer(node) -> bool:
+    """True inside a backward pass when exactly one recorded consumer feeds
+    gradient into ``node`` in that pass."""
+    return bool(_pass_counts) and _pass_counts[-1].get(node) == 1
 
 
 class Context:
@@ -150,6 +182,14 @@ def backward(root, grad_output=None):
     if start is None:
         return
     pending = _consumer_counts(start)
+    _pass_counts.append(dict(pending))
+    try:
+        _run_pass(root, start, grad_output, pending)
+    finally:
+        _pass_counts.pop()
+
+
+def _run_pass(root, start, grad_output, pending):
     grads = {start: grad_output}       # gradient buffer per node, this pass only
     outputs = {start: root}            # node -> a tensor it produced (for .grad)
     ready = deque([start])

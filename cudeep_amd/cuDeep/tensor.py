@@ -36,13 +36,19 @@ from ._core import (
     conv2d_forward as _conv2d_forward,
     gelu as _gelu,
     linear_forward as _linear_forward,
+    linear_input_grad as _linear_input_grad,
     linear_weight_grad as _linear_weight_grad,
     matmul_ex as _matmul_ex,
     relu as _relu,
     sum as _sum,
     sum_reduce_rows as _sum_reduce_rows,
 )
-from .autograd import Function, backward as _run_backward
+from .autograd import (
+    Function,
+    backward as _run_backward,
+    fuse_activation_backward_enabled as _fusion_on,
+    sole_consumer as _sole_consumer,
+)
 
 
 def _np_dtype(dtype) -> type:
@@ -70,13 +76,18 @@ def _to_raw(data, dtype) -> _RawTensor:
 class Tensor:
     """GPU tensor with reverse-mode autograd."""
 
-    __slots__ = ("_data", "grad", "requires_grad", "_grad_fn")
+    # _act_applied: on a gradient, the Context of the activation whose
+    # derivative the gradient already carries (set by the consumer that
+    # fused it into its GEMM epilogue; that activation's backward then
+    # passes the gradient through).
+    __slots__ = ("_data", "grad", "requires_grad", "_grad_fn", "_act_applied")
 
     def __init__(self, data, requires_grad=False, dtype=None):
         self._data = _to_raw(data, dtype)
         self.grad: Optional[Tensor] = None
         self.requires_grad = bool(requires_grad)
         self._grad_fn = None
+        self._act_applied = None
 
     @classmethod
     def _wrap(cls, raw, requires_grad=False) -> "Tensor":
@@ -86,6 +97,7 @@ class Tensor:
         t.grad = None
         t.requires_grad = requires_grad
         t._grad_fn = None
+        t._act_applied = None
         return t
 
     def _plus(self, other: "Tensor") -> "Tensor":
@@ -361,7 +373,8 @@ class SumOp(Function):
 
 
 class _ActivationOp(Function):
-    """y = act(x) elementwise; backward from the saved input."""
+    """y = act(x) elementwise; backward from the saved input (none when the
+    consumer of y already applied act'(x) in its GEMM epilogue)."""
 
     NAME = ""
     FORWARD = None
@@ -369,10 +382,13 @@ class _ActivationOp(Function):
     @classmethod
     def forward(cls, ctx, a):
         ctx.save_for_backward(a)
+        ctx.activation, ctx.aux = cls.NAME, a._data
         return Tensor._wrap(cls.FORWARD(a._data))
 
     @classmethod
     def backward(cls, ctx, g):
+        if g._act_applied is ctx:
+            return g
         (a,) = ctx.saved_tensors
         return Tensor._wrap(_activation_backward(g._data, a._data, cls.NAME))
 
@@ -401,24 +417,56 @@ class BroadcastAddOp(Function):
                 Tensor._wrap(_sum_reduce_rows(g._data)) if need_r else None)
 
 
+def _fusable_activation(x: Tensor):
+    """The Context of the activation that produced x, when a consumer GEMM
+    can apply its derivative in the epilogue: x is the direct output of a
+    recorded float32 ReLU / GELU (an activation op, or a Linear with that
+    activation fused) and the caller is its only consumer in this backward
+    pass (GELU's derivative must not multiply a gradient twice, and a sum of
+    contributions is formed after the consumers run).  Its ``aux`` is what
+    the derivative reads (the input of the activation; for ReLU the output
+    serves as well, since y > 0 exactly where x > 0)."""
+    node = x._grad_fn
+    if node is None or not _fusion_on() or not _sole_consumer(node):
+        return None
+    ctx = node.ctx
+    if getattr(ctx, "activation", "none") not in ("relu", "gelu"):
+        return None
+    aux = getattr(ctx, "aux", None)
+    if aux is None or aux.dtype() != DType.float32 or x.dtype() != DType.float32:
+        return None
+    return ctx
+
+
 class LinearOp(Function):
     """y = act(x W^T + b) as one fused GEMM (bias and ReLU / GELU in the
     epilogue).  Backward: dZ = act'(...) dY, dX = dZ W (NN GEMM), and
     dW = dZ^T x with db = column sums of dZ from the same launch (a column of
     ones appended to x).  For ReLU the mask is taken from y (y > 0 exactly
     where x W^T + b > 0); GELU keeps the pre-activation, so its activation is
-    a separate launch when recorded."""
+    a separate launch when recorded.
+
+    When x itself came out of a recorded ReLU / GELU (a Linear with that
+    activation, or the activation op), dX is formed with that activation's
+    derivative in the GEMM epilogue -- dX = act'(aux) (.) (dZ W) -- and
+    marked, so the producer's backward skips its own activation-backward
+    launch (the reference runs it as a kernel of its own,
+    python/cuDeep/tensor.py:430-443 then activation_kernel.cu:256-319).  The
+    epilogue uses the elementwise kernel's formulas, so the gradients are the
+    same bits either way.  A gradient that other consumers add to loses the
+    mark (the sum is a new tensor), and the producer then applies its
+    derivative to the sum, as it must."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, activation):
         raw_b = bias._data if bias is not None else None
         ctx.activation = activation
         if activation == "gelu":
-            ctx.pre = _linear_forward(x._data, weight._data, raw_b, "none")
-            y = _gelu(ctx.pre)
+            ctx.aux = _linear_forward(x._data, weight._data, raw_b, "none")
+            y = _gelu(ctx.aux)
         else:
             y = _linear_forward(x._data, weight._data, raw_b, activation)
-            ctx.out = y
+            ctx.aux = y
         ctx.save_for_backward(x, weight)
         return Tensor._wrap(y)
 
@@ -429,11 +477,17 @@ class LinearOp(Function):
         need_x, need_w = flags[0], flags[1]
         need_b = len(flags) > 2 and flags[2]
         dz = g._data
-        if ctx.activation == "relu":
-            dz = _activation_backward(dz, ctx.out, "relu")
-        elif ctx.activation == "gelu":
-            dz = _activation_backward(dz, ctx.pre, "gelu")
-        gx = Tensor._wrap(_matmul_ex(dz, weight._data, False, False)) if need_x else None
+        if ctx.activation != "none" and g._act_applied is not ctx:
+            dz = _activation_backward(dz, ctx.aux, ctx.activation)
+        gx = None
+        if need_x:
+            producer = _fusable_activation(x)
+            if producer is not None:
+                gx = Tensor._wrap(_linear_input_grad(dz, weight._data, producer.aux,
+                                                     producer.activation))
+                gx._act_applied = producer
+            else:
+                gx = Tensor._wrap(_matmul_ex(dz, weight._data, False, False))
         gw = gb = None
         if need_w:
             raw_w, raw_b = _linear_weight_grad(dz, x._data, bool(need_b))

@@ -70,6 +70,19 @@ void launch_linear_weight_grad(const float* dz, const float* x, float* grad_w, f
                                int64_t batch, int64_t out_features, int64_t in_features,
                                hipStream_t stream = nullptr, int precision = -1);
 
+// Input gradient of a Linear layer with the activation derivative of the
+// layer that produced its input applied in the same launch:
+// grad_x[batch, in] = act'(aux) (.) (dz W), for dz [batch, out], weight
+// [out, in] and aux [batch, in] row-major -- the producer's saved
+// pre-activation (GELU / SiLU / Sigmoid) or, for ReLU, its output.  With
+// epilogue None (aux ignored, may be null) it is the plain dz W.  Replaces
+// MatMulOp.backward's dA GEMM followed by activation_backward on the result
+// (python/cuDeep/tensor.py:430-443, src/bindings/module.cpp:837-872).
+void launch_linear_input_grad(const float* dz, const float* weight, const float* aux,
+                              float* grad_x, int64_t batch, int64_t out_features,
+                              int64_t in_features, GemmEpilogue act,
+                              hipStream_t stream = nullptr, int precision = -1);
+
 void launch_matmul_dgemm_ex(const double* A, const double* B, double* C, int64_t M,
                             int64_t N, int64_t K, bool transA, bool transB, int64_t lda,
                             int64_t ldb, int64_t ldc, hipStream_t stream = nullptr);

@@ -21,6 +21,12 @@ public:
 
     void* allocate(size_t nbytes);
     void deallocate(void* ptr);
+    // Returns a block that work already enqueued on `stream` may still use:
+    // the pool records an event there and hands the block out again only
+    // once that event has completed, so a later user on any stream
+    // (including non-blocking ones, which do not wait for the null stream)
+    // cannot overwrite it while the earlier kernel runs.
+    void deallocate_after(void* ptr, hipStream_t stream);
     void release_cached();
     size_t allocated_bytes() const { return allocated_bytes_; }
     size_t cached_bytes() const { return cached_bytes_; }
@@ -32,7 +38,18 @@ private:
     MemoryPool() = default;
     ~MemoryPool();
 
+    struct Pending {
+        void* ptr;
+        size_t nbytes;
+        hipEvent_t done;
+    };
+    // Moves pending blocks whose event has completed (all of them, after
+    // waiting, when `wait`) to the free lists.  Caller holds mutex_.
+    void reclaim_locked(bool wait);
+
     std::unordered_map<size_t, std::vector<void*>> free_blocks_;
+    std::vector<Pending> pending_;
+    std::vector<hipEvent_t> spare_events_;
     std::unordered_map<void*, size_t> allocated_blocks_;
     std::mutex mutex_;
     size_t allocated_bytes_ = 0;

@@ -276,6 +276,86 @@ def test_mlp_c4_forward_backward_vs_oracle(cd, prec):
         assert e < tol, kname
 
 
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+@pytest.mark.parametrize("prec", ["fp32", "tf32"])
+def test_activation_backward_fused_into_consumer_gemm(cd, act, prec, monkeypatch):
+    """A Linear whose input came out of a ReLU / GELU forms its input
+    gradient with the activation derivative in its GEMM epilogue, and the
+    activation's own backward launch is skipped (the reference runs it as a
+    kernel of its own: tensor.py:430-443, activation_kernel.cu:256-319).
+    Every parameter and input gradient is bit for bit the unfused one, with
+    ragged sizes and three layers; an activation output feeding two layers
+    keeps its own backward (applied to the summed gradient)."""
+    from cudeep_amd.cuDeep import autograd
+    from cudeep_amd.cuDeep import tensor as tmod
+    nn, T = cd.nn, cd.Tensor
+    cd.set_matmul_precision(prec)
+    rng = np.random.default_rng(11 if act == "relu" else 12)
+    dims = [300, 200, 96, 10]
+    params = []
+    for fi, fo in zip(dims[:-1], dims[1:]):
+        params.append(((rng.standard_normal((fo, fi)) / np.sqrt(fi)).astype(np.float32),
+                       (rng.standard_normal(fo) * 0.1).astype(np.float32)))
+    x = rng.standard_normal((517, 300)).astype(np.float32)
+    g = rng.standard_normal((517, 10)).astype(np.float32)
+    calls = []
+    real = tmod._activation_backward
+
+    def counting(*args):
+        calls.append(args[2])
+        return real(*args)
+
+    monkeypatch.setattr(tmod, "_activation_backward", counting)
+    Act = nn.ReLU if act == "relu" else nn.GELU
+
+    def linear(i):
+        layer = nn.Linear(dims[i], dims[i + 1])
+        layer._parameters["weight"] = nn.Parameter(T.from_numpy(params[i][0]))
+        layer._parameters["bias"] = nn.Parameter(T.from_numpy(params[i][1]))
+        return layer
+
+    def run(fuse):
+        autograd.set_fuse_activation_backward(fuse)
+        try:
+            calls.clear()
+            model = nn.Sequential(linear(0), Act(), linear(1), Act(), linear(2))
+            X = T.from_numpy(x, requires_grad=True)
+            model(X).backward(T.from_numpy(g))
+            grads = [X.grad.numpy()]
+            for p in model.parameters():
+                grads.append(p.grad.numpy())
+            return grads, len(calls)
+        finally:
+            autograd.set_fuse_activation_backward(True)
+
+    say("fused activation backward", act, prec)
+    fused, n_fused = run(True)
+    plain, n_plain = run(False)
+    assert (n_fused, n_plain) == (0, 2)
+    assert len(fused) == 7
+    for a, b in zip(fused, plain):
+        assert a.dtype == np.float32 and np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+    # two consumers of one activation output: no fusion, one backward launch
+    calls.clear()
+    l0, l1, l2 = linear(0), linear(1), nn.Linear(200, 96)
+    l2._parameters["weight"] = nn.Parameter(T.from_numpy(params[1][0][::-1].copy()))
+    X = T.from_numpy(x, requires_grad=True)
+    h = Act()(l0(X)) if act == "gelu" else l0(X, activation="relu")
+    out = l1(h) + l2(h)
+    out.backward(T.from_numpy(g[:, :1].repeat(96, 1)))
+    assert len(calls) == 1
+    W0, b0 = params[0]
+    z = x.astype(np.float64) @ W0.T.astype(np.float64) + b0
+    dh = g[:, :1].repeat(96, 1).astype(np.float64) @ (params[1][0] + params[1][0][::-1]).astype(np.float64)
+    if act == "relu":
+        dz = dh * (z > 0)
+    else:
+        dz = dh * oracle.gelu_grad(z)
+    assert oracle.rel_fro(l0._parameters["bias"].grad.numpy(), dz.sum(0)) < 1e-4
+
+
 # ---- nn.Conv2d (reference tests/unit/test_layers.py:58-75) -----------------
 
 def test_conv2d_layer_shapes(cd):

@@ -262,7 +262,8 @@ def test_weight_grad_with_fused_bias_grad(M, N, K, prec):
 
 @pytest.mark.parametrize("M,N,K,transA", [(1, 100, 5000, True), (16, 4096, 1024, False),
                                           (7, 33, 2049, True), (12, 520, 70000, True),
-                                          (16, 64, 1024, False), (10, 257, 8191, True)])
+                                          (16, 64, 1024, False), (10, 257, 8191, True),
+                                          (5, 37, 3001, False)])
 @pytest.mark.parametrize("prec", [0, 1])
 def test_skinny_m_long_k(M, N, K, transA, prec):
     """M <= 16 with K >= 1024 (the 10-wide layer's weight-gradient shape): the
@@ -294,6 +295,38 @@ def test_skinny_m_long_k(M, N, K, transA, prec):
     ref = np.maximum(want + bias, 0.0)
     # ReLU is 1-Lipschitz: the error stays within the product's (+ the bias add's rounding)
     assert np.linalg.norm(Y - ref) <= (2 * e_ref + 2.0 ** -23) * np.linalg.norm(want + bias)
+
+
+@pytest.mark.parametrize("act", BWD_ACTS)
+@pytest.mark.parametrize("M,N,K", [(10, 256, 8192), (5, 37, 3001), (16, 1030, 1024)])
+@pytest.mark.parametrize("prec", [0, 1])
+def test_skinny_m_bwd_epilogue(act, M, N, K, prec):
+    """The skinny-M route (M <= 16, K >= 1024: a Linear input gradient
+    dH = (dZ W) * act'(H) at a batch of <= 16) with an activation-backward
+    epilogue, which its slice reduction applies: bit for bit the same
+    product followed by the elementwise activation-backward kernel, with
+    ragged widths and aux a view whose leading dimension exceeds N."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(17 * M + N + K + prec)
+    A = normal(rng, (M, K))
+    B = normal(rng, (K, N), 1.0 / np.sqrt(K))
+    Zwide = normal(rng, (M, N + 7))
+    code = {"relu": cd.EPI_BWD_RELU, "gelu": cd.EPI_BWD_GELU, "silu": cd.EPI_BWD_SILU,
+            "sigmoid": cd.EPI_BWD_SIGMOID}[act]
+    fwd_code = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU, "silu": cd.EPI_SILU,
+                "sigmoid": cd.EPI_SIGMOID}[act]
+    say("skinny M bwd epilogue", act, M, N, K, prec)
+    gA, gB = dev(A), dev(B)
+    aux = dev(Zwide)[:, :N]
+    assert aux.stride(0) == N + 7
+    fused = host(ops().gemm(gA, gB, precision=prec, epilogue=code, aux=aux))
+    P = ops().gemm(gA, gB, precision=prec)
+    sep = host(ops().activation_backward(P, dev(np.ascontiguousarray(Zwide[:, :N])), fwd_code))
+    assert np.array_equal(fused.view(np.uint32), sep.view(np.uint32))
+    if act == "relu":
+        want = oracle.dgemm(A, B) * oracle.relu_grad(Zwide[:, :N])
+        e_ref = oracle.rel_fro(oracle.sgemm_seqfma(A, B) * (Zwide[:, :N] > 0), want)
+        assert oracle.rel_fro(fused, want) <= 2 * e_ref + 2.0 ** -24
 
 
 def test_fused_bias_grad_k_zero_and_empty_columns():

@@ -6,7 +6,6 @@ whose scratch use shrinks (stale partials of the previous call must not
 leak into the next), on both backward-weight kernels, in every precision
 mode.  Layers whose scratch exceeds the fixed per-GPU array are refused
 before any launch."""
-import ctypes
 
 import numpy as np
 import pytest
@@ -51,8 +50,10 @@ def test_refuses_layers_beyond_the_scratch_before_any_launch():
     big = (1, 1, 2 ** 15, 2 ** 15, 1, 1, 1, 1, 1, 0, 0)
     need = L.lib().cdx_conv2d_backward_weight_workspace_size(*_args(big))
     assert need > NOALLOC_BYTES
-    fake = ctypes.c_void_p(0x1000)
-    st = L.lib().cdx_conv2d_backward_weight_f32_noalloc(fake, fake, fake, *_args(big), 0, None)
+    # NULL tensors: the refusal comes before any pointer is used; were it to
+    # regress, the general entry point's NULL check would stop the call
+    # before any kernel launch.
+    st = L.lib().cdx_conv2d_backward_weight_f32_noalloc(None, None, None, *_args(big), 0, None)
     assert st == L.CDX_ERR_UNSUPPORTED
     msg = L.lib().cdx_last_error().decode()
     assert str(need) in msg and str(NOALLOC_BYTES) in msg
