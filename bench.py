@@ -449,23 +449,21 @@ def cpu_baseline(n=4096):
     rng = np.random.default_rng(2)
     A = rng.standard_normal((n, n)).astype(np.float32)
     B = rng.standard_normal((n, n)).astype(np.float32)
-    oracle.sgemm_seqfma(A, B)                      # warmup
-    ts = []
-    for _ in range(3):
-        t = time.perf_counter()
-        oracle.sgemm_seqfma(A, B)
-        ts.append(time.perf_counter() - t)
-    t_med = statistics.median(ts)
-    t = time.perf_counter()
-    A @ B
-    t_np = time.perf_counter() - t
+    t_med = _cpu_time(lambda: oracle.sgemm_seqfma(A, B))
+    # the other configs on the same (still warm) OpenMP threads, before NumPy:
+    # its BLAS threads keep spinning for a while after a call and then compete
+    # with the oracle's threads for the cores
+    configs = cpu_configs()
+    t_np = _cpu_time(lambda: A @ B)
     flops = 2.0 * n ** 3
     return {"value": flops / t_med / 1e12, "unit": "TFLOP/s", "cores": oracle.num_threads(),
             "kind": "port",
             "sample": f"full {n}^3 FP32 GEMM, seq-FMA host reference (oracle/oracle.c), "
                       f"1 warmup + median of 3 ({t_med:.2f} s each)",
             "numpy_f32_tflops": flops / t_np / 1e12,
-            "configs": cpu_configs()}
+            "numpy_sample": "NumPy float32 A @ B on the same operands, all cores, "
+                            "1 warmup + median of 3, timed after the host reference",
+            "configs": configs}
 
 
 def _cpu_time(fn, reps=3):

@@ -13,7 +13,7 @@ namespace {
 using namespace split;
 
 // Configuration choice, shared by the launcher and the workspace query.
-enum class BfCfg { SkinnyM, Huge, Large, Small };
+enum class BfCfg { SkinnyM, Huge, KAlt, Large, Small };
 
 BfCfg choose_bf(const GemmArgs& g, int terms) {
     if (g.M <= 64 && g.N >= 4096) return BfCfg::SkinnyM;
@@ -21,7 +21,9 @@ BfCfg choose_bf(const GemmArgs& g, int terms) {
     // form fits in 256 registers without spilling.
     if (terms == 3 && ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<CfgHuge>(g))
         return BfCfg::Huge;
-    if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return BfCfg::Large;
+    const int64_t tiles128 = ceil_div(g.M, 128) * ceil_div(g.N, 128);
+    if (tiles128 >= 256 && kalt_fits(g)) return BfCfg::KAlt;
+    if (tiles128 >= 256) return BfCfg::Large;
     return BfCfg::Small;
 }
 
@@ -40,6 +42,7 @@ int dispatch(const GemmArgs& g, hipStream_t stream) {
                 return launch_ops<CfgHuge, TERMS>(g, stream);
             }
             return set_error(CDX_ERR_UNSUPPORTED, "gemm: no four-term Huge configuration");
+        case BfCfg::KAlt: return launch_kalt_ops<TERMS>(g, stream);
         case BfCfg::Large: return launch_ops<CfgLarge, TERMS>(g, stream);
         default: return launch_ops<CfgSmall, TERMS>(g, stream);
     }
@@ -80,6 +83,8 @@ size_t gemm_bf16x3_workspace(const GemmArgs& g, int terms) {
     switch (choose_bf(g, terms)) {
         case BfCfg::SkinnyM: return ws_of<CfgSkinnyM>(g);
         case BfCfg::Huge: return ws_of<CfgHuge>(g);
+        case BfCfg::KAlt:
+            return splitk_bytes(g, (g.M / 128) * (g.N / 128), 32);   // launch_kalt_ops's policy
         case BfCfg::Large: return ws_of<CfgLarge>(g);
         default: return ws_of<CfgSmall>(g);
     }

@@ -936,6 +936,257 @@ void gemm_pingpong_kernel(KParams p) {
     }
 }
 
+template <int OPA, int OPB, bool SPLITN, int TERMS>
+__global__ __launch_bounds__(512)
+void gemm_kalt_kernel(KParams p) {
+    constexpr int BM = 128, BN = 128, BK = 32, NTG = 256, GROUP_M = 8, ES = 4;
+    constexpr int STRIDE = BK + 8;                 // ushort units, 16 B pad
+    constexpr int A_PLANE = BM * STRIDE, B_PLANE = BN * STRIDE;
+    constexpr int B_OFF = 2 * A_PLANE;             // stage: A hi, A lo, B hi, B lo
+    constexpr int STAGE = 2 * (A_PLANE + B_PLANE);
+    __shared__ __attribute__((aligned(16))) unsigned short lds[4 * STAGE];
+    static_assert(4 * STAGE * 2 >= 8 * 2048 * 4, "the hand-over needs 64 KiB");
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+    const int grp = wave >> 2;
+    const int gtid = tid & (NTG - 1);
+    const int wm0 = ((wave & 3) >> 1) * 64;
+    const int wn0 = (wave & 1) * 64;
+    const int l16 = lane & 15;
+    const int lq = lane >> 4;
+
+    int tm, tn;
+    tile_of_block((int)(p.M / BM), (int)(p.N / BN), GROUP_M, tm, tn);
+    const int64_t bm = (int64_t)tm * BM, bn = (int64_t)tn * BN;
+    if (gridDim.y > 1) {
+        const int64_t k0 = (int64_t)blockIdx.y * p.k_chunk;
+        p.A = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? k0 : k0 * p.lda);
+        p.B = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? k0 * p.ldb : k0);
+        p.K = p.K - k0 < p.k_chunk ? p.K - k0 : p.k_chunk;
+        p.C += (int64_t)blockIdx.y * p.M * p.N;
+    }
+    if (gridDim.z > 1) {
+        p.A = static_cast<const char*>(p.A) + ES * (int64_t)blockIdx.z * p.sa;
+        p.B = static_cast<const char*>(p.B) + ES * (int64_t)blockIdx.z * p.sb;
+        p.C += (int64_t)blockIdx.z * p.sc;
+    }
+
+    using LoaderA = SplitLoader<BM, BK, NTG, OPA == CDX_OP_N, false>;
+    using LoaderB = SplitLoader<BN, BK, NTG, OPB == CDX_OP_T, false>;
+    static_assert(LoaderA::NV == 1 && LoaderB::NV == 1, "one 4 x 4 block per thread");
+    LoaderA la0, la1;   // two staging sets (three terms): loads three slots ahead
+    LoaderB lb0, lb1;
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    shortx8 fa[4][2], fb[4][2];   // [16-row block][plane 0 = hi, 1 = lo]
+    auto read_frags = [&](const unsigned short* s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl)
+                fa[i][pl] = *reinterpret_cast<const shortx8*>(
+                    s + pl * A_PLANE + (wm0 + i * 16 + l16) * STRIDE + 8 * lq);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl)
+                fb[j][pl] = *reinterpret_cast<const shortx8*>(
+                    s + B_OFF + pl * B_PLANE + (wn0 + j * 16 + l16) * STRIDE + 8 * lq);
+    };
+    auto mfma = [](const shortx8& a, const shortx8& b, const floatx4& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    };
+    // per-element term order of gemm_bf16x3_kernel: three terms lo*hi,
+    // hi*lo, then hi*hi; four terms summed from zero, small terms first,
+    // then added to the accumulator.  `issue_a` / `issue_b` (global loads of
+    // a later k-tile) go between the MFMAs, fenced so the compiler keeps
+    // them there: issued from the memory slot, where they queue behind the
+    // fragment reads, split and stores of the same wave, they cost ~35 % of
+    // the kernel's time (2048^3 with and without them: 67.5 / 43.8 us).
+    auto fence = []() { __builtin_amdgcn_sched_barrier(0); };
+    auto math = [&](auto&& issue_a, auto&& issue_b) {
+        __builtin_amdgcn_s_setprio(1);
+        if constexpr (TERMS == 4) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                floatx4 t[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) t[j] = mfma(fa[i][1], fb[j][1], floatx4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int j = 0; j < 4; ++j) t[j] = mfma(fa[i][1], fb[j][0], t[j]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) t[j] = mfma(fa[i][0], fb[j][1], t[j]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    t[j] = mfma(fa[i][0], fb[j][0], t[j]);
+                    acc[i][j] += t[j];
+                }
+                if (i == 0) { fence(); issue_a(); fence(); }
+                if (i == 1) { fence(); issue_b(); fence(); }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fa[i][1], fb[j][0], acc[i][j]);
+            fence();
+            issue_a();
+            fence();
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fa[i][0], fb[j][1], acc[i][j]);
+            fence();
+            issue_b();
+            fence();
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = mfma(fa[i][0], fb[j][0], acc[i][j]);
+        }
+        __builtin_amdgcn_s_setprio(0);
+    };
+    auto slot = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    const uint32_t lda_b = (uint32_t)(p.lda * ES), ldb_b = (uint32_t)(p.ldb * ES);
+    const uint32_t offa = LoaderA::tile_offset(lda_b, gtid);
+    const uint32_t offb = LoaderB::tile_offset(ldb_b, gtid);
+    const char* baseA = static_cast<const char*>(p.A) + ES * (OPA == CDX_OP_N ? bm * p.lda : bm);
+    const char* baseB = static_cast<const char*>(p.B) + ES * (OPB == CDX_OP_N ? bn : bn * p.ldb);
+    const int64_t stepA = OPA == CDX_OP_N ? (int64_t)ES * BK : (int64_t)BK * p.lda * ES;
+    const int64_t stepB = OPB == CDX_OP_N ? (int64_t)BK * p.ldb * ES : (int64_t)ES * BK;
+    // this group's k-tiles: grp, grp + 2, grp + 4, ...
+    const int64_t nk = p.K / BK;
+    const int64_t nkg = grp == 0 ? (nk + 1) / 2 : nk / 2;
+    auto load = [&](LoaderA& a, LoaderB& b, int64_t j) {
+        const int64_t t = 2 * j + grp;
+        a.load_at(baseA + t * stepA, lda_b, offa);
+        b.load_at(baseB + t * stepB, ldb_b, offb);
+    };
+    // the MFMAs of the current k-tile with the loads of this group's k-tile
+    // j into (a, b) between them (none when j is past its last one)
+    auto math_loading = [&](LoaderA& a, LoaderB& b, int64_t j) {
+        const bool go = j < nkg;
+        const int64_t t = 2 * j + grp;
+        math([&]() { if (go) a.load_at(baseA + t * stepA, lda_b, offa); },
+             [&]() { if (go) b.load_at(baseB + t * stepB, ldb_b, offb); });
+    };
+    auto store = [&](const LoaderA& a, const LoaderB& b, unsigned short* s) {
+        a.template store<STRIDE>(s, s + A_PLANE, gtid);
+        b.template store<STRIDE>(s + B_OFF, s + B_OFF + B_PLANE, gtid);
+    };
+    unsigned short* mine = lds + 2 * grp * STAGE;   // the group's two stages
+    // Iteration j of the group: its stage j&1 holds k-tile j; the staging set
+    // (a, b) holds k-tile j+1 (loaded three slots earlier), which goes to the
+    // other stage, and then, between the MFMAs, loads k-tile j+3; the other
+    // set holds k-tile j+2.
+    auto iteration = [&](int64_t j, LoaderA& a, LoaderB& b, int cur) {
+        read_frags(mine + cur * STAGE);
+        if (j + 1 < nkg) store(a, b, mine + (cur ^ 1) * STAGE);
+        slot();
+        math_loading(a, b, j + 3);
+        slot();
+    };
+
+    if constexpr (TERMS == 3) {
+        if (nkg > 0) {
+            load(la0, lb0, 0);
+            store(la0, lb0, mine);
+            if (nkg > 1) load(la1, lb1, 1);
+            if (nkg > 2) load(la0, lb0, 2);
+        }
+        __syncthreads();
+        if (grp == 1) slot();
+        int64_t j = 0;
+        for (; j + 1 < nkg; j += 2) {
+            iteration(j, la1, lb1, 0);
+            iteration(j + 1, la0, lb0, 1);
+        }
+        if (j < nkg) iteration(j, la1, lb1, 0);
+    } else {
+        // four terms: the two-level partial sums leave room for one set
+        // (k-tile j+1 stored, then k-tile j+2 loaded, in the same slot)
+        if (nkg > 0) {
+            load(la0, lb0, 0);
+            store(la0, lb0, mine);
+            if (nkg > 1) load(la0, lb0, 1);
+        }
+        __syncthreads();
+        if (grp == 1) slot();
+        for (int64_t j = 0; j < nkg; ++j) {
+            read_frags(mine + (j & 1) * STAGE);
+            if (j + 1 < nkg) store(la0, lb0, mine + ((j + 1) & 1) * STAGE);
+            slot();
+            math_loading(la0, lb0, j + 2);
+            slot();
+        }
+    }
+    // both groups end on the same barrier count (group 0: 2 ceil(nk/2),
+    // group 1: 1 + 2 floor(nk/2)), after which the stages are free
+    {
+        const int64_t b0 = 2 * ((nk + 1) / 2), b1 = 1 + 2 * (nk / 2);
+        const int64_t total = b0 > b1 ? b0 : b1;
+        for (int64_t b = grp == 0 ? b0 : b1; b < total; ++b) slot();
+    }
+
+    // hand-over: group 0 keeps rows 0-31 of each wave's 64 x 64 sub-tile and
+    // gives rows 32-63 to group 1, which does the opposite; slot (w, h) holds
+    // half h of wave w's sub-tile as 8 blocks x 64 lanes x 4 values
+    floatx4* red = reinterpret_cast<floatx4*>(lds);
+    const int w = wave & 3;
+    floatx4 res[2][4];
+    if (grp == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) red[((w * 2 + 1) * 8 + i * 4 + j) * 64 + lane] = acc[2 + i][j];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) red[((w * 2 + 0) * 8 + i * 4 + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (grp == 0) {   // even k-tiles (here) + odd (handed over)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                res[i][j] = acc[i][j] + red[((w * 2 + 0) * 8 + i * 4 + j) * 64 + lane];
+    } else {          // even k-tiles (handed over) + odd (here)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                res[i][j] = red[((w * 2 + 1) * 8 + i * 4 + j) * 64 + lane] + acc[2 + i][j];
+    }
+
+    const int rm0 = wm0 + 32 * grp;   // first row of this wave's half
+    const EpiArgs epi{p.C, p.ldc, p.M, p.N, p.n_split, p.ldc_split,
+                      p.bias, p.bias_mode, p.epilogue, p.aux, p.ldaux};
+    NanBits<2, 4> nb;
+    const bool repair = any_nan(res);
+    if (repair) nan_bits(res, nb);
+    write_acc<2, 4, false, SPLITN>(res, epi, bm + rm0, bn + wn0, lane);
+    if (repair)
+        repair_nan_outputs<2, 4, OPA, OPB>(nb, epi, reinterpret_cast<const float*>(baseA),
+                                           (int64_t)(lda_b / 4),
+                                           reinterpret_cast<const float*>(baseB),
+                                           (int64_t)(ldb_b / 4), nk * BK, bm, bn, rm0, wn0, lane);
+}
+
 template <class CF, int OPA, int OPB, bool CHECK, bool SPLITN, int TERMS, int IN = kInF32>
 int launch_cfg(const KParams& kp, int vec, int splits, hipStream_t stream) {
     int64_t tiles = ceil_div(kp.M, CF::BM) * ceil_div(kp.N, CF::BN);
@@ -984,6 +1235,39 @@ int launch_pingpong(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t 
     else
         hipLaunchKernelGGL((gemm_pingpong_kernel<OPA, OPB, false, IN>), grid, dim3(512), 0, stream, kp);
     return hip_error(hipGetLastError(), "gemm_pingpong_kernel launch");
+}
+
+template <int OPA, int OPB, int TERMS>
+int launch_kalt(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp{g.A, g.B, g.C, g.bias, g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
+               g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
+               g.stride_a, g.stride_b, g.stride_c, g.batch, g.aux, g.ldaux};
+    const int64_t tiles = (g.M / 128) * (g.N / 128);
+    if (tiles > INT32_MAX) return set_error(CDX_ERR_UNSUPPORTED, "gemm: too many tiles");
+    if (kp.batch < 1 || kp.batch > 65535) return set_error(CDX_ERR_UNSUPPORTED, "gemm: batch out of range");
+    const dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)kp.batch);
+    if (g.n_split > 0)
+        hipLaunchKernelGGL((gemm_kalt_kernel<OPA, OPB, true, TERMS>), grid, dim3(512), 0, stream, kp);
+    else
+        hipLaunchKernelGGL((gemm_kalt_kernel<OPA, OPB, false, TERMS>), grid, dim3(512), 0, stream, kp);
+    return hip_error(hipGetLastError(), "gemm_kalt_kernel launch");
+}
+
+// The k-alternating 128 x 128 kernel (three or four terms); the dispatcher
+// sends it problems for which kalt_fits() holds.
+template <int TERMS>
+int launch_kalt_ops(const GemmArgs& g0, hipStream_t stream) {
+    constexpr int BK = 32;
+    const int64_t tiles = (g0.M / 128) * (g0.N / 128);
+    return with_splitk(g0, tiles, BK, stream,
+                       [&](const GemmArgs& g, int splits, int64_t k_chunk) {
+        if (k_chunk % BK != 0)
+            return set_error(CDX_ERR_UNSUPPORTED, "gemm: k slice not a multiple of the k-tile");
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_N) return launch_kalt<CDX_OP_N, CDX_OP_N, TERMS>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_N && g.opB == CDX_OP_T) return launch_kalt<CDX_OP_N, CDX_OP_T, TERMS>(g, splits, k_chunk, stream);
+        if (g.opA == CDX_OP_T && g.opB == CDX_OP_N) return launch_kalt<CDX_OP_T, CDX_OP_N, TERMS>(g, splits, k_chunk, stream);
+        return launch_kalt<CDX_OP_T, CDX_OP_T, TERMS>(g, splits, k_chunk, stream);
+    });
 }
 
 // The ping-pong kernel for fp32 operands (three terms) or 16-bit ones; the
@@ -1052,6 +1336,15 @@ inline bool pingpong_fits(const GemmArgs& g) {
     return g.lda < (int64_t(1) << 22) && g.ldb < (int64_t(1) << 22);
 }
 
+// The k-alternating kernel: aligned fp32 operands (M, N % 128, K % 32,
+// 16-byte bases and leading dimensions) whose 128-row panels span less than
+// 4 GiB (32-bit offsets, as the ping-pong kernel's).
+inline bool kalt_fits(const GemmArgs& g) {
+    return ((uintptr_t)g.A % 16 == 0) && ((uintptr_t)g.B % 16 == 0) && g.lda % 4 == 0 &&
+           g.ldb % 4 == 0 && g.stride_a % 4 == 0 && g.stride_b % 4 == 0 && g.K > 0 &&
+           g.M % 128 == 0 && g.N % 128 == 0 && g.K % 32 == 0 && pingpong_fits(g);
+}
+
 // 16-bit operands: one plane and one MFMA per fragment pair, so a k-tile of
 // 64 costs the LDS of the split kernel's 32.
 using Cfg16Huge = Cfg<256, 256, 64, 128, 64, 8, true, 1>;
@@ -1073,6 +1366,8 @@ extern template int launch_ops<Cfg16Small, 1, kInF16>(const GemmArgs&, hipStream
 extern template int launch_ops<Cfg16Huge, 1, kInBF16>(const GemmArgs&, hipStream_t);
 extern template int launch_ops<Cfg16Large, 1, kInBF16>(const GemmArgs&, hipStream_t);
 extern template int launch_ops<Cfg16Small, 1, kInBF16>(const GemmArgs&, hipStream_t);
+extern template int launch_kalt_ops<3>(const GemmArgs&, hipStream_t);
+extern template int launch_kalt_ops<4>(const GemmArgs&, hipStream_t);
 extern template int launch_pingpong_ops<kInF32>(const GemmArgs&, hipStream_t);
 extern template int launch_pingpong_ops<kInF16>(const GemmArgs&, hipStream_t);
 extern template int launch_pingpong_ops<kInBF16>(const GemmArgs&, hipStream_t);

@@ -337,6 +337,59 @@ def test_tf32mode_256_tile_path(tA, tB, K):
     assert _checksum_identity(opA, opB, C) < 1e-4
 
 
+@pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("K", [32, 64, 96, 544, 2080])
+@pytest.mark.parametrize("prec_name", ["PREC_TF32MODE", "PREC_TF32MODE4"])
+def test_tf32mode_kalt_path(tA, tB, K, prec_name):
+    """The k-alternating 128 x 128 TF32-mode kernel, which 2048 x 2048
+    outputs select (256 tiles of 128 x 128, too few of 256 x 256): its two
+    wave groups take alternate k-tiles and add their sums at the end.  K = 32
+    leaves the second group without a k-tile; K = 96 and 2080 give odd k-tile
+    counts (the groups end on padded barrier counts); both variants (three
+    terms with two staging sets, four with one).  Gate: relFro on sampled
+    rows <= the emulated reference TF32 error, and the checksum identity."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(2000 + K + 2 * tA + tB)
+    n = 2048
+    A = normal(rng, (K, n) if tA else (n, K))
+    B = normal(rng, (n, K) if tB else (K, n))
+    say("tf32 k-alternating path", tA, tB, K, prec_name)
+    C = host(ops().gemm(dev(A), dev(B), transA=tA, transB=tB,
+                        precision=getattr(cd, prec_name)))
+    opA = np.ascontiguousarray(A.T if tA else A)
+    opB = np.ascontiguousarray(B.T if tB else B)
+    for rows in ((0, 40), (n // 2 - 24, n // 2 + 24), (n - 40, n)):
+        C64 = oracle.dgemm(opA, opB, rows=rows)
+        e = oracle.rel_fro(C[rows[0]:rows[1]], C64)
+        e_rz = oracle.rel_fro(oracle.gemm_tf32emu(opA, opB, "rz", rows=rows), C64)
+        e_rne = oracle.rel_fro(oracle.gemm_tf32emu(opA, opB, "rne", rows=rows), C64)
+        assert e <= min(e_rz, e_rne), (rows, e, e_rz, e_rne)
+    assert _checksum_identity(opA, opB, C) < 1e-4
+
+
+@pytest.mark.parametrize("epi,bias_mode", [("gelu", "col"), ("relu", "row")])
+@pytest.mark.parametrize("prec_name", ["PREC_TF32MODE", "PREC_TF32MODE4"])
+def test_tf32mode_kalt_epilogue(epi, bias_mode, prec_name):
+    """Bias + activation epilogue of the k-alternating kernel (each wave
+    group writes half of every wave's sub-tile after the hand-over)."""
+    import cudeep_amd as cd
+    rng = np.random.default_rng(1200)
+    M, N, K = 2048, 2048, 160
+    A = normal(rng, (M, K))
+    W = normal(rng, (N, K))
+    bias = normal(rng, (M if bias_mode == "row" else N,))
+    bm = {"row": cd.BIAS_ROW, "col": cd.BIAS_COL}[bias_mode]
+    ep = {"relu": cd.EPI_RELU, "gelu": cd.EPI_GELU}[epi]
+    say("tf32 k-alternating epilogue", epi, bias_mode, prec_name)
+    C = host(ops().gemm(dev(A), dev(W), transB=True, precision=getattr(cd, prec_name),
+                        bias=dev(bias), bias_mode=bm, epilogue=ep))
+    for rows in ((0, 64), (1000, 1064), (M - 64, M)):
+        Z = oracle.dgemm(A, np.ascontiguousarray(W.T), rows=rows)
+        Z = Z + (bias[rows[0]:rows[1], None] if bias_mode == "row" else bias[None, :])
+        want = oracle.activation(Z, epi)
+        assert np.max(np.abs(C[rows[0]:rows[1]] - want)) <= 2e-5 * np.abs(Z).max() + 1e-6
+
+
 @pytest.mark.parametrize("epi,bias_mode", [("gelu", "col"), ("relu", "row"), ("silu", "none")])
 def test_tf32mode_256_tile_epilogue(epi, bias_mode):
     """Bias + activation epilogue of the 256 x 256 TF32-mode kernel (the
@@ -611,8 +664,10 @@ def _classes(C):
     (300, 200, 784, False, False),       # ragged tiles (bounds-checked kernel)
     (300, 200, 784, True, True),         # both operands transposed
     (128, 128, 4096, False, False),      # split-K slices repair their own k-range
-    (4096, 4096, 64, False, False),      # two-group 256 x 256 kernel
+    (4096, 4096, 64, False, False),      # two-group 256 x 256 kernel (four terms: k-alternating)
     (4096, 4096, 64, True, False),
+    (2048, 2048, 96, False, False),      # k-alternating 128 x 128 kernel, odd k-tile count
+    (2048, 2048, 96, True, True),
 ])
 def test_tf32mode_special_values_follow_reference(M, N, K, tA, tB):
     """TF32 modes: +-Inf, NaN and finite operands beyond bf16's range give the
