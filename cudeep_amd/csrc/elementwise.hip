@@ -164,24 +164,28 @@ void fill_kernel(T* __restrict__ y, int64_t n, T v) {
 // Sum of the split-K partials in slice order, then the GEMM epilogue of
 // each element (store_one: bias, activation or activation backward, output
 // map, ones column) -- the same float operations as the unsplit kernels'.
+// A thread owns one column of a row (rows over blockIdx.y, columns over
+// blockIdx.x): coalesced loads and no index division.
 __global__ __launch_bounds__(256)
 void splitk_reduce_kernel(const float* __restrict__ P, int splits, EpiArgs e) {
     const int64_t MN = e.M * e.N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t m = i / e.N, n = i - m * e.N;
-        float v = P[i];
-        // slices in order; 8 loads in flight per group instead of one at a time
-        int s = 1;
-        for (; s + 7 < splits; s += 8) {
-            float t[8];
+    for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < e.N;
+         n += (int64_t)gridDim.x * blockDim.x) {
+        for (int64_t m = blockIdx.y; m < e.M; m += gridDim.y) {
+            const float* __restrict__ p = P + m * e.N + n;
+            float v = p[0];
+            // slices in order; 8 loads in flight per group instead of one at a time
+            int s = 1;
+            for (; s + 7 < splits; s += 8) {
+                float t[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] = P[(int64_t)(s + u) * MN + i];
+                for (int u = 0; u < 8; ++u) t[u] = p[(int64_t)(s + u) * MN];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v += t[u];
+                for (int u = 0; u < 8; ++u) v += t[u];
+            }
+            for (; s < splits; ++s) v += p[(int64_t)s * MN];
+            store_one(e, m, n, v);
         }
-        for (; s < splits; ++s) v += P[(int64_t)s * MN + i];
-        store_one(e, m, n, v);
     }
 }
 
@@ -197,8 +201,11 @@ unsigned grid_for(int64_t n) {
 int launch_splitk_reduce(const float* P, int splits, const GemmArgs& g, hipStream_t stream) {
     const EpiArgs e{g.C, g.ldc, g.M, g.N, g.n_split, g.ldc_split, g.bias, g.bias_mode,
                     g.epilogue, g.aux, g.ldaux, g.colsum, g.ones_col};
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(g.M * g.N)), dim3(256), 0, stream,
-                       P, splits, e);
+    int64_t gx = ceil_div(g.N, 256), gy = g.M;
+    if (gx > 65535) gx = 65535;
+    if (gy > 65535) gy = 65535;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0,
+                       stream, P, splits, e);
     return hip_error(hipGetLastError(), "splitk_reduce_kernel launch");
 }
 

@@ -936,6 +936,27 @@ void gemm_pingpong_kernel(KParams p) {
     }
 }
 
+// 128 x 128 tiles on a k-alternating two-group schedule, for problems with
+// too few 256 x 256 tiles to fill the GPU (2048^3: 64 of them, 256 of these).
+// The eight waves form two groups of four, one wave of each group per SIMD.
+// Each group owns the WHOLE tile -- its waves 64 x 64 sub-tiles -- and the
+// groups take alternate k-tiles (group 0 the even ones, group 1 the odd
+// ones), each group through its own two LDS stages (4 x 40 KiB).  A group
+// works a k-tile j in two barrier-separated slots:
+//     MEM   read all A / B fragments of k-tile j; split + store k-tile j+1
+//           (from registers) into the group's other stage
+//     MATH  the k-tile's 48 (three terms) or 64 (four terms) MFMAs, with the
+//           global loads of k-tile j+3 (three terms: two staging sets) or
+//           j+2 (four terms: one set) issued between them
+// and group 1 runs one slot behind group 0, so on every SIMD one wave
+// issues MFMAs while the other reads, splits and stores.  Against the
+// 128 x 128 in-step kernel (8 waves of 32 x 64 all reading, then all
+// multiplying) the LDS traffic per MFMA is 25 % lower -- 64 x 64 wave
+// tiles -- and the LDS and MFMA phases overlap.  At the end each group hands
+// one half of every wave's accumulators to the other through LDS, both add
+// the even-k-tile sum to the odd one in that order, and each writes its half
+// of the tile.  Aligned problems only (M, N % 128, K % 32, 16-byte operands);
+// the launcher checks that 128 operand rows span less than 4 GiB.
 template <int OPA, int OPB, bool SPLITN, int TERMS>
 __global__ __launch_bounds__(512)
 void gemm_kalt_kernel(KParams p) {
