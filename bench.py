@@ -315,7 +315,8 @@ def bench_mlp_api(steps, warmup, precision):
         y = model(X)
         y.backward(dY)
 
-    ms, _ = time_launches(step, steps, warmup)
+    # (untimed settling: the first steps fill the runtime's allocation caches)
+    ms, _ = time_launches(step, steps, warmup, min_warm_s=0.2)
     cuDeep.set_matmul_precision(prev)
     flops = 3 * 2.0 * 8192 * (784 * 256 + 256 * 10)
     return {"step_ms": ms, "step_tflops": flops / (ms * 1e-3) / 1e12}
@@ -424,7 +425,7 @@ def bench_conv_api(steps, warmup, precision):
     x = T.from_numpy(rng.standard_normal((32, 64, 56, 56), dtype=np.float32))
     dy = T.from_numpy(rng.standard_normal((32, 64, 56, 56), dtype=np.float32))
     with cuDeep.no_grad():
-        fwd_ms, _ = time_launches(lambda: conv(x), steps, warmup)
+        fwd_ms, _ = time_launches(lambda: conv(x), steps, warmup, min_warm_s=0.2)
     xg = T.from_numpy(rng.standard_normal((32, 64, 56, 56), dtype=np.float32), requires_grad=True)
 
     def step():
@@ -432,7 +433,7 @@ def bench_conv_api(steps, warmup, precision):
         xg.grad = None
         conv(xg).backward(dy)
 
-    step_ms, _ = time_launches(step, steps, warmup)
+    step_ms, _ = time_launches(step, steps, warmup, min_warm_s=0.2)
     cuDeep.set_matmul_precision(prev)
     fl = 2.0 * 32 * 64 * 56 * 56 * 64 * 9
     return {"fwd_ms": fwd_ms, "fwd_tflops": fl / (fwd_ms * 1e-3) / 1e12,

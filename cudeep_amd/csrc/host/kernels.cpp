@@ -51,30 +51,27 @@ int act_code(ActivationType a) {
 }
 
 // Scratch for one launch.  On the null stream it comes from the runtime's
-// exact-size MemoryPool cache -- after the first call of a size a map lookup,
-// where the stream-ordered pool costs tens of microseconds of host time for
-// a large block -- and is handed back when the launch is enqueued, behind an
-// event recorded after the launch: the pool gives the block out again only
-// once that event has completed, so no later user, on whatever stream,
-// overwrites it while the kernel still runs.  On any other stream the C-ABI
-// allocates stream-ordered itself.
+// exact-size scratch cache (MemoryPool::allocate_scratch) -- after the first
+// call of a size a map lookup, where the stream-ordered pool costs tens of
+// microseconds of host time for a large block -- and is handed back when the
+// launch is enqueued: that cache serves only later null-stream launches,
+// which the null stream orders after this one, never tensor storage.  On any
+// other stream the C-ABI allocates stream-ordered itself.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
-    hipStream_t stream = nullptr;
-    Workspace(size_t n, hipStream_t s) : stream(s) {
+    Workspace(size_t n, hipStream_t s) {
         if (n > 0 && s == nullptr) {
-            ptr = device_malloc(n);
+            ptr = MemoryPool::instance().allocate_scratch(n);
             bytes = n;
         }
     }
     ~Workspace() {
         if (!ptr) return;
         try {
-            MemoryPool::instance().deallocate_after(ptr, stream);
+            MemoryPool::instance().deallocate_scratch(ptr);
         } catch (...) {
-            // no event could be recorded: the block stays allocated (never
-            // handed out again) rather than throwing from a destructor
+            // (only an unknown pointer throws; never from a destructor)
         }
     }
     Workspace(const Workspace&) = delete;

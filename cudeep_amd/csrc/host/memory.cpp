@@ -2,9 +2,8 @@
 // (interface of the reference's src/memory.cu:7-97): exact-size caching
 // allocator with a mutex and byte counters; synchronous copies when no
 // stream is given.  The pool object lives until process exit and is never
-// destroyed, so no hipFree runs after the HIP runtime has shut down.  Blocks
-// returned with deallocate_after wait behind an event until the work that
-// used them has finished.
+// destroyed, so no hipFree runs after the HIP runtime has shut down.  Kernel
+// scratch of null-stream launches has a cache of its own (allocate_scratch).
 #include "../../../include/cudeep/memory.hpp"
 
 namespace cudeep {
@@ -16,25 +15,25 @@ MemoryPool& MemoryPool::instance() {
 
 MemoryPool::~MemoryPool() { release_cached(); }
 
-void MemoryPool::reclaim_locked(bool wait) {
-    size_t kept = 0;
-    for (Pending& p : pending_) {
-        const hipError_t e = wait ? hipEventSynchronize(p.done) : hipEventQuery(p.done);
-        if (e == hipErrorNotReady) {
-            pending_[kept++] = p;
-            continue;
-        }
-        CUDEEP_CHECK_HIP(e);
-        free_blocks_[p.nbytes].push_back(p.ptr);
-        spare_events_.push_back(p.done);
+void* MemoryPool::device_alloc_locked(size_t nbytes) {
+    void* ptr = nullptr;
+    hipError_t e = hipMalloc(&ptr, nbytes);
+    if (e != hipSuccess) {
+        // give both caches back to the runtime and retry once
+        for (auto* cache : {&free_blocks_, &free_scratch_})
+            for (auto& kv : *cache)
+                for (void* p : kv.second) (void)hipFree(p);
+        free_blocks_.clear();
+        free_scratch_.clear();
+        cached_bytes_ = 0;
+        CUDEEP_CHECK_HIP(hipMalloc(&ptr, nbytes));
     }
-    pending_.resize(kept);
+    return ptr;
 }
 
 void* MemoryPool::allocate(size_t nbytes) {
     if (nbytes == 0) return nullptr;
     std::lock_guard<std::mutex> lock(mutex_);
-    if (!pending_.empty()) reclaim_locked(false);
     void* ptr = nullptr;
     auto it = free_blocks_.find(nbytes);
     if (it != free_blocks_.end() && !it->second.empty()) {
@@ -42,17 +41,7 @@ void* MemoryPool::allocate(size_t nbytes) {
         it->second.pop_back();
         cached_bytes_ -= nbytes;
     } else {
-        hipError_t e = hipMalloc(&ptr, nbytes);
-        if (e != hipSuccess) {
-            // give the cache (pending blocks too, once their users are done)
-            // back to the runtime and retry once
-            reclaim_locked(true);
-            for (auto& kv : free_blocks_)
-                for (void* p : kv.second) (void)hipFree(p);
-            free_blocks_.clear();
-            cached_bytes_ = 0;
-            CUDEEP_CHECK_HIP(hipMalloc(&ptr, nbytes));
-        }
+        ptr = device_alloc_locked(nbytes);
     }
     allocated_blocks_[ptr] = nbytes;
     allocated_bytes_ += nbytes;
@@ -71,36 +60,42 @@ void MemoryPool::deallocate(void* ptr) {
     cached_bytes_ += n;
 }
 
-void MemoryPool::deallocate_after(void* ptr, hipStream_t stream) {
+void* MemoryPool::allocate_scratch(size_t nbytes) {
+    if (nbytes == 0) return nullptr;
+    std::lock_guard<std::mutex> lock(mutex_);
+    void* ptr = nullptr;
+    auto it = free_scratch_.find(nbytes);
+    if (it != free_scratch_.end() && !it->second.empty()) {
+        ptr = it->second.back();
+        it->second.pop_back();
+        cached_bytes_ -= nbytes;
+    } else {
+        ptr = device_alloc_locked(nbytes);
+    }
+    scratch_blocks_[ptr] = nbytes;
+    allocated_bytes_ += nbytes;
+    return ptr;
+}
+
+void MemoryPool::deallocate_scratch(void* ptr) {
     if (!ptr) return;
     std::lock_guard<std::mutex> lock(mutex_);
-    auto it = allocated_blocks_.find(ptr);
-    if (it == allocated_blocks_.end()) throw std::runtime_error("MemoryPool: unknown pointer");
+    auto it = scratch_blocks_.find(ptr);
+    if (it == scratch_blocks_.end()) throw std::runtime_error("MemoryPool: unknown scratch pointer");
     const size_t n = it->second;
-    hipEvent_t ev = nullptr;
-    if (!spare_events_.empty()) {
-        ev = spare_events_.back();
-        spare_events_.pop_back();
-    } else {
-        CUDEEP_CHECK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-    }
-    const hipError_t e = hipEventRecord(ev, stream);
-    if (e != hipSuccess) {
-        spare_events_.push_back(ev);
-        CUDEEP_CHECK_HIP(e);
-    }
-    allocated_blocks_.erase(it);
+    scratch_blocks_.erase(it);
     allocated_bytes_ -= n;
-    pending_.push_back({ptr, n, ev});
+    free_scratch_[n].push_back(ptr);
     cached_bytes_ += n;
 }
 
 void MemoryPool::release_cached() {
     std::lock_guard<std::mutex> lock(mutex_);
-    reclaim_locked(true);
-    for (auto& kv : free_blocks_)
-        for (void* p : kv.second) (void)hipFree(p);
+    for (auto* cache : {&free_blocks_, &free_scratch_})
+        for (auto& kv : *cache)
+            for (void* p : kv.second) (void)hipFree(p);
     free_blocks_.clear();
+    free_scratch_.clear();
     cached_bytes_ = 0;
 }
 

@@ -21,12 +21,13 @@ public:
 
     void* allocate(size_t nbytes);
     void deallocate(void* ptr);
-    // Returns a block that work already enqueued on `stream` may still use:
-    // the pool records an event there and hands the block out again only
-    // once that event has completed, so a later user on any stream
-    // (including non-blocking ones, which do not wait for the null stream)
-    // cannot overwrite it while the earlier kernel runs.
-    void deallocate_after(void* ptr, hipStream_t stream);
+    // Kernel scratch of launches on the null stream (a separate exact-size
+    // cache): a block returned while the launch that used it may still run
+    // goes only to later null-stream launches, which the null stream orders
+    // after it -- never to tensor storage, which may be written from a
+    // non-blocking stream at once.
+    void* allocate_scratch(size_t nbytes);
+    void deallocate_scratch(void* ptr);
     void release_cached();
     size_t allocated_bytes() const { return allocated_bytes_; }
     size_t cached_bytes() const { return cached_bytes_; }
@@ -38,18 +39,13 @@ private:
     MemoryPool() = default;
     ~MemoryPool();
 
-    struct Pending {
-        void* ptr;
-        size_t nbytes;
-        hipEvent_t done;
-    };
-    // Moves pending blocks whose event has completed (all of them, after
-    // waiting, when `wait`) to the free lists.  Caller holds mutex_.
-    void reclaim_locked(bool wait);
+    // hipMalloc, retrying once after giving the cached blocks back.
+    // Caller holds mutex_.
+    void* device_alloc_locked(size_t nbytes);
 
     std::unordered_map<size_t, std::vector<void*>> free_blocks_;
-    std::vector<Pending> pending_;
-    std::vector<hipEvent_t> spare_events_;
+    std::unordered_map<size_t, std::vector<void*>> free_scratch_;
+    std::unordered_map<void*, size_t> scratch_blocks_;
     std::unordered_map<void*, size_t> allocated_blocks_;
     std::mutex mutex_;
     size_t allocated_bytes_ = 0;
