@@ -139,6 +139,30 @@ size_t col_bytes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH, 
     return (size_t)(IC * KH * KW) * (size_t)(batch * OH * OW) * sizeof(float);
 }
 
+// Images per im2col + GEMM round of the column route: the whole batch while
+// its column buffer stays within 128 MiB, else equal rounds below that.  A
+// round's buffer, input and output then stay in the 256 MB Infinity Cache
+// between the im2col write and the GEMM read (C5, 32 x 64 x 56^2 3x3: two
+// rounds of 16 images, 116 MB of columns each -- 145 -> 139 us FP32, 118 ->
+// 106 us in TF32 mode; rounds of 8 images run the GEMM on too few tiles, 169
+// us).  The sums are the same: every output column is one image's.
+constexpr size_t kColRoundBytes = (size_t)128 << 20;
+
+int64_t col_round_images(int64_t batch, size_t per_image_bytes) {
+    const size_t total = per_image_bytes * (size_t)batch;
+    if (per_image_bytes == 0 || total <= kColRoundBytes) return batch;
+    const int64_t rounds = (int64_t)((total + kColRoundBytes - 1) / kColRoundBytes);
+    return (batch + rounds - 1) / rounds;
+}
+
+// Workspace of the column route: one round's column buffer.
+size_t col_round_bytes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH,
+                       int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
+    if (batch <= 0) return 0;
+    const size_t per = col_bytes(1, IC, IH, IW, KH, KW, SH, SW, PH, PW);
+    return per * (size_t)col_round_images(batch, per);
+}
+
 // The reference's forward dispatch (conv_kernel.cu:242-275) below its
 // Winograd route: a layer whose column buffer would exceed 4 MiB runs the
 // implicit GEMM (no buffer) unless it is a 3x3 stride-1 layer with >= 16
@@ -344,7 +368,7 @@ size_t cdx_conv2d_forward_workspace_size(int64_t batch, int64_t in_channels, int
     if (forward_takes_implicit(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
                                stride_w, pad_h, pad_w))
         return 0;
-    return col_bytes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
+    return col_round_bytes(batch, in_channels, in_h, in_w, kernel_h, kernel_w, stride_h, stride_w,
                      pad_h, pad_w);
 }
 
@@ -375,8 +399,8 @@ int cdx_conv2d_forward_implicit_f32(const float* input, const float* weight, con
 
 namespace {
 
-// im2col + one GEMM into NCHW; blocked_sum asks the FP32 GEMM for its
-// two-level k sum (see GemmArgs).
+// im2col + one GEMM into NCHW per round of images (col_round_images);
+// blocked_sum asks the FP32 GEMM for its two-level k sum (see GemmArgs).
 int conv_forward_im2col(const float* input, const float* weight, const float* bias,
                         float* output, int64_t batch, int64_t in_channels,
                         int64_t out_channels, int64_t in_h, int64_t in_w, int64_t kernel_h,
@@ -390,11 +414,13 @@ int conv_forward_im2col(const float* input, const float* weight, const float* bi
         return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: bad precision");
     const int64_t OH = conv_out(in_h, kernel_h, stride_h, pad_h);
     const int64_t OW = conv_out(in_w, kernel_w, stride_w, pad_w);
-    const int64_t S = OH * OW, BS = batch * S, Kc = in_channels * kernel_h * kernel_w;
+    const int64_t S = OH * OW, Kc = in_channels * kernel_h * kernel_w;
     if (batch == 0 || out_channels == 0 || S == 0) return CDX_OK;
     if (!output || !weight || (Kc > 0 && !input))
         return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: NULL pointer");
-    const size_t need = (size_t)Kc * (size_t)BS * sizeof(float);
+    const size_t per_image = (size_t)Kc * (size_t)S * sizeof(float);
+    const int64_t round = col_round_images(batch, per_image);
+    const size_t need = per_image * (size_t)round;
     float* col = static_cast<float*>(workspace);
     bool owned = false;
     if (workspace) {
@@ -406,17 +432,21 @@ int conv_forward_im2col(const float* input, const float* weight, const float* bi
         if (st) return st;
         owned = true;
     }
-    if (Kc > 0) {
-        st = cdx::launch_im2col_f32(input, col, batch, in_channels, in_h, in_w, kernel_h,
-                                    kernel_w, stride_h, stride_w, pad_h, pad_w, stream);
-    }
-    if (!st) {
-        // weight[OC, Kc] * col[Kc, B*S] -> NCHW: addr = oc*S + (n/S)*OC*S + n%S
-        cdx::GemmArgs g{CDX_OP_N, CDX_OP_N, out_channels, BS, Kc, weight, Kc > 0 ? Kc : 1,
-                        col, BS, output, S, S, out_channels * S,
-                        bias, bias ? CDX_BIAS_ROW : CDX_BIAS_NONE, CDX_EPI_NONE};
-        g.blocked_sum = blocked_sum;
-        st = run_gemm(precision, g, stream);
+    for (int64_t b0 = 0; b0 < batch && !st; b0 += round) {
+        const int64_t nb = batch - b0 < round ? batch - b0 : round, ns = nb * S;
+        if (Kc > 0) {
+            st = cdx::launch_im2col_f32(input + b0 * in_channels * in_h * in_w, col, nb,
+                                        in_channels, in_h, in_w, kernel_h, kernel_w, stride_h,
+                                        stride_w, pad_h, pad_w, stream);
+        }
+        if (!st) {
+            // weight[OC, Kc] * col[Kc, nb*S] -> NCHW: addr = oc*S + (n/S)*OC*S + n%S
+            cdx::GemmArgs g{CDX_OP_N, CDX_OP_N, out_channels, ns, Kc, weight, Kc > 0 ? Kc : 1,
+                            col, ns, output + b0 * out_channels * S, S, S, out_channels * S,
+                            bias, bias ? CDX_BIAS_ROW : CDX_BIAS_NONE, CDX_EPI_NONE};
+            g.blocked_sum = blocked_sum;
+            st = run_gemm(precision, g, stream);
+        }
     }
     if (owned) {
         int st2 = cdx::stream_free(col, stream, "cdx_conv2d_forward_f32: scratch");
@@ -665,10 +695,12 @@ size_t cdx_conv2d_backward_data_workspace_size(int64_t batch, int64_t in_channel
                         stride_h, stride_w, pad_h, pad_w))   // flipped filter only
         return (size_t)in_channels * out_channels * (size_t)(kernel_h * kernel_w) * sizeof(float);
     if (bwd_data_as_forward(out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w)) {
-        // flipped filter [IC, OC, KH, KW] + im2col of grad_out [OC*KH*KW, B*IH*IW]
+        // flipped filter [IC, OC, KH, KW] + one round's im2col of grad_out
+        // [OC*KH*KW, nb*IH*IW] (the forward column route on the transposed conv)
         const size_t khw = (size_t)(kernel_h * kernel_w);
-        return ((size_t)in_channels * out_channels * khw +
-                (size_t)out_channels * khw * (size_t)(batch * in_h * in_w)) * sizeof(float);
+        return (size_t)in_channels * out_channels * khw * sizeof(float) +
+               col_round_bytes(batch, out_channels, z.OH, z.OW, kernel_h, kernel_w, 1, 1,
+                               kernel_h - 1 - pad_h, kernel_w - 1 - pad_w);
     }
     // grad_col [Kc, BS] + (batch > 1) grad_out in [OC, BS]
     size_t n = (size_t)z.Kc * z.BS + (batch > 1 ? (size_t)out_channels * z.BS : 0);
