@@ -8,9 +8,12 @@ with A, B, C resident in HBM.  The same run also reports, under "extra":
 TF32-mode (bf16x3) GEMM at 2048^3 / 4096^3 (C3), the MLP Linear stack (C4)
 and the im2col + GEMM Conv2d (C5).
 
-Timing: W untimed warmup steps, then K steps bracketed by
-torch.cuda.synchronize(); kernel durations come from HIP events recorded on
-the stream the library launches on (torch's current stream).
+Timing: W untimed warmup steps, then K back-to-back steps between one HIP
+event pair recorded on the stream the library launches on (torch's current
+stream), bracketed by torch.cuda.synchronize().  The headline's roofline
+figure divides the FLOPs of one launch by the timed region's duration over
+K (its average launch duration); per-launch event pairs, timed after the
+region, are reported beside it.
 
 cpu_baseline: the repo's host reference SGEMM (oracle/, the sequential-FMA
 restatement of the reference SGEMM, OpenMP over all host cores) timed on
@@ -61,11 +64,17 @@ def parse():
     return p.parse_args()
 
 
-def time_launches(fn, steps, warmup, min_warm_s=0.0):
+def time_launches(fn, steps, warmup, min_warm_s=0.0, per_call=False):
     """Runs fn() warmup times (and, with min_warm_s, keeps going in batches
-    of 10 until that much wall time has passed), then `steps` times with a
-    HIP event pair around each launch on the current stream.  Returns (mean
-    ms per step from the bracketing events, list of per-launch ms)."""
+    of 10 until that much wall time has passed), then times exactly `steps`
+    back-to-back calls between one HIP event pair on the current stream,
+    with a device synchronisation on both sides.  Returns (mean ms per step,
+    per-launch ms list or None).  per_call: afterwards, `steps` more calls,
+    each between an event pair of its own, give per-launch durations.  Those
+    calls are not the timed region: on this runtime a timing event recorded
+    between two calls leaves the GPU idle for 6-10 us (C5 conv route in TF32
+    mode: 109 us per call with a pair per call, 100 us without; 4096^3 FP32
+    GEMM: 987 against 981 us)."""
     import torch
     t0 = time.perf_counter()
     for _ in range(warmup):
@@ -75,20 +84,25 @@ def time_launches(fn, steps, warmup, min_warm_s=0.0):
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
     outer0 = torch.cuda.Event(enable_timing=True)
     outer1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     outer0.record()
+    for _ in range(steps):
+        fn()
+    outer1.record()
+    torch.cuda.synchronize()
+    ms = outer0.elapsed_time(outer1) / steps
+    if not per_call:
+        return ms, None
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
     for e0, e1 in evs:
         e0.record()
         fn()
         e1.record()
-    outer1.record()
     torch.cuda.synchronize()
-    per = [e0.elapsed_time(e1) for e0, e1 in evs]
-    return outer0.elapsed_time(outer1) / steps, per
+    return ms, [e0.elapsed_time(e1) for e0, e1 in evs]
 
 
 def per_launch_ms(steps, warmup, fn, reps=20):
@@ -121,7 +135,7 @@ def bench_gemm(n, precision, steps, warmup, seed, min_warm_s=0.0):
     else:
         def f():
             ops.gemm(A, B, precision=precision, out=C)
-    ms, per = time_launches(f, steps, warmup, min_warm_s)
+    ms, per = time_launches(f, steps, warmup, min_warm_s, per_call=True)
     flops = 2.0 * n ** 3
     return {"n": n, "ms_per_step": ms, "kernel_ms_mean": statistics.mean(per),
             "kernel_ms_median": statistics.median(per),
@@ -138,7 +152,8 @@ def bench_gemm16(n, dtype, steps, warmup, seed, min_warm_s=0.0):
     A = torch.randn((n, n), device="cuda", generator=g).to(td)
     B = torch.randn((n, n), device="cuda", generator=g).to(td)
     C = torch.empty((n, n), device="cuda")
-    ms, per = time_launches(lambda: ops.gemm16(A, B, out=C), steps, warmup, min_warm_s)
+    ms, per = time_launches(lambda: ops.gemm16(A, B, out=C), steps, warmup, min_warm_s,
+                            per_call=True)
     flops = 2.0 * n ** 3
     return {"n": n, "ms_per_step": ms, "kernel_ms_median": statistics.median(per),
             "tflops": flops / (ms * 1e-3) / 1e12,
@@ -603,7 +618,9 @@ def main():
         cpu = cpu_baseline()
         log("cpu:", cpu)
 
-    achieved = 2.0 * 4096 ** 3 / (head["kernel_ms_mean"] * 1e-3) / 1e12
+    # average launch duration of the headline kernel over the timed region
+    # (K launches of cdx_sgemm_f32's one kernel, back to back)
+    achieved = 2.0 * 4096 ** 3 / (head["ms_per_step"] * 1e-3) / 1e12
     # HBM bytes per launch of the headline kernel, measured offline with two
     # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a plain-copy
     # calibration; see profiles/gemm_f32_4096_pmc_traffic.md.

@@ -140,19 +140,33 @@ size_t col_bytes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_t KH, 
 }
 
 // Images per im2col + GEMM round of the column route: the whole batch while
-// its column buffer stays within 128 MiB, else equal rounds below that.  A
-// round's buffer, input and output then stay in the 256 MB Infinity Cache
-// between the im2col write and the GEMM read (C5, 32 x 64 x 56^2 3x3: two
-// rounds of 16 images, 116 MB of columns each -- 145 -> 139 us FP32, 118 ->
-// 106 us in TF32 mode; rounds of 8 images run the GEMM on too few tiles, 169
-// us).  The sums are the same: every output column is one image's.
+// its column buffer stays within 128 MiB, else rounds below that (the last
+// one takes the remainder).  A round's buffer, input and output then stay in
+// the 256 MB Infinity Cache between the im2col write and the GEMM read (C5,
+// 32 x 64 x 56^2 3x3, 231 MB of columns: 145 -> 139 us FP32 and 118 -> 106
+// us in TF32 mode with two rounds of 16 images).  Among round sizes from the
+// cap down to half of it, the one whose rounds need the fewest waves of GEMM
+// tiles over the 256 CUs is taken, the largest on a tie; tiles are counted
+// as the 64-column tiles of one 64-channel row (the output-channel-skinny
+// GEMM's; the size query does not see the channel count).  C5's rounds of
+// 16 run 784 tiles each, four waves where 3.06 are work, so 18 + 14 images
+// (882 + 686 tiles: 4 + 3 waves against 4 + 4).  The sums are the same:
+// every output column is one image's.
 constexpr size_t kColRoundBytes = (size_t)128 << 20;
 
-int64_t col_round_images(int64_t batch, size_t per_image_bytes) {
+int64_t col_round_images(int64_t batch, size_t per_image_bytes, int64_t pixels) {
     const size_t total = per_image_bytes * (size_t)batch;
     if (per_image_bytes == 0 || total <= kColRoundBytes) return batch;
-    const int64_t rounds = (int64_t)((total + kColRoundBytes - 1) / kColRoundBytes);
-    return (batch + rounds - 1) / rounds;
+    const int64_t cap = std::max<int64_t>(1, (int64_t)(kColRoundBytes / per_image_bytes));
+    auto waves = [&](int64_t nb) {
+        return cdx::ceil_div(cdx::ceil_div(nb * pixels, (int64_t)64), (int64_t)256);
+    };
+    int64_t best = cap, best_cost = -1;
+    for (int64_t r = cap; r >= std::max<int64_t>(1, cap / 2); --r) {
+        const int64_t cost = (batch / r) * waves(r) + (batch % r ? waves(batch % r) : 0);
+        if (best_cost < 0 || cost < best_cost) { best = r; best_cost = cost; }
+    }
+    return best;
 }
 
 // Workspace of the column route: one round's column buffer.
@@ -160,7 +174,8 @@ size_t col_round_bytes(int64_t batch, int64_t IC, int64_t IH, int64_t IW, int64_
                        int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW) {
     if (batch <= 0) return 0;
     const size_t per = col_bytes(1, IC, IH, IW, KH, KW, SH, SW, PH, PW);
-    return per * (size_t)col_round_images(batch, per);
+    const int64_t S = conv_out(IH, KH, SH, PH) * conv_out(IW, KW, SW, PW);
+    return per * (size_t)col_round_images(batch, per, S);
 }
 
 // The reference's forward dispatch (conv_kernel.cu:242-275) below its
@@ -419,7 +434,7 @@ int conv_forward_im2col(const float* input, const float* weight, const float* bi
     if (!output || !weight || (Kc > 0 && !input))
         return set_error(CDX_ERR_INVALID_ARG, "cdx_conv2d_forward_f32: NULL pointer");
     const size_t per_image = (size_t)Kc * (size_t)S * sizeof(float);
-    const int64_t round = col_round_images(batch, per_image);
+    const int64_t round = col_round_images(batch, per_image, S);
     const size_t need = per_image * (size_t)round;
     float* col = static_cast<float*>(workspace);
     bool owned = false;

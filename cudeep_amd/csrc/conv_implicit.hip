@@ -283,8 +283,12 @@ struct RfArgs {
 // PP: window positions per thread (CP <= 256 PP).  MASKED: a chunk has
 // padded taps or the last chunk has fewer than ICT channels, so some filter
 // values read are zeroed; otherwise every filter element read is in range
-// and used as loaded.
-template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL>
+// and used as loaded.  RUN (stride-1 columns, FN dividing OW): column n of
+// pixel block j is pixel s0 + FN*n + j instead of s0 + 16*j + n, so a
+// lane's FN pixels are consecutive in one output row and their window
+// addresses are one per-tap base plus the constants 4*j (the LDS reads'
+// immediate offsets): 4 address adds per 16-k group instead of 4*FN.
+template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN>
 __global__ __launch_bounds__(RF_NT)
 void conv_rowwin_kernel(RfArgs p) {
     constexpr int TN = 16 * FN;   // output pixels per tile
@@ -325,10 +329,12 @@ void conv_rowwin_kernel(RfArgs p) {
 
     // this lane's pixel offsets in the window (pixels past the image read
     // the tile's first pixel; their results are not stored)
+    // (RUN: a lane's run of FN pixels lies wholly inside or past the image,
+    // since S and the run's first pixel are multiples of FN)
     int base[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int s = s0 + 16 * j + l16;
+    for (int j = 0; j < (RUN ? 1 : FN); ++j) {
+        const int s = RUN ? s0 + FN * l16 : s0 + 16 * j + l16;
         const uint32_t sc = (uint32_t)(s < p.S ? s : s0);
         const uint32_t oh = div_u31(sc, p.div_ow);
         const int ow = (int)(sc - oh * (uint32_t)p.OW);
@@ -434,7 +440,7 @@ void conv_rowwin_kernel(RfArgs p) {
     int pb[FN];
     auto set_buffer = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) pb[j] = 4 * (buf + base[j]);
+        for (int j = 0; j < (RUN ? 1 : FN); ++j) pb[j] = 4 * (buf + base[j]);
     };
     auto compute = [&](const AFrag& a, int g) {
         const int4 o = *reinterpret_cast<const int4*>(off + 16 * g + 4 * lq);
@@ -450,10 +456,17 @@ void conv_rowwin_kernel(RfArgs p) {
             }
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (RUN) {
+                const float* src = reinterpret_cast<const float*>(lfb + pb[0] + oq[q]);
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                bv[j][q] = *reinterpret_cast<const float*>(lfb + pb[j] + oq[q]);
+                for (int j = 0; j < FN; ++j) bv[j][q] = src[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    bv[j][q] = *reinterpret_cast<const float*>(lfb + pb[j] + oq[q]);
+            }
+        }
         floatx4 (&tgt)[FN] = TWO_LEVEL ? part : acc;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -525,7 +538,7 @@ void conv_rowwin_kernel(RfArgs p) {
     float* yimg = p.y + (int64_t)b * p.img_y;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const int s = s0 + 16 * j + l16;
+        const int s = RUN ? s0 + FN * l16 + j : s0 + 16 * j + l16;
         if (s >= p.S) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -596,12 +609,20 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
     return best;
 }
 
+template <int FN, int PP, bool VECW, bool MASKED, bool RUN>
+void rowwin_go_run(const RfArgs& p, bool two_level, dim3 grid, size_t lds, hipStream_t stream) {
+    if (two_level)
+        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, true, RUN>), grid, dim3(RF_NT), lds, stream, p);
+    else
+        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, false, RUN>), grid, dim3(RF_NT), lds, stream, p);
+}
+
 template <int FN, int PP, bool VECW, bool MASKED>
 void rowwin_go(const RfArgs& p, bool two_level, dim3 grid, size_t lds, hipStream_t stream) {
-    if (two_level)
-        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, true>), grid, dim3(RF_NT), lds, stream, p);
+    if (p.SW == 1 && p.OW % FN == 0)
+        rowwin_go_run<FN, PP, VECW, MASKED, true>(p, two_level, grid, lds, stream);
     else
-        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, false>), grid, dim3(RF_NT), lds, stream, p);
+        rowwin_go_run<FN, PP, VECW, MASKED, false>(p, two_level, grid, lds, stream);
 }
 
 template <int FN, int PP>

@@ -79,14 +79,19 @@ def test_conv_argument_validation():
     assert _status("cdx_conv2d_forward_f32", fake, fake, None, fake, 1, 1, 1, 4, 4, 3, 3,
                    1, 1, 0, 0, 0, fake, 4, None) == L.CDX_ERR_WORKSPACE
     # workspace size query = K_col * OH * OW * 4 per image of a round: the whole
-    # batch while its column buffer fits 128 MiB, else equal rounds below it
-    # (C5: 231 MB -> two rounds of 16 images)
+    # batch while its column buffer fits 128 MiB, else rounds of at most 18
+    # C5 images (7.2 MB each), sized for whole waves of 64-column GEMM tiles:
+    # C5 32 -> 18 + 14 (882 + 686 tiles, 4 + 3 waves of 256; 16 + 16 needs 8),
+    # 33 -> 18 + 15 (17 + 16 needs 8 waves)
     assert L.lib().cdx_conv2d_forward_workspace_size(32, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
-        == 576 * 16 * 56 * 56 * 4
+        == 576 * 18 * 56 * 56 * 4
     assert L.lib().cdx_conv2d_forward_workspace_size(2, 3, 9, 9, 3, 3, 1, 1, 1, 1) \
         == 27 * 2 * 81 * 4
     assert L.lib().cdx_conv2d_forward_workspace_size(33, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
-        == 576 * 17 * 56 * 56 * 4
+        == 576 * 18 * 56 * 56 * 4
+    # 40 images -> 15 + 15 + 10 (3 + 3 + 2 waves; 18 + 18 + 4 needs 4 + 4 + 1)
+    assert L.lib().cdx_conv2d_forward_workspace_size(40, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
+        == 576 * 15 * 56 * 56 * 4
     # backward data, stride 1 (row-window implicit kernel): the flipped filter only
     assert L.lib().cdx_conv2d_backward_data_workspace_size(32, 64, 64, 56, 56, 3, 3, 1, 1, 1, 1) \
         == 64 * 64 * 9 * 4
