@@ -568,9 +568,6 @@ struct RfPlan {
 RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW, int64_t KH,
                    int64_t KW, int64_t SH, int64_t SW, int64_t PH, int64_t PW, bool two_level) {
     RfPlan best;
-    // workgroups one CU holds by registers (4 waves each): 4, or 3 with the
-    // two-level sum's second accumulator set
-    const int64_t by_regs = two_level ? 3 : 4;
     const int64_t OH = (IH + 2 * PH - KH) / SH + 1, OW = (IW + 2 * PW - KW) / SW + 1;
     const int64_t lim = INT32_MAX / 2;
     const int64_t S = OH * OW, khw = KH * KW;
@@ -585,6 +582,13 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
         const int64_t rows = std::min<int64_t>(OH, (OW - 1 + tn - 1) / OW + 1);
         const int64_t nr = (rows - 1) * SH + KH, wp = (OW - 1) * SW + KW, cp = nr * wp;
         if (cp > 4 * RF_NT) continue;   // at most 4 window positions per thread
+        // workgroups per CU the registers allow (4 waves each): 4 at <= 128
+        // VGPRs -- every one-level form, and the two-level forms with
+        // consecutive-pixel lanes except FN 8 with 4 window positions per
+        // thread -- else 3 (the other two-level forms: up to ~157 VGPRs)
+        const int pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
+        const bool run = SW == 1 && OW % fn == 0;
+        const int64_t by_regs = !two_level || (run && (fn <= 7 || pp <= 2)) ? 4 : 3;
         const int64_t wgs = batch * ceil_div(S, tn) * ceil_div(OC, RF_BM);
         const int64_t per_cu = ceil_div(wgs, 256);
         int64_t ict = 16;
@@ -601,7 +605,7 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
                 best_cost = cost;
                 best.fn = fn; best.ict = (int)ict; best.nr = (int)nr; best.wp = (int)wp;
                 best.kcp = (int)kcp; best.eb = (int)((ict + 1) * cp);
-                best.pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
+                best.pp = pp;
                 best.lds = (size_t)lds;
             }
         }
