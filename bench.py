@@ -38,6 +38,7 @@ FP32_PEAK_TFLOPS = 157.3      # MI355X dense FP32 MFMA
 BF16_PEAK_TFLOPS = 2516.6     # MI355X dense BF16 MFMA; bf16x3 logical ceiling = /3
 HEAD_SETTLE_S = 0.3           # untimed clock-settling launches before the headline
 HBM_PEAK_GBS = 8000.0
+MLP_SETTLE_S = 0.3            # untimed settling launches before each C4 step line
 
 
 def log(*a):
@@ -230,8 +231,12 @@ def bench_mlp(steps, warmup, precision):
         bwd_layer1()
         bwd_dx()
 
-    fwd_ms, _ = time_launches(fwd, steps, warmup)
-    bwd_ms, _ = time_launches(bwd, steps, warmup)
+    # (each step line keeps launching untimed for MLP_SETTLE_S after its warmup:
+    # the first C4 lines of a process otherwise read ~10 us per step slower, for
+    # a few hundred ms after the previous line's load, with every kernel's own
+    # graph-timed duration unchanged)
+    fwd_ms, _ = time_launches(fwd, steps, warmup, min_warm_s=MLP_SETTLE_S)
+    bwd_ms, _ = time_launches(bwd, steps, warmup, min_warm_s=MLP_SETTLE_S)
     fwd_flops = 2.0 * 8192 * (784 * 256 + 256 * 10)
     bwd_flops = 2 * fwd_flops
 
@@ -251,7 +256,7 @@ def bench_mlp(steps, warmup, precision):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
-    graph_ms, _ = time_launches(graph.replay, steps, warmup)
+    graph_ms, _ = time_launches(graph.replay, steps, warmup, min_warm_s=MLP_SETTLE_S)
 
     # The same step with its independent branches on two side streams, each
     # launch on its own workspace: with the output gradient dY2 given, layer
@@ -282,7 +287,7 @@ def bench_mlp(steps, warmup, precision):
     graph2 = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph2):
         step_forked()
-    graph2_ms, _ = time_launches(graph2.replay, steps, warmup)
+    graph2_ms, _ = time_launches(graph2.replay, steps, warmup, min_warm_s=MLP_SETTLE_S)
     # the big forward GEMM and the two narrow products on their own, each as
     # a HIP graph of 20 back-to-back launches (kernel time, not the ~20 us
     # per-launch host cost of an eager ctypes call)
@@ -301,7 +306,7 @@ def bench_mlp(steps, warmup, precision):
             "step_graph_forked_tflops": (fwd_flops + bwd_flops) / (graph2_ms * 1e-3) / 1e12,
             "fwd1_fused_ms": l1_ms,
             "fwd1_fused_tflops": 2.0 * 8192 * 784 * 256 / (l1_ms * 1e-3) / 1e12,
-            "fwd2_ms": l2_ms, "dh_masked_ms": dh_ms}
+            "fwd2_ms": l2_ms, "dh_masked_ms": dh_ms, "settle_s": MLP_SETTLE_S}
 
 
 def bench_mlp_api(steps, warmup, precision):
