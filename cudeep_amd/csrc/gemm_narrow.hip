@@ -272,22 +272,24 @@ SkinnyPlan skinny_plan(const GemmArgs& g) {
 // the slice contribute exact zeros (both factors zeroed, so no Inf * 0).
 constexpr int SM_U = 8;   // rows per thread in flight
 
-// acc[m][c] += op(A)(m, k) * b[c] for m = M .. 15, op(A)(m, k) taken from
+// acc[m][c] += op(A)(m, k) * b[c] for m = M .. MT-1, op(A)(m, k) taken from
 // lane m of this lane's 16-lane row (DPP row_newbcast:m, control 0x150 + m).
-template <int M>
-__device__ __forceinline__ void skinny_fma_rows(float (&acc)[16][4], int a_bits, const float (&b)[4]) {
-    if constexpr (M < 16) {
+template <int M, int MT>
+__device__ __forceinline__ void skinny_fma_rows(float (&acc)[MT][4], int a_bits, const float (&b)[4]) {
+    if constexpr (M < MT) {
         const float am = __int_as_float(__builtin_amdgcn_update_dpp(0, a_bits, 0x150 + M, 0xf, 0xf, false));
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[M][c] = fmaf(am, b[c], acc[M][c]);
-        skinny_fma_rows<M + 1>(acc, a_bits, b);
+        skinny_fma_rows<M + 1, MT>(acc, a_bits, b);
     }
 }
-template <int OPA>
+// MT: rows computed, M rounded up to 4, 8, 12 or 16 (rows past M are
+// computed from row M-1 and never stored).
+template <int OPA, int MT>
 __global__ __launch_bounds__(256)
 void gemm_skinny_m_partial_kernel(NarrowArgs p, int64_t nb, int64_t ones_col, int64_t kc,
                                   float* __restrict__ P) {
-    __shared__ float red[4][16][SM_COLS];
+    __shared__ float red[4][MT][SM_COLS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c4 = tid & 15, rg = tid >> 4;
     const int64_t n0 = (int64_t)blockIdx.x * SM_COLS + 4 * c4;
@@ -295,9 +297,9 @@ void gemm_skinny_m_partial_kernel(NarrowArgs p, int64_t nb, int64_t ones_col, in
     const int64_t ke = kb + kc < p.K ? kb + kc : p.K;
     const int64_t ma = c4 < p.M ? c4 : p.M - 1;
     const bool whole = p.vec_b && n0 + 3 < nb;
-    float acc[16][4];
+    float acc[MT][4];
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
     for (int64_t k0 = kb + rg; k0 < ke; k0 += 16 * SM_U) {
@@ -323,11 +325,11 @@ void gemm_skinny_m_partial_kernel(NarrowArgs p, int64_t nb, int64_t ones_col, in
             a[u] = ok ? av : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < SM_U; ++u) skinny_fma_rows<0>(acc, __float_as_int(a[u]), b[u]);
+        for (int u = 0; u < SM_U; ++u) skinny_fma_rows<0, MT>(acc, __float_as_int(a[u]), b[u]);
     }
     // the wave's 4 row groups (lanes 16 apart hold the same columns)
 #pragma unroll
-    for (int m = 0; m < 16; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float v = acc[m][c];
@@ -337,7 +339,7 @@ void gemm_skinny_m_partial_kernel(NarrowArgs p, int64_t nb, int64_t ones_col, in
         }
     if (lane < 16) {
 #pragma unroll
-        for (int m = 0; m < 16; ++m)
+        for (int m = 0; m < MT; ++m)
             if (m < p.M) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) red[wave][m][4 * lane + c] = acc[m][c];
@@ -406,6 +408,24 @@ int narrow_kind(const GemmArgs& g) {
     return 0;
 }
 
+namespace {
+
+// the partial kernel for M rounded up to mt rows
+template <int OPA>
+void skinny_partial_go(int mt, dim3 grid, hipStream_t stream, const NarrowArgs& p, int64_t nb,
+                       int64_t ones_col, int64_t kc, float* part) {
+    if (mt == 4)
+        hipLaunchKernelGGL((gemm_skinny_m_partial_kernel<OPA, 4>), grid, dim3(256), 0, stream, p, nb, ones_col, kc, part);
+    else if (mt == 8)
+        hipLaunchKernelGGL((gemm_skinny_m_partial_kernel<OPA, 8>), grid, dim3(256), 0, stream, p, nb, ones_col, kc, part);
+    else if (mt == 12)
+        hipLaunchKernelGGL((gemm_skinny_m_partial_kernel<OPA, 12>), grid, dim3(256), 0, stream, p, nb, ones_col, kc, part);
+    else
+        hipLaunchKernelGGL((gemm_skinny_m_partial_kernel<OPA, 16>), grid, dim3(256), 0, stream, p, nb, ones_col, kc, part);
+}
+
+}  // namespace
+
 size_t skinny_m_workspace(const GemmArgs& g) {
     return (size_t)skinny_plan(g).slices * (size_t)g.M * (size_t)g.N * sizeof(float);
 }
@@ -424,12 +444,9 @@ static int launch_skinny_m(const GemmArgs& g, const NarrowArgs& p, hipStream_t s
         st = stream_alloc(reinterpret_cast<void**>(&part), bytes, stream, "gemm skinny-M scratch");
         if (st) return st;
     }
-    if (g.opA == CDX_OP_N)
-        hipLaunchKernelGGL(gemm_skinny_m_partial_kernel<CDX_OP_N>, grid1, dim3(256), 0, stream, p,
-                           nb, g.ones_col, sp.kc, part);
-    else
-        hipLaunchKernelGGL(gemm_skinny_m_partial_kernel<CDX_OP_T>, grid1, dim3(256), 0, stream, p,
-                           nb, g.ones_col, sp.kc, part);
+    const int mt = g.M <= 4 ? 4 : g.M <= 8 ? 8 : g.M <= 12 ? 12 : 16;
+    if (g.opA == CDX_OP_N) skinny_partial_go<CDX_OP_N>(mt, grid1, stream, p, nb, g.ones_col, sp.kc, part);
+    else skinny_partial_go<CDX_OP_T>(mt, grid1, stream, p, nb, g.ones_col, sp.kc, part);
     st = hip_error(hipGetLastError(), "gemm_skinny_m_partial_kernel launch");
     if (!st) {
         const EpiArgs e{g.C, g.ldc, g.M, g.N, g.n_split, g.ldc_split, g.bias, g.bias_mode,
