@@ -536,15 +536,36 @@ void conv_rowwin_kernel(RfArgs p) {
     // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
     // column l % 16; output (oc, s) -> y[b][oc][s] + bias[oc]
     float* yimg = p.y + (int64_t)b * p.img_y;
+    if constexpr (RUN) {
+        // (a lane's pixels are FN apart across its 16-lane row: the tile goes
+        // through LDS -- [64 channels][TN pixels] at a pitch of TN + 1 -- so
+        // that each store instruction writes consecutive pixels of a row)
+        constexpr int TP = TN + 1;
+        float* tile = reinterpret_cast<float*>(rf_smem);
+        __syncthreads();   // every wave's last window reads are done
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int s = RUN ? s0 + FN * l16 + j : s0 + 16 * j + l16;
-        if (s >= p.S) continue;
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int oc = oc0 + wm0 + 4 * lq + r;
-            if (oc < p.OC)
-                yimg[(int64_t)oc * p.S + s] = acc[j][r] + (p.bias ? p.bias[oc] : 0.0f);
+            for (int r = 0; r < 4; ++r) tile[(wm0 + 4 * lq + r) * TP + FN * l16 + j] = acc[j][r];
+        __syncthreads();
+        const int npx = p.S - s0 < TN ? p.S - s0 : TN;
+        for (int i = tid; i < RF_BM * TN; i += RF_NT) {
+            const int ocl = i / TN, px = i - ocl * TN;
+            const int oc = oc0 + ocl;
+            if (px < npx && oc < p.OC)
+                yimg[(int64_t)oc * p.S + s0 + px] = tile[ocl * TP + px] + (p.bias ? p.bias[oc] : 0.0f);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int s = s0 + 16 * j + l16;
+            if (s >= p.S) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int oc = oc0 + wm0 + 4 * lq + r;
+                if (oc < p.OC)
+                    yimg[(int64_t)oc * p.S + s] = acc[j][r] + (p.bias ? p.bias[oc] : 0.0f);
+            }
         }
     }
 }
@@ -595,7 +616,9 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
         while (ict > 1 && ict / 2 >= IC) ict /= 2;
         for (; ict >= 1; ict /= 2) {
             const int64_t kcp = ceil_div(ict * khw, 16) * 16;
-            const int64_t lds = (kcp + 2 * (ict + 1) * cp) * 4;
+            // (consecutive-pixel lanes stage the output tile through LDS too)
+            const int64_t lds = std::max<int64_t>((kcp + 2 * (ict + 1) * cp) * 4,
+                                                  run ? (int64_t)RF_BM * (tn + 1) * 4 : 0);
             if (lds > RF_LDS_MAX || kcp > RF_KCP_MAX) continue;
             const int64_t resident = std::min<int64_t>(by_regs, (160 * 1024) / lds);
             const double cost = (double)per_cu * tn * ((double)kcp / (double)(ict * khw)) *
