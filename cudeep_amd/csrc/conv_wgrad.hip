@@ -397,9 +397,23 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     const int wm0 = (wave / TL::WAVES_N) * 16 * FMW, wn0 = (wave % TL::WAVES_N) * 16 * JB;
 
     const int tiles_n = (int)ceil_div(p.IC, ICT);
-    const int64_t bm = (int64_t)(blockIdx.x / tiles_n) * RW_BM;
-    const int64_t bic = (int64_t)(blockIdx.x % tiles_n) * ICT;
-    const int r_begin = blockIdx.y * p.rows_chunk;
+    // Workgroups go to the 8 XCDs round-robin by linear id.  Where the grid
+    // allows, the ids are renumbered so that every tile of a k-slice runs on
+    // one XCD: the tiles of a slice read the same dY rows, which its L2 then
+    // fetches once instead of once per tile.
+    uint32_t tile = blockIdx.x, slice = blockIdx.y;
+    {
+        const uint32_t total = gridDim.x * gridDim.y, per_xcd = total / 8;
+        if (total % 8 == 0 && per_xcd % gridDim.x == 0) {
+            const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
+            const uint32_t l = (lin % 8) * per_xcd + lin / 8;
+            tile = l % gridDim.x;
+            slice = l / gridDim.x;
+        }
+    }
+    const int64_t bm = (int64_t)(tile / tiles_n) * RW_BM;
+    const int64_t bic = (int64_t)(tile % tiles_n) * ICT;
+    const int r_begin = slice * p.rows_chunk;
     const int r_end = min(p.rows_total, r_begin + p.rows_chunk);
     const int nk = r_end - r_begin;
 
@@ -691,7 +705,7 @@ void conv_wgrad_rows_kernel(RwArgs p) {
 
     // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
     // column l % 16
-    float* out = p.out + (int64_t)blockIdx.y * p.OC * p.Kc;
+    float* out = p.out + (int64_t)slice * p.OC * p.Kc;
 #pragma unroll
     for (int i = 0; i < FMW; ++i)
 #pragma unroll
