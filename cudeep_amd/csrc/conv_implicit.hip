@@ -301,10 +301,22 @@ void conv_rowwin_kernel(RfArgs p) {
     const int l16 = lane & 15, lq = lane >> 4;
     const int wm0 = wave * 16;   // each wave: 16 output channels x the tile's TN pixels
 
-    const uint32_t bx = blockIdx.x;
+    // Workgroups go to the 8 XCDs round-robin by linear id; where the grid
+    // allows, the ids are renumbered so that consecutive pixel tiles (whose
+    // windows share halo rows) run on one XCD and share its L2.
+    uint32_t bx = blockIdx.x, by = blockIdx.y;
+    {
+        const uint32_t total = gridDim.x * gridDim.y, per_xcd = total / 8;
+        if (total % 8 == 0) {
+            const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
+            const uint32_t l = (lin % 8) * per_xcd + lin / 8;
+            bx = l % gridDim.x;
+            by = l / gridDim.x;
+        }
+    }
     const uint32_t b = div_u31(bx, p.div_tiles);
     const int s0 = (int)(bx - b * (uint32_t)p.tiles_img) * TN;
-    const int oc0 = blockIdx.y * RF_BM;
+    const int oc0 = by * RF_BM;
     const int oh_lo = (int)div_u31((uint32_t)s0, p.div_ow);
     const float* ximg = p.x + (int64_t)b * p.img_x;
 
