@@ -197,6 +197,41 @@ def test_conv_implicit_parity(g):
     assert e0 <= 2 * e0_ref + 2.0 ** -24, (e0, e0_ref)
 
 
+@pytest.mark.parametrize("g", [
+    (1, 17, 9, 40, 10, 3, 3, 1, 1, 1, 1),     # OW 40: 8 and 5 divide it; 17 channels: masked chunk
+    (3, 64, 13, 56, 64, 3, 3, 1, 1, 1, 1),    # OW 56 (C5's width): 8 and 7; tiles run past S
+    (2, 3, 11, 35, 100, 3, 3, 1, 1, 1, 1),    # OW 35: 7 and 5; 3 channels, 100 output channels
+    (2, 24, 7, 70, 33, 5, 5, 1, 1, 2, 2),     # 5x5, OW 70: 7 and 5; 2 + 4 halo rows
+    (1, 40, 6, 120, 64, 3, 3, 1, 1, 1, 1),    # OW 120: 8 and 5; wider window, more positions per thread
+    (2, 8, 10, 56, 16, 3, 3, 1, 1, 0, 1),     # no vertical padding
+])
+def test_rowwin_consecutive_pixel_lanes(g):
+    """Stride-1 layers whose output width the row-window kernel's pixel-block
+    count divides: each lane then takes consecutive pixels of one output row
+    and reads them at immediate offsets, with the output tile staged through
+    LDS.  The implicit forward (one-level k sum) and the stride-1 backward
+    data through the same kernel (two-level sum, the flipped filter) both
+    pass the gates of the other geometries: <= 2 x the reference routes'
+    errors against fp64."""
+    Bn, C, H, W, OC, KH, KW, SH, SW, PH, PW = g
+    rng = np.random.default_rng(900 + sum(g))
+    x = normal(rng, (Bn, C, H, W))
+    w = normal(rng, (OC, C, KH, KW), std=np.sqrt(2.0 / (C * KH * KW)))
+    b = normal(rng, (OC,), 0.1)
+    st, pd = (SH, SW), (PH, PW)
+    say("conv rowwin consecutive lanes", g)
+    y = host(ops().conv2d_implicit(dev(x), dev(w), dev(b), st, pd))
+    e, e_ref = _implicit_gate(x, w, b, st, pd, y)
+    assert e <= 2 * e_ref + 2.0 ** -24, (e, e_ref)
+    OH = oracle.conv_out_size(H, KH, SH, PH)
+    OW = oracle.conv_out_size(W, KW, SW, PW)
+    dy = normal(rng, (Bn, OC, OH, OW))
+    dx = host(ops().conv2d_backward_data(dev(dy), dev(w), x.shape, st, pd))
+    dx64 = oracle.conv2d_backward_data64(dy, w, x.shape, st, pd)
+    ex_ref = oracle.rel_fro(oracle.conv2d_backward_data_ref(dy, w, x.shape, st, pd), dx64)
+    assert oracle.rel_fro(dx, dx64) <= 2 * ex_ref + 2.0 ** -24
+
+
 @pytest.mark.parametrize("name", ["conv_identity_1x1", "conv_3x3_ones", "conv_3x3_bias",
                                   "conv_3x3_pad1"])
 def test_conv_implicit_kats(kats, name):
