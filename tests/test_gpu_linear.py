@@ -263,12 +263,14 @@ def test_weight_grad_with_fused_bias_grad(M, N, K, prec):
 @pytest.mark.parametrize("M,N,K,transA", [(1, 100, 5000, True), (16, 4096, 1024, False),
                                           (7, 33, 2049, True), (12, 520, 70000, True),
                                           (16, 64, 1024, False), (10, 257, 8191, True),
-                                          (5, 37, 3001, False)])
+                                          (5, 37, 3001, False), (4, 100, 2048, True),
+                                          (8, 64, 1500, False), (13, 129, 1024, True)])
 @pytest.mark.parametrize("prec", [0, 1])
 def test_skinny_m_long_k(M, N, K, transA, prec):
     """M <= 16 with K >= 1024 (the 10-wide layer's weight-gradient shape): the
-    split-K FMA kernel and its slice reduction -- ragged and unaligned
-    widths, op(A) either way, the slice cap (K = 70000), with the ones
+    split-K FMA kernel (its row count M rounded up to 4, 8, 12 or 16, each
+    with M at and off the boundary) and its slice reduction -- ragged and
+    unaligned widths, op(A) either way, the slice cap (K = 70000), with the ones
     column (bias gradient) on a caller workspace, and with a bias + ReLU
     epilogue applied by the reduction."""
     import torch
