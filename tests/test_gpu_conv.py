@@ -152,6 +152,26 @@ def test_conv_c5_full_batch_sampled(prec):
             assert e <= min(errs)
 
 
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_c5_rounds_same_bits_as_single_images(prec):
+    """The im2col route runs C5's 32 images in rounds (18 + 14: column
+    buffers within 128 MiB): images on either side of the round boundary
+    come out bit for bit as when each image is convolved alone (one round,
+    one GEMM of 3136 columns), since every output column's k-sum is one
+    image's in the same order."""
+    rng = np.random.default_rng(5151)
+    x = normal(rng, (32, 64, 56, 56))
+    w = normal(rng, (64, 64, 3, 3), std=np.sqrt(2.0 / 576))
+    b = normal(rng, (64,), 0.1)
+    say("conv C5 rounds vs single images prec", prec)
+    gx, gw, gb = dev(x), dev(w), dev(b)
+    y = host(ops().conv2d_forward(gx, gw, gb, (1, 1), (1, 1), precision=prec))
+    for i in (0, 17, 18, 31):
+        yi = host(ops().conv2d_forward(gx[i:i + 1].contiguous(), gw, gb, (1, 1), (1, 1),
+                                       precision=prec))
+        assert np.array_equal(yi[0].view(np.uint32), y[i].view(np.uint32)), i
+
+
 IMPLICIT_GEOMS = [  # (B, C, H, W, OC, KH, KW, SH, SW, PH, PW)
     (2, 3, 20, 21, 32, 7, 7, 1, 1, 3, 3),      # 7x7 stem-like, Kc = 147 (% 4 != 0)
     (2, 5, 11, 13, 70, 5, 5, 2, 2, 2, 2),      # OC > one 64-channel tile
