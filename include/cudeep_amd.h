@@ -213,15 +213,18 @@ int cdx_im2col_f32(const float* input, float* col,
                    int64_t stride_h, int64_t stride_w,
                    int64_t pad_h, int64_t pad_w, hipStream_t stream);
 
-/* Bytes of workspace cdx_conv2d_forward_f32 needs: the im2col buffer, or 0
- * for layers it sends to the implicit GEMM (see below). */
+/* Bytes of workspace cdx_conv2d_forward_f32 needs: the im2col buffer of one
+ * round of images (the whole batch while its buffer stays within 128 MiB,
+ * else rounds below that sized for whole waves of GEMM tiles), or 0 for
+ * layers it sends to the implicit GEMM (see below). */
 size_t cdx_conv2d_forward_workspace_size(
     int64_t batch, int64_t in_channels, int64_t in_h, int64_t in_w,
     int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
     int64_t pad_h, int64_t pad_w);
 
 /* NCHW conv forward: im2col -> one GEMM weight[OC,K_col] * col -> NCHW
- * output with the bias added in the GEMM epilogue (no transpose pass).
+ * output with the bias added in the GEMM epilogue (no transpose pass), per
+ * round of images (same sums as one pass over the batch).
  * Layers whose column buffer would exceed 4 MiB, other than 3x3 stride-1
  * layers with >= 16 output pixels per image, run the implicit GEMM of
  * cdx_conv2d_forward_implicit_f32 instead (no workspace), as the reference
