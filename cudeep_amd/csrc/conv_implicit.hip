@@ -278,6 +278,10 @@ struct RfArgs {
     int nchunks, tiles_img;
     int64_t img_x, img_y;     // IC*IH*IW, OC*S
     DivMagic div_ow, div_wp, div_tiles, div_khw, div_kw;
+    // split last round (RUN forms, one channel block): workgroups
+    // [0, n_full) take whole tiles, [n_full, n_full + n_half) half tiles
+    // (tile n_full + h/2, output channels 32 (h%2) .. +32); n_full = 0: off
+    uint32_t n_full, n_half;
 };
 
 // PP: window positions per thread (CP <= 256 PP).  MASKED: a chunk has
@@ -288,9 +292,17 @@ struct RfArgs {
 // lane's FN pixels are consecutive in one output row and their window
 // addresses are one per-tap base plus the constants 4*j (the LDS reads'
 // immediate offsets): 4 address adds per 16-k group instead of 4*FN.
-template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN>
-__global__ __launch_bounds__(RF_NT)
-void conv_rowwin_kernel(RfArgs p) {
+//
+// HALF: the workgroup takes half a tile -- output channels 32 * oc_half ..
+// +32 -- and its waves split each 16-k group's four MFMA k-steps: wave w
+// computes channels 16 (w & 1) .. +16 over k-steps 2 (w >> 1) and
+// 2 (w >> 1) + 1, and the two halves of every output are added in the
+// epilogue (k-steps 0-1 + k-steps 2-3).  A last round of 2r half tiles
+// instead of r whole ones puts 3.5 tiles' MFMA work on every CU at C5
+// (896 tiles on 256 CUs) where whole tiles put 4 on half of them.
+template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN, bool HALF>
+__device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32_t by,
+                                            int oc_half) {
     constexpr int TN = 16 * FN;   // output pixels per tile
     // LDS: tap byte offsets [KCP] | window buffer 0 [EB] | window buffer 1 [EB]
     extern __shared__ __attribute__((aligned(16))) int rf_smem[];
@@ -299,21 +311,11 @@ void conv_rowwin_kernel(RfArgs p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lq = lane >> 4;
-    const int wm0 = wave * 16;   // each wave: 16 output channels x the tile's TN pixels
+    // each wave: 16 output channels x the tile's TN pixels (HALF: over half
+    // of the k-steps)
+    const int wm0 = HALF ? 32 * oc_half + 16 * (wave & 1) : wave * 16;
+    const int hq = HALF ? wave >> 1 : 0;
 
-    // Workgroups go to the 8 XCDs round-robin by linear id; where the grid
-    // allows, the ids are renumbered so that consecutive pixel tiles (whose
-    // windows share halo rows) run on one XCD and share its L2.
-    uint32_t bx = blockIdx.x, by = blockIdx.y;
-    {
-        const uint32_t total = gridDim.x * gridDim.y, per_xcd = total / 8;
-        if (total % 8 == 0) {
-            const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
-            const uint32_t l = (lin % 8) * per_xcd + lin / 8;
-            bx = l % gridDim.x;
-            by = l / gridDim.x;
-        }
-    }
     const uint32_t b = div_u31(bx, p.div_tiles);
     const int s0 = (int)(bx - b * (uint32_t)p.tiles_img) * TN;
     const int oc0 = by * RF_BM;
@@ -454,6 +456,34 @@ void conv_rowwin_kernel(RfArgs p) {
 #pragma unroll
         for (int j = 0; j < (RUN ? 1 : FN); ++j) pb[j] = 4 * (buf + base[j]);
     };
+    auto compute_half = [&](const AFrag& a, int g) {
+        // k-steps 2 hq and 2 hq + 1 of the group (wave-uniform selects)
+        const int4 o = *reinterpret_cast<const int4*>(off + 16 * g + 4 * lq);
+        const int oq[2] = {hq ? o.z : o.x, hq ? o.w : o.y};
+        float av[2], bv[FN][2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float v = hq ? a.v[0][2 + q] : a.v[0][q];
+            if constexpr (MASKED) {
+                const float vo = opaque(v);
+                av[q] = (a.ok >> (2 * hq + q)) & 1 ? vo : 0.0f;
+            } else {
+                av[q] = v;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float* src = reinterpret_cast<const float*>(lfb + pb[0] + oq[q]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bv[j][q] = src[j];
+        }
+        floatx4 (&tgt)[FN] = TWO_LEVEL ? part : acc;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                tgt[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[q], bv[j][q], tgt[j], 0, 0, 0);
+    };
     auto compute = [&](const AFrag& a, int g) {
         const int4 o = *reinterpret_cast<const int4*>(off + 16 * g + 4 * lq);
         const int oq[4] = {o.x, o.y, o.z, o.w};
@@ -517,7 +547,8 @@ void conv_rowwin_kernel(RfArgs p) {
         // the slice stores, which wait for them, behind)
         slice_load(c + 1, g);
         __builtin_amdgcn_sched_barrier(0);
-        compute(a, g);
+        if constexpr (HALF) compute_half(a, g);
+        else compute(a, g);
         a_load(a);
         if (TWO_LEVEL && (gi & 1)) fold();
         __builtin_amdgcn_sched_barrier(0);
@@ -552,20 +583,26 @@ void conv_rowwin_kernel(RfArgs p) {
         // (a lane's pixels are FN apart across its 16-lane row: the tile goes
         // through LDS -- [64 channels][TN pixels] at a pitch of TN + 1 -- so
         // that each store instruction writes consecutive pixels of a row)
+        // (HALF: rows 0-31 hold k-steps 0-1 of the half tile's 32 channels,
+        // rows 32-63 k-steps 2-3)
         constexpr int TP = TN + 1;
         float* tile = reinterpret_cast<float*>(rf_smem);
         __syncthreads();   // every wave's last window reads are done
+        const int row0 = HALF ? 32 * hq + 16 * (wave & 1) : wm0;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) tile[(wm0 + 4 * lq + r) * TP + FN * l16 + j] = acc[j][r];
+            for (int r = 0; r < 4; ++r) tile[(row0 + 4 * lq + r) * TP + FN * l16 + j] = acc[j][r];
         __syncthreads();
         const int npx = p.S - s0 < TN ? p.S - s0 : TN;
-        for (int i = tid; i < RF_BM * TN; i += RF_NT) {
+        constexpr int ROWS = HALF ? RF_BM / 2 : RF_BM;
+        for (int i = tid; i < ROWS * TN; i += RF_NT) {
             const int ocl = i / TN, px = i - ocl * TN;
-            const int oc = oc0 + ocl;
+            const int oc = oc0 + (HALF ? 32 * oc_half : 0) + ocl;
+            float v = tile[ocl * TP + px];
+            if constexpr (HALF) v += tile[(ocl + 32) * TP + px];
             if (px < npx && oc < p.OC)
-                yimg[(int64_t)oc * p.S + s0 + px] = tile[ocl * TP + px] + (p.bias ? p.bias[oc] : 0.0f);
+                yimg[(int64_t)oc * p.S + s0 + px] = v + (p.bias ? p.bias[oc] : 0.0f);
         }
     } else {
 #pragma unroll
@@ -580,6 +617,31 @@ void conv_rowwin_kernel(RfArgs p) {
             }
         }
     }
+}
+
+template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN>
+__global__ __launch_bounds__(RF_NT)
+void conv_rowwin_kernel(RfArgs p) {
+    // Workgroups go to the 8 XCDs round-robin by linear id; where the grid
+    // allows, the ids are renumbered so that consecutive pixel tiles (whose
+    // windows share halo rows) run on one XCD and share its L2.
+    const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
+    auto xcd_order = [](uint32_t i, uint32_t n) {
+        return n % 8 == 0 ? (i % 8) * (n / 8) + i / 8 : i;
+    };
+    if constexpr (RUN) {
+        if (p.n_full > 0) {   // one channel block (gridDim.y == 1)
+            if (lin < p.n_full) {
+                rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, false>(p, xcd_order(lin, p.n_full), 0, 0);
+            } else {
+                const uint32_t u = xcd_order(lin - p.n_full, p.n_half);
+                rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, true>(p, p.n_full + u / 2, 0, (int)(u & 1));
+            }
+            return;
+        }
+    }
+    const uint32_t l = xcd_order(lin, gridDim.x * gridDim.y);
+    rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, false>(p, l % gridDim.x, l / gridDim.x, 0);
 }
 
 // Launch plan of the row-window form, or ok = false where no window fits
@@ -703,6 +765,19 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
     p.div_tiles = div_magic(p.tiles_img); p.div_khw = div_magic(p.KHW); p.div_kw = div_magic(KW);
     const bool vecw = p.Kc % 4 == 0 && p.kc_real % 4 == 0 && (uintptr_t)w % 16 == 0;
     const bool masked = IC % pl.ict != 0 || p.kc_real != p.KCP;
+    // Split last round (consecutive-pixel forms with one channel block, at
+    // most four tiles per CU so that all are resident at once): whole tiles
+    // for the whole rounds of 256 CUs, the remaining r <= 128 tiles as 2r
+    // half tiles, so no CU holds more than half a tile above the average.
+    p.n_full = p.n_half = 0;
+    {
+        const int64_t T = batch * p.tiles_img, rem = T % 256;
+        if (SW == 1 && OW % pl.fn == 0 && OC <= RF_BM && T > 256 && T <= 4 * 256 && rem > 0 &&
+            rem <= 128) {
+            p.n_full = (uint32_t)(T - rem);
+            p.n_half = (uint32_t)(2 * rem);
+        }
+    }
     const int64_t chunk = (int64_t)65535 * RF_BM;   // output channels per launch (grid y)
     for (int64_t oc0 = 0; oc0 < OC; oc0 += chunk) {
         const int64_t oc_n = OC - oc0 < chunk ? OC - oc0 : chunk;
@@ -710,7 +785,8 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
         p.w = w + oc0 * p.Kc;
         p.bias = bias ? bias + oc0 : nullptr;
         p.y = y + oc0 * p.S;
-        const dim3 grid((unsigned)(batch * p.tiles_img), (unsigned)ceil_div(oc_n, RF_BM));
+        const dim3 grid = p.n_full > 0 ? dim3(p.n_full + p.n_half, 1u)
+                                       : dim3((unsigned)(batch * p.tiles_img), (unsigned)ceil_div(oc_n, RF_BM));
         if (pl.fn == 8) rowwin_go_fn<8>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
         else if (pl.fn == 7) rowwin_go_fn<7>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
         else rowwin_go_fn<5>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);

@@ -286,6 +286,24 @@ def test_conv_forward_large_7x7_takes_implicit_route(prec):
     assert e <= 2 * e_ref
 
 
+def test_conv_implicit_c5_3x3_split_last_round():
+    """C5's 3x3 layer through the row-window implicit kernel: 896 tiles on
+    256 CUs run as 768 whole tiles plus the last 128 as 256 half tiles (32
+    output channels each, the four k-steps of every 16-k group split over
+    two waves and added in the epilogue).  Image 0 (whole tiles) and images
+    28 and 31 (half tiles) pass the implicit route's parity gate."""
+    rng = np.random.default_rng(7078)
+    x = normal(rng, (32, 64, 56, 56))
+    w = normal(rng, (64, 64, 3, 3), std=np.sqrt(2.0 / 576))
+    b = normal(rng, (64,), 0.1)
+    say("conv implicit C5 3x3")
+    y = host(ops().conv2d_implicit(dev(x), dev(w), dev(b), (1, 1), (1, 1)))
+    assert y.shape == (32, 64, 56, 56) and np.isfinite(y).all()
+    e, e_ref = _implicit_gate(x, w, b, (1, 1), (1, 1), y[[0, 28, 31]], batches=(0, 28, 31))
+    print(f"C5 3x3 implicit items 0, 28, 31: gpu={e:.3e} reference implicit route={e_ref:.3e}")
+    assert e <= 2 * e_ref
+
+
 def test_conv_workspace_and_no_bias():
     import torch
     rng = np.random.default_rng(77)
