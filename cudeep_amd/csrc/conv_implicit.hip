@@ -278,6 +278,7 @@ struct RfArgs {
     int nchunks, tiles_img;
     int64_t img_x, img_y;     // IC*IH*IW, OC*S
     DivMagic div_ow, div_wp, div_tiles, div_khw, div_kw;
+    int IW4;    // IW / 4 (vector staging)
     // split last round (RUN forms, one channel block): workgroups
     // [0, n_full) take whole tiles, [n_full, n_full + n_half) half tiles
     // (tile n_full + h/2, output channels 32 (h%2) .. +32); n_full = 0: off
@@ -300,7 +301,7 @@ struct RfArgs {
 // epilogue (k-steps 0-1 + k-steps 2-3).  A last round of 2r half tiles
 // instead of r whole ones puts 3.5 tiles' MFMA work on every CU at C5
 // (896 tiles on 256 CUs) where whole tiles put 4 on half of them.
-template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN, bool HALF>
+template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN, bool VST, bool HALF>
 __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32_t by,
                                             int oc_half) {
     constexpr int TN = 16 * FN;   // output pixels per tile
@@ -336,9 +337,17 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
         }
         off[k] = 4 * o;
     }
-    for (int i = tid; i < p.CP; i += RF_NT) {
-        lf[zplane + i] = 0.0f;
-        lf[p.EB + zplane + i] = 0.0f;
+    if constexpr (VST) {
+        // both window buffers all zero: vector staging writes only the
+        // input's own columns of in-image rows, so the padding columns,
+        // rows outside the image and the zero planes stay zero
+        for (int i = tid; i < 2 * p.EB; i += RF_NT) lf[i] = 0.0f;
+        __syncthreads();
+    } else {
+        for (int i = tid; i < p.CP; i += RF_NT) {
+            lf[zplane + i] = 0.0f;
+            lf[p.EB + zplane + i] = 0.0f;
+        }
     }
 
     // this lane's pixel offsets in the window (pixels past the image read
@@ -363,12 +372,13 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
     // window buffer after its MFMAs, so few registers stay live and the
     // filter loads stay in flight.  Loads are issued from in-range addresses;
     // out-of-image positions and channels past IC are zeroed when stored.
-    int pos[PP];
+    constexpr int SPP = VST ? 1 : PP;   // scalar positions per thread
+    int pos[SPP];
     uint32_t pos_ok = 0;
-    {
+    if constexpr (!VST) {
         const int ih_lo = oh_lo * p.SH - p.PH;
 #pragma unroll
-        for (int m = 0; m < PP; ++m) {
+        for (int m = 0; m < SPP; ++m) {
             const int q = tid + RF_NT * m;
             const uint32_t qc = (uint32_t)(q < p.CP ? q : 0);
             const uint32_t r = div_u31(qc, p.div_wp);
@@ -378,29 +388,88 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
             pos_ok |= ok ? 1u << m : 0u;
         }
     }
+    // Vector staging (VST: stride-1 rows, IW % 4 == 0, 16-byte aligned
+    // input): slot t = tid + 256 m of a group covers channel t / (NR*IW4) of
+    // the group, window row r and input columns 4 c4 .. 4 c4 + 3 -- one
+    // 16-byte load and four LDS stores (the window rows keep their pitch, so
+    // the columns are 4-byte aligned only); slots on rows outside the image
+    // load from the plane's start and store nothing.
+    int vg[VST ? PP : 1], vl[VST ? PP : 1], vh[VST ? PP : 1];
+    uint32_t vmask = 0;
+    if constexpr (VST) {
+        const int per_ch = p.NR * p.IW4;
+        const int ih_lo = oh_lo * p.SH - p.PH;
+#pragma unroll
+        for (int m = 0; m < PP; ++m) {
+            const int t = tid + RF_NT * m;
+            const int h = t / per_ch, rem = t - h * per_ch;
+            const int r = rem / p.IW4, c4 = rem - r * p.IW4;
+            const int ih = ih_lo + r;
+            const bool act = t < RF_CPG * per_ch && (unsigned)ih < (unsigned)p.IH;
+            vg[m] = act ? ih * p.IW + 4 * c4 : 0;
+            vl[m] = r * p.WP + p.PW + 4 * c4;
+            vh[m] = h < RF_CPG ? h : 0;
+            vmask |= act ? 1u << m : 0u;
+        }
+    }
+    floatx4 vv[VST ? PP : 1];
+    auto vslice_load = [&](int c, int g) {
+#pragma unroll
+        for (int m = 0; m < PP; ++m) {
+            const int icl = min(RF_CPG * g + vh[m], p.ICT - 1), ic = c * p.ICT + icl;
+            const int icc = ic < p.IC ? ic : 0;
+            vv[m] = *reinterpret_cast<const floatx4*>(ximg + (int64_t)icc * p.plane + vg[m]);
+        }
+    };
+    auto vslice_store = [&](int c, int dst, int g) {
+#pragma unroll
+        for (int m = 0; m < PP; ++m) {
+            const int icl = min(RF_CPG * g + vh[m], p.ICT - 1), ic = c * p.ICT + icl;
+            const bool keep = ic < p.IC;
+            floatx4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float u = opaque(vv[m][e]);
+                v[e] = keep ? u : 0.0f;
+            }
+            if ((vmask >> m) & 1) {
+                float* d = lf + dst + icl * p.CP + vl[m];
+                d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+            }
+        }
+    };
+
     // (groups past the chunk's channels restage its last channel: the same
     // values again, so every group issues the same loads and stores)
-    float sv[RF_CPG][PP];
+    float sv[RF_CPG][SPP];
     auto slice_load = [&](int c, int g) {
+        if constexpr (VST) {
+            vslice_load(c, g);
+        } else {
 #pragma unroll
-        for (int h = 0; h < RF_CPG; ++h) {
-            const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
-            const int icc = ic < p.IC ? ic : 0;   // wave-uniform
-            const float* src = ximg + icc * p.plane;
+            for (int h = 0; h < RF_CPG; ++h) {
+                const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
+                const int icc = ic < p.IC ? ic : 0;   // wave-uniform
+                const float* src = ximg + icc * p.plane;
 #pragma unroll
-            for (int m = 0; m < PP; ++m) sv[h][m] = src[pos[m]];
+                for (int m = 0; m < SPP; ++m) sv[h][m] = src[pos[m]];
+            }
         }
     };
     auto slice_store = [&](int c, int dst, int g) {
+        if constexpr (VST) {
+            vslice_store(c, dst, g);
+        } else {
 #pragma unroll
-        for (int h = 0; h < RF_CPG; ++h) {
-            const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
-            const uint32_t ok = ic < p.IC ? pos_ok : 0u;
-            float* d = lf + dst + icl * p.CP + tid;
+            for (int h = 0; h < RF_CPG; ++h) {
+                const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
+                const uint32_t ok = ic < p.IC ? pos_ok : 0u;
+                float* d = lf + dst + icl * p.CP + tid;
 #pragma unroll
-            for (int m = 0; m < PP; ++m) {
-                const float v = opaque(sv[h][m]);
-                if (tid + RF_NT * m < p.CP) d[RF_NT * m] = (ok >> m) & 1 ? v : 0.0f;
+                for (int m = 0; m < SPP; ++m) {
+                    const float v = opaque(sv[h][m]);
+                    if (tid + RF_NT * m < p.CP) d[RF_NT * m] = (ok >> m) & 1 ? v : 0.0f;
+                }
             }
         }
     };
@@ -619,7 +688,7 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
     }
 }
 
-template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN>
+template <int FN, int PP, bool VECW, bool MASKED, bool TWO_LEVEL, bool RUN, bool VST>
 __global__ __launch_bounds__(RF_NT)
 void conv_rowwin_kernel(RfArgs p) {
     // Workgroups go to the 8 XCDs round-robin by linear id; where the grid
@@ -632,16 +701,16 @@ void conv_rowwin_kernel(RfArgs p) {
     if constexpr (RUN) {
         if (p.n_full > 0) {   // one channel block (gridDim.y == 1)
             if (lin < p.n_full) {
-                rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, false>(p, xcd_order(lin, p.n_full), 0, 0);
+                rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, VST, false>(p, xcd_order(lin, p.n_full), 0, 0);
             } else {
                 const uint32_t u = xcd_order(lin - p.n_full, p.n_half);
-                rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, true>(p, p.n_full + u / 2, 0, (int)(u & 1));
+                rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, VST, true>(p, p.n_full + u / 2, 0, (int)(u & 1));
             }
             return;
         }
     }
     const uint32_t l = xcd_order(lin, gridDim.x * gridDim.y);
-    rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, false>(p, l % gridDim.x, l / gridDim.x, 0);
+    rowwin_body<FN, PP, VECW, MASKED, TWO_LEVEL, RUN, VST, false>(p, l % gridDim.x, l / gridDim.x, 0);
 }
 
 // Launch plan of the row-window form, or ok = false where no window fits
@@ -649,6 +718,7 @@ void conv_rowwin_kernel(RfArgs p) {
 struct RfPlan {
     bool ok = false;
     int fn = 0, ict = 0, nr = 0, wp = 0, kcp = 0, eb = 0, pp = 0;
+    int vpp = 0;     // 16-byte staging slots per thread, 0: scalar staging only
     size_t lds = 0;
 };
 
@@ -675,15 +745,26 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
     for (const int fn : {8, 7, 5}) {
         const int64_t tn = 16 * fn;
         const int64_t rows = std::min<int64_t>(OH, (OW - 1 + tn - 1) / OW + 1);
-        const int64_t nr = (rows - 1) * SH + KH, wp = (OW - 1) * SW + KW, cp = nr * wp;
+        const int64_t nr = (rows - 1) * SH + KH, wp0 = (OW - 1) * SW + KW;
+        // vector staging: stride-1 rows of whole 16-byte groups
+        const bool vst = SW == 1 && OW % fn == 0 && IW % 4 == 0 &&
+                         RF_CPG * nr * (IW / 4) <= 4 * RF_NT;
+        const int64_t wp = wp0, cp = nr * wp;
         if (cp > 4 * RF_NT) continue;   // at most 4 window positions per thread
+        const int pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
+        const int64_t vslots = ceil_div(RF_CPG * nr * (IW / 4), RF_NT);
+        const int vpp = vst ? (vslots <= 1 ? 1 : vslots <= 2 ? 2 : 4) : 0;
+        const bool run = SW == 1 && OW % fn == 0;
         // workgroups per CU the registers allow (4 waves each): 4 at <= 128
         // VGPRs -- every one-level form, and the two-level forms with
-        // consecutive-pixel lanes except FN 8 with 4 window positions per
-        // thread -- else 3 (the other two-level forms: up to ~157 VGPRs)
-        const int pp = cp <= RF_NT ? 1 : cp <= 2 * RF_NT ? 2 : 4;
-        const bool run = SW == 1 && OW % fn == 0;
-        const int64_t by_regs = !two_level || (run && (fn <= 7 || pp <= 2)) ? 4 : 3;
+        // consecutive-pixel lanes except those with 4 slots per thread and
+        // FN 8 (scalar staging) or FN >= 7 (vector staging) -- else 3 (the
+        // other two-level forms: up to ~152 VGPRs in the gfx950 build)
+        const int64_t by_regs =
+            !two_level ? 4
+            : !run     ? 3
+            : vst      ? (vpp == 4 && fn >= 7 ? 3 : 4)
+                       : (fn <= 7 || pp <= 2 ? 4 : 3);
         const int64_t wgs = batch * ceil_div(S, tn) * ceil_div(OC, RF_BM);
         const int64_t per_cu = ceil_div(wgs, 256);
         int64_t ict = 16;
@@ -703,6 +784,7 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
                 best.fn = fn; best.ict = (int)ict; best.nr = (int)nr; best.wp = (int)wp;
                 best.kcp = (int)kcp; best.eb = (int)((ict + 1) * cp);
                 best.pp = pp;
+                best.vpp = vpp;
                 best.lds = (size_t)lds;
             }
         }
@@ -710,40 +792,43 @@ RfPlan rowwin_plan(int64_t batch, int64_t IC, int64_t OC, int64_t IH, int64_t IW
     return best;
 }
 
-template <int FN, int PP, bool VECW, bool MASKED, bool RUN>
+template <int FN, int PP, bool VECW, bool MASKED, bool RUN, bool VST>
 void rowwin_go_run(const RfArgs& p, bool two_level, dim3 grid, size_t lds, hipStream_t stream) {
     if (two_level)
-        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, true, RUN>), grid, dim3(RF_NT), lds, stream, p);
+        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, true, RUN, VST>), grid, dim3(RF_NT), lds, stream, p);
     else
-        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, false, RUN>), grid, dim3(RF_NT), lds, stream, p);
+        hipLaunchKernelGGL((conv_rowwin_kernel<FN, PP, VECW, MASKED, false, RUN, VST>), grid, dim3(RF_NT), lds, stream, p);
 }
 
+// vst: vector staging (PP then counts 16-byte slots per thread)
 template <int FN, int PP, bool VECW, bool MASKED>
-void rowwin_go(const RfArgs& p, bool two_level, dim3 grid, size_t lds, hipStream_t stream) {
-    if (p.SW == 1 && p.OW % FN == 0)
-        rowwin_go_run<FN, PP, VECW, MASKED, true>(p, two_level, grid, lds, stream);
+void rowwin_go(const RfArgs& p, bool two_level, bool vst, dim3 grid, size_t lds, hipStream_t stream) {
+    if (vst)
+        rowwin_go_run<FN, PP, VECW, MASKED, true, true>(p, two_level, grid, lds, stream);
+    else if (p.SW == 1 && p.OW % FN == 0)
+        rowwin_go_run<FN, PP, VECW, MASKED, true, false>(p, two_level, grid, lds, stream);
     else
-        rowwin_go_run<FN, PP, VECW, MASKED, false>(p, two_level, grid, lds, stream);
+        rowwin_go_run<FN, PP, VECW, MASKED, false, false>(p, two_level, grid, lds, stream);
 }
 
 template <int FN, int PP>
-void rowwin_go_pp(const RfArgs& p, bool vecw, bool masked, bool two_level, dim3 grid, size_t lds,
-                  hipStream_t stream) {
+void rowwin_go_pp(const RfArgs& p, bool vecw, bool masked, bool two_level, bool vst, dim3 grid,
+                  size_t lds, hipStream_t stream) {
     if (vecw) {
-        if (masked) rowwin_go<FN, PP, true, true>(p, two_level, grid, lds, stream);
-        else rowwin_go<FN, PP, true, false>(p, two_level, grid, lds, stream);
+        if (masked) rowwin_go<FN, PP, true, true>(p, two_level, vst, grid, lds, stream);
+        else rowwin_go<FN, PP, true, false>(p, two_level, vst, grid, lds, stream);
     } else {
-        if (masked) rowwin_go<FN, PP, false, true>(p, two_level, grid, lds, stream);
-        else rowwin_go<FN, PP, false, false>(p, two_level, grid, lds, stream);
+        if (masked) rowwin_go<FN, PP, false, true>(p, two_level, vst, grid, lds, stream);
+        else rowwin_go<FN, PP, false, false>(p, two_level, vst, grid, lds, stream);
     }
 }
 
 template <int FN>
-void rowwin_go_fn(const RfArgs& p, int pp, bool vecw, bool masked, bool two_level, dim3 grid,
-                  size_t lds, hipStream_t stream) {
-    if (pp == 1) rowwin_go_pp<FN, 1>(p, vecw, masked, two_level, grid, lds, stream);
-    else if (pp == 2) rowwin_go_pp<FN, 2>(p, vecw, masked, two_level, grid, lds, stream);
-    else rowwin_go_pp<FN, 4>(p, vecw, masked, two_level, grid, lds, stream);
+void rowwin_go_fn(const RfArgs& p, int pp, bool vecw, bool masked, bool two_level, bool vst,
+                  dim3 grid, size_t lds, hipStream_t stream) {
+    if (pp == 1) rowwin_go_pp<FN, 1>(p, vecw, masked, two_level, vst, grid, lds, stream);
+    else if (pp == 2) rowwin_go_pp<FN, 2>(p, vecw, masked, two_level, vst, grid, lds, stream);
+    else rowwin_go_pp<FN, 4>(p, vecw, masked, two_level, vst, grid, lds, stream);
 }
 
 int launch_rowwin(const float* x, const float* w, const float* bias, float* y, int64_t batch,
@@ -757,6 +842,11 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
     p.KW = (int)KW; p.KHW = (int)(KH * KW); p.SH = (int)SH; p.SW = (int)SW;
     p.PH = (int)PH; p.PW = (int)PW; p.Kc = (int)(IC * KH * KW); p.plane = (int)(IH * IW);
     p.ICT = pl.ict; p.NR = pl.nr; p.WP = pl.wp; p.CP = pl.nr * pl.wp;
+    p.IW4 = (int)(IW / 4);
+    // vector staging where the rows allow it and the input is 16-byte
+    // aligned
+    const bool vst = pl.vpp > 0 && (uintptr_t)x % 16 == 0;
+    const int pp = vst ? pl.vpp : pl.pp;
     p.kc_real = pl.ict * p.KHW; p.KCP = pl.kcp; p.EB = pl.eb;
     p.nchunks = (int)ceil_div(IC, pl.ict);
     p.tiles_img = (int)ceil_div(p.S, 16 * pl.fn);
@@ -787,9 +877,9 @@ int launch_rowwin(const float* x, const float* w, const float* bias, float* y, i
         p.y = y + oc0 * p.S;
         const dim3 grid = p.n_full > 0 ? dim3(p.n_full + p.n_half, 1u)
                                        : dim3((unsigned)(batch * p.tiles_img), (unsigned)ceil_div(oc_n, RF_BM));
-        if (pl.fn == 8) rowwin_go_fn<8>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
-        else if (pl.fn == 7) rowwin_go_fn<7>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
-        else rowwin_go_fn<5>(p, pl.pp, vecw, masked, two_level, grid, pl.lds, stream);
+        if (pl.fn == 8) rowwin_go_fn<8>(p, pp, vecw, masked, two_level, vst, grid, pl.lds, stream);
+        else if (pl.fn == 7) rowwin_go_fn<7>(p, pp, vecw, masked, two_level, vst, grid, pl.lds, stream);
+        else rowwin_go_fn<5>(p, pp, vecw, masked, two_level, vst, grid, pl.lds, stream);
         const int st = hip_error(hipGetLastError(), "conv_rowwin_kernel launch");
         if (st) return st;
     }
