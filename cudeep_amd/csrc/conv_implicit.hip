@@ -36,6 +36,7 @@
 // line.)
 // FP32 products in every precision mode, as the reference's kernel.
 #include <algorithm>
+#include <type_traits>
 
 #include "cdx_internal.hpp"
 
@@ -341,7 +342,11 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
         // both window buffers all zero: vector staging writes only the
         // input's own columns of in-image rows, so the padding columns,
         // rows outside the image and the zero planes stay zero
-        for (int i = tid; i < 2 * p.EB; i += RF_NT) lf[i] = 0.0f;
+        // (16-byte stores: lf is 16-byte aligned, KCP being a multiple of 16)
+        const int n4 = (2 * p.EB) >> 2;
+        for (int i = tid; i < n4; i += RF_NT)
+            reinterpret_cast<floatx4*>(lf)[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 4 * n4 + tid; i < 2 * p.EB; i += RF_NT) lf[i] = 0.0f;
         __syncthreads();
     } else {
         for (int i = tid; i < p.CP; i += RF_NT) {
@@ -412,16 +417,17 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
             vmask |= act ? 1u << m : 0u;
         }
     }
-    floatx4 vv[VST ? PP : 1];
-    auto vslice_load = [&](int c, int g) {
+    using VSlice = floatx4[VST ? PP : 1];
+    VSlice vv;
+    auto vslice_load_to = [&](VSlice& d, int c, int g) {
 #pragma unroll
         for (int m = 0; m < PP; ++m) {
             const int icl = min(RF_CPG * g + vh[m], p.ICT - 1), ic = c * p.ICT + icl;
             const int icc = ic < p.IC ? ic : 0;
-            vv[m] = *reinterpret_cast<const floatx4*>(ximg + (int64_t)icc * p.plane + vg[m]);
+            d[m] = *reinterpret_cast<const floatx4*>(ximg + (int64_t)icc * p.plane + vg[m]);
         }
     };
-    auto vslice_store = [&](int c, int dst, int g) {
+    auto vslice_store_from = [&](const VSlice& sv4, int c, int dst, int g) {
 #pragma unroll
         for (int m = 0; m < PP; ++m) {
             const int icl = min(RF_CPG * g + vh[m], p.ICT - 1), ic = c * p.ICT + icl;
@@ -429,7 +435,7 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
             floatx4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float u = opaque(vv[m][e]);
+                const float u = opaque(sv4[m][e]);
                 v[e] = keep ? u : 0.0f;
             }
             if ((vmask >> m) & 1) {
@@ -438,40 +444,43 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
             }
         }
     };
+    auto vslice_load = [&](int c, int g) { vslice_load_to(vv, c, g); };
+    auto vslice_store = [&](int c, int dst, int g) { vslice_store_from(vv, c, dst, g); };
 
     // (groups past the chunk's channels restage its last channel: the same
     // values again, so every group issues the same loads and stores)
-    float sv[RF_CPG][SPP];
-    auto slice_load = [&](int c, int g) {
-        if constexpr (VST) {
-            vslice_load(c, g);
-        } else {
+    using SSlice = float[RF_CPG][SPP];
+    SSlice sv;
+    auto sslice_load_to = [&](SSlice& d, int c, int g) {
 #pragma unroll
-            for (int h = 0; h < RF_CPG; ++h) {
-                const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
-                const int icc = ic < p.IC ? ic : 0;   // wave-uniform
-                const float* src = ximg + icc * p.plane;
+        for (int h = 0; h < RF_CPG; ++h) {
+            const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
+            const int icc = ic < p.IC ? ic : 0;   // wave-uniform
+            const float* src = ximg + icc * p.plane;
 #pragma unroll
-                for (int m = 0; m < SPP; ++m) sv[h][m] = src[pos[m]];
+            for (int m = 0; m < SPP; ++m) d[h][m] = src[pos[m]];
+        }
+    };
+    auto sslice_store_from = [&](const SSlice& sd, int c, int dst, int g) {
+#pragma unroll
+        for (int h = 0; h < RF_CPG; ++h) {
+            const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
+            const uint32_t ok = ic < p.IC ? pos_ok : 0u;
+            float* d = lf + dst + icl * p.CP + tid;
+#pragma unroll
+            for (int m = 0; m < SPP; ++m) {
+                const float v = opaque(sd[h][m]);
+                if (tid + RF_NT * m < p.CP) d[RF_NT * m] = (ok >> m) & 1 ? v : 0.0f;
             }
         }
     };
+    auto slice_load = [&](int c, int g) {
+        if constexpr (VST) vslice_load(c, g);
+        else sslice_load_to(sv, c, g);
+    };
     auto slice_store = [&](int c, int dst, int g) {
-        if constexpr (VST) {
-            vslice_store(c, dst, g);
-        } else {
-#pragma unroll
-            for (int h = 0; h < RF_CPG; ++h) {
-                const int icl = min(RF_CPG * g + h, p.ICT - 1), ic = c * p.ICT + icl;
-                const uint32_t ok = ic < p.IC ? pos_ok : 0u;
-                float* d = lf + dst + icl * p.CP + tid;
-#pragma unroll
-                for (int m = 0; m < SPP; ++m) {
-                    const float v = opaque(sv[h][m]);
-                    if (tid + RF_NT * m < p.CP) d[RF_NT * m] = (ok >> m) & 1 ? v : 0.0f;
-                }
-            }
-        }
+        if constexpr (VST) vslice_store(c, dst, g);
+        else sslice_store_from(sv, c, dst, g);
     };
 
     // filter fragments for one 16-k group: row oc0 + wm0 + l16 (rows past
@@ -593,8 +602,7 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
         }
     };
 
-    // Every group issues the same loads (past the last chunk they read
-    // valid, unused addresses and store into the idle buffer), so the loop
+    // Within each loop below every group issues the same loads, so the code
     // is straight-line and each wait covers only the loads it needs.  Two
     // filter fragment sets alternate: a group computes with its set, then
     // refills it with the group two ahead (no register copies, so a refill
@@ -603,46 +611,87 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
     AFrag a0, a1;
     a_load(a0);
     a_load(a1);
-    for (int g = 0; g * RF_CPG < p.ICT; ++g) {
-        slice_load(0, g);
-        slice_store(0, 0, g);
+    {
+        // chunk 0's window with NPRO groups' slices in flight at a time (the
+        // accumulators and B fragments are not live yet; loads of groups
+        // past the chunk's channels are clamped to its last channel)
+        constexpr int NPRO = (VST ? PP : SPP) == 1 ? 4 : (VST ? PP : SPP) == 2 ? 2 : 1;
+        VSlice pv[VST ? NPRO : 1];
+        SSlice ps[VST ? 1 : NPRO];
+        for (int g0 = 0; g0 * RF_CPG < p.ICT; g0 += NPRO) {
+#pragma unroll
+            for (int i = 0; i < NPRO; ++i) {
+                if constexpr (VST) vslice_load_to(pv[i], 0, g0 + i);
+                else sslice_load_to(ps[i], 0, g0 + i);
+            }
+#pragma unroll
+            for (int i = 0; i < NPRO; ++i) {
+                if ((g0 + i) * RF_CPG < p.ICT) {
+                    if constexpr (VST) vslice_store_from(pv[i], 0, 0, g0 + i);
+                    else sslice_store_from(ps[i], 0, 0, g0 + i);
+                }
+            }
+        }
     }
     __syncthreads();
     int gi = 0, c = 0, g = 0;
     int cb = 0, nb = p.EB;   // window buffer of chunk c, and of chunk c + 1
     set_buffer(cb);
-    auto step = [&](AFrag& a) {
+    auto step = [&](AFrag& a, auto stage) {
+        // STAGE: stage chunk c + 1's window (every chunk but the last).
         // (scheduling barriers keep the slice loads ahead of the MFMAs and
         // the slice stores, which wait for them, behind)
-        slice_load(c + 1, g);
+        constexpr bool STAGE = decltype(stage)::value;
+        if constexpr (STAGE) slice_load(c + 1, g);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (HALF) compute_half(a, g);
         else compute(a, g);
         a_load(a);
         if (TWO_LEVEL && (gi & 1)) fold();
         __builtin_amdgcn_sched_barrier(0);
-        slice_store(c + 1, nb, g);
+        if constexpr (STAGE) slice_store(c + 1, nb, g);
         ++gi;
         if (++g == nkg) {
-            // the rest of chunk c + 1's window (chunks with fewer groups
-            // than channel pairs: 1x1 taps); then every wave's reads of
-            // buffer cb and writes of buffer nb are complete
-            for (int h = nkg; h * RF_CPG < p.ICT; ++h) {
-                slice_load(c + 1, h);
-                slice_store(c + 1, nb, h);
+            if constexpr (STAGE) {
+                // the rest of chunk c + 1's window (chunks with fewer groups
+                // than channel pairs: 1x1 taps); then every wave's reads of
+                // buffer cb and writes of buffer nb are complete
+                for (int h = nkg; h * RF_CPG < p.ICT; ++h) {
+                    slice_load(c + 1, h);
+                    slice_store(c + 1, nb, h);
+                }
+                __syncthreads();
             }
-            __syncthreads();
             ++c;
             g = 0;
             const int t = cb; cb = nb; nb = t;
             set_buffer(cb);
         }
     };
-    for (int t = 0; t + 1 < groups; t += 2) {
-        step(a0);
-        step(a1);
+    // groups of chunks 0 .. nchunks-2 stage the next chunk; the last
+    // chunk's do not (group t computes with a0 for even t, a1 for odd t)
+    const std::bool_constant<true> staged;
+    const std::bool_constant<false> last;
+    const int gs = (p.nchunks - 1) * nkg;
+    int t = 0;
+    for (; t + 1 < gs; t += 2) {
+        step(a0, staged);
+        step(a1, staged);
     }
-    if (groups & 1) step(a0);
+    if (gs & 1) {
+        step(a0, staged);
+        for (t = gs; t + 1 < groups; t += 2) {
+            step(a1, last);
+            step(a0, last);
+        }
+        if (t < groups) step(a1, last);
+    } else {
+        for (t = gs; t + 1 < groups; t += 2) {
+            step(a0, last);
+            step(a1, last);
+        }
+        if (t < groups) step(a0, last);
+    }
     if (TWO_LEVEL && (groups & 1)) fold();
 
     // D layout of a 16x16 block: register r of lane l is row 4*(l/16) + r,
