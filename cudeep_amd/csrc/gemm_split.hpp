@@ -62,12 +62,18 @@ struct KParams {
     int64_t ldaux;
 };
 
-__device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
-    __bf16 h = (__bf16)x;
-    float r = x - (float)h;
-    __bf16 l = (__bf16)r;
-    hi = __builtin_bit_cast(unsigned short, h);
-    lo = __builtin_bit_cast(unsigned short, l);
+// Splits two values at once: one v_cvt_pk_bf16_f32 rounds both to bf16
+// (RNE) into one register (a in the low half), whose halves widen back to
+// fp32 with a shift and a mask; the exact residuals are rounded by a second
+// v_cvt_pk_bf16_f32.  hi / lo come out as packed bf16 pairs.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    const float ha = __builtin_bit_cast(float, h << 16);
+    const float hb = __builtin_bit_cast(float, h & 0xffff0000u);
+    hi = h;
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a - ha, b - hb}, bf16x2_t));
 }
 
 __device__ __forceinline__ float ld_guard(const float* p, bool ok) { return ok ? *p : 0.0f; }
@@ -203,16 +209,11 @@ struct SplitLoader {
                         x[q] = r == 0 ? t.x : r == 1 ? t.y : r == 2 ? t.z : t.w;
                     }
                 }
-                unsigned short h[4], l[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) split_bf16(x[q], h[q], l[q]);
                 int mn = (KCONTIG ? br : bc) * 4 + r;
                 int kk = (KCONTIG ? bc : br) * 4;
                 uint2 hv, lv;
-                hv.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-                hv.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
-                lv.x = (uint32_t)l[0] | ((uint32_t)l[1] << 16);
-                lv.y = (uint32_t)l[2] | ((uint32_t)l[3] << 16);
+                split_bf16x2(x[0], x[1], hv.x, lv.x);
+                split_bf16x2(x[2], x[3], hv.y, lv.y);
                 *reinterpret_cast<uint2*>(hi + mn * STRIDE + kk) = hv;
                 *reinterpret_cast<uint2*>(lo + mn * STRIDE + kk) = lv;
             }
