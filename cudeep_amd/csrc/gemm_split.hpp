@@ -1090,20 +1090,28 @@ void gemm_kalt_kernel(KParams p) {
     const int64_t stepA = OPA == CDX_OP_N ? (int64_t)ES * BK : (int64_t)BK * p.lda * ES;
     const int64_t stepB = OPB == CDX_OP_N ? (int64_t)BK * p.ldb * ES : (int64_t)ES * BK;
     // this group's k-tiles: grp, grp + 2, grp + 4, ...
-    const int64_t nk = p.K / BK;
+    const int64_t nk = p.K / BK;   // >= 1 (the launcher takes K > 0)
     const int64_t nkg = grp == 0 ? (nk + 1) / 2 : nk / 2;
-    auto load = [&](LoaderA& a, LoaderB& b, int64_t j) {
+    // k-tile of the group's j-th, clamped to the last one: every load is
+    // issued, those past the group's k-tiles from valid addresses (their
+    // values unused), so the compiler's wait before a store counts exactly
+    // the loads issued after that store's set -- with conditional loads it
+    // has to wait for all of them, the set loaded one slot earlier included
+    auto ktile = [&](int64_t j) {
         const int64_t t = 2 * j + grp;
+        return t < nk ? t : nk - 1;
+    };
+    auto load = [&](LoaderA& a, LoaderB& b, int64_t j) {
+        const int64_t t = ktile(j);
         a.load_at(baseA + t * stepA, lda_b, offa);
         b.load_at(baseB + t * stepB, ldb_b, offb);
     };
     // the MFMAs of the current k-tile with the loads of this group's k-tile
-    // j into (a, b) between them (none when j is past its last one)
+    // j into (a, b) between them
     auto math_loading = [&](LoaderA& a, LoaderB& b, int64_t j) {
-        const bool go = j < nkg;
-        const int64_t t = 2 * j + grp;
-        math([&]() { if (go) a.load_at(baseA + t * stepA, lda_b, offa); },
-             [&]() { if (go) b.load_at(baseB + t * stepB, ldb_b, offb); });
+        const int64_t t = ktile(j);
+        math([&]() { a.load_at(baseA + t * stepA, lda_b, offa); },
+             [&]() { b.load_at(baseB + t * stepB, ldb_b, offb); });
     };
     auto store = [&](const LoaderA& a, const LoaderB& b, unsigned short* s) {
         a.template store<STRIDE>(s, s + A_PLANE, gtid);
@@ -1123,12 +1131,10 @@ void gemm_kalt_kernel(KParams p) {
     };
 
     if constexpr (TERMS == 3) {
-        if (nkg > 0) {
-            load(la0, lb0, 0);
-            store(la0, lb0, mine);
-            if (nkg > 1) load(la1, lb1, 1);
-            if (nkg > 2) load(la0, lb0, 2);
-        }
+        load(la0, lb0, 0);
+        if (nkg > 0) store(la0, lb0, mine);
+        load(la1, lb1, 1);
+        load(la0, lb0, 2);
         __syncthreads();
         if (grp == 1) slot();
         int64_t j = 0;
@@ -1140,11 +1146,9 @@ void gemm_kalt_kernel(KParams p) {
     } else {
         // four terms: the two-level partial sums leave room for one set
         // (k-tile j+1 stored, then k-tile j+2 loaded, in the same slot)
-        if (nkg > 0) {
-            load(la0, lb0, 0);
-            store(la0, lb0, mine);
-            if (nkg > 1) load(la0, lb0, 1);
-        }
+        load(la0, lb0, 0);
+        if (nkg > 0) store(la0, lb0, mine);
+        load(la0, lb0, 1);
         __syncthreads();
         if (grp == 1) slot();
         for (int64_t j = 0; j < nkg; ++j) {
