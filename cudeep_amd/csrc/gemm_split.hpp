@@ -325,6 +325,56 @@ struct HalfLoader {
     }
 };
 
+// k-contiguous 16-bit operands of the ping-pong kernel (unchecked loads
+// only): blocks of 4 rows x 8 k, so each load moves 16 bytes -- half the
+// load instructions of HalfLoader's 8-byte loads for the same tile (the
+// texture addresser's per-instruction cost is what the 16-bit ping-pong
+// kernel's loads are bound by) -- and each row is stored with one 16-byte
+// LDS write.  Eight consecutive threads cover one 128-byte row segment of a
+// 64-k tile, as with HalfLoader.
+template <int BMN, int BK, int NT>
+struct HalfLoader16 {
+    static constexpr int NB = (BMN / 4) * (BK / 8);
+    static constexpr int NV = NB / NT;
+    static_assert(NB % NT == 0 && BK % 8 == 0, "whole 4 x 8 blocks per thread");
+    uint4 v[NV][4];   // v[blk][q]: row q of the block, 8 k
+    static constexpr int ES = 2;
+    __device__ __forceinline__ static void block_coords(int blk, int& bc, int& br) {
+        bc = blk % (BK / 8);
+        br = blk / (BK / 8);
+    }
+    __device__ __forceinline__ static uint32_t tile_offset(uint32_t ld_bytes, int tid) {
+        int bc, br;
+        block_coords(tid, bc, br);
+        return (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 8 * ES);
+    }
+    __device__ __forceinline__ static uint64_t block_step(int b, uint32_t ld_bytes) {
+        constexpr int ROWS = NT / (BK / 8) * 4;   // block rows between a thread's blocks
+        return (uint64_t)b * ROWS * ld_bytes;
+    }
+    __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
+                                            uint32_t off) {
+#pragma unroll
+        for (int b = 0; b < NV; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[b][q] = load_global<uint4>(
+                    uniform_ptr(base + block_step(b, ld_bytes) + (uint64_t)(q * ld_bytes)) + off);
+    }
+    // Writes the plane, layout [mn][STRIDE] (k contiguous), ushort units.
+    template <int STRIDE>
+    __device__ __forceinline__ void store(unsigned short* __restrict__ plane, int tid) const {
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int bc, br;
+            block_coords(tid + b * NT, bc, br);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                *reinterpret_cast<uint4*>(plane + (br * 4 + r) * STRIDE + bc * 8) = v[b][r];
+        }
+    }
+};
+
 // Special operand values in the split kernels.  The reference's TF32 MMA
 // takes raw fp32 bits (matmul_kernel.cu:186-201), so an infinite operand
 // gives IEEE results: +-Inf, or NaN for Inf * 0 and Inf - Inf.  The split
@@ -768,10 +818,15 @@ void gemm_pingpong_kernel(KParams p) {
         p.C += (int64_t)blockIdx.z * p.sc;
     }
 
-    using LoaderA = std::conditional_t<H16, HalfLoader<BM, BK, NT, OPA == CDX_OP_N, false>,
-                                       SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>>;
-    using LoaderB = std::conditional_t<H16, HalfLoader<BN, BK, NT, OPB == CDX_OP_T, false>,
-                                       SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>>;
+    // (16-bit k-contiguous operands: 16-byte loads)
+    using LoaderA = std::conditional_t<
+        H16,
+        std::conditional_t<OPA == CDX_OP_N, HalfLoader16<BM, BK, NT>, HalfLoader<BM, BK, NT, false, false>>,
+        SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>>;
+    using LoaderB = std::conditional_t<
+        H16,
+        std::conditional_t<OPB == CDX_OP_T, HalfLoader16<BN, BK, NT>, HalfLoader<BN, BK, NT, false, false>>,
+        SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>>;
     static_assert(LoaderA::NB % NT == 0 && LoaderB::NB % NT == 0, "whole blocks per thread");
     LoaderA la;
     LoaderB lb;
