@@ -375,6 +375,65 @@ struct HalfLoader16 {
     }
 };
 
+// m/n-contiguous 16-bit operands of the ping-pong kernel (unchecked loads
+// only): blocks of 4 k x 8 mn, 16-byte loads (half of HalfLoader's load
+// instructions), transposed in registers into eight 4-k runs per block.
+// As in HalfLoader, the k-blocks of a column group go to consecutive threads
+// (k fastest): each store instruction then writes 16 threads' 8-byte runs
+// contiguously along one LDS row.
+template <int BMN, int BK, int NT>
+struct HalfLoader16T {
+    static constexpr int NB = (BMN / 8) * (BK / 4);
+    static constexpr int NV = NB / NT;
+    static_assert(NB % NT == 0 && BMN % 8 == 0 && BK % 4 == 0, "whole 4 x 8 blocks per thread");
+    uint4 v[NV][4];   // v[blk][q]: k row q of the block, 8 mn
+    static constexpr int ES = 2;
+    __device__ __forceinline__ static void block_coords(int blk, int& bc, int& br) {
+        br = blk % (BK / 4);
+        bc = blk / (BK / 4);
+    }
+    __device__ __forceinline__ static uint32_t tile_offset(uint32_t ld_bytes, int tid) {
+        int bc, br;
+        block_coords(tid, bc, br);
+        return (uint32_t)(br * 4) * ld_bytes + (uint32_t)(bc * 8 * ES);
+    }
+    __device__ __forceinline__ static uint64_t block_step(int b) {
+        constexpr int COLS = NT / (BK / 4) * 8;   // mn between a thread's blocks
+        return (uint64_t)b * COLS * ES;
+    }
+    __device__ __forceinline__ void load_at(const char* __restrict__ base, uint32_t ld_bytes,
+                                            uint32_t off) {
+#pragma unroll
+        for (int b = 0; b < NV; ++b)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[b][q] = load_global<uint4>(base + block_step(b) + (uint64_t)(q * ld_bytes) + off);
+    }
+    // Writes the plane, layout [mn][STRIDE] (k contiguous), ushort units.
+    template <int STRIDE>
+    __device__ __forceinline__ void store(unsigned short* __restrict__ plane, int tid) const {
+        // 16-bit element e of a row's 8: dword e / 2, half e % 2
+        auto pair = [](uint32_t lo_row, uint32_t hi_row, int h) {
+            return h ? (lo_row >> 16) | (hi_row & 0xFFFF0000u) : (lo_row & 0xFFFFu) | (hi_row << 16);
+        };
+#pragma unroll
+        for (int b = 0; b < NV; ++b) {
+            int bc, br;
+            block_coords(tid + b * NT, bc, br);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int w = e >> 1, h = e & 1;
+                const uint32_t r0 = (&v[b][0].x)[w], r1 = (&v[b][1].x)[w];
+                const uint32_t r2 = (&v[b][2].x)[w], r3 = (&v[b][3].x)[w];
+                uint2 hv;
+                hv.x = pair(r0, r1, h);
+                hv.y = pair(r2, r3, h);
+                *reinterpret_cast<uint2*>(plane + (bc * 8 + e) * STRIDE + br * 4) = hv;
+            }
+        }
+    }
+};
+
 // Special operand values in the split kernels.  The reference's TF32 MMA
 // takes raw fp32 bits (matmul_kernel.cu:186-201), so an infinite operand
 // gives IEEE results: +-Inf, or NaN for Inf * 0 and Inf - Inf.  The split
@@ -818,14 +877,14 @@ void gemm_pingpong_kernel(KParams p) {
         p.C += (int64_t)blockIdx.z * p.sc;
     }
 
-    // (16-bit k-contiguous operands: 16-byte loads)
+    // (16-bit operands: 16-byte loads)
     using LoaderA = std::conditional_t<
         H16,
-        std::conditional_t<OPA == CDX_OP_N, HalfLoader16<BM, BK, NT>, HalfLoader<BM, BK, NT, false, false>>,
+        std::conditional_t<OPA == CDX_OP_N, HalfLoader16<BM, BK, NT>, HalfLoader16T<BM, BK, NT>>,
         SplitLoader<BM, BK, NT, OPA == CDX_OP_N, false>>;
     using LoaderB = std::conditional_t<
         H16,
-        std::conditional_t<OPB == CDX_OP_T, HalfLoader16<BN, BK, NT>, HalfLoader<BN, BK, NT, false, false>>,
+        std::conditional_t<OPB == CDX_OP_T, HalfLoader16<BN, BK, NT>, HalfLoader16T<BN, BK, NT>>,
         SplitLoader<BN, BK, NT, OPB == CDX_OP_T, false>>;
     static_assert(LoaderA::NB % NT == 0 && LoaderB::NB % NT == 0, "whole blocks per thread");
     LoaderA la;
