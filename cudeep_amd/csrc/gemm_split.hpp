@@ -326,7 +326,8 @@ struct HalfLoader {
 };
 
 // k-contiguous 16-bit operands of the ping-pong kernel (unchecked loads
-// only): blocks of 4 rows x 8 k, so each load moves 16 bytes -- half the
+// only; rows at 8-element multiples, which the dispatcher checks): blocks of
+// 4 rows x 8 k, so each load moves 16 bytes -- half the
 // load instructions of HalfLoader's 8-byte loads for the same tile (the
 // texture addresser's per-instruction cost is what the 16-bit ping-pong
 // kernel's loads are bound by) -- and each row is stored with one 16-byte
@@ -376,7 +377,8 @@ struct HalfLoader16 {
 };
 
 // m/n-contiguous 16-bit operands of the ping-pong kernel (unchecked loads
-// only): blocks of 4 k x 8 mn, 16-byte loads (half of HalfLoader's load
+// only; rows at 8-element multiples): blocks of 4 k x 8 mn, 16-byte loads
+// (half of HalfLoader's load
 // instructions), transposed in registers into eight 4-k runs per block.
 // As in HalfLoader, the k-blocks of a column group go to consecutive threads
 // (k fastest): each store instruction then writes 16 threads' 8-byte runs

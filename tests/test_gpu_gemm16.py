@@ -134,6 +134,36 @@ def test_gemm16_256_tile_path(tA, tB, K, dtype):
     assert np.linalg.norm(lhs - rhs) / np.linalg.norm(rhs) < 1e-5
 
 
+@pytest.mark.parametrize("pad", [4, 8])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_gemm16_256_tile_padded_rows(pad, dtype):
+    """M = N = 4096 with leading dimensions K + pad: rows at 8-element
+    multiples (pad 8) take the two-group kernel, whose 16-bit loads move 8
+    elements per lane; rows at 4-element multiples only (pad 4) fall back to
+    the 256 x 256 in-step kernel.  Both against the oracle on sampled rows."""
+    import torch
+    from cudeep_amd import _lib as L
+    rng = np.random.default_rng(3100 + pad)
+    n, K = 4096, 192
+    Ap, _ = _operands(rng, (n, K + pad), dtype)
+    Bp, _ = _operands(rng, (K, n + pad), dtype)
+    A32 = Ap.float().cpu().numpy()[:, :K]
+    B32 = Bp.float().cpu().numpy()[:, :n]
+    C = torch.empty((n, n), device="cuda")
+    dt = L.DTYPE_F16 if dtype == "f16" else L.DTYPE_BF16
+    say("gemm16 padded rows", dtype, pad)
+    L.call("cdx_gemm16_ex", dt, 0, 0, n, n, K, Ap.data_ptr(), K + pad, Bp.data_ptr(), n + pad,
+           C.data_ptr(), n, None, 0, 0, torch.cuda.current_stream().cuda_stream)
+    Ch = host(C)
+    opA, opB = np.ascontiguousarray(A32), np.ascontiguousarray(B32)
+    for r0 in (0, 2000, n - 48):
+        rows = (r0, r0 + 48)
+        C64 = oracle.dgemm(opA, opB, rows=rows)
+        e = oracle.rel_fro(Ch[r0:r0 + 48], C64)
+        e_ideal = oracle.rel_fro(oracle.gemm_tf32emu(opA, opB, "rne", rows=rows), C64)
+        assert e <= 2 * e_ideal, (rows, e, e_ideal)
+
+
 def test_hgemm_entry_point_and_epilogue():
     import cudeep_amd as cd
     rng = np.random.default_rng(65)
