@@ -59,17 +59,18 @@ bool tn_split_to_f32(const GemmArgs& g, int terms) {
            splitk_applies(ceil_div(g.M, CfgSmall::BM) * ceil_div(g.N, CfgSmall::BN), g.K);
 }
 
-// The two-group kernel loads 16-bit operands 16 bytes (8 elements) per lane,
-// so its rows and batch strides must start at 8-element multiples (the
-// in-step kernel's loads move 4 elements).
+// The 16-bit kernels' unchecked loads move 16 bytes (8 elements) per lane,
+// so their rows and batch strides must start at 8-element multiples (else
+// the checked in-step forms run, 4 elements per load).
 bool rows_of_8(const GemmArgs& g) {
     return g.lda % 8 == 0 && g.ldb % 8 == 0 && g.stride_a % 8 == 0 && g.stride_b % 8 == 0;
 }
 
 template <int IN>
 int dispatch16(const GemmArgs& g, hipStream_t stream) {
-    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<Cfg16Huge>(g)) {
-        if (pingpong_fits(g) && rows_of_8(g)) return launch_pingpong_ops<IN>(g, stream);
+    if (ceil_div(g.M, 256) * ceil_div(g.N, 256) >= 256 && aligned_for<Cfg16Huge>(g) &&
+        rows_of_8(g)) {
+        if (pingpong_fits(g)) return launch_pingpong_ops<IN>(g, stream);
         return launch_ops<Cfg16Huge, 1, IN>(g, stream);
     }
     if (ceil_div(g.M, 128) * ceil_div(g.N, 128) >= 256) return launch_ops<Cfg16Large, 1, IN>(g, stream);
