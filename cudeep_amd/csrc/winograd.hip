@@ -133,6 +133,58 @@ void wino_input_kernel(const float* __restrict__ x, float* __restrict__ V, WinoG
     }
 }
 
+// The same transform where IW % 4 == 0, PW = 4 - SH <= 2 and the input is
+// 16-byte aligned: each patch row comes from three aligned 16-byte loads of
+// input columns 4 tw - 4 .. 4 tw + 7 (each wholly inside or outside the row,
+// since IW % 4 == 0; consecutive lanes, whose tiles are 4 columns apart,
+// read consecutive 16-byte words) instead of six 4-byte loads.  Same
+// arithmetic per tile as wino_input_kernel.
+template <int SH>
+__global__ __launch_bounds__(256)
+void wino_input_v4_kernel(const float* __restrict__ x, float* __restrict__ V, WinoGeom g) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // ic * NT + tile
+    if (q >= g.IC * g.NT) return;
+    const int64_t ic = q / g.NT, tile = q - ic * g.NT;
+    const int64_t per_img = g.TH * g.TW;
+    const int64_t b = tile / per_img, r = tile - b * per_img;
+    const int64_t th = r / g.TW, tw = r - th * g.TW;
+    const int64_t h0 = th * 4 - g.PH, a = tw * 4 - 4;   // first loaded column; w0 = a + SH
+    const float* src = x + (b * g.IC + ic) * g.IH * g.IW;
+    float d[6][6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const int64_t ih = h0 + i;
+        const bool rok = ih >= 0 && ih < g.IH;
+        float row[12];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const int64_t col = a + 4 * c;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (rok && col >= 0 && col < g.IW)
+                v = *reinterpret_cast<const float4*>(src + ih * g.IW + col);
+            row[4 * c] = v.x; row[4 * c + 1] = v.y; row[4 * c + 2] = v.z; row[4 * c + 3] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 6; ++j) d[i][j] = row[SH + j];
+    }
+    float tmp[6][6], col6[6], t[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+#pragma unroll
+        for (int i = 0; i < 6; ++i) col6[i] = d[i][j];
+        wino_bt(col6, t);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) tmp[i][j] = t[i];
+    }
+    const int64_t plane = g.IC * g.NT;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        wino_bt(tmp[i], t);
+#pragma unroll
+        for (int j = 0; j < 6; ++j) V[(i * 6 + j) * plane + q] = t[j];
+    }
+}
+
 __global__ __launch_bounds__(256)
 void wino_output_kernel(const float* __restrict__ Mm, const float* __restrict__ bias,
                         float* __restrict__ y, WinoGeom g) {
@@ -212,9 +264,17 @@ int launch_conv2d_winograd_f32(const float* input, const float* weight, const fl
                            stream, weight, U, OC, IC);
     int st = hip_error(hipGetLastError(), "wino_filter_kernel launch");
     if (st) return st;
-    hipLaunchKernelGGL(wino_input_kernel, dim3(blocks_for(IC * g.NT)), dim3(256), 0, stream,
-                       input, V, g);
-    st = hip_error(hipGetLastError(), "wino_input_kernel launch");
+    if (IW % 4 == 0 && PW >= 0 && PW <= 2 && (uintptr_t)input % 16 == 0) {
+        const dim3 grid(blocks_for(IC * g.NT));
+        if (PW == 0) hipLaunchKernelGGL(wino_input_v4_kernel<4>, grid, dim3(256), 0, stream, input, V, g);
+        else if (PW == 1) hipLaunchKernelGGL(wino_input_v4_kernel<3>, grid, dim3(256), 0, stream, input, V, g);
+        else hipLaunchKernelGGL(wino_input_v4_kernel<2>, grid, dim3(256), 0, stream, input, V, g);
+        st = hip_error(hipGetLastError(), "wino_input_v4_kernel launch");
+    } else {
+        hipLaunchKernelGGL(wino_input_kernel, dim3(blocks_for(IC * g.NT)), dim3(256), 0, stream,
+                           input, V, g);
+        st = hip_error(hipGetLastError(), "wino_input_kernel launch");
+    }
     if (st) return st;
 
     // 36 GEMMs M_a[OC, NT] = U_a[OC, IC] * V_a[IC, NT] in one batched launch
