@@ -21,6 +21,8 @@
 // Compared with im2col + GEMM this moves ~2.3x fewer HBM bytes at C5
 // (V and M are 36/16 of the input / output size, against the 9x im2col
 // buffer) and does 4x fewer multiplies in the GEMM.
+#include <type_traits>
+
 #include "cdx_internal.hpp"
 
 namespace cdx {
@@ -63,11 +65,8 @@ __device__ __forceinline__ void wino_at(const float* m, float* o) {
 // spatial axes reversed (tap t read from 8 - t): the stride-1 transposed
 // convolution's filter, for backward data.
 template <bool FLIP>
-__global__ __launch_bounds__(256)
-void wino_filter_kernel(const float* __restrict__ w, float* __restrict__ U, int64_t OC,
-                        int64_t IC) {
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // oc * IC + ic
-    if (p >= OC * IC) return;
+__device__ __forceinline__ void wino_filter_one(const float* __restrict__ w, float* __restrict__ U,
+                                                int64_t OC, int64_t IC, int64_t p) {
     float g[9];
     if (FLIP) {
         const int64_t oc = p / IC, ic = p - oc * IC;
@@ -92,6 +91,15 @@ void wino_filter_kernel(const float* __restrict__ w, float* __restrict__ U, int6
 #pragma unroll
         for (int j = 0; j < 6; ++j) U[(i * 6 + j) * plane + p] = u[j];
     }
+}
+
+template <bool FLIP>
+__global__ __launch_bounds__(256)
+void wino_filter_kernel(const float* __restrict__ w, float* __restrict__ U, int64_t OC,
+                        int64_t IC) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // oc * IC + ic
+    if (p >= OC * IC) return;
+    wino_filter_one<FLIP>(w, U, OC, IC, p);
 }
 
 __global__ __launch_bounds__(256)
@@ -140,10 +148,8 @@ void wino_input_kernel(const float* __restrict__ x, float* __restrict__ V, WinoG
 // read consecutive 16-byte words) instead of six 4-byte loads.  Same
 // arithmetic per tile as wino_input_kernel.
 template <int SH>
-__global__ __launch_bounds__(256)
-void wino_input_v4_kernel(const float* __restrict__ x, float* __restrict__ V, WinoGeom g) {
-    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // ic * NT + tile
-    if (q >= g.IC * g.NT) return;
+__device__ __forceinline__ void wino_input_v4_one(const float* __restrict__ x, float* __restrict__ V,
+                                                  const WinoGeom& g, int64_t q) {
     const int64_t ic = q / g.NT, tile = q - ic * g.NT;
     const int64_t per_img = g.TH * g.TW;
     const int64_t b = tile / per_img, r = tile - b * per_img;
@@ -183,6 +189,24 @@ void wino_input_v4_kernel(const float* __restrict__ x, float* __restrict__ V, Wi
 #pragma unroll
         for (int j = 0; j < 6; ++j) V[(i * 6 + j) * plane + q] = t[j];
     }
+}
+
+// The filter transform rides in the same launch: workgroups [0, fblocks)
+// transform the filter (independent of the input transform, and consumed
+// only by the GEMM after both), the rest the input -- one launch, and the
+// filter's short, latency-bound work overlaps the input transform.
+template <int SH, bool FLIP>
+__global__ __launch_bounds__(256)
+void wino_filter_input_v4_kernel(const float* __restrict__ w, float* __restrict__ U,
+                                 const float* __restrict__ x, float* __restrict__ V, WinoGeom g,
+                                 int64_t fblocks) {
+    if ((int64_t)blockIdx.x < fblocks) {
+        const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // oc * IC + ic
+        if (p < g.OC * g.IC) wino_filter_one<FLIP>(w, U, g.OC, g.IC, p);
+        return;
+    }
+    const int64_t q = ((int64_t)blockIdx.x - fblocks) * blockDim.x + threadIdx.x;   // ic * NT + tile
+    if (q < g.IC * g.NT) wino_input_v4_one<SH>(x, V, g, q);
 }
 
 __global__ __launch_bounds__(256)
@@ -256,21 +280,30 @@ int launch_conv2d_winograd_f32(const float* input, const float* weight, const fl
     float* V = U + 36 * OC * IC;
     float* Mm = V + 36 * IC * g.NT;
 
-    if (flip_filter)
-        hipLaunchKernelGGL(wino_filter_kernel<true>, dim3(blocks_for(OC * IC)), dim3(256), 0,
-                           stream, weight, U, OC, IC);
-    else
-        hipLaunchKernelGGL(wino_filter_kernel<false>, dim3(blocks_for(OC * IC)), dim3(256), 0,
-                           stream, weight, U, OC, IC);
-    int st = hip_error(hipGetLastError(), "wino_filter_kernel launch");
-    if (st) return st;
+    int st;
     if (IW % 4 == 0 && PW >= 0 && PW <= 2 && (uintptr_t)input % 16 == 0) {
-        const dim3 grid(blocks_for(IC * g.NT));
-        if (PW == 0) hipLaunchKernelGGL(wino_input_v4_kernel<4>, grid, dim3(256), 0, stream, input, V, g);
-        else if (PW == 1) hipLaunchKernelGGL(wino_input_v4_kernel<3>, grid, dim3(256), 0, stream, input, V, g);
-        else hipLaunchKernelGGL(wino_input_v4_kernel<2>, grid, dim3(256), 0, stream, input, V, g);
-        st = hip_error(hipGetLastError(), "wino_input_v4_kernel launch");
+        // filter + input transforms in one launch
+        const int64_t fb = blocks_for(OC * IC);
+        const dim3 grid((unsigned)(fb + blocks_for(IC * g.NT)));
+        auto go = [&](auto sh, auto flip) {
+            hipLaunchKernelGGL((wino_filter_input_v4_kernel<decltype(sh)::value, decltype(flip)::value>),
+                               grid, dim3(256), 0, stream, weight, U, input, V, g, fb);
+        };
+        using F = std::false_type;
+        using T = std::true_type;
+        if (PW == 0) flip_filter ? go(std::integral_constant<int, 4>{}, T{}) : go(std::integral_constant<int, 4>{}, F{});
+        else if (PW == 1) flip_filter ? go(std::integral_constant<int, 3>{}, T{}) : go(std::integral_constant<int, 3>{}, F{});
+        else flip_filter ? go(std::integral_constant<int, 2>{}, T{}) : go(std::integral_constant<int, 2>{}, F{});
+        st = hip_error(hipGetLastError(), "wino_filter_input_v4_kernel launch");
     } else {
+        if (flip_filter)
+            hipLaunchKernelGGL(wino_filter_kernel<true>, dim3(blocks_for(OC * IC)), dim3(256), 0,
+                               stream, weight, U, OC, IC);
+        else
+            hipLaunchKernelGGL(wino_filter_kernel<false>, dim3(blocks_for(OC * IC)), dim3(256), 0,
+                               stream, weight, U, OC, IC);
+        st = hip_error(hipGetLastError(), "wino_filter_kernel launch");
+        if (st) return st;
         hipLaunchKernelGGL(wino_input_kernel, dim3(blocks_for(IC * g.NT)), dim3(256), 0, stream,
                            input, V, g);
         st = hip_error(hipGetLastError(), "wino_input_kernel launch");
