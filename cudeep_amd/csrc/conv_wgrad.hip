@@ -454,6 +454,8 @@ void conv_wgrad_rows_kernel(RwArgs p) {
     // (left of the segment) when hp < PW, else BKP + hp (right of it); input
     // column ow0 - PW + pos
     const bool h_thread = tid < 2 * SH_::X_ROWS;
+    // waves holding halo threads (wave-uniform): only they load and store halo columns
+    const bool h_wave = __builtin_amdgcn_readfirstlane(tid >> 6) < (2 * SH_::X_ROWS + 63) / 64;
     int h_src = 0, h_row = 0, h_c1 = 0, h_c2 = 0, h_kh = 0, h_col = 0;
     bool h_ok = false;
     if (h_thread) {
@@ -537,15 +539,18 @@ void conv_wgrad_rows_kernel(RwArgs p) {
                 }
             }
         }
-        {
-            // every thread loads (non-halo threads the input's first element),
-            // so no branch splits the load sequence
+        if (h_wave) {
+            // every thread of a halo wave loads (non-halo threads the input's
+            // first element); the other waves issue no halo load at all
             const int iw = ow0 + h_col;
             const bool ok = valid && h_thread && h_ok &&
                             (unsigned)(l_oh - p.PH + h_kh) < (unsigned)p.IH &&
                             (unsigned)iw < (unsigned)p.IW;
             st.vh = *(ok ? xk + h_src : p.x);
             st.ok = (st.ok & 0x7fffffffu) | ((uint32_t)ok << 31);
+        } else {
+            st.vh = 0.0f;
+            st.ok &= 0x7fffffffu;
         }
         if (valid && ++ld_seg == p.nseg) {
             ld_seg = 0;
@@ -582,7 +587,7 @@ void conv_wgrad_rows_kernel(RwArgs p) {
                     sX[x_row[u] + c2] = v;
                 }
             }
-        {
+        if (h_wave) {
             const float v = zsel(st.vh, st.ok >> 31);
             float* dummy = lds + 2 * SEGS * STAGE + tid;
             *(h_thread ? sX + h_row + h_c1 : dummy) = v;
