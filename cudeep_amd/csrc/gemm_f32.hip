@@ -411,8 +411,7 @@ int launch_cfg(const KParams& kp, int splits, hipStream_t stream) {
     return hip_error(hipGetLastError(), "gemm_f32_mfma_kernel launch");
 }
 
-template <class CF, int OPA, int OPB, bool BLK>
-int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+KParams kparams_of(const GemmArgs& g, int64_t k_chunk) {
     KParams kp{static_cast<const float*>(g.A), static_cast<const float*>(g.B), g.C, g.bias,
                g.M, g.N, g.K, g.lda, g.ldb, g.ldc,
                g.n_split, g.ldc_split, g.bias_mode, g.epilogue, k_chunk,
@@ -424,6 +423,12 @@ int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stre
     // 14 us with both operands scalar)
     kp.vec_a = ((uintptr_t)g.A % 16 == 0) && g.lda % 4 == 0 && g.stride_a % 4 == 0;
     kp.vec_b = ((uintptr_t)g.B % 16 == 0) && g.ldb % 4 == 0 && g.stride_b % 4 == 0;
+    return kp;
+}
+
+template <class CF, int OPA, int OPB, bool BLK>
+int launch_mode(const GemmArgs& g, int splits, int64_t k_chunk, hipStream_t stream) {
+    KParams kp = kparams_of(g, k_chunk);
     bool aligned = g.ones_col < 0 && kp.vec_a && kp.vec_b && g.K > 0 && g.M % CF::BM == 0 &&
                    g.N % CF::BN == 0 &&
                    g.K % CF::BK == 0 && k_chunk % CF::BK == 0;
@@ -482,7 +487,9 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    one tile row: 64 x 100352 x 576 in 70-72 us, against 73-74 with 4
 //    waves of 32x32, 81 with 8 waves of 16x32 or 32x16, 81 with 64x128
 //    tiles of 8 waves of 16x64, 79-84 with 64x32 / 32x64 tiles, 123-125
-//    with 64x128 / 64x256 tiles of 32x64 waves, 218 with BK = 32.
+//    with 64x128 / 64x256 tiles of 32x64 waves, 218 with BK = 32.  A short
+//    last round of tiles runs as 64x32 / 64x16 tiles (gemm_f32_skinny_rem_kernel):
+//    that product 70.8 -> 64.4 us, C5's first im2col round 42.1 -> 39.3.
 //  * NarrowN: N <= 16 (the MLP's 10-class layer): 32x16 tiles, 2 waves, and
 //    a deep k-tile (64): such products read A once and are bound by the
 //    latency of their k-loop, so each workgroup takes few, large k-steps and
@@ -503,6 +510,66 @@ using CfgSkinnyM = Cfg<64, 64, 16, 16, 64, 1, 2>;
 using CfgNarrowN = Cfg<32, 16, 64, 16, 16, 8, 2>;
 using CfgW112 = Cfg<128, 112, 16, 16, 112, 8, 2>;
 using CfgSplitTall = Cfg<128, 64, 16, 32, 32, 8, 2>;
+using CfgSkinnyHalf = Cfg<64, 32, 16, 16, 32, 1, 2>;
+using CfgSkinnyQuarter = Cfg<64, 16, 16, 16, 16, 1, 2>;
+
+// SkinnyM products whose 64-column tiles leave a last round over the 256 CUs
+// well short of full: those last tiles run as f = 2 or 4 times as many
+// 64 x (64 / f) tiles (same 256 threads, waves of 16 x 64 / f) after the full
+// ones, so the busiest CU's share of the last round drops from one tile to
+// ceil(rem * f / 256) / f of one (C5's im2col rounds, 882 and 686 tiles: 4 ->
+// 3.5 and 3 -> 2.75 tiles).  Every output keeps its k order: the sums are the
+// same bits as on 64 x 64 tiles.  NN, whole tiles only.
+template <class CFR, bool SPLITN, bool BLK>
+__global__ __launch_bounds__(CfgSkinnyM::NT)
+void gemm_f32_skinny_rem_kernel(KParams p, int full_tiles) {
+    static_assert(CfgSkinnyM::NT == CFR::NT && CFR::BM == CfgSkinnyM::BM, "same block, same rows");
+    constexpr int L1 = Geo<CfgSkinnyM, CDX_OP_N, CDX_OP_N>::LDS_FLOATS;
+    constexpr int L2 = Geo<CFR, CDX_OP_N, CDX_OP_N>::LDS_FLOATS;
+    __shared__ __attribute__((aligned(16))) float lds[L1 > L2 ? L1 : L2];
+    const int b = blockIdx.x;
+    if (b < full_tiles)
+        gemm_tile<CfgSkinnyM, CDX_OP_N, CDX_OP_N, kLoadAlignedVec, SPLITN, BLK>(
+            p, 0, (int64_t)b * CfgSkinnyM::BN, lds);
+    else
+        gemm_tile<CFR, CDX_OP_N, CDX_OP_N, kLoadAlignedVec, SPLITN, BLK>(
+            p, 0, (int64_t)full_tiles * CfgSkinnyM::BN + (int64_t)(b - full_tiles) * CFR::BN, lds);
+}
+
+// Full tile count and split factor f of the last round when the split launch
+// applies: an unsplit NN product of exactly one 64-row tile, whole 64-column
+// tiles, whole k-tiles, 16-byte loadable operands, and a last round of rem
+// tiles that f splits to less than one tile per CU: f = 4 for rem <= 64
+// (1/4) and 128 < rem <= 192 (3/4), f = 2 for 64 < rem <= 128 (1/2).
+bool skinny_rem_plan(const GemmArgs& g, int64_t& full, int& f) {
+    const KParams kp = kparams_of(g, g.K);
+    if (g.M != CfgSkinnyM::BM || g.N % CfgSkinnyM::BN != 0 || g.K <= 0 ||
+        g.K % CfgSkinnyM::BK != 0 || g.batch != 1 || g.ones_col >= 0 || !kp.vec_a ||
+        !kp.vec_b || g.opA != CDX_OP_N || g.opB != CDX_OP_N)
+        return false;
+    const int64_t tiles = g.N / CfgSkinnyM::BN, rem = tiles % 256;
+    if (rem == 0 || rem > 192 || tiles + 3 * rem > INT32_MAX) return false;
+    full = tiles - rem;
+    f = rem > 64 && rem <= 128 ? 2 : 4;
+    return true;
+}
+
+template <bool BLK>
+int launch_skinny_rem(const GemmArgs& g, int64_t full, int f, hipStream_t stream) {
+    const KParams kp = kparams_of(g, g.K);
+    const int64_t rem = g.N / CfgSkinnyM::BN - full;
+    const dim3 grid((unsigned)(full + f * rem)), block(CfgSkinnyM::NT);
+    const bool sn = g.n_split > 0;
+    if (f == 2 && sn)
+        hipLaunchKernelGGL((gemm_f32_skinny_rem_kernel<CfgSkinnyHalf, true, BLK>), grid, block, 0, stream, kp, (int)full);
+    else if (f == 2)
+        hipLaunchKernelGGL((gemm_f32_skinny_rem_kernel<CfgSkinnyHalf, false, BLK>), grid, block, 0, stream, kp, (int)full);
+    else if (sn)
+        hipLaunchKernelGGL((gemm_f32_skinny_rem_kernel<CfgSkinnyQuarter, true, BLK>), grid, block, 0, stream, kp, (int)full);
+    else
+        hipLaunchKernelGGL((gemm_f32_skinny_rem_kernel<CfgSkinnyQuarter, false, BLK>), grid, block, 0, stream, kp, (int)full);
+    return hip_error(hipGetLastError(), "gemm_f32_skinny_rem_kernel launch");
+}
 
 // Configuration choice, shared by the launcher and the workspace query.
 enum class F32Cfg { NarrowN, SkinnyM, Huge, Large, Medium, W112, SplitTall };
@@ -566,6 +633,11 @@ int launch_gemm_f32(const GemmArgs& g, hipStream_t stream) {
     if (narrow_kind(g)) return launch_gemm_narrow(g, stream);
     bool blocked;
     const F32Cfg c = choose_f32(g, blocked);
+    int64_t full = 0;
+    int f = 1;
+    if (c == F32Cfg::SkinnyM && skinny_rem_plan(g, full, f))
+        return blocked ? launch_skinny_rem<true>(g, full, f, stream)
+                       : launch_skinny_rem<false>(g, full, f, stream);
     if (blocked) {
         switch (c) {
             case F32Cfg::NarrowN: return launch_blocked<CfgNarrowN>(g, stream);

@@ -211,6 +211,34 @@ def test_fp32_mid_size_tile_choice(M, N, K, tA, tB):
     assert _checksum_identity(A.T if tA else A, B.T if tB else B, C) < 1e-5
 
 
+@pytest.mark.parametrize("tiles", [20, 100, 256 + 40, 256 + 100, 512 + 150, 512 + 174])
+@pytest.mark.parametrize("K", [48, 576])
+def test_fp32_skinny_last_round_split(tiles, K):
+    """64-row NN products whose 64-column tiles leave a short last round over
+    the 256 CUs run that round as 64 x 32 or 64 x 16 tiles (the conv GEMM's
+    shape).  The same columns inside a wider product of whole rounds only
+    (every tile 64 x 64) must come out bit for bit the same; sampled columns
+    across the full / split boundary and the last ones against the seq-FMA
+    restatement; the column-checksum identity over the whole product."""
+    N = 64 * tiles
+    Nw = 64 * 256 * ((tiles + 255) // 256)          # whole rounds: no split tiles
+    rng = np.random.default_rng(tiles * 7 + K)
+    A = normal(rng, (64, K))
+    Bw = normal(rng, (K, Nw))
+    B = np.ascontiguousarray(Bw[:, :N])
+    say("fp32 skinny split", tiles, K)
+    C = host(ops().gemm(dev(A), dev(B)))
+    Cw = host(ops().gemm(dev(A), dev(Bw)))
+    assert np.array_equal(C.view(np.uint32), Cw[:, :N].view(np.uint32))
+    full = 64 * (tiles - tiles % 256)
+    for c0 in sorted({max(0, full - 96), N - 192}):
+        Bs = np.ascontiguousarray(B[:, c0:c0 + 192])
+        C64, e_ref = _ref_errors(A, Bs)
+        e = oracle.rel_fro(np.ascontiguousarray(C[:, c0:c0 + 192]), C64)
+        assert e <= 2 * e_ref, (c0, e, e_ref)
+    assert _checksum_identity(A, B, C) < 1e-5
+
+
 @pytest.mark.parametrize("M,N,K", [(8192, 784, 256), (5000, 784, 100), (4100, 1008, 77)])
 @pytest.mark.parametrize("tA,tB", [(False, False), (False, True), (True, False), (True, True)])
 def test_fp32_w112_tiles(M, N, K, tA, tB):
