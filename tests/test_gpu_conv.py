@@ -587,3 +587,23 @@ def test_conv_f64_full_precision_operands():
     assert abs(float(np.sum(x * dx)) - lin) <= 1e-12 * abs(lin)
     assert abs(float(np.sum(w * dw)) - lin) <= 1e-12 * abs(lin)
     assert np.allclose(db, dy.sum(axis=(0, 2, 3)), rtol=1e-14, atol=0)
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_conv_three_rounds_same_bits_as_single_images(prec):
+    """A batch of 40 C5-size images runs the im2col route in three rounds of
+    15 + 15 + 10 images through one 15-image column buffer (the round size
+    with the fewest waves of GEMM tiles): images at both round boundaries and
+    at the ends come out bit for bit as when convolved alone."""
+    rng = np.random.default_rng(5252)
+    x = normal(rng, (40, 64, 56, 56))
+    w = normal(rng, (64, 64, 3, 3), std=np.sqrt(2.0 / 576))
+    b = normal(rng, (64,), 0.1)
+    say("conv 40 images three rounds prec", prec)
+    assert ops().conv2d_workspace_bytes(x.shape, w.shape, (1, 1), (1, 1)) == 15 * 576 * 3136 * 4
+    gx, gw, gb = dev(x), dev(w), dev(b)
+    y = host(ops().conv2d_forward(gx, gw, gb, (1, 1), (1, 1), precision=prec))
+    for i in (0, 14, 15, 29, 30, 39):
+        yi = host(ops().conv2d_forward(gx[i:i + 1].contiguous(), gw, gb, (1, 1), (1, 1),
+                                       precision=prec))
+        assert np.array_equal(yi[0].view(np.uint32), y[i].view(np.uint32)), i
