@@ -607,3 +607,26 @@ def test_conv_three_rounds_same_bits_as_single_images(prec):
         yi = host(ops().conv2d_forward(gx[i:i + 1].contiguous(), gw, gb, (1, 1), (1, 1),
                                        precision=prec))
         assert np.array_equal(yi[0].view(np.uint32), y[i].view(np.uint32)), i
+
+
+@pytest.mark.parametrize("H,W", [(22, 1024), (20, 1024)])
+def test_conv_backward_data_wide_rows_gemm_route(H, W):
+    """Stride-1 backward data of 1024-pixel-wide rows takes the im2col + GEMM
+    route of the transposed convolution (its row window does not fit in
+    LDS) with a two-level k sum: 64 output channels x 352 / 320 column tiles,
+    whose last round over the 256 CUs (96 / 64 tiles) runs as half / quarter
+    tiles.  FP32 against the reference's route (GEMM + col2im) to 2x its
+    error vs fp64."""
+    rng = np.random.default_rng(H * 1000 + W)
+    C = OC = 64
+    w = normal(rng, (OC, C, 3, 3), std=np.sqrt(2.0 / (C * 9)))
+    dy = normal(rng, (1, OC, H, W))
+    xs = (1, C, H, W)
+    assert ops().conv2d_backward_data_workspace_bytes(xs, w.shape, (1, 1), (1, 1)) > w.size * 4
+    say("conv bwd data wide rows", H, W)
+    dx = host(ops().conv2d_backward_data(dev(dy), dev(w), xs, (1, 1), (1, 1), precision=0))
+    dx64 = oracle.conv2d_backward_data64(dy, w, xs, (1, 1), (1, 1))
+    e_ref = oracle.rel_fro(oracle.conv2d_backward_data_ref(dy, w, xs, (1, 1), (1, 1)), dx64)
+    e = oracle.rel_fro(dx, dx64)
+    print(f"bwd data {H}x{W}: gpu={e:.3e} reference route={e_ref:.3e}")
+    assert e <= 2 * e_ref + 2.0 ** -24
