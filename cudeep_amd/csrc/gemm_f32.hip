@@ -488,8 +488,7 @@ int launch_blocked(const GemmArgs& g, hipStream_t stream) {
 //    waves of 32x32, 81 with 8 waves of 16x32 or 32x16, 81 with 64x128
 //    tiles of 8 waves of 16x64, 79-84 with 64x32 / 32x64 tiles, 123-125
 //    with 64x128 / 64x256 tiles of 32x64 waves, 218 with BK = 32.  A short
-//    last round of tiles runs as 64x32 / 64x16 tiles (gemm_f32_skinny_rem_kernel):
-//    that product 70.8 -> 64.4 us, C5's first im2col round 42.1 -> 39.3.
+//    last round of tiles runs as 64x32 / 64x16 tiles (gemm_f32_skinny_rem_kernel).
 //  * NarrowN: N <= 16 (the MLP's 10-class layer): 32x16 tiles, 2 waves, and
 //    a deep k-tile (64): such products read A once and are bound by the
 //    latency of their k-loop, so each workgroup takes few, large k-steps and
@@ -517,9 +516,11 @@ using CfgSkinnyQuarter = Cfg<64, 16, 16, 16, 16, 1, 2>;
 // well short of full: those last tiles run as f = 2 or 4 times as many
 // 64 x (64 / f) tiles (same 256 threads, waves of 16 x 64 / f) after the full
 // ones, so the busiest CU's share of the last round drops from one tile to
-// ceil(rem * f / 256) / f of one (C5's im2col rounds, 882 and 686 tiles: 4 ->
-// 3.5 and 3 -> 2.75 tiles).  Every output keeps its k order: the sums are the
-// same bits as on 64 x 64 tiles.  NN, whole tiles only.
+// ceil(rem * f / 256) / f of one.  C5's im2col rounds, 882 and 686 tiles: 4
+// -> 3.5 tiles, 42.1 -> 39.3 us, and 3 -> 2.75 tiles, unchanged at 33.3 us;
+// the whole batch, 1568 tiles: 7 -> 6.25, 70.8 -> 64.4 us.  Every output
+// keeps its k order: the sums are the same bits as on 64 x 64 tiles.  NN,
+// whole tiles only.
 template <class CFR, bool SPLITN, bool BLK>
 __global__ __launch_bounds__(CfgSkinnyM::NT)
 void gemm_f32_skinny_rem_kernel(KParams p, int full_tiles) {
