@@ -681,10 +681,15 @@ void conv_wgrad_rows_kernel(RwArgs p) {
         load_g(st);
         store_g(st, 0);
         __syncthreads();
+        // (wave priority 1 over the MFMAs: on a SIMD shared with waves
+        // storing their staging sets, the MFMA chains issue first -- C5
+        // 84.9 -> 84.0 us, same bits)
         for (int k = 0; k < nkt; ++k) {
             const bool more = k + 1 < nkt;
             if (more) load_g(st);
+            __builtin_amdgcn_s_setprio(1);
             compute_g(k & 1);
+            __builtin_amdgcn_s_setprio(0);
             if (more) store_g(st, (k & 1) ^ 1);
             __syncthreads();
         }
