@@ -641,14 +641,14 @@ __device__ __forceinline__ void rowwin_body(const RfArgs& p, uint32_t bx, uint32
         // STAGE: stage chunk c + 1's window (every chunk but the last).
         // (scheduling barriers keep the slice loads ahead of the MFMAs and
         // the slice stores, which wait for them, behind)
-        // (wave priority 1 from the B reads and MFMAs through the filter
-        // refill: on a SIMD shared with waves staging, this wave's MFMA
-        // chain issues first -- C5 forward 72.6 -> 71.6 us, backward data
-        // 75.3 -> 74.2, 7x7 380 -> 379, same bits)
+        // (wave priority 1 from the slice loads through the filter refill,
+        // the slice stores at 0: on a SIMD shared with waves storing their
+        // slices, this wave's MFMA chain issues first -- C5 forward 72.6 ->
+        // 71.5 us, backward data 75.3 -> 73.9, 7x7 380 -> 373, same bits)
         constexpr bool STAGE = decltype(stage)::value;
+        __builtin_amdgcn_s_setprio(1);
         if constexpr (STAGE) slice_load(c + 1, g);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(1);
         if constexpr (HALF) compute_half(a, g);
         else compute(a, g);
         a_load(a);
